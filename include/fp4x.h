@@ -1,0 +1,165 @@
+/* fp4x — decode-shaped (M <= 16) quantized GEMV kernels for MI355X (gfx950).
+ *
+ * C ABI of libfp4x.so.  Every entry point takes raw device pointers, sizes,
+ * and the HIP stream to launch on (hipStream_t passed as void*).  Calls are
+ * asynchronous on that stream, allocate no device memory, read no device
+ * memory from the host, and are capturable into HIP graphs.  They return
+ * FP4X_OK (0) or a negative error code; fp4x_last_error() describes the last
+ * failure on the calling thread.
+ *
+ * Bracketed references name the plugin-kernel interface (file:line in the
+ * reference tree) each entry point replaces.  Packed layouts are unchanged
+ * from the reference:
+ *   MXFP8  w u8/e4m3fn [N, K], s u8/e8m0 [N, K/32]
+ *   W8 g64 q int8 [N, K], s fp32 (or fp16) [N, K/64]
+ *   W6 g32 L u8 [N, K/2] (low nibble = even k), H u8 [N, K/4] (bit pairs of
+ *          k%4 = 0, 2, 1, 3), S fp16 [N, K/32]; weight = (lo | hi<<4) - 32
+ *   NVFP4  P u8 [N, K/2] (e2m1, low nibble = even k), S e4m3fn [N, K/16], gs fp32
+ *   INT2   P u8 [N, K/4] (element j of a 4-group in bit pair (0,2,1,3)[j]),
+ *          S fp16 or e4m3fn [N, K/G]; weight = (code - 1.5) * s
+ * Activations x are bf16 [M, K] with row stride x_stride elements (16-byte
+ * aligned, x_stride % 8 == 0).  Outputs are [M, N] row-major in out_dtype.
+ *
+ * Split-K (ksplit > 1): `part` is fp32 scratch of fp4x_splitk_sizes()
+ * floats and `tickets` int32 scratch of that many counters, zeroed once
+ * before first use.  Every call leaves the tickets at zero again.  Calls that
+ * share scratch must be ordered (same stream); concurrent calls race.
+ */
+#ifndef FP4X_H_
+#define FP4X_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FP4X_ABI_VERSION 1
+
+enum {
+  FP4X_OK = 0,
+  FP4X_ERR_ARG = -1,     /* invalid shape, alignment or argument */
+  FP4X_ERR_LAUNCH = -2,  /* the HIP runtime rejected a launch */
+};
+
+/* dtypes of outputs and scales */
+enum { FP4X_DT_BF16 = 0, FP4X_DT_F32 = 1, FP4X_DT_F16 = 2, FP4X_DT_E4M3 = 3 };
+
+/* weight formats (fp4x_layout, fp4x_splitk_sizes, fp4x_dequant_bf16) */
+enum {
+  FP4X_FMT_MX8 = 0,
+  FP4X_FMT_W8_F32 = 1,
+  FP4X_FMT_W8_F16 = 2,
+  FP4X_FMT_W6 = 3,
+  FP4X_FMT_NV4 = 4,
+  FP4X_FMT_INT2_F16 = 5,
+  FP4X_FMT_INT2_E4M3 = 6,
+  FP4X_FMT_BF16 = 7,
+};
+
+const char* fp4x_last_error(void);
+int fp4x_abi_version(void);
+
+/* Lane layout of a K slice: lanes per row and 16-byte chunks per lane. */
+int fp4x_layout(int fmt, int k_slice, int* lpr, int* cpl);
+
+/* Scratch needed by a split-K call: fp32 slots and int32 tickets. */
+int fp4x_splitk_sizes(int fmt, int M, int N, int K, int ksplit, int batch, int64_t* part_floats,
+                      int64_t* n_tickets);
+
+/* y = x . bf16(e4m3(w) * 2^(s-127))^T, fp32 accumulate.
+ * [mx8_linear -> _run -> _mx8, x/fp4x_kernels.py:65-66, :50-62, :9-29] */
+int fp4x_mx8_linear(const void* x, int64_t x_stride, const void* w, const void* s, void* out, int out_dtype,
+                    int M, int N, int K, int ksplit, float* part, int* tickets, void* stream);
+
+/* y = x . w^T with bf16 weights w [N, K].
+ * [bf16_linear -> _run -> _bg, x/fp4x_kernels.py:69-70, :50-62, :32-47] */
+int fp4x_bf16_linear(const void* x, int64_t x_stride, const void* w, void* out, int out_dtype, int M, int N, int K,
+                     int ksplit, float* part, int* tickets, void* stream);
+
+/* y = x . bf16(q * s)^T, s fp32 (FP4X_DT_F32, the reference layout) or fp16.
+ * [w8_linear -> _run -> _w8, x/fp4x_kernels.py:147-148, :50-62, :116-135] */
+int fp4x_w8_linear(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* out,
+                   int out_dtype, int M, int N, int K, int ksplit, float* part, int* tickets, void* stream);
+
+/* fp4x_w8_linear over `layers` independent (x, q, s, out) entries in one
+ * launch; *_lstride are the per-layer strides in elements of each tensor.
+ * [one w8_linear launch per router gate, x/fp4patch.py:264-272; batching
+ * independent layers into one launch is this library's extension] */
+int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, const void* q, int64_t q_lstride,
+                          const void* s, int s_dtype, int64_t s_lstride, void* out, int out_dtype,
+                          int64_t out_lstride, int layers, int M, int N, int K, int ksplit, float* part,
+                          int* tickets, void* stream);
+
+/* y = x . bf16(((lo | hi << 4) - 32) * S)^T.
+ * [w6_linear -> _run -> _w6, x/fp4x_kernels.py:270-271, :151-176] */
+int fp4x_w6_linear(const void* x, int64_t x_stride, const void* L, const void* H, const void* S, void* out,
+                   int out_dtype, int M, int N, int K, int ksplit, float* part, int* tickets, void* stream);
+
+/* y = gs * (x . bf16(e2m1(P) * e4m3(S))^T).
+ * [nv4_linear -> _nv4, x/fp4x_kernels.py:102-113, :73-99] */
+int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* S, float gs, void* out,
+                    int out_dtype, int M, int N, int K, int ksplit, float* part, int* tickets, void* stream);
+
+/* y = x . bf16((code - 1.5) * S)^T (times rs[n] when rs != NULL), out [M, N].
+ * s_fmt = FP4X_DT_F16 or FP4X_DT_E4M3; G = K / S.shape[1].
+ * [int2_logits -> _int2_head, x/fp4x_kernels.py:359-364, :304-325] */
+int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
+                     void* out, int out_dtype, int M, int N, int K, int G, void* stream);
+
+/* Top-C of each row of bf16 logits [M, V] under the total order (value
+ * descending, then index ascending; -0 equals +0, NaN is largest); idx_out
+ * int64 [M, C] lists the selected indices in that order.  C <= min(V, 2048);
+ * logits 16-byte aligned with stride % 8 == 0.
+ * [torch.topk(coarse, C) in the fast head, x/fp4patch.py:377] */
+int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int64_t* idx_out, void* stream);
+
+/* In place: out[m, idx[m, c]] = cast(sum_k float(e4m3(w)*2^(s-127)) * float(x[m, k])).
+ * out is [M, V] in out_dtype, x bf16 [M, K] contiguous, idx int64 [M, C].
+ * [refine_mx8_ -> _refine_mx8, x/fp4x_kernels.py:384-388, :367-381] */
+int fp4x_refine_mx8(void* out, int out_dtype, int64_t out_stride, const void* x, const int64_t* idx, int M, int C,
+                    const void* w, const void* s, int K, int V, void* stream);
+
+/* Mixer down projection: split-K W8 GEMV whose last workgroup per row tile
+ * writes di = bf16(sum) [M, N] and bot = bf16(sc * sigmoid(sc)) [M, lr] with
+ * sc = bf16(di / hc), then re-arms its ticket.
+ * [HCFused.down -> _hc_down, x/fp4x_kernels.py:503-510, :438-467] */
+int fp4x_hc_down(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* di, void* bot,
+                 int M, int N, int K, int lr, int hc, int ksplit, float* part, int* tickets, void* stream);
+
+/* Mixer up projection over stream-interleaved rows (tile of hc*bj rows holds
+ * rows s*H + j*bj + t), with the gate/stream-mean epilogue:
+ * out[m, j] = bf16(sum_s bf16(nrm[m, s*H + j] * bf16(sigmoid(bf16(acc)))) / hc).
+ * [HCFused.up -> _hc_up, x/fp4x_kernels.py:519-526, :470-493] */
+int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* si, int s_dtype, const void* nrm,
+               int64_t nrm_stride, void* out, int M, int K, int H, int hc, int bj, void* stream);
+
+/* Unfused mixer epilogues (the b12x run_scaled_silu / run_gate_mean ops the
+ * plugin calls, x/fp4patch.py:238-246, at the rounding points of
+ * x/fp4x_kernels.py:461-464 and :486-493).
+ * scaled_silu: bot[m, n] = bf16(sc * sigmoid(sc)), sc = bf16(d[m, n] / hc), n < lr.
+ * gate_mean:   out[m, j] as in fp4x_hc_up, from bf16 gate logits g [M, hc*H]. */
+int fp4x_hc_scaled_silu(const void* d, int64_t d_stride, void* bot, int M, int lr, int hc, void* stream);
+int fp4x_hc_gate_mean(const void* nrm, int64_t nrm_stride, const void* g, int64_t g_stride, void* out, int M, int H,
+                      int hc, void* stream);
+
+/* bf16 operand of each weight as the GEMV kernels decode it, out bf16 [N, K].
+ * w0/w1/s are the format's planes (w1 only for W6).
+ * [the in-kernel dequant of _mx8/_w8/_w6/_nv4/_int2_head, x/fp4x_kernels.py:19-23,
+ *  :126-129, :161-170, :84-92, :317-322] */
+int fp4x_dequant_bf16(int fmt, const void* w0, const void* w1, const void* s, int N, int K, int G, void* out,
+                      void* stream);
+
+/* fp32 MXFP8 dequant, out [N, K].  [mx8_dequant, x/fp4x_kernels.py:261-267] */
+int fp4x_mx8_dequant(const void* w, const void* s, int N, int K, float* out, void* stream);
+
+/* out[i] = a[i].lo*b[i].lo + a[i].hi*b[i].hi + c[i] with v_dot2_f32_bf16, the
+ * accumulation step of every GEMV here.  No counterpart in the reference:
+ * exposed so tests can pin the step's rounding against the oracle's model. */
+int fp4x_dot2_bf16(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FP4X_H_ */

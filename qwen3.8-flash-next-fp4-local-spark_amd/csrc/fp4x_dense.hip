@@ -1,0 +1,340 @@
+// Dense decode GEMVs (MXFP8, W8 g64, W6 g32, NVFP4, INT2 coarse head), the
+// layer-batched W8 launch, and the dequant kernels, behind a C ABI.
+#include "fp4x_kernels.h"
+#include "../../include/fp4x.h"
+#include <cstdio>
+
+namespace fp4x {
+
+// GEMV launches are instantiated in the fp4x_gemv_*.hip translation units.
+extern template int launch_gemv<FmtBF16, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtMX8, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtW8<false>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtW8<true>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtW6, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtNV4, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtInt2<false, 16>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtInt2<false, 32>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtInt2<false, 0>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtInt2<true, 16>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtInt2<true, 32>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv<FmtInt2<true, 0>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+
+static thread_local std::string g_err;
+void set_error(const std::string& msg) { g_err = msg; }
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error(std::string(what) + ": launch failed: " + hipGetErrorString(e));
+    return FP4X_ERR_LAUNCH;
+  }
+  return FP4X_OK;
+}
+
+static int fail(int code, const char* fmt, long long a = 0, long long b = 0, long long c = 0) {
+  char buf[256];
+  snprintf(buf, sizeof buf, fmt, a, b, c);
+  set_error(buf);
+  return code;
+}
+
+static bool aligned(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
+
+struct FmtInfo {
+  int kpc;      // weights per 16-byte chunk
+  int kmult;    // K must be a multiple of this
+};
+
+static FmtInfo fmt_info(int fmt) {
+  switch (fmt) {
+    case FP4X_FMT_MX8: return {16, 32};
+    case FP4X_FMT_W8_F32: case FP4X_FMT_W8_F16: return {16, 64};
+    case FP4X_FMT_W6: return {32, 32};
+    case FP4X_FMT_NV4: return {32, 32};
+    case FP4X_FMT_INT2_F16: case FP4X_FMT_INT2_E4M3: return {64, 64};
+    case FP4X_FMT_BF16: return {16, 16};
+    default: return {0, 0};
+  }
+}
+
+// Shared validation of shapes, split and activation layout.
+static int validate(int fmt, const void* x, int64_t x_stride, int M, int N, int K, int ksplit,
+                    const float* part, const int* tickets) {
+  const FmtInfo fi = fmt_info(fmt);
+  if (!fi.kpc) return fail(FP4X_ERR_ARG, "unknown weight format %lld", fmt);
+  if (M < 0 || M > 16) return fail(FP4X_ERR_ARG, "M=%lld outside [0, 16]", M);
+  if (N < 0 || K <= 0) return fail(FP4X_ERR_ARG, "bad shape N=%lld K=%lld", N, K);
+  if (K % fi.kmult) return fail(FP4X_ERR_ARG, "K=%lld must be a multiple of %lld", K, fi.kmult);
+  if (ksplit < 1 || ksplit > 64 || K % ksplit || (K / ksplit) % fi.kpc)
+    return fail(FP4X_ERR_ARG, "ksplit=%lld must divide K=%lld into multiples of %lld", ksplit, K, fi.kpc);
+  if (ksplit > 1 && (!part || !tickets)) return fail(FP4X_ERR_ARG, "ksplit=%lld needs split-K scratch", ksplit);
+  if (M > 0 && (!aligned(x, 16) || x_stride % 8 || x_stride < K))
+    return fail(FP4X_ERR_ARG, "x must be 16-byte aligned with a row stride (%lld) that is a multiple of 8 and >= K (%lld)",
+                x_stride, K);
+  return FP4X_OK;
+}
+
+static GemvLaunch base_launch(int fmt, const void* x, int64_t x_stride, void* out, int out_dtype, int64_t out_stride,
+                              int M, int N, int K, int ksplit, float* part, int* tickets) {
+  GemvLaunch p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.x_stride = x_stride;
+  p.out = out;
+  p.out_dtype = out_dtype;
+  p.out_stride = out_stride;
+  p.gs = 1.0f;
+  p.M = M;
+  p.N = N;
+  p.ksplit = ksplit;
+  const int chunks = (K / ksplit) / fmt_info(fmt).kpc;
+  p.lpr = layout_lpr(chunks);
+  p.cpl = (chunks + p.lpr - 1) / p.lpr;
+  p.part = part;
+  p.tickets = tickets;
+  p.pa.K = K;
+  p.pa.G = 0;
+  return p;
+}
+
+}  // namespace fp4x
+
+using namespace fp4x;
+
+extern "C" {
+
+const char* fp4x_last_error(void) { return g_err.c_str(); }
+
+int fp4x_abi_version(void) { return FP4X_ABI_VERSION; }
+
+int fp4x_layout(int fmt, int k_slice, int* lpr, int* cpl) {
+  const FmtInfo fi = fmt_info(fmt);
+  if (!fi.kpc || k_slice <= 0 || k_slice % fi.kpc) return fail(FP4X_ERR_ARG, "bad layout query fmt=%lld k=%lld", fmt, k_slice);
+  const int chunks = k_slice / fi.kpc;
+  *lpr = layout_lpr(chunks);
+  *cpl = (chunks + *lpr - 1) / *lpr;
+  return FP4X_OK;
+}
+
+int fp4x_splitk_sizes(int fmt, int M, int N, int K, int ksplit, int batch, int64_t* part_floats, int64_t* n_tickets) {
+  const FmtInfo fi = fmt_info(fmt);
+  if (!fi.kpc || ksplit < 1 || K % ksplit || (K / ksplit) % fi.kpc) return fail(FP4X_ERR_ARG, "bad split-K query");
+  const int chunks = (K / ksplit) / fi.kpc;
+  const int lpr = layout_lpr(chunks);
+  const int tile_rows = kWaves * (64 / lpr);   // RPL = 1
+  *part_floats = (int64_t)batch * ksplit * mt_of(M < 1 ? 1 : M) * N;
+  *n_tickets = (int64_t)batch * ((N + tile_rows - 1) / tile_rows);
+  return FP4X_OK;
+}
+
+int fp4x_mx8_linear(const void* x, int64_t x_stride, const void* w, const void* s, void* out, int out_dtype,
+                    int M, int N, int K, int ksplit, float* part, int* tickets, void* stream) {
+  int rc = validate(FP4X_FMT_MX8, x, x_stride, M, N, K, ksplit, part, tickets);
+  if (rc) return rc;
+  if (!aligned(w, 16)) return fail(FP4X_ERR_ARG, "mx8: weight rows must be 16-byte aligned");
+  if (M == 0 || N == 0) return FP4X_OK;
+  GemvLaunch p = base_launch(FP4X_FMT_MX8, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
+  p.pa.w0 = static_cast<const uint8_t*>(w);
+  p.pa.s = static_cast<const uint8_t*>(s);
+  return launch_gemv<FmtMX8, EpiStore>(p, 1, (hipStream_t)stream);
+}
+
+int fp4x_bf16_linear(const void* x, int64_t x_stride, const void* w, void* out, int out_dtype, int M, int N, int K,
+                     int ksplit, float* part, int* tickets, void* stream) {
+  int rc = validate(FP4X_FMT_BF16, x, x_stride, M, N, K, ksplit, part, tickets);
+  if (rc) return rc;
+  if (!aligned(w, 16)) return fail(FP4X_ERR_ARG, "bf16: weight rows must be 16-byte aligned");
+  if (M == 0 || N == 0) return FP4X_OK;
+  GemvLaunch p = base_launch(FP4X_FMT_BF16, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
+  p.pa.w0 = static_cast<const uint8_t*>(w);
+  return launch_gemv<FmtBF16, EpiStore>(p, 1, (hipStream_t)stream);
+}
+
+int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, const void* q, int64_t q_lstride,
+                          const void* s, int s_dtype, int64_t s_lstride, void* out, int out_dtype, int64_t out_lstride,
+                          int layers, int M, int N, int K, int ksplit, float* part, int* tickets, void* stream) {
+  const int fmt = s_dtype == FP4X_DT_F16 ? FP4X_FMT_W8_F16 : FP4X_FMT_W8_F32;
+  if (s_dtype != FP4X_DT_F16 && s_dtype != FP4X_DT_F32) return fail(FP4X_ERR_ARG, "w8: scale dtype %lld", s_dtype);
+  int rc = validate(fmt, x, x_stride, M, N, K, ksplit, part, tickets);
+  if (rc) return rc;
+  if (layers < 0) return fail(FP4X_ERR_ARG, "w8: layers=%lld", layers);
+  if (!aligned(q, 16) || (layers > 1 && (q_lstride % 16 || x_lstride % 8)))
+    return fail(FP4X_ERR_ARG, "w8: weight (and per-layer strides) must be 16-byte aligned");
+  if (!aligned(s, s_dtype == FP4X_DT_F16 ? 2 : 4)) return fail(FP4X_ERR_ARG, "w8: misaligned scales");
+  if (M == 0 || N == 0 || layers == 0) return FP4X_OK;
+  GemvLaunch p = base_launch(fmt, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
+  p.x_bstride = x_lstride;
+  p.pa.w0 = static_cast<const uint8_t*>(q);
+  p.pa.s = static_cast<const uint8_t*>(s);
+  p.w0_bstride = q_lstride;
+  p.s_bstride = s_lstride * (s_dtype == FP4X_DT_F16 ? 2 : 4);
+  p.out_bstride = out_lstride;
+  if (fmt == FP4X_FMT_W8_F16) return launch_gemv<FmtW8<true>, EpiStore>(p, layers, (hipStream_t)stream);
+  return launch_gemv<FmtW8<false>, EpiStore>(p, layers, (hipStream_t)stream);
+}
+
+int fp4x_w8_linear(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* out, int out_dtype,
+                   int M, int N, int K, int ksplit, float* part, int* tickets, void* stream) {
+  return fp4x_w8_linear_layers(x, x_stride, 0, q, 0, s, s_dtype, 0, out, out_dtype, 0, 1, M, N, K, ksplit, part,
+                               tickets, stream);
+}
+
+int fp4x_w6_linear(const void* x, int64_t x_stride, const void* L, const void* H, const void* S, void* out,
+                   int out_dtype, int M, int N, int K, int ksplit, float* part, int* tickets, void* stream) {
+  int rc = validate(FP4X_FMT_W6, x, x_stride, M, N, K, ksplit, part, tickets);
+  if (rc) return rc;
+  if (!aligned(L, 16) || !aligned(H, 8) || !aligned(S, 2)) return fail(FP4X_ERR_ARG, "w6: misaligned planes");
+  if (M == 0 || N == 0) return FP4X_OK;
+  GemvLaunch p = base_launch(FP4X_FMT_W6, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
+  p.pa.w0 = static_cast<const uint8_t*>(L);
+  p.pa.w1 = static_cast<const uint8_t*>(H);
+  p.pa.s = static_cast<const uint8_t*>(S);
+  return launch_gemv<FmtW6, EpiStore>(p, 1, (hipStream_t)stream);
+}
+
+int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* S, float gs, void* out, int out_dtype,
+                    int M, int N, int K, int ksplit, float* part, int* tickets, void* stream) {
+  int rc = validate(FP4X_FMT_NV4, x, x_stride, M, N, K, ksplit, part, tickets);
+  if (rc) return rc;
+  if (!aligned(P, 16) || !aligned(S, 2)) return fail(FP4X_ERR_ARG, "nv4: misaligned planes");
+  if (M == 0 || N == 0) return FP4X_OK;
+  GemvLaunch p = base_launch(FP4X_FMT_NV4, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
+  p.pa.w0 = static_cast<const uint8_t*>(P);
+  p.pa.s = static_cast<const uint8_t*>(S);
+  p.gs = gs;
+  return launch_gemv<FmtNV4, EpiStore>(p, 1, (hipStream_t)stream);
+}
+
+int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
+                     void* out, int out_dtype, int M, int N, int K, int G, void* stream) {
+  const int fmt = s_fmt == FP4X_DT_E4M3 ? FP4X_FMT_INT2_E4M3 : FP4X_FMT_INT2_F16;
+  if (s_fmt != FP4X_DT_E4M3 && s_fmt != FP4X_DT_F16) return fail(FP4X_ERR_ARG, "int2: scale format %lld", s_fmt);
+  int rc = validate(fmt, x, x_stride, M, N, K, 1, nullptr, nullptr);
+  if (rc) return rc;
+  if (!(G == 16 || G == 32 || (G >= 64 && G % 64 == 0)) || K % G)
+    return fail(FP4X_ERR_ARG, "int2: group size G=%lld must be 16, 32 or a multiple of 64 dividing K=%lld", G, K);
+  if (!aligned(P, 16) || !aligned(S, s_fmt == FP4X_DT_E4M3 ? (G == 16 ? 4 : 1) : (G == 16 ? 8 : 2)))
+    return fail(FP4X_ERR_ARG, "int2: misaligned planes");
+  if (M == 0 || N == 0) return FP4X_OK;
+  GemvLaunch p = base_launch(fmt, x, x_stride, out, out_dtype, N, M, N, K, 1, nullptr, nullptr);
+  p.pa.w0 = static_cast<const uint8_t*>(P);
+  p.pa.s = static_cast<const uint8_t*>(S);
+  p.pa.G = G;
+  p.rs = rs;
+  hipStream_t st = (hipStream_t)stream;
+  if (fmt == FP4X_FMT_INT2_F16) {
+    if (G == 16) return launch_gemv<FmtInt2<false, 16>, EpiStore>(p, 1, st);
+    if (G == 32) return launch_gemv<FmtInt2<false, 32>, EpiStore>(p, 1, st);
+    return launch_gemv<FmtInt2<false, 0>, EpiStore>(p, 1, st);
+  }
+  if (G == 16) return launch_gemv<FmtInt2<true, 16>, EpiStore>(p, 1, st);
+  if (G == 32) return launch_gemv<FmtInt2<true, 32>, EpiStore>(p, 1, st);
+  return launch_gemv<FmtInt2<true, 0>, EpiStore>(p, 1, st);
+}
+
+}  // extern "C"
+
+// ----------------------------------------------------------------------------
+// Dequant kernels: the bf16 operand each GEMV feeds to its dot (same device
+// decode functions), and the fp32 MXFP8 dequant (x/fp4x_kernels.py:261-267).
+namespace fp4x {
+
+template <class F>
+__global__ __launch_bounds__(256) void dequant_bf16_kernel(PlaneArgs pa, int N, uint16_t* out) {
+  const int cpr = pa.K / F::KPC;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)N * cpr) return;
+  const int64_t row = t / cpr;
+  const int c = (int)(t - row * cpr);
+  const typename F::Chunk ch = F::load(pa, row, c);
+#pragma unroll
+  for (int sub = 0; sub < F::SUB; ++sub) {
+    uint32_t w[8];
+    F::deq16(ch, sub, w);
+    uint4* o = reinterpret_cast<uint4*>(out + row * pa.K + c * F::KPC + sub * 16);
+    o[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    o[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  }
+}
+
+__global__ __launch_bounds__(256) void mx8_dequant_f32_kernel(const uint8_t* w, const uint8_t* s, int N, int K,
+                                                              float* out) {
+  const int cpr = K / 16;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)N * cpr) return;
+  const int64_t row = t / cpr;
+  const int c = (int)(t - row * cpr);
+  const uint4 q = ld_u128(w + row * K + c * 16);
+  const float sc = e8m0_to_f32(ld_u8(s + row * (K / 32) + (c >> 1)));
+  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+  float4* o = reinterpret_cast<float4*>(out + row * K + c * 16);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x2_t a = fp8x2_to_f32x2<false>(d[i], sc), b = fp8x2_to_f32x2<true>(d[i], sc);
+    o[i] = make_float4(a.x, a.y, b.x, b.y);
+  }
+}
+
+__global__ __launch_bounds__(256) void dot2_kernel(const uint32_t* a, const uint32_t* b, const float* c, float* out,
+                                                   int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = dot2_bf16(a[i], b[i], c[i]);
+}
+
+}  // namespace fp4x
+
+extern "C" {
+
+int fp4x_dot2_bf16(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n, void* stream) {
+  if (n < 0) return fail(FP4X_ERR_ARG, "dot2: n=%lld", n);
+  if (n == 0) return FP4X_OK;
+  hipLaunchKernelGGL(dot2_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, a, b, c, out, n);
+  return check_launch("dot2");
+}
+
+int fp4x_dequant_bf16(int fmt, const void* w0, const void* w1, const void* s, int N, int K, int G, void* out,
+                      void* stream) {
+  const FmtInfo fi = fmt_info(fmt);
+  if (!fi.kpc || N < 0 || K <= 0 || K % fi.kmult) return fail(FP4X_ERR_ARG, "dequant: bad format/shape");
+  if ((fmt == FP4X_FMT_INT2_F16 || fmt == FP4X_FMT_INT2_E4M3) &&
+      (!(G == 16 || G == 32 || (G >= 64 && G % 64 == 0)) || K % G))
+    return fail(FP4X_ERR_ARG, "dequant: bad INT2 group size %lld", G);
+  if (!aligned(w0, 16) || !aligned(out, 16)) return fail(FP4X_ERR_ARG, "dequant: misaligned buffers");
+  if (N == 0) return FP4X_OK;
+  PlaneArgs pa{static_cast<const uint8_t*>(w0), static_cast<const uint8_t*>(w1), static_cast<const uint8_t*>(s), K, G};
+  const int64_t threads = (int64_t)N * (K / fi.kpc);
+  dim3 grid((unsigned)((threads + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  uint16_t* o = static_cast<uint16_t*>(out);
+  switch (fmt) {
+    case FP4X_FMT_MX8: hipLaunchKernelGGL(dequant_bf16_kernel<FmtMX8>, grid, dim3(256), 0, st, pa, N, o); break;
+    case FP4X_FMT_W8_F32: hipLaunchKernelGGL(dequant_bf16_kernel<FmtW8<false>>, grid, dim3(256), 0, st, pa, N, o); break;
+    case FP4X_FMT_W8_F16: hipLaunchKernelGGL(dequant_bf16_kernel<FmtW8<true>>, grid, dim3(256), 0, st, pa, N, o); break;
+    case FP4X_FMT_W6: hipLaunchKernelGGL(dequant_bf16_kernel<FmtW6>, grid, dim3(256), 0, st, pa, N, o); break;
+    case FP4X_FMT_NV4: hipLaunchKernelGGL(dequant_bf16_kernel<FmtNV4>, grid, dim3(256), 0, st, pa, N, o); break;
+    case FP4X_FMT_BF16: hipLaunchKernelGGL(dequant_bf16_kernel<FmtBF16>, grid, dim3(256), 0, st, pa, N, o); break;
+    case FP4X_FMT_INT2_F16:
+      if (G == 16) hipLaunchKernelGGL((dequant_bf16_kernel<FmtInt2<false, 16>>), grid, dim3(256), 0, st, pa, N, o);
+      else if (G == 32) hipLaunchKernelGGL((dequant_bf16_kernel<FmtInt2<false, 32>>), grid, dim3(256), 0, st, pa, N, o);
+      else hipLaunchKernelGGL((dequant_bf16_kernel<FmtInt2<false, 0>>), grid, dim3(256), 0, st, pa, N, o);
+      break;
+    default:
+      if (G == 16) hipLaunchKernelGGL((dequant_bf16_kernel<FmtInt2<true, 16>>), grid, dim3(256), 0, st, pa, N, o);
+      else if (G == 32) hipLaunchKernelGGL((dequant_bf16_kernel<FmtInt2<true, 32>>), grid, dim3(256), 0, st, pa, N, o);
+      else hipLaunchKernelGGL((dequant_bf16_kernel<FmtInt2<true, 0>>), grid, dim3(256), 0, st, pa, N, o);
+      break;
+  }
+  return check_launch("dequant_bf16");
+}
+
+int fp4x_mx8_dequant(const void* w, const void* s, int N, int K, float* out, void* stream) {
+  if (N < 0 || K <= 0 || K % 32) return fail(FP4X_ERR_ARG, "mx8_dequant: K=%lld must be a multiple of 32", K);
+  if (!aligned(w, 16) || !aligned(out, 16)) return fail(FP4X_ERR_ARG, "mx8_dequant: misaligned buffers");
+  if (N == 0) return FP4X_OK;
+  const int64_t threads = (int64_t)N * (K / 16);
+  hipLaunchKernelGGL(mx8_dequant_f32_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(s), N, K, out);
+  return check_launch("mx8_dequant");
+}
+
+}  // extern "C"

@@ -1,0 +1,370 @@
+// Decode-shaped (M <= 16) quantized GEMV engine for gfx950.
+//
+// y[m, n] = sum_k x[m, k] * w[n, k] with x bf16 and w dequantized to the
+// bf16 operand the plugin's kernels feed to their dot (x/fp4x_kernels.py:23,
+// :92, :129, :170, :322), fp32 accumulation.
+//
+// Work decomposition (one definition, used by every kernel so that results
+// of different entry points are bitwise comparable):
+//   * A weight row is cut into 16-byte "chunks" of the main packed plane
+//     (16 fp8/int8 weights, 32 W6/NVFP4 weights, 64 INT2 weights).
+//   * `lpr` lanes (a power of two) share one row; lane `l` of the group owns
+//     chunks l, l + lpr, l + 2*lpr, ... of the row (or of the row's K slice
+//     under split-K), so a group reads lpr*16 contiguous bytes per load.
+//   * Each lane accumulates its chunks in increasing k with v_dot2_f32_bf16
+//     on (weight pair, activation pair), starting from 0.0f.
+//   * The lpr partials are combined by the butterfly in group_allreduce.
+//   * Split-K: slice s of ksplit equal K slices writes its fp32 partial to
+//     slot s; the last-arriving workgroup of a row tile sums slots 0..ks-1
+//     in order (((p0 + p1) + p2) + ...), runs the epilogue and re-arms the
+//     tile's ticket to 0.  No fp32 atomics: results are deterministic.
+//   * Activations are staged once per workgroup in LDS (or read from global
+//     memory when the K slice does not fit).
+#pragma once
+#include "fp4x_device.h"
+
+namespace fp4x {
+
+constexpr int kWaves = 4;           // waves per workgroup
+constexpr int kThreads = kWaves * 64;
+constexpr int kCplBatch = 8;        // chunks per lane loaded in one batch
+constexpr int kLdsXBytes = 64 * 1024;
+
+// Lanes per row for a row (slice) of `chunks` 16-byte chunks: the smallest
+// power of two giving at most 8 chunks per lane, capped at 64.
+__host__ __device__ inline int layout_lpr(int chunks) {
+  int want = (chunks + 7) / 8;
+  int lpr = 1;
+  while (lpr < want && lpr < 64) lpr <<= 1;
+  return lpr;
+}
+
+// ------------------------------------------------------------------ formats
+struct PlaneArgs {
+  const uint8_t* w0;   // main packed plane
+  const uint8_t* w1;   // auxiliary plane (W6 high bits)
+  const uint8_t* s;    // scales
+  int K;               // full row length in weights
+  int G;               // INT2 group size
+};
+
+// MXFP8: fp8 e4m3fn [N, K] + e8m0 [N, K/32]  (x/fp4x_kernels.py:9-29)
+struct FmtMX8 {
+  static constexpr int KPC = 16, SUB = 1;
+  struct Chunk { uint4 q; uint32_t e; };
+  __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
+    Chunk ch;
+    ch.q = ld_u128(a.w0 + row * a.K + c * 16);
+    ch.e = ld_u8(a.s + row * (a.K / 32) + (c >> 1));
+    return ch;
+  }
+  __device__ static Chunk zero() { Chunk ch; ch.q = make_uint4(0, 0, 0, 0); ch.e = 127; return ch; }
+  __device__ static void deq16(const Chunk& ch, int, uint32_t (&w)[8]) {
+    const float sc = e8m0_to_f32(ch.e);
+    w[0] = fp8x2_to_bf16x2<false>(ch.q.x, sc); w[1] = fp8x2_to_bf16x2<true>(ch.q.x, sc);
+    w[2] = fp8x2_to_bf16x2<false>(ch.q.y, sc); w[3] = fp8x2_to_bf16x2<true>(ch.q.y, sc);
+    w[4] = fp8x2_to_bf16x2<false>(ch.q.z, sc); w[5] = fp8x2_to_bf16x2<true>(ch.q.z, sc);
+    w[6] = fp8x2_to_bf16x2<false>(ch.q.w, sc); w[7] = fp8x2_to_bf16x2<true>(ch.q.w, sc);
+  }
+};
+
+// W8 g64: int8 [N, K] + fp32 (or fp16) [N, K/64]  (x/fp4x_kernels.py:116-135)
+// bf16(q*s): fma(q + 128, s, -128*s) is the single rounding of the exact q*s,
+// i.e. the fp32 product the reference forms, then rounded to bf16.
+template <bool F16S>
+struct FmtW8 {
+  static constexpr int KPC = 16, SUB = 1;
+  struct Chunk { uint4 q; uint32_t s; };
+  __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
+    Chunk ch;
+    ch.q = ld_u128(a.w0 + row * a.K + c * 16);
+    if constexpr (F16S) ch.s = ld_u16(a.s + (row * (a.K / 64) + (c >> 2)) * 2);
+    else ch.s = ld_u32(a.s + (row * (a.K / 64) + (c >> 2)) * 4);
+    return ch;
+  }
+  __device__ static Chunk zero() { Chunk ch; ch.q = make_uint4(0, 0, 0, 0); ch.s = 0; return ch; }
+  __device__ static float scale(uint32_t s) {
+    if constexpr (F16S) return f16_to_f32((uint16_t)s);
+    else return __uint_as_float(s);
+  }
+  __device__ static uint32_t pair4(uint32_t d, float s, float ms, uint32_t& hi) {
+    const uint32_t u = d ^ 0x80808080u;   // q + 128 per byte
+    float f0 = __builtin_fmaf(ubyte_to_f32<0>(u), s, ms);
+    float f1 = __builtin_fmaf(ubyte_to_f32<1>(u), s, ms);
+    float f2 = __builtin_fmaf(ubyte_to_f32<2>(u), s, ms);
+    float f3 = __builtin_fmaf(ubyte_to_f32<3>(u), s, ms);
+    hi = pack_bf16x2(f2, f3);
+    return pack_bf16x2(f0, f1);
+  }
+  __device__ static void deq16(const Chunk& ch, int, uint32_t (&w)[8]) {
+    const float s = scale(ch.s);
+    const float ms = -128.0f * s;
+    w[0] = pair4(ch.q.x, s, ms, w[1]);
+    w[2] = pair4(ch.q.y, s, ms, w[3]);
+    w[4] = pair4(ch.q.z, s, ms, w[5]);
+    w[6] = pair4(ch.q.w, s, ms, w[7]);
+  }
+};
+
+// W6 g32: lo-nibble plane L [N, K/2], hi-2-bit plane H [N, K/4], fp16 [N, K/32]
+// (x/fp4x_kernels.py:151-176, packing :197-200).  Code c = lo | hi << 4 in
+// [0, 63], q = c - 32; in an H byte the hi bits of k%4 = 0, 2, 1, 3 sit in
+// bit pairs 0, 1, 2, 3.
+struct FmtW6 {
+  static constexpr int KPC = 32, SUB = 2;
+  struct Chunk { uint4 lo; uint2 hi; uint32_t s; };
+  __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
+    Chunk ch;
+    ch.lo = ld_u128(a.w0 + row * (a.K / 2) + c * 16);
+    ch.hi = ld_u64(a.w1 + row * (a.K / 4) + c * 8);
+    ch.s = ld_u16(a.s + (row * (a.K / 32) + c) * 2);
+    return ch;
+  }
+  __device__ static Chunk zero() {
+    Chunk ch; ch.lo = make_uint4(0, 0, 0, 0); ch.hi = make_uint2(0, 0); ch.s = 0; return ch;
+  }
+  // 8 weights: lo nibbles from dword L (nibble i = weight i), hi bits from
+  // the two H bytes hb0 (weights 0-3) and hb1 (weights 4-7) of `hd`.
+  __device__ static void codes8(uint32_t L, uint32_t g0, uint32_t g1, uint32_t g2, uint32_t g3,
+                                int hbyte, uint32_t& c03, uint32_t& c47) {
+    const uint32_t ev = L & 0x0F0F0F0Fu;          // nibbles 0,2,4,6
+    const uint32_t od = (L >> 4) & 0x0F0F0F0Fu;   // nibbles 1,3,5,7
+    const uint32_t lo03 = perm_b32(od, ev, 0x05010400u);  // [n0, n1, n2, n3]
+    const uint32_t lo47 = perm_b32(od, ev, 0x07030602u);  // [n4, n5, n6, n7]
+    // g_t holds (hi of weight 4j+t) << 4 in byte j.
+    const uint32_t j0 = hbyte, j1 = hbyte + 1;
+    const uint32_t a0 = perm_b32(g1, g0, 0x0c0c0400u | (j0 * 0x0101u));
+    const uint32_t b0 = perm_b32(g3, g2, 0x04000c0cu | (j0 * 0x01010000u));
+    const uint32_t a1 = perm_b32(g1, g0, 0x0c0c0400u | (j1 * 0x0101u));
+    const uint32_t b1 = perm_b32(g3, g2, 0x04000c0cu | (j1 * 0x01010000u));
+    c03 = lo03 | a0 | b0;
+    c47 = lo47 | a1 | b1;
+  }
+  __device__ static void deq4(uint32_t c, float s, float ms, uint32_t& p01, uint32_t& p23) {
+    float f0 = __builtin_fmaf(ubyte_to_f32<0>(c), s, ms);
+    float f1 = __builtin_fmaf(ubyte_to_f32<1>(c), s, ms);
+    float f2 = __builtin_fmaf(ubyte_to_f32<2>(c), s, ms);
+    float f3 = __builtin_fmaf(ubyte_to_f32<3>(c), s, ms);
+    p01 = pack_bf16x2(f0, f1);
+    p23 = pack_bf16x2(f2, f3);
+  }
+  __device__ static void deq16(const Chunk& ch, int sub, uint32_t (&w)[8]) {
+    const float s = f16_to_f32((uint16_t)ch.s);
+    const float ms = -32.0f * s;
+    const uint32_t L0 = sub ? ch.lo.z : ch.lo.x;
+    const uint32_t L1 = sub ? ch.lo.w : ch.lo.y;
+    const uint32_t hd = sub ? ch.hi.y : ch.hi.x;
+    const uint32_t g0 = (hd << 4) & 0x30303030u;  // k%4 == 0 (bits 1:0)
+    const uint32_t g1 = hd & 0x30303030u;         // k%4 == 1 (bits 5:4)
+    const uint32_t g2 = (hd << 2) & 0x30303030u;  // k%4 == 2 (bits 3:2)
+    const uint32_t g3 = (hd >> 2) & 0x30303030u;  // k%4 == 3 (bits 7:6)
+    uint32_t c0, c1, c2, c3;
+    codes8(L0, g0, g1, g2, g3, 0, c0, c1);
+    codes8(L1, g0, g1, g2, g3, 2, c2, c3);
+    deq4(c0, s, ms, w[0], w[1]);
+    deq4(c1, s, ms, w[2], w[3]);
+    deq4(c2, s, ms, w[4], w[5]);
+    deq4(c3, s, ms, w[6], w[7]);
+  }
+};
+
+// NVFP4: e2m1 pairs P [N, K/2] (low nibble = even k), e4m3 S [N, K/16]
+// (x/fp4x_kernels.py:73-99).  Values e2m1 * e4m3 are exact in bf16.  The fp32
+// global scale multiplies the accumulated sum (x/fp4x_kernels.py:94).
+struct FmtNV4 {
+  static constexpr int KPC = 32, SUB = 2;
+  struct Chunk { uint4 q; uint32_t s; };
+  __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
+    Chunk ch;
+    ch.q = ld_u128(a.w0 + row * (a.K / 2) + c * 16);
+    ch.s = ld_u16(a.s + row * (a.K / 16) + c * 2);
+    return ch;
+  }
+  __device__ static Chunk zero() { Chunk ch; ch.q = make_uint4(0, 0, 0, 0); ch.s = 0; return ch; }
+  __device__ static void deq16(const Chunk& ch, int sub, uint32_t (&w)[8]) {
+    const f32x2_t sc2 = fp8x2_to_f32x2<false>(ch.s, 1.0f);
+    const float sc = sub ? sc2.y : sc2.x;
+    const uint32_t d0 = sub ? ch.q.z : ch.q.x;
+    const uint32_t d1 = sub ? ch.q.w : ch.q.y;
+    w[0] = fp4x2_to_bf16x2<0>(d0, sc); w[1] = fp4x2_to_bf16x2<1>(d0, sc);
+    w[2] = fp4x2_to_bf16x2<2>(d0, sc); w[3] = fp4x2_to_bf16x2<3>(d0, sc);
+    w[4] = fp4x2_to_bf16x2<0>(d1, sc); w[5] = fp4x2_to_bf16x2<1>(d1, sc);
+    w[6] = fp4x2_to_bf16x2<2>(d1, sc); w[7] = fp4x2_to_bf16x2<3>(d1, sc);
+  }
+};
+
+// INT2 coarse head: codes P [N, K/4] (element j of each 4-group in bit pair
+// ORDER[j], ORDER = (0, 2, 1, 3)), group scales S [N, K/G] fp16 or e4m3
+// (x/fp4x_kernels.py:304-357).  Weight = bf16((code - 1.5) * s).
+// GC: 16 or 32 (group size known at compile time) or 0 (any G >= 64).
+template <bool E4M3, int GC>
+struct FmtInt2 {
+  static constexpr int KPC = 64, SUB = 4;
+  struct Chunk { uint4 q; uint2 s; };
+  __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
+    Chunk ch;
+    ch.q = ld_u128(a.w0 + row * (a.K / 4) + c * 16);
+    const int ng = a.K / a.G;                     // groups per row
+    constexpr int B = E4M3 ? 1 : 2;               // scale bytes
+    const uint8_t* sp = a.s + (row * ng) * B;
+    if constexpr (GC == 16) {
+      if constexpr (E4M3) { ch.s.x = ld_u32(sp + c * 4); ch.s.y = 0; }
+      else ch.s = ld_u64(sp + c * 8);
+    } else if constexpr (GC == 32) {
+      if constexpr (E4M3) ch.s.x = ld_u16(sp + c * 2);
+      else ch.s.x = ld_u32(sp + c * 4);
+      ch.s.y = 0;
+    } else {
+      const int g = (c * 64) / a.G;
+      ch.s.x = E4M3 ? ld_u8(sp + g) : ld_u16(sp + g * 2);
+      ch.s.y = 0;
+    }
+    return ch;
+  }
+  __device__ static Chunk zero() { Chunk ch; ch.q = make_uint4(0, 0, 0, 0); ch.s = make_uint2(0, 0); return ch; }
+  __device__ static float group_scale(const Chunk& ch, int sub) {
+    int idx;
+    if constexpr (GC == 16) idx = sub;
+    else if constexpr (GC == 32) idx = sub >> 1;
+    else idx = 0;
+    if constexpr (E4M3) {
+      const uint32_t b = (idx < 4) ? (ch.s.x >> (8 * idx)) & 0xffu : 0u;
+      return fp8x2_to_f32x2<false>(b, 1.0f).x;
+    } else {
+      const uint32_t h = (idx < 2) ? (ch.s.x >> (16 * idx)) : (ch.s.y >> (16 * (idx - 2)));
+      return f16_to_f32((uint16_t)(h & 0xffffu));
+    }
+  }
+  __device__ static void deq16(const Chunk& ch, int sub, uint32_t (&w)[8]) {
+    const float s = group_scale(ch, sub);
+    const float p = 0.5f * s, q = 1.5f * s;       // exact in fp32
+    const uint32_t d0 = pack_bf16x2(-q, -p);      // codes 0, 1
+    const uint32_t d1 = pack_bf16x2(p, q);        // codes 2, 3
+    const uint32_t lut_lo = perm_b32(d1, d0, 0x06040200u);  // low bytes of v0..v3
+    const uint32_t lut_hi = perm_b32(d1, d0, 0x07050301u);  // high bytes of v0..v3
+    const uint32_t cw = sub == 0 ? ch.q.x : sub == 1 ? ch.q.y : sub == 2 ? ch.q.z : ch.q.w;
+    const uint32_t e0 = cw & 0x03030303u;          // element 0 of each 4-group
+    const uint32_t e1 = (cw >> 4) & 0x03030303u;   // element 1 (bit pair 2)
+    const uint32_t e2 = (cw >> 2) & 0x03030303u;   // element 2 (bit pair 1)
+    const uint32_t e3 = (cw >> 6) & 0x03030303u;   // element 3 (bit pair 3)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // selector [c, c+4, c', c'+4] picks (lo, hi) bytes of v_c and v_c'
+      const uint32_t sp = 0x04040000u | (uint32_t(j) * 0x0101u) | (uint32_t(j) * 0x01010000u);
+      const uint32_t s01 = perm_b32(e1, e0, sp) | 0x04000400u;
+      const uint32_t s23 = perm_b32(e3, e2, sp) | 0x04000400u;
+      w[2 * j] = perm_b32(lut_hi, lut_lo, s01);
+      w[2 * j + 1] = perm_b32(lut_hi, lut_lo, s23);
+    }
+  }
+};
+
+// BF16 weights [N, K] (x/fp4x_kernels.py:32-47): a chunk is 32 bytes (16
+// weights) already in the dot operand format.
+struct FmtBF16 {
+  static constexpr int KPC = 16, SUB = 1;
+  struct Chunk { uint4 a, b; };
+  __device__ static Chunk load(const PlaneArgs& p, int64_t row, int c) {
+    Chunk ch;
+    const uint8_t* base = p.w0 + row * p.K * 2 + c * 32;
+    ch.a = ld_u128(base);
+    ch.b = ld_u128(base + 16);
+    return ch;
+  }
+  __device__ static Chunk zero() { Chunk ch; ch.a = make_uint4(0, 0, 0, 0); ch.b = ch.a; return ch; }
+  __device__ static void deq16(const Chunk& ch, int, uint32_t (&w)[8]) {
+    w[0] = ch.a.x; w[1] = ch.a.y; w[2] = ch.a.z; w[3] = ch.a.w;
+    w[4] = ch.b.x; w[5] = ch.b.y; w[6] = ch.b.z; w[7] = ch.b.w;
+  }
+};
+
+// ------------------------------------------------------------------ core
+// Load one batch of chunks for RPL rows.  Row r of this lane is rows[r]
+// (negative = no row); chunk j is c0 + lrow + (jb + j) * lpr, and chunks at
+// or past cend (the end of the K slice) are neither loaded nor used.
+template <class F, int RPL>
+struct ChunkBatch {
+  typename F::Chunk ch[RPL][kCplBatch];
+};
+
+template <class F, int RPL>
+__device__ __forceinline__ void load_batch(ChunkBatch<F, RPL>& b, const PlaneArgs& a, const int64_t (&rows)[RPL],
+                                           int c0, int cend, int lrow, int lpr, int jb, int cpl) {
+#pragma unroll
+  for (int j = 0; j < kCplBatch; ++j) {
+    const int jj = jb + j;
+    const int c = c0 + lrow + jj * lpr;
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      if (jj < cpl && rows[r] >= 0 && c < cend) b.ch[r][j] = F::load(a, rows[r], c);
+      else b.ch[r][j] = F::zero();
+    }
+  }
+}
+
+// x[m][k] lives at xs[m * xstride + k - kx0] (LDS or global, bf16).
+// Rows m >= M of x are not read (their accumulators stay 0).
+template <class F, int MT, int RPL, class XPtr>
+__device__ __forceinline__ void compute_batch(const ChunkBatch<F, RPL>& b, XPtr xs, int xstride, int kx0, int M,
+                                              int c0, int cend, int lrow, int lpr, int jb, int cpl,
+                                              float (&acc)[RPL][MT]) {
+#pragma unroll
+  for (int j = 0; j < kCplBatch; ++j) {
+    const int jj = jb + j;
+    if (jj >= cpl) break;
+    const int c = c0 + lrow + jj * lpr;
+    if (c >= cend) continue;
+#pragma unroll
+    for (int sub = 0; sub < F::SUB; ++sub) {
+      const int k = c * F::KPC + sub * 16;
+      uint32_t w[RPL][8];
+#pragma unroll
+      for (int r = 0; r < RPL; ++r) F::deq16(b.ch[r][j], sub, w[r]);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        if (m >= M) break;
+        const uint4* xp = reinterpret_cast<const uint4*>(xs + (int64_t)m * xstride + (k - kx0));
+        const uint4 xa = xp[0], xb = xp[1];
+        const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) {
+          float t = acc[r][m];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) t = dot2_bf16(w[r][i], xv[i], t);
+          acc[r][m] = t;
+        }
+      }
+    }
+  }
+}
+
+// Stage x[0:M, k0:k0+ks] (bf16, row stride xstride elements) into LDS as
+// [MT][ks], zero rows m >= M.  ks is a multiple of 16.
+template <int MT>
+__device__ __forceinline__ void stage_x(uint16_t* lds, const uint16_t* x, int64_t xstride, int M, int k0, int ks) {
+  const int per_row = ks / 8;  // uint4 per row
+  const int total = MT * per_row;
+  for (int i = threadIdx.x; i < total; i += blockDim.x) {
+    const int m = i / per_row, q = i - m * per_row;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (m < M) v = *reinterpret_cast<const uint4*>(x + m * xstride + k0 + q * 8);
+    reinterpret_cast<uint4*>(lds + m * ks)[q] = v;
+  }
+}
+
+// Split-K slot protocol.  `part` is [ksplit][MT][N] fp32 for this batch entry.
+// Returns true in the (single) last-arriving workgroup of the tile, after all
+// slot writes of the tile are visible to it.
+__device__ __forceinline__ bool splitk_arrive(int* ticket, int ksplit) {
+  __shared__ int last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const int old = ticket_acq_rel(ticket);
+    last = (old == ksplit - 1);
+  }
+  __syncthreads();
+  return last != 0;
+}
+
+}  // namespace fp4x

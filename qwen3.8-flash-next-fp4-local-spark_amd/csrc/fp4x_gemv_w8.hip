@@ -1,0 +1,8 @@
+// Explicit GEMV instantiations (one translation unit per weight format, so
+// the library compiles in parallel).
+#include "fp4x_kernels.h"
+
+namespace fp4x {
+template int launch_gemv<FmtW8<false>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+template int launch_gemv<FmtW8<true>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+}  // namespace fp4x

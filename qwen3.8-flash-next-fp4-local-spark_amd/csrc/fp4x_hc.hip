@@ -1,0 +1,213 @@
+// Hyper-connection mixer kernels (decode, M <= 16, W8 weights).
+//
+// Fused path (x/fp4x_kernels.py:429-526):
+//   hc_down: split-K W8 GEMV; the last-arriving workgroup of each row tile
+//            sums the slice partials, writes di = bf16(sum) and the
+//            bottleneck bot = bf16(silu(bf16(di / hc))) for rows < lr, and
+//            re-arms the tile ticket.
+//   hc_up:   W8 GEMV over stream-interleaved rows; a tile of hc*bj stored rows
+//            holds the hc stream rows of bj output columns, so the sigmoid
+//            gate and the stream mean run in the same workgroup.
+// Unfused path (the plugin's 6-kernel mixer, x/fp4patch.py:231-247): W8 GEMV
+// with the same split, scaled-SiLU kernel, W8 GEMV, gate-mean kernel.  Both
+// paths share the GEMV core, the K split and every epilogue function, so they
+// agree bit for bit.
+#include "fp4x_kernels.h"
+#include "../../include/fp4x.h"
+
+namespace fp4x {
+
+// out[m, j] = bf16(sum_s bf16(nrm_s * bf16(sigmoid(g_s))) / hc), s = 0..hc-1
+// in order; g_s are bf16-valued gate logits (x/fp4x_kernels.py:486-493).
+template <class GF, class NF>
+__device__ __forceinline__ uint16_t hc_gate_mean(GF g, NF nrm, int hc) {
+  float tot = 0.0f;
+  for (int s = 0; s < hc; ++s) {
+    const float gate = round_bf16(sigmoid_f32(g(s)));
+    tot += round_bf16(nrm(s) * gate);
+  }
+  return f32_to_bf16(tot / (float)hc);
+}
+
+struct HcUpArgs {
+  const uint16_t* bot; int64_t bot_stride;
+  PlaneArgs pa;          // interleaved q [hc*H, K], s [hc*H, K/64]
+  const uint16_t* nrm; int64_t nrm_stride;
+  uint16_t* out;         // [M, H]
+  int M, K, H, hc, bj, lpr, cpl;
+};
+
+template <class F, int MT>
+__global__ __launch_bounds__(1024) void hc_up_kernel(HcUpArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_x[];      // [MT][K] bf16, then [MT][T] fp32 gates
+  const int T = p.hc * p.bj;                              // stored rows per tile
+  float* gl = reinterpret_cast<float*>(lds_x + MT * p.K);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lpr = p.lpr, lrow = lane & (lpr - 1), slot = lane / lpr, spw = 64 / lpr;
+  const int rt = wave * spw + slot;                       // row within tile
+  const int64_t tile0 = (int64_t)blockIdx.x * T;
+  int64_t rows[1] = {rt < T ? tile0 + rt : -1};
+  float acc[1][MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[0][m] = 0.0f;
+  for (int jb = 0; jb < p.cpl; jb += kCplBatch) {
+    ChunkBatch<F, 1> cb;
+    load_batch<F, 1>(cb, p.pa, rows, 0, p.K / F::KPC, lrow, lpr, jb, p.cpl);
+    if (jb == 0) {
+      stage_x<MT>(lds_x, p.bot, p.bot_stride, p.M, 0, p.K);
+      __syncthreads();
+    }
+    compute_batch<F, MT, 1>(cb, (const uint16_t*)lds_x, p.K, 0, MT, 0, p.K / F::KPC, lrow, lpr, jb, p.cpl, acc);
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[0][m] = group_allreduce(acc[0][m], lpr);
+  if (lrow == 0 && rt < T)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) gl[m * T + rt] = round_bf16(acc[0][m]);
+  __syncthreads();
+  for (int t = threadIdx.x; t < p.M * p.bj; t += blockDim.x) {
+    const int m = t / p.bj, jj = t - m * p.bj;
+    const int64_t j = (int64_t)blockIdx.x * p.bj + jj;
+    const float* gm = gl + m * T + jj;
+    const uint16_t* nm = p.nrm + m * p.nrm_stride + j;
+    const int64_t H = p.H;
+    p.out[(int64_t)m * p.H + j] =
+        hc_gate_mean([&](int s) { return gm[s * p.bj]; }, [&](int s) { return bf16_to_f32(nm[s * H]); }, p.hc);
+  }
+}
+
+__global__ __launch_bounds__(256) void hc_scaled_silu_kernel(const uint16_t* d, int64_t d_stride, uint16_t* bot,
+                                                             int M, int lr, int hc) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)M * lr) return;
+  const int m = (int)(t / lr), n = (int)(t - (int64_t)m * lr);
+  bot[t] = hc_scaled_silu(bf16_to_f32(d[m * d_stride + n]), hc);
+}
+
+__global__ __launch_bounds__(256) void hc_gate_mean_kernel(const uint16_t* nrm, int64_t nrm_stride, const uint16_t* g,
+                                                           int64_t g_stride, uint16_t* out, int M, int H, int hc) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)M * H) return;
+  const int m = (int)(t / H);
+  const int64_t j = t - (int64_t)m * H;
+  const uint16_t* gm = g + m * g_stride + j;
+  const uint16_t* nm = nrm + m * nrm_stride + j;
+  out[t] = hc_gate_mean([&](int s) { return bf16_to_f32(gm[(int64_t)s * H]); },
+                        [&](int s) { return bf16_to_f32(nm[(int64_t)s * H]); }, hc);
+}
+
+static int hc_fail(const char* msg) {
+  set_error(msg);
+  return FP4X_ERR_ARG;
+}
+
+static bool al(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
+
+}  // namespace fp4x
+
+using namespace fp4x;
+
+extern "C" {
+
+int fp4x_hc_down(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* di, void* bot,
+                 int M, int N, int K, int lr, int hc, int ksplit, float* part, int* tickets, void* stream) {
+  if (s_dtype != FP4X_DT_F32 && s_dtype != FP4X_DT_F16) return hc_fail("hc_down: scale dtype must be fp32 or fp16");
+  if (M < 0 || M > 16 || N <= 0 || K <= 0 || K % 64) return hc_fail("hc_down: bad shape (M <= 16, K % 64 == 0)");
+  if (lr < 0 || lr > N || hc <= 0) return hc_fail("hc_down: need 0 <= lr <= N and hc > 0");
+  if (ksplit < 1 || ksplit > 64 || K % ksplit || (K / ksplit) % 16) return hc_fail("hc_down: ksplit must divide K into multiples of 16");
+  if (ksplit > 1 && (!part || !tickets)) return hc_fail("hc_down: split-K needs scratch");
+  if (M > 0 && (!al(x, 16) || x_stride % 8 || x_stride < K)) return hc_fail("hc_down: x must be 16-byte aligned, stride % 8 == 0");
+  if (!al(q, 16) || !al(s, s_dtype == FP4X_DT_F16 ? 2 : 4)) return hc_fail("hc_down: misaligned weights");
+  if (M == 0) return FP4X_OK;
+  GemvLaunch p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.x_stride = x_stride;
+  p.pa.w0 = static_cast<const uint8_t*>(q);
+  p.pa.s = static_cast<const uint8_t*>(s);
+  p.pa.K = K;
+  p.out = di;
+  p.out_dtype = FP4X_DT_BF16;
+  p.out_stride = N;
+  p.out2 = bot;
+  p.lr = lr;
+  p.hc = hc;
+  p.gs = 1.0f;
+  p.M = M;
+  p.N = N;
+  p.ksplit = ksplit;
+  const int chunks = (K / ksplit) / 16;
+  p.lpr = layout_lpr(chunks);
+  p.cpl = (chunks + p.lpr - 1) / p.lpr;
+  p.part = part;
+  p.tickets = tickets;
+  hipStream_t st = (hipStream_t)stream;
+  if (s_dtype == FP4X_DT_F16) return launch_gemv<FmtW8<true>, EpiHcDown>(p, 1, st);
+  return launch_gemv<FmtW8<false>, EpiHcDown>(p, 1, st);
+}
+
+int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* si, int s_dtype, const void* nrm,
+               int64_t nrm_stride, void* out, int M, int K, int H, int hc, int bj, void* stream) {
+  if (s_dtype != FP4X_DT_F32 && s_dtype != FP4X_DT_F16) return hc_fail("hc_up: scale dtype must be fp32 or fp16");
+  if (M < 0 || M > 16 || K <= 0 || K % 64 || H <= 0 || hc <= 0 || bj <= 0 || H % bj)
+    return hc_fail("hc_up: bad shape (M <= 16, K % 64 == 0, H % bj == 0)");
+  const int chunks = K / 16;
+  const int lpr = layout_lpr(chunks), spw = 64 / lpr;
+  const int T = hc * bj;
+  if (T % spw || T / spw > 16) return hc_fail("hc_up: hc*bj must be a multiple of the rows per wave and at most 16 waves");
+  const int mt = mt_of(M < 1 ? 1 : M);
+  const size_t lds = (size_t)mt * K * 2 + (size_t)mt * T * 4;
+  if (lds > 64 * 1024) return hc_fail("hc_up: K too large for the LDS activation stage");
+  if (M > 0 && (!al(bot, 16) || bot_stride % 8 || bot_stride < K)) return hc_fail("hc_up: bot must be 16-byte aligned, stride % 8 == 0");
+  if (!al(qi, 16) || !al(si, s_dtype == FP4X_DT_F16 ? 2 : 4)) return hc_fail("hc_up: misaligned weights");
+  if (M == 0) return FP4X_OK;
+  HcUpArgs p{};
+  p.bot = static_cast<const uint16_t*>(bot);
+  p.bot_stride = bot_stride;
+  p.pa.w0 = static_cast<const uint8_t*>(qi);
+  p.pa.s = static_cast<const uint8_t*>(si);
+  p.pa.K = K;
+  p.nrm = static_cast<const uint16_t*>(nrm);
+  p.nrm_stride = nrm_stride;
+  p.out = static_cast<uint16_t*>(out);
+  p.M = M; p.K = K; p.H = H; p.hc = hc; p.bj = bj;
+  p.lpr = lpr;
+  p.cpl = (chunks + lpr - 1) / lpr;
+  dim3 grid(H / bj), block((T / spw) * 64);
+  hipStream_t st = (hipStream_t)stream;
+#define FP4X_UP(MT_)                                                                                      \
+  if (s_dtype == FP4X_DT_F16) hipLaunchKernelGGL((hc_up_kernel<FmtW8<true>, MT_>), grid, block, lds, st, p); \
+  else hipLaunchKernelGGL((hc_up_kernel<FmtW8<false>, MT_>), grid, block, lds, st, p);
+  switch (mt) {
+    case 1: FP4X_UP(1) break;
+    case 2: FP4X_UP(2) break;
+    case 3: FP4X_UP(3) break;
+    case 4: FP4X_UP(4) break;
+    case 8: FP4X_UP(8) break;
+    default: FP4X_UP(16) break;
+  }
+#undef FP4X_UP
+  return check_launch("hc_up");
+}
+
+int fp4x_hc_scaled_silu(const void* d, int64_t d_stride, void* bot, int M, int lr, int hc, void* stream) {
+  if (M < 0 || lr < 0 || hc <= 0 || d_stride < lr) return hc_fail("hc_scaled_silu: bad shape");
+  const int64_t n = (int64_t)M * lr;
+  if (n == 0) return FP4X_OK;
+  hipLaunchKernelGGL(hc_scaled_silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const uint16_t*>(d), d_stride, static_cast<uint16_t*>(bot), M, lr, hc);
+  return check_launch("hc_scaled_silu");
+}
+
+int fp4x_hc_gate_mean(const void* nrm, int64_t nrm_stride, const void* g, int64_t g_stride, void* out, int M, int H,
+                      int hc, void* stream) {
+  if (M < 0 || H < 0 || hc <= 0 || nrm_stride < (int64_t)hc * H || g_stride < (int64_t)hc * H)
+    return hc_fail("hc_gate_mean: bad shape");
+  const int64_t n = (int64_t)M * H;
+  if (n == 0) return FP4X_OK;
+  hipLaunchKernelGGL(hc_gate_mean_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const uint16_t*>(nrm), nrm_stride, static_cast<const uint16_t*>(g), g_stride,
+                     static_cast<uint16_t*>(out), M, H, hc);
+  return check_launch("hc_gate_mean");
+}
+
+}  // extern "C"

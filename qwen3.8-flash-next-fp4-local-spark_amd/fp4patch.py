@@ -1,0 +1,339 @@
+"""vLLM general plugin: MI355X decode GEMVs for the FP4-Local hybrid MoE model.
+
+Entry point ``[vllm.general_plugins] fp4x = fp4patch:register`` with the
+reference plugin's environment flags and hooks (x/fp4patch.py):
+
+  FP4X_MX8=1        MXFP8 dense linears with M <= FP4X_MX8_MAXM rows read the
+                    packed fp8 rows + e8m0 scale rows and run the fp4x GEMV
+                    (FP4X_DENSE=mx8|w6|nv4, FP4X_NV4_SHAPES=NxK,...).
+  FP4X_HC=1         hyper-connection projections through fp4x GEMVs (M <= 16);
+                    FP4X_HC_W8=1 int8 g64 weights, FP4X_HC_FUSED=1 two fused
+                    kernels per mixer, FP4X_HC_W8_MTP=1 also the MTP mixers,
+                    FP4X_GATE=w8|bf16 router gates, FP4X_MTP_W8=1 MTP linears.
+  FP4X_FAST_HEAD=1  target LM head for decode rows: INT2 coarse pass, top-C
+                    (FP4X_HEAD_C, default 512) and exact MXFP8 rescore
+                    (FP4X_HEAD_G INT2 group size, default 16).
+
+Every install is wrapped so that a failing patch only logs; every hook falls
+back to the original method outside its decode shapes.  The kernels are the
+HIP kernels of fp4x_kernels (libfp4x.so).
+"""
+import os
+import sys
+
+# (N, K) -> (BN, BK, KSPLIT, warps).  Only KSPLIT (K slices summed in order)
+# affects the MI355X kernels; BN/BK/warps are kept for the shape assertion.
+CFG_MX8 = {(16384, 2560): (32, 512, 1, 4), (96, 2560): (16, 128, 4, 2), (13312, 2560): (32, 512, 1, 4),
+           (640, 2560): (16, 512, 1, 4), (1280, 2560): (16, 512, 1, 4), (2560, 6144): (32, 512, 1, 4),
+           (2560, 640): (32, 128, 1, 4)}
+CFG_W6 = {(16384, 2560): (32, 256, 1, 4), (96, 2560): (16, 256, 2, 4), (13312, 2560): (32, 256, 1, 4),
+          (640, 2560): (16, 256, 1, 4), (1280, 2560): (16, 256, 1, 4), (2560, 6144): (32, 256, 1, 4),
+          (2560, 640): (32, 128, 1, 4)}
+CFG_NV4 = {}
+CFG_BG = {(336, 10240): (16, 512, 4, 4), (10240, 320): (32, 64, 1, 4), (512, 2560): (16, 256, 1, 4)}
+CFG_HC_NV4 = {(336, 10240): (16, 128, 2, 4), (10240, 320): (32, 64, 4, 1)}
+# The fused mixer's down cfg and the W8 down entry share KSPLIT so that the
+# fused and unfused mixers give identical results.
+HC_DOWN_CFG = (32, 256, 8, 4)
+CFG_W8 = {(336, 10240): (32, 256, 8, 4), (10240, 320): (32, 64, 1, 8), (512, 2560): (16, 512, 1, 4)}
+_stats = {"mx8": 0, "mx8_skip": 0}
+
+
+def _log(msg):
+    print(f"[fp4x] {msg}", file=sys.stderr, flush=True)
+
+
+def _mx8_cfg(n, k):
+    c = CFG_MX8.get((n, k))
+    if c is None:
+        bk = 512 if k % 512 == 0 else 256 if k % 256 == 0 else 128 if k % 128 == 0 else 64
+        c = (32, bk, 1, 4)
+    return c
+
+
+def _patch_mx8():
+    import torch
+    from vllm.model_executor.kernels.linear import b12x_blockscaled as BB
+    import fp4x_kernels as F
+    maxm = int(os.environ.get("FP4X_MX8_MAXM", "16"))
+    dense_mode = os.environ.get("FP4X_DENSE", "mx8")  # mx8 (exact) | w6 | nv4
+    nv4_shapes = {tuple(int(v) for v in t.split("x")) for t in os.environ.get("FP4X_NV4_SHAPES", "").split(",") if t}
+    qmax = int(os.environ.get("FP4X_DENSE_QMAX", "31"))
+    clip = int(os.environ.get("FP4X_DENSE_CLIP", "0"))
+    for flag in ("FP4X_DENSE_STATS", "FP4X_DENSE_AWQ"):
+        if os.environ.get(flag):
+            _log(f"{flag} (activation-aware quality probe) is not part of this build; ignored")
+    cache = {}
+    orig = BB.B12xBlockscaledLinear.run
+
+    def mode_for(n, k):
+        return "nv4" if (n, k) in nv4_shapes else dense_mode
+
+    def lowbit(self, w, s):
+        key = id(self)
+        q = cache.get(key)
+        if q is None and not torch.cuda.is_current_stream_capturing():
+            wf = F.mx8_dequant(w, s)
+            q = F.quantize_nv4(wf) if mode_for(*w.shape) != "w6" else F.quantize_w6(wf, qmax, clip)
+            cache[key] = q
+            del wf
+            if len(cache) in (1, 200):
+                _log(f"dense {dense_mode}: quantized {len(cache)} layers")
+        return q
+
+    seen = set()
+
+    def run(self, source, bias):
+        key = (self.recipe, tuple(source.shape), bias is None, getattr(self.packed, "padded_in_features", None),
+               getattr(self.packed, "in_features", None))
+        if key not in seen and len(seen) < 60:
+            seen.add(key)
+            _log(f"run {key}")
+        if self.recipe == "mxfp8" and source.dim() == 2 and source.shape[0] <= maxm and bias is None:
+            pk = self.packed
+            w = pk.weight.values
+            if w.dtype == torch.uint8:
+                w = w.view(torch.float8_e4m3fn)
+            if pk.padded_in_features == pk.in_features and w.dtype == torch.float8_e4m3fn and w.dim() == 2:
+                s = pk.weight.scale_rows.view(torch.uint8).view(w.shape[0], -1)
+                n, k = w.shape
+                _stats["mx8"] += 1
+                if (_stats["mx8"] + _stats["mx8_skip"]) % 20000 == 0:
+                    _log(f"stats {_stats}")
+                if dense_mode != "mx8" and n < 100000:
+                    q = lowbit(self, w, s)
+                    if q is not None:
+                        if mode_for(n, k) == "w6":
+                            return F.w6_linear(source, *q, CFG_W6.get((n, k)) or (32, 256, 1, 4))
+                        return F.nv4_linear(source, *q, CFG_NV4.get((n, k)) or
+                                            (32, 256 if k % 256 == 0 else 128 if k % 128 == 0 else 64, 4))
+                if os.environ.get("FP4X_MX8_ZERO") == "1":
+                    return torch.zeros((source.shape[0], n), dtype=source.dtype, device=source.device)
+                return F.mx8_linear(source, w, s, _mx8_cfg(n, k))
+        _stats["mx8_skip"] += 1
+        if (_stats["mx8"] + _stats["mx8_skip"]) % 20000 == 0:
+            _log(f"stats {_stats}")
+        return orig(self, source, bias)
+
+    BB.B12xBlockscaledLinear.run = run
+    _log(f"MXFP8 decode GEMV installed (M <= {maxm})")
+
+
+def _patch_hc():
+    import torch
+    from vllm.models.qwen4_exp.nvidia import hyperconnection as HC
+    from vllm.utils.torch_utils import direct_register_custom_op
+    import fp4x_kernels as F
+
+    zero = os.environ.get("FP4X_HC_ZERO") == "1"
+    w8 = os.environ.get("FP4X_HC_W8") == "1"
+    hc_nv4 = os.environ.get("FP4X_HC_NV4") == "1"
+    hc_w6 = os.environ.get("FP4X_HC_W6") == "1"
+    q4, q6, q8 = {}, {}, {}
+    cnt = [0]
+
+    def _quantized(store, w, fn):
+        key = (w.data_ptr(), tuple(w.shape))
+        qs = store.get(key)
+        if qs is None and not torch.cuda.is_current_stream_capturing():
+            qs = store[key] = fn(w)
+        return qs
+
+    def _bg(x: torch.Tensor, w: torch.Tensor, allow_w8: bool) -> torch.Tensor:
+        cnt[0] += 1
+        if cnt[0] in (1, 100, 10000):
+            _log(f"hc op call #{cnt[0]} x={tuple(x.shape)} w={tuple(w.shape)}")
+        small = x.shape[0] <= 16
+        if zero and small:
+            return torch.zeros((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
+        if hc_nv4 and allow_w8 and small:
+            qs = _quantized(q4, w, F.quantize_nv4)
+            if qs is not None:
+                return F.nv4_linear(x.contiguous(), *qs, CFG_HC_NV4.get(tuple(w.shape)) or (32, 64, 4, 1))
+        if hc_w6 and allow_w8 and small and tuple(w.shape) != (512, 2560):
+            qs = _quantized(q6, w, F.quantize_w6)
+            if qs is not None:
+                return F.w6_linear(x.contiguous(), *qs, (32, 256 if w.shape[1] % 256 == 0 else 64, 1, 4))
+        if w8 and allow_w8 and small:
+            qs = _quantized(q8, w, F.quantize_w8)
+            if qs is not None:
+                if len(q8) in (1, 100):
+                    _log(f"HC W8 quantized {len(q8)} weights")
+                return F.w8_linear(x.contiguous(), *qs,
+                                   CFG_W8.get(tuple(w.shape)) or (32, 256 if w.shape[1] % 256 == 0 else 64, 1, 4))
+        if small:
+            n, k = w.shape
+            return F.bf16_linear(x.contiguous(), w, CFG_BG.get((n, k)) or (32, 256 if k % 256 == 0 else 64, 1, 4))
+        return torch.nn.functional.linear(x, w)
+
+    def _bg_fake(x: torch.Tensor, w: torch.Tensor, allow_w8: bool) -> torch.Tensor:
+        return x.new_empty((x.shape[0], w.shape[0]))
+
+    direct_register_custom_op(op_name="fp4x_bf16_linear", op_func=_bg, fake_impl=_bg_fake)
+    op = torch.ops.vllm.fp4x_bf16_linear
+    orig = HC.GatedResidual._mix_normalized
+    fused = w8 and os.environ.get("FP4X_HC_FUSED") == "1"
+    fx = []
+    qu = {}
+
+    def _mix_fused(self, normalized):
+        wd = (self.input_mix_weight_down_block_inject if self.use_combine else self.input_mix_weight_down).weight
+        wu = self.input_mix_weight_up.weight
+        kd, ku = (wd.data_ptr(), tuple(wd.shape)), (wu.data_ptr(), tuple(wu.shape))
+        if kd not in q8 or ku not in qu or not fx:
+            if torch.cuda.is_current_stream_capturing():
+                return None
+            if not fx:
+                fx.append(F.HCFused(normalized.device, n_down=max(336, wd.shape[0])))
+            if kd not in q8:
+                q8[kd] = F.quantize_w8(wd)
+            if ku not in qu:
+                qu[ku] = F.HCFused.interleave_up(*F.quantize_w8(wu), self.hc_count, 8)
+                if len(qu) in (1, 97):
+                    _log(f"HC fused: prepared {len(qu)} mixers")
+        x = normalized.contiguous()
+        di, bot = fx[0].down(x, *q8[kd], self.lora_rank, self.hc_count, HC_DOWN_CFG)
+        block_input = F.HCFused.up(bot, *qu[ku], x, self.hc_count, (8, 64, 4))
+        injection = di[:, self.lora_rank: self.lora_rank + self.hc_count] if self.use_combine else None
+        return block_input, injection
+
+    def _mix_normalized(self, normalized):
+        if self.tp_size > 1:
+            return orig(self, normalized)
+        aw = "mtp" not in (self._preparation_prefix or "") or os.environ.get("FP4X_HC_W8_MTP") == "1"
+        if fused and aw and normalized.shape[0] <= 16:
+            r = _mix_fused(self, normalized)
+            if r is not None:
+                return r
+        if self.use_combine:
+            down_and_injection = op(normalized, self.input_mix_weight_down_block_inject.weight, aw)
+            projected_down = down_and_injection[:, : self.lora_rank]
+            injection = down_and_injection[:, self.lora_rank: self.lora_rank + self.hc_count]
+        else:
+            projected_down = op(normalized, self.input_mix_weight_down.weight, aw)
+            injection = None
+        small = normalized.shape[0] <= 16 and projected_down.is_cuda
+        # The scaled-SiLU and gate-mean epilogues run on the fp4x kernels (the
+        # rounding points of the fused mixer) for decode shapes.
+        bottleneck = (F.hc_scaled_silu(projected_down, self.lora_rank, self.hc_count) if small
+                      else HC.hc_silu(projected_down, self.hc_count))
+        gate_logits = op(bottleneck, self.input_mix_weight_up.weight, aw)
+        block_input = (F.hc_gate_mean(normalized, gate_logits, self.hc_count) if small
+                       else HC.hc_gate_mix(normalized, gate_logits, self.hc_count))
+        return block_input, injection
+
+    HC.GatedResidual._mix_normalized = _mix_normalized
+    _log("HC decode GEMV installed")
+    mtp_w8 = os.environ.get("FP4X_MTP_W8") == "1"
+    gate_mode = os.environ.get("FP4X_GATE", "")  # target router gates: w8 | bf16
+    if mtp_w8 or gate_mode:
+        from vllm.model_executor.layers.linear import UnquantizedLinearMethod
+        orig_apply = UnquantizedLinearMethod.apply
+        gate_calls = [0]
+
+        def apply(self, layer, x, bias=None):
+            if bias is None and layer.weight.dim() == 2:
+                prefix = str(getattr(layer, "prefix", ""))
+                if mtp_w8 and prefix.startswith("mtp."):
+                    x2 = x.reshape(-1, x.shape[-1])
+                    return op(x2, layer.weight, True).view(*x.shape[:-1], layer.weight.shape[0])
+                if gate_mode and prefix.endswith(".mlp.gate") and x.reshape(-1, x.shape[-1]).shape[0] <= 16:
+                    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+                    gate_calls[0] += 1
+                    if gate_calls[0] in (1, 1000):
+                        _log(f"router gate {gate_mode} call #{gate_calls[0]} {prefix} x={tuple(x2.shape)}")
+                    if gate_mode == "w8":
+                        y = op(x2, layer.weight, True)
+                    else:
+                        y = F.bf16_linear(x2, layer.weight, CFG_BG.get(tuple(layer.weight.shape)) or (16, 256, 1, 4))
+                    return y.view(*x.shape[:-1], layer.weight.shape[0])
+            return orig_apply(self, layer, x, bias)
+
+        UnquantizedLinearMethod.apply = apply
+        _log(f"UnquantizedLinear decode hook: mtp_w8={mtp_w8} gate={gate_mode or 'off'}")
+
+
+def _patch_fast_head():
+    """Target LM head for decode rows: INT2 coarse pass over the vocabulary,
+    top-C candidates per row, exact MXFP8 logits scattered in for them.  The
+    argmax is exact whenever the true argmax is among the coarse top-C."""
+    import torch
+    from vllm.models.qwen4_exp.nvidia import model as MD
+    import fp4x_kernels as F
+    C = int(os.environ.get("FP4X_HEAD_C", "512"))
+    G = int(os.environ.get("FP4X_HEAD_G", "16"))
+    orig = MD.Qwen4ExpForCausalLM.compute_logits
+    st = {}
+
+    def build(self, h):
+        lp = self.logits_processor
+        if lp.scale != 1.0 or lp.soft_cap is not None:
+            st["off"] = True
+            _log("fast head disabled (scale/soft_cap)")
+            return
+        pk = self.lm_head.b12x_mxfp8_packed_weight
+        w = pk.weight.values
+        sc = pk.weight.scale_rows.view(torch.uint8).view(w.shape[0], -1)
+        st["w"], st["s"] = w, sc
+        wf = F.mx8_dequant(w, sc)
+        st["int2"] = os.environ.get("FP4X_HEAD_COARSE", "int2") == "int2"
+        st["coarse"] = F.quantize_int2(wf, group=G) if st["int2"] else F.quantize_nv4(wf)
+        del wf
+        ref = orig(self, h)
+        st["V"], st["dtype"] = ref.shape[-1], ref.dtype
+        out = fast(self, h)
+        same = (out.argmax(-1) == ref.argmax(-1)).float().mean().item()
+        top = torch.topk(ref.float(), 20, dim=-1).indices
+        err = (out.float().gather(1, top) - ref.float().gather(1, top)).abs().max().item()
+        _log(f"fast head built: C={C} G={G}; self-check argmax agree {same:.3f}, top20 max|d| {err:.2e}")
+        if same < 1.0 or err > 1e-2:
+            st["off"] = True
+            _log("fast head self-check failed -> disabled")
+
+    def fast(self, h):
+        if st["int2"]:
+            P, S = st["coarse"]
+            coarse = F.int2_logits(h, P, S, st["w"].shape[0], out_dtype=torch.bfloat16)
+        else:
+            P, S, gs = st["coarse"]
+            coarse = F.nv4_linear(h, P, S, gs, (32, 256, 4))
+        idx = F.topk_rows(coarse, C)
+        return F.refine_mx8_(coarse, h, idx, st["w"], st["s"])
+
+    def compute_logits(self, hidden_states):
+        h = hidden_states
+        if st.get("off") or h.dim() != 2 or h.shape[0] > 16 or h.shape[0] == 0:
+            return orig(self, hidden_states)
+        if "coarse" not in st:
+            if torch.cuda.is_current_stream_capturing():
+                return orig(self, hidden_states)
+            build(self, h.contiguous())
+            if st.get("off"):
+                return orig(self, hidden_states)
+        return fast(self, h.contiguous())
+
+    MD.Qwen4ExpForCausalLM.compute_logits = compute_logits
+    _log("fast target head patch installed")
+
+
+# Reference flags whose patches are outside this build (draft head, disk PLE
+# embeddings, drafter weight swap, MoE ablations, graph debugging).
+_NOT_BUILT = ("FP4X_KEEP_GRAPH", "FP4X_MOE_ZERO", "FP4X_MOE_TAU", "FP4X_MTP_PATCH", "FP4X_PLE_SPIN",
+              "FP4X_PLE_EARLY", "FP4X_PLE_QD", "FP4X_DRAFT_VOCAB")
+
+
+def register():
+    for flag in _NOT_BUILT:
+        if os.environ.get(flag):
+            _log(f"{flag} is not part of the MI355X build; ignored")
+    if os.environ.get("FP4X_FAST_HEAD") == "1":
+        try:
+            _patch_fast_head()
+        except Exception as e:
+            _log(f"fast head patch failed: {type(e).__name__}: {e}")
+    for flag, fn in (("FP4X_MX8", _patch_mx8), ("FP4X_HC", _patch_hc)):
+        if os.environ.get(flag) == "1":
+            try:
+                fn()
+            except Exception as e:  # never break serving because of an optional patch
+                _log(f"{flag} patch failed: {type(e).__name__}: {e}")

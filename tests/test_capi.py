@@ -1,0 +1,75 @@
+"""libfp4x.so loads, exports every entry point include/fp4x.h declares, and
+rejects bad arguments before touching a GPU (no kernel launches here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fp4x.h")
+LIB = os.path.join(ROOT, "qwen3.8-flash-next-fp4-local-spark_amd", "libfp4x.so")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(fp4x_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail("libfp4x.so is not built (run __graft_entry__.build())")
+    return ctypes.CDLL(LIB)
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    for must in ("fp4x_mx8_linear", "fp4x_w8_linear", "fp4x_w6_linear", "fp4x_nv4_linear", "fp4x_int2_logits",
+                 "fp4x_topk_rows", "fp4x_refine_mx8", "fp4x_hc_down", "fp4x_hc_up", "fp4x_hc_scaled_silu",
+                 "fp4x_hc_gate_mean", "fp4x_bf16_linear", "fp4x_w8_linear_layers", "fp4x_mx8_dequant"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version_and_binding(lib):
+    import _fp4x
+    assert lib.fp4x_abi_version() == _fp4x.ABI_VERSION
+    assert set(_fp4x._SIGS) >= set(declared())
+
+
+def test_layout_query(lib):
+    import _fp4x
+    assert _fp4x.layout(_fp4x.FMT_MX8, 2560) == (32, 5)     # 160 chunks of 16 fp8
+    assert _fp4x.layout(_fp4x.FMT_INT2_F16, 2560) == (8, 5)  # 40 chunks of 64 codes
+    assert _fp4x.layout(_fp4x.FMT_W8_F32, 640) == (8, 5)
+    assert _fp4x.layout(_fp4x.FMT_W6, 2560) == (16, 5)
+    assert _fp4x.layout(_fp4x.FMT_W8_F32, 10240) == (64, 10)
+    with pytest.raises(ValueError):
+        _fp4x.layout(_fp4x.FMT_MX8, 24)
+
+
+def test_argument_errors_without_gpu(lib):
+    import _fp4x
+    L = _fp4x.lib()
+    # M > 16, K not a multiple of the group, split without scratch: rejected before any launch
+    assert L.fp4x_mx8_linear(None, 2560, None, None, None, 0, 17, 64, 2560, 1, None, None, None) == _fp4x.ERR_ARG
+    assert b"M=17" in L.fp4x_last_error()
+    assert L.fp4x_w8_linear(None, 100, None, None, 1, None, 0, 1, 8, 100, 1, None, None, None) == _fp4x.ERR_ARG
+    assert L.fp4x_w6_linear(None, 2560, None, None, None, None, 0, 1, 8, 2560, 4, None, None, None) == _fp4x.ERR_ARG
+    assert L.fp4x_int2_logits(None, 2560, None, None, 2, None, None, 0, 1, 8, 2560, 48, None) == _fp4x.ERR_ARG
+    assert L.fp4x_topk_rows(None, 64, 1, 64, 65, None, None) == _fp4x.ERR_ARG
+    assert L.fp4x_hc_up(None, 640, None, None, 1, None, 10240, None, 1, 640, 2560, 4, 3, None) == _fp4x.ERR_ARG
+    # empty problems are no-ops
+    assert L.fp4x_mx8_linear(None, 2560, None, None, None, 0, 0, 64, 2560, 1, None, None, None) == _fp4x.OK
+
+
+def test_splitk_sizes():
+    import _fp4x
+    part, tick = _fp4x.splitk_sizes(_fp4x.FMT_W8_F32, 3, 640, 10240, 16)
+    assert part == 16 * 3 * 640
+    assert tick == 640 // 32                  # 4 waves x 8 rows per tile (lpr 8)

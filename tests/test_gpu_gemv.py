@@ -1,0 +1,194 @@
+"""GPU parity of the dense decode GEMVs against the oracle.
+
+* dequant: the bf16 operand each kernel decodes is bit-exact with the
+  oracle's dequantize-then-round (all formats, all fp8 codes).
+* GEMV: |y - y_oracle| <= 1e-2 + 2e-3 |y_oracle| against the fp32-accumulated
+  oracle, for M = 1..20 (M > 16 runs as 16-row launches), split-K and tails;
+  and bit-exact against the oracle replaying the kernels' summation order.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as fm
+from oracle import gemv as og
+from oracle import ordered
+from oracle import quant as oq
+
+from gpu_helpers import act, assert_tol, bf16_bits, bf16_dev, dev, to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def F():
+    import fp4x_kernels
+    return fp4x_kernels
+
+
+def weights(rng, n, k, scale=0.02):
+    return (rng.standard_normal((n, k)) * scale).astype(np.float32)
+
+
+# ------------------------------------------------------------------ dequant
+def test_dequant_mx8_all_codes(gpu, F):
+    codes = np.tile(np.arange(256, dtype=np.uint8), 64).reshape(64, 256)
+    codes[codes == 0x7F] = 0x7E
+    codes[codes == 0xFF] = 0xFE
+    exps = np.random.default_rng(0).integers(100, 140, (64, 8)).astype(np.uint8)
+    exps[0] = 127
+    w, s = dev(codes), dev(exps)
+    got = bf16_bits(F.dequant_operand("mx8", w, None, s, K=256))
+    want = fm.bf16_bits(oq.mx8_dequant(codes, exps))
+    assert np.array_equal(got, want)
+    got32 = F.mx8_dequant(w, s).cpu().numpy()
+    assert np.array_equal(got32.view(np.uint32), oq.mx8_dequant(codes, exps).view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["w8", "w8_f16", "w6", "nv4", "int2", "int2_g32", "int2_g128", "int2_e4m3"])
+def test_dequant_operand_bit_exact(gpu, F, fmt):
+    rng = np.random.default_rng(1)
+    n, k = 64, 512
+    w = weights(rng, n, k)
+    w[3] = 0.0
+    if fmt.startswith("w8"):
+        q, s = oq.quantize_w8(w)
+        s16 = fmt == "w8_f16"
+        sd = s.astype(np.float16) if s16 else s
+        got = F.dequant_operand(fmt, dev(q), None, dev(sd), K=k)
+        want = og.operand("w8", q, sd.astype(np.float32))
+    elif fmt == "w6":
+        L, H, S = oq.quantize_w6(w)
+        got = F.dequant_operand("w6", dev(L), dev(H), dev(S), K=k)
+        want = og.operand("w6", L, H, S)
+    elif fmt == "nv4":
+        P, S, gs = oq.quantize_nv4(w)
+        got = F.dequant_operand("nv4", dev(P), None, dev(S), K=k)
+        want = og.operand("nv4", P, S)
+    elif fmt == "int2_e4m3":
+        P, S, R = oq.quantize_int2(w, scale_fmt="e4m3")
+        got = F.dequant_operand("int2_e4m3", dev(P), None, dev(S), K=k, G=16)
+        want = og.operand("int2", P, S, scale_fmt="e4m3")
+    else:
+        G = {"int2": 16, "int2_g32": 32, "int2_g128": 128}[fmt]
+        P, S = oq.quantize_int2(w, group=G)
+        got = F.dequant_operand("int2", dev(P), None, dev(S), K=k, G=G)
+        want = og.operand("int2", P, S)
+    assert np.array_equal(bf16_bits(got), fm.bf16_bits(want))
+
+
+# ------------------------------------------------------------------ GEMVs
+def prep(fmt, rng, n, k):
+    w = weights(rng, n, k)
+    if fmt == "mx8":
+        q, s = oq.quantize_mx8(w)
+        return (dev(q), dev(s)), og.operand("mx8", q, s), 1.0
+    if fmt == "w8":
+        q, s = oq.quantize_w8(w)
+        return (dev(q), dev(s)), og.operand("w8", q, s), 1.0
+    if fmt == "w6":
+        L, H, S = oq.quantize_w6(w)
+        return (dev(L), dev(H), dev(S)), og.operand("w6", L, H, S), 1.0
+    if fmt == "nv4":
+        P, S, gs = oq.quantize_nv4(w)
+        return (dev(P), dev(S).view(torch.float8_e4m3fn), gs), og.operand("nv4", P, S), gs
+    if fmt == "bf16":
+        wb = fm.round_bf16(w)
+        return (bf16_dev(wb),), wb, 1.0
+    raise ValueError(fmt)
+
+
+def run(F, fmt, x_t, planes, ks, out_dtype=torch.bfloat16):
+    if fmt == "mx8":
+        return F.mx8_linear(x_t, *planes, (32, 64, ks, 4), out_dtype)
+    if fmt == "w8":
+        return F.w8_linear(x_t, *planes, (32, 64, ks, 4), out_dtype)
+    if fmt == "w6":
+        return F.w6_linear(x_t, *planes, (32, 64, ks, 4), out_dtype)
+    if fmt == "nv4":
+        return F.nv4_linear(x_t, *planes, (32, 64, 4, ks), out_dtype)
+    return F.bf16_linear(x_t, *planes, (32, 64, ks, 4), out_dtype)
+
+
+KPC = {"mx8": 16, "w8": 16, "w6": 32, "nv4": 32, "bf16": 16}
+FMT = {"mx8": 0, "w8": 1, "w6": 3, "nv4": 4, "bf16": 7}
+
+
+@pytest.mark.parametrize("fmt", ["mx8", "w8", "w6", "nv4", "bf16"])
+@pytest.mark.parametrize("M", [1, 3, 5, 16, 20])
+def test_gemv_parity(gpu, F, fmt, M):
+    rng = np.random.default_rng(100 + M)
+    n, k = 1000, 2560           # N tail: 1000 is not a multiple of any row tile
+    planes, w_op, gs = prep(fmt, rng, n, k)
+    x, xb = act(rng, M, k)
+    y = run(F, fmt, bf16_dev(x), planes, 1)
+    ref = og.matmul_f32(x, w_op) * np.float32(gs)
+    print(f"{fmt} M={M}: max|d| {np.abs(to_f32(y) - ref).max():.3g}")
+    assert_tol(to_f32(y), ref, what=f"{fmt} M={M}")
+    # bit-exact against the oracle replaying the kernel's order (16-row blocks)
+    import _fp4x
+    lpr, _ = _fp4x.layout(FMT[fmt], k)
+    wb = fm.bf16_bits(w_op)
+    exact = np.concatenate([ordered.ordered_gemv(xb[m0:m0 + 16], wb, KPC[fmt], lpr, gs=gs)
+                            for m0 in range(0, M, 16)])
+    assert np.array_equal(bf16_bits(y), fm.bf16_bits(exact))
+
+
+@pytest.mark.parametrize("fmt", ["mx8", "w8", "w6", "nv4"])
+@pytest.mark.parametrize("ks", [2, 4, 5])
+def test_gemv_split_k(gpu, F, fmt, ks):
+    rng = np.random.default_rng(7 + ks)
+    n, k = 520, 2560
+    planes, w_op, gs = prep(fmt, rng, n, k)
+    x, xb = act(rng, 3, k)
+    y = run(F, fmt, bf16_dev(x), planes, ks, torch.float32)
+    import _fp4x
+    lpr, _ = _fp4x.layout(FMT[fmt], k // ks)
+    exact = ordered.ordered_gemv(xb, fm.bf16_bits(w_op), KPC[fmt], lpr, ksplit=ks, gs=gs)
+    assert np.array_equal(to_f32(y).view(np.uint32), exact.view(np.uint32))
+    # repeated calls reuse the re-armed tickets and give identical results
+    for _ in range(3):
+        y2 = run(F, fmt, bf16_dev(x), planes, ks, torch.float32)
+        assert torch.equal(y, y2)
+
+
+def test_gemv_out_dtypes_and_strided_x(gpu, F):
+    rng = np.random.default_rng(5)
+    planes, w_op, _ = prep("mx8", rng, 256, 512)
+    x, _ = act(rng, 4, 1024)
+    xt = bf16_dev(x)[:, 256:768]                     # row stride 1024, offset view
+    ref = og.matmul_f32(x[:, 256:768], w_op)
+    for dt in (torch.bfloat16, torch.float32, torch.float16):
+        y = F.mx8_linear(xt, *planes, (32, 64, 1, 4), dt)
+        assert y.dtype == dt
+        assert_tol(to_f32(y), ref, what=str(dt))
+
+
+def test_gemv_shape_errors(gpu, F):
+    rng = np.random.default_rng(6)
+    planes, _, _ = prep("mx8", rng, 64, 512)
+    x = bf16_dev(act(rng, 2, 512)[0])
+    with pytest.raises(AssertionError):
+        F.mx8_linear(x, *planes, (32, 512, 3, 4))     # K not divisible by KSPLIT*BK (reference precondition)
+    with pytest.raises(TypeError):
+        F.mx8_linear(x.float(), *planes, (32, 64, 1, 4))
+    y = F.mx8_linear(x[:0], *planes, (32, 64, 1, 4))
+    assert y.shape == (0, 64)
+
+
+def test_w8_fp16_scales_and_layers(gpu, F):
+    rng = np.random.default_rng(9)
+    Ly, n, k, M = 6, 512, 2560, 3
+    ws = [weights(rng, n, k) for _ in range(Ly)]
+    qs = [oq.quantize_w8(w) for w in ws]
+    xs = [act(rng, M, k)[0] for _ in range(Ly)]
+    for s_dtype in (np.float32, np.float16):
+        q3 = dev(np.stack([q for q, _ in qs]))
+        s3 = dev(np.stack([s.astype(s_dtype) for _, s in qs]))
+        x3 = bf16_dev(np.stack(xs))
+        y = F.w8_linear_layers(x3, q3, s3, torch.float32)
+        for i in range(Ly):
+            ref = og.matmul_f32(xs[i], og.operand("w8", qs[i][0], qs[i][1].astype(s_dtype).astype(np.float32)))
+            assert_tol(to_f32(y[i]), ref, what=f"layer {i}")
+            single = F.w8_linear(x3[i], q3[i], s3[i], (16, 512, 1, 4), torch.float32)
+            assert torch.equal(single, y[i])

@@ -1,0 +1,139 @@
+"""GPU parity of the fast LM head (INT2 coarse -> top-C -> exact MXFP8 refine).
+
+The oracle replays the kernels' summation order, so coarse logits, the top-C
+set (value desc, index asc) and the refined logits must agree exactly; the
+argmax must be identical.  Full size: V = 248,320, K = 2560, M = 3, G = 16,
+C = 512, N(0, 0.02) weights with 64 seeded rows x4.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as fm
+from oracle import gemv as og
+from oracle import head as oh
+from oracle import quant as oq
+
+from gpu_helpers import act, assert_tol, bf16_bits, bf16_dev, dev, to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def F():
+    import fp4x_kernels
+    return fp4x_kernels
+
+
+def lpr_of(fmt, k):
+    import _fp4x
+    return _fp4x.layout(fmt, k)[0]
+
+
+# ------------------------------------------------------------------ top-k
+@pytest.mark.parametrize("V,C", [(248320, 512), (1000, 512), (4096, 4096), (50000, 2048), (100, 1)])
+def test_topk_rows_total_order(gpu, F, V, C):
+    rng = np.random.default_rng(V + C)
+    vals = fm.round_bf16((rng.standard_normal((3, V)) * 2).astype(np.float32))
+    vals[1] = fm.round_bf16(np.round(vals[1] * 4) / 4)          # heavy ties
+    bits = fm.bf16_bits(vals)
+    bits[2, :7] = [0x8000, 0x0000, 0x7FC0, 0xFF80, 0x7F80, 0xFFC1, 0x0001]   # -0, +0, NaN, -inf, inf, -NaN, denormal
+    t = dev(bits.view(np.int16)).view(torch.bfloat16)
+    got = F.topk_rows(t, C).cpu().numpy()
+    want = oh.topk_total_order(bits, C)
+    assert np.array_equal(got, want)
+
+
+def test_topk_all_equal_exact_path(gpu, F):
+    V, C = 300000, 512
+    bits = np.full((2, V), fm.bf16_bits(np.float32(1.5)), np.uint16)
+    bits[1, 123456] = fm.bf16_bits(np.float32(2.0))
+    t = dev(bits.view(np.int16)).view(torch.bfloat16)
+    got = F.topk_rows(t, C).cpu().numpy()
+    assert np.array_equal(got, oh.topk_total_order(bits, C))
+    assert got[0].tolist() == list(range(C)) and got[1, 0] == 123456
+
+
+# ------------------------------------------------------------------ refine
+def test_refine_mx8_exact(gpu, F):
+    rng = np.random.default_rng(21)
+    V, K, M, C = 20000, 2560, 3, 512
+    w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    q, s = oq.quantize_mx8(w)
+    x, xb = act(rng, M, K)
+    idx = np.stack([rng.choice(V, C, replace=False) for _ in range(M)]).astype(np.int64)
+    out = torch.zeros((M, V), dtype=torch.bfloat16, device=gpu)
+    F.refine_mx8_(out, bf16_dev(x), dev(idx), dev(q), dev(s))
+    exact = oh.mx8_rows(xb, q, s, idx, lpr_of(0, K))
+    got = bf16_bits(out)
+    assert np.array_equal(np.take_along_axis(got, idx, 1), fm.bf16_bits(exact))
+    mask = np.ones((M, V), bool)
+    np.put_along_axis(mask, idx, False, 1)
+    assert np.all(got[mask] == 0)
+    # fp32 out: the exact sums themselves
+    out32 = torch.zeros((M, V), dtype=torch.float32, device=gpu)
+    F.refine_mx8_(out32, bf16_dev(x), dev(idx), dev(q), dev(s))
+    assert np.array_equal(np.take_along_axis(out32.cpu().numpy(), idx, 1).view(np.uint32), exact.view(np.uint32))
+    ref = og.matmul_f32(x, oq.mx8_dequant(q[idx[0]], s[idx[0]]))[0]
+    assert_tol(np.take_along_axis(out32.cpu().numpy(), idx, 1)[0], ref, what="refine vs matmul")
+
+
+# ------------------------------------------------------------------ INT2 coarse
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_int2_logits_exact(gpu, F, M):
+    rng = np.random.default_rng(31 + M)
+    V, K = 8192, 2560
+    w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    P, S = oq.quantize_int2(w)
+    x, xb = act(rng, M, K)
+    y = F.int2_logits(bf16_dev(x), dev(P), dev(S), V)             # fp32 out (reference default)
+    exact = oh.int2_coarse(xb, P, S, 16, lpr_of(5, K))
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), exact.view(np.uint32))
+    assert_tol(y.cpu().numpy(), og.int2_logits(x, P, S), what="int2 vs matmul")
+    yb = F.int2_logits(bf16_dev(x), dev(P), dev(S), V, out_dtype=torch.bfloat16)
+    assert np.array_equal(bf16_bits(yb), fm.bf16_bits(exact))
+
+
+def test_int2_row_scale_variant(gpu, F):
+    rng = np.random.default_rng(41)
+    V, K = 2048, 2560
+    w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    P, S, R = oq.quantize_int2(w, scale_fmt="e4m3")
+    x, _ = act(rng, 3, K)
+    y = F.int2_logits(bf16_dev(x), dev(P), dev(S).view(torch.float8_e4m3fn), V, RS=dev(R))
+    assert_tol(y.cpu().numpy(), og.int2_logits(x, P, S, scale_fmt="e4m3", RS=R), what="int2 e4m3 + RS")
+
+
+# ------------------------------------------------------------------ full head
+def synth_head(gpu, F, V=248320, K=2560, seed=2):
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    w = torch.randn((V, K), generator=g, device=gpu) * 0.02
+    rows = torch.randperm(V, generator=g, device=gpu)[:64]
+    w[rows] *= 4
+    q, s = F.quantize_mx8(w)
+    del w
+    P, S = F.quantize_int2(F.mx8_dequant(q, s), group=16)
+    return q, s, P, S
+
+
+def test_fast_head_full_size_exact(gpu, F):
+    V, K, M, C = 248320, 2560, 3, 512
+    q, s, P, S = synth_head(gpu, F, V, K)
+    rng = np.random.default_rng(1000)
+    x, xb = act(rng, M, K)
+    xt = bf16_dev(x)
+    coarse = F.int2_logits(xt, P, S, V, out_dtype=torch.bfloat16)
+    idx = F.topk_rows(coarse, C)
+    coarse_bits = bf16_bits(coarse)
+    out = F.refine_mx8_(coarse, xt, idx, q, s)
+    Pn, Sn, qn, sn = P.cpu().numpy(), S.cpu().numpy(), q.cpu().numpy(), s.cpu().numpy()
+    o_coarse, o_idx, o_out = oh.fast_head(xb, Pn, Sn, 16, qn, sn, C, lpr_of(5, K), lpr_of(0, K))
+    assert np.array_equal(coarse_bits, o_coarse), "coarse logits"
+    assert np.array_equal(idx.cpu().numpy(), o_idx), "top-512 set and order"
+    got = bf16_bits(out)
+    assert np.array_equal(got, o_out), "refined logits"
+    am = out.float().argmax(-1).cpu().numpy()
+    assert np.array_equal(am, np.argmax(fm.bf16_to_f32(o_out), -1))
+    # the exact full-vocabulary MXFP8 argmax agrees (true argmax inside the top-512)
+    full = F.mx8_linear(xt, q, s, (32, 512, 1, 4), torch.float32)
+    assert np.array_equal(am, full.argmax(-1).cpu().numpy())

@@ -1,0 +1,174 @@
+"""Oracle quantizers pinned against the reference's own golden vectors
+(tests/golden/make_golden.py) and invariants; the product's torch weight
+preparation checked against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as fm
+from oracle import quant as oq
+from oracle import hc as ohc
+
+
+def test_w8_golden(golden):
+    q, s = oq.quantize_w8(golden["w8_w"])
+    assert np.array_equal(q, golden["w8_q"])
+    assert np.array_equal(s.view(np.uint32), golden["w8_s"].view(np.uint32))
+    # tie row: values at .5 steps of a power-of-two scale round half to even
+    assert list(q[7, :9]) == [127, 2, -4, 0, 0, 2, 126, -126, 64]
+
+
+def test_w6_golden(golden):
+    L, H, S = oq.quantize_w6(golden["w6_w"])
+    assert np.array_equal(L, golden["w6_L"]) and np.array_equal(H, golden["w6_H"])
+    assert np.array_equal(S.view(np.uint16), golden["w6_S"].view(np.uint16))
+    codes = oq.w6_codes(L, H) - 32
+    assert list(codes[7, :8]) == [31, 2, -4, 30, -30, 0, 0, 8]
+    assert list(codes[7, 32:36]) == [-31, -30, 2, -2]
+
+
+def test_w6_clip_search_golden(golden):
+    L, H, S = oq.quantize_w6(golden["w6_w"], qmax=15, clip_search=3)
+    assert np.array_equal(L, golden["w6c_L"]) and np.array_equal(H, golden["w6c_H"])
+    assert np.array_equal(S.view(np.uint16), golden["w6c_S"].view(np.uint16))
+
+
+def test_mx8_dequant_golden(golden):
+    got = oq.mx8_dequant(golden["mx8_w"], golden["mx8_s"])
+    assert np.array_equal(got.view(np.uint32), golden["mx8_deq"].view(np.uint32))
+
+
+def test_nv4_golden(golden):
+    P, S, gs = oq.quantize_nv4(golden["nv4_w"])
+    assert gs == float(golden["nv4_gs"])
+    assert np.array_equal(P, golden["nv4_P"]) and np.array_equal(S, golden["nv4_S"])
+    deq = oq.dequant_nv4(P, S, gs)
+    assert np.array_equal(deq.view(np.uint32), golden["nv4_deq"].view(np.uint32))
+
+
+@pytest.mark.parametrize("grp", [16, 32])
+def test_int2_golden(golden, grp):
+    P, S = oq.quantize_int2(golden["int2_w"], group=grp)
+    assert np.array_equal(P, golden[f"int2g{grp}_P"])
+    assert np.array_equal(S.view(np.uint16), golden[f"int2g{grp}_S"].view(np.uint16))
+    deq = oq.dequant_int2(P, S)
+    assert np.array_equal(deq.view(np.uint32), golden[f"int2g{grp}_deq"].view(np.uint32))
+
+
+def test_int2_e4m3_golden(golden):
+    P, S, R = oq.quantize_int2(golden["int2_w"], scale_fmt="e4m3", group=16)
+    assert np.array_equal(P, golden["int2e_P"]) and np.array_equal(S, golden["int2e_S"])
+    assert np.array_equal(R.view(np.uint32), golden["int2e_R"].view(np.uint32))
+
+
+def test_interleave_golden(golden):
+    idx = oq.interleave_up_rows(32, 4, 2)
+    assert np.array_equal(golden["il_q"][idx], golden["il_qi"])
+
+
+# ---------------------------------------------------------------- invariants
+def test_w8_invariants():
+    w = np.random.default_rng(3).standard_normal((16, 256)).astype(np.float32) * 0.02
+    q, s = oq.quantize_w8(w)
+    err = np.abs(oq.dequant_w8(q, s) - w).reshape(16, 4, 64)
+    assert np.all(err <= s[..., None] * 0.5000001)
+    assert np.abs(q.astype(np.int32)).max() == 127
+
+
+def test_w6_layout_roundtrip():
+    rng = np.random.default_rng(4)
+    codes = rng.integers(0, 64, (8, 64)).astype(np.int32)
+    lo, hi = codes & 15, codes >> 4
+    L = (lo[:, 0::2] | (lo[:, 1::2] << 4)).astype(np.uint8)
+    H = (hi[:, 0::4] | (hi[:, 2::4] << 2) | (hi[:, 1::4] << 4) | (hi[:, 3::4] << 6)).astype(np.uint8)
+    assert np.array_equal(oq.w6_codes(L, H), codes)
+    # the hi bits of k%4 = 0, 2, 1, 3 occupy bit pairs 0, 1, 2, 3
+    assert oq.w6_codes(np.zeros((1, 2), np.uint8), np.array([[0b11_01_10_00]], np.uint8))[0].tolist() == \
+        [0, 1 << 4, 2 << 4, 3 << 4]
+
+
+def test_int2_order_and_levels():
+    P = np.array([[0b11_01_10_00]], np.uint8)   # bit pairs 0..3 hold codes 0, 2, 1, 3
+    assert oq.int2_codes(P)[0].tolist() == [0, 1, 2, 3]   # element j in bit pair ORDER[j]
+    w = np.random.default_rng(5).standard_normal((4, 64)).astype(np.float32)
+    P, S = oq.quantize_int2(w)
+    err = np.abs(oq.dequant_int2(P, S) - w).reshape(4, 4, 16)
+    assert np.all(err <= S.astype(np.float32)[..., None] * 1.0 + 1e-6)
+
+
+def test_mx8_quantizer_ocp_rules():
+    rng = np.random.default_rng(6)
+    w = rng.standard_normal((8, 128)).astype(np.float32) * 0.02
+    w[0, :32] = 0.0
+    q, s = oq.quantize_mx8(w)
+    amax = np.abs(w.reshape(8, 4, 32)).max(-1)
+    nz = amax > 0
+    assert np.array_equal(s[nz].astype(np.int64) - 127, np.floor(np.log2(amax[nz])).astype(np.int64) - 8)
+    assert s[0, 0] == 0
+    deq = oq.mx8_dequant(q, s)
+    X = np.exp2(s.astype(np.float64) - 127).repeat(32, 1)
+    v = w / X                                   # element in units of the shared scale, |v| < 512
+    d = deq / X
+    sat = np.abs(v) >= 448
+    assert np.all(d[sat] == np.sign(v[sat]) * 448)
+    normal = ~sat & (np.abs(v) >= 2.0 ** -6)
+    assert np.all(np.abs(d - v)[normal] <= np.abs(v)[normal] * 2.0 ** -4)   # half an e4m3 ulp
+    sub = np.abs(v) < 2.0 ** -6
+    assert np.all(np.abs(d - v)[sub] <= 2.0 ** -10)                         # half a subnormal step
+
+
+def test_nv4_invariants():
+    w = np.random.default_rng(7).standard_normal((8, 64)).astype(np.float32) * 0.02
+    P, S, gs = oq.quantize_nv4(w)
+    assert np.all(np.isin(oq.nv4_values(P), fm.E2M1))
+    assert gs == max(float(np.abs(w).max()) / 6.0 / 448.0, 1e-30)
+
+
+# ---------------------------------------------------------------- product weight prep
+@pytest.fixture(scope="module")
+def F():
+    import fp4x_kernels
+    return fp4x_kernels
+
+
+def test_product_quantizers_match_oracle(F, golden):
+    w = torch.from_numpy(golden["w8_w"])
+    q, s = F.quantize_w8(w)
+    assert np.array_equal(q.numpy(), golden["w8_q"]) and np.array_equal(s.numpy(), golden["w8_s"])
+    L, H, S = F.quantize_w6(torch.from_numpy(golden["w6_w"]))
+    assert np.array_equal(L.numpy(), golden["w6_L"]) and np.array_equal(H.numpy(), golden["w6_H"])
+    assert np.array_equal(S.numpy().view(np.uint16), golden["w6_S"].view(np.uint16))
+    L, H, S = F.quantize_w6(torch.from_numpy(golden["w6_w"]), 15, 3)
+    assert np.array_equal(L.numpy(), golden["w6c_L"]) and np.array_equal(S.numpy(), golden["w6c_S"])
+    P, S, gs = F.quantize_nv4(torch.from_numpy(golden["nv4_w"]))
+    assert np.array_equal(P.numpy(), golden["nv4_P"]) and gs == float(golden["nv4_gs"])
+    assert np.array_equal(S.view(torch.uint8).numpy(), golden["nv4_S"])
+    assert np.array_equal(F.dequant_nv4(P, S, gs).numpy(), golden["nv4_deq"])
+    for grp in (16, 32):
+        P, S = F.quantize_int2(torch.from_numpy(golden["int2_w"]), group=grp)
+        assert np.array_equal(P.numpy(), golden[f"int2g{grp}_P"])
+        assert np.array_equal(F.dequant_int2(P, S).numpy(), golden[f"int2g{grp}_deq"])
+    P, S, R = F.quantize_int2(torch.from_numpy(golden["int2_w"]), scale_fmt="e4m3")
+    assert np.array_equal(S.view(torch.uint8).numpy(), golden["int2e_S"]) and np.array_equal(R.numpy(), golden["int2e_R"])
+    qi, si = F.HCFused.interleave_up(torch.from_numpy(golden["il_q"]), torch.arange(32.).view(32, 1), 4, 2)
+    assert np.array_equal(qi.numpy(), golden["il_qi"])
+
+
+def test_product_mx8_quantizer_matches_oracle(F):
+    rng = np.random.default_rng(8)
+    w = rng.standard_normal((16, 256)).astype(np.float32) * 0.02
+    w[1, :32] = 0
+    w[2, 32:64] *= 1e5
+    w[3, :32] = 1e-41      # fp32 subnormal block
+    q, s = F.quantize_mx8(torch.from_numpy(w))
+    oq_q, oq_s = oq.quantize_mx8(w)
+    assert np.array_equal(s.numpy(), oq_s)
+    assert np.array_equal(q.numpy(), oq_q)
+
+
+def test_hc_oracle_closed_forms():
+    # sigmoid(0) = 1/2: silu(0) = 0; gate-mean of equal streams is the stream value times the gate
+    assert ohc.scaled_silu(np.zeros((1, 4), np.float32), 4).tolist() == [[0.0] * 4]
+    nrm = np.full((1, 8), 2.0, np.float32)
+    g = np.zeros((1, 8), np.float32)
+    assert ohc.gate_mean(nrm, g, 4).tolist() == [[1.0, 1.0]]
