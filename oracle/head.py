@@ -41,10 +41,11 @@ def int2_coarse(x_bits, P, S, G, lpr):
 
 
 def mx8_rows(x_bits, w_codes, s_u8, rows, lpr):
-    """Exact MXFP8 sums of the gathered rows rows [M, C] (kernel order)."""
+    """Exact MXFP8 sums of the gathered rows rows [M, C]: the rescore kernel's
+    order with IEEE fma steps (ordered model 2)."""
     uniq, inv = np.unique(rows, return_inverse=True)
     w_op = bf16_bits(quant.mx8_dequant(w_codes[uniq], s_u8[uniq]))
-    return ordered.ordered_gemv(x_bits, w_op, kpc=16, lpr=lpr, rows=inv.reshape(rows.shape))
+    return ordered.ordered_gemv(x_bits, w_op, kpc=16, lpr=lpr, rows=inv.reshape(rows.shape), mode=ordered.FMA)
 
 
 def fast_head(x_bits, P, S, G, w_codes, s_u8, C, lpr_int2, lpr_mx8):

@@ -7,8 +7,13 @@ import numpy as np
 
 from . import build as _build
 
-# v_dot2_f32_bf16 rounding model; tests/test_gpu_dot2.py checks it against
-# the hardware on crafted and random operands (see ordered.c for the models).
+# Step models (ordered.c).  FMA (two IEEE fma, low element first) is the
+# rescore kernel's step and is exact.  DOT2_MODE models v_dot2_f32_bf16 by a
+# single rounding of the exact three-term sum; the hardware's rounding of
+# that instruction differs in the last bit for about 12% of random operands
+# (tests/test_gpu_dot2.py measures it), so sums built from it are compared to
+# this model within a per-step one-ulp bound (step_bound).
+FMA = 2
 DOT2_MODE = 0
 
 _LIB = None
@@ -59,6 +64,36 @@ def ordered_gemv(x_bits, w_bits, kpc, lpr, ksplit=1, gs=1.0, rows=None, mode=Non
     lib().oracle_ordered_gemv(_p(x_bits), _p(w_bits), None if rows is None else _p(rows), M, N, K, kpc, ksplit, lpr,
                               float(gs), DOT2_MODE if mode is None else mode, _p(out))
     return out
+
+
+def step_bound(x, w, kpc, lpr, ksplit=1):
+    """|error| bound of a sum built from steps that may each differ by one
+    fp32 ulp of the running partial: n_steps * 2^-23 * sum_k |x_k w_k|.
+    x, w: fp32 values [M, K], [N, K]."""
+    K = x.shape[1]
+    chunks = K // ksplit // kpc
+    cpl = -(-chunks // lpr)
+    n_steps = cpl * kpc // 2 + max(lpr.bit_length() - 1, 0) + ksplit + 1
+    l1 = np.abs(np.asarray(x, np.float64)) @ np.abs(np.asarray(w, np.float64)).T
+    return n_steps * 2.0 ** -23 * l1
+
+
+def mfma_bound(x, w, ksplit=1):
+    """|error| bound of an MFMA-accumulated sum against the exact sum:
+    v_mfma_f32_16x16x32_bf16 adds 32 products to its accumulator with an
+    error of at most 2.53 * 2^-23 * (L1 of those terms) (measured on random
+    operands spanning 2^48), chained over K/32 instructions, plus the wave and
+    K-slice additions.  x, w: fp32 values [M, K], [N, K]."""
+    K = x.shape[1]
+    n_events = 3 * (K // 32) + 16 + ksplit
+    l1 = np.abs(np.asarray(x, np.float64)) @ np.abs(np.asarray(w, np.float64)).T
+    return n_events * 2.0 ** -23 * l1
+
+
+def exact_sum(x, w):
+    """float64 x @ w.T (exact for bf16-valued operands at these sizes up to
+    float64 rounding, far below the fp32 bounds it is compared with)."""
+    return np.asarray(x, np.float64) @ np.asarray(w, np.float64).T
 
 
 def int2_operand_bits(P, S_f16, G):

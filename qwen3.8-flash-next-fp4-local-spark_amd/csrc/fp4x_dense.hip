@@ -1,26 +1,38 @@
 // Dense decode GEMVs (MXFP8, W8 g64, W6 g32, NVFP4, INT2 coarse head), the
 // layer-batched W8 launch, and the dequant kernels, behind a C ABI.
-#include "fp4x_kernels.h"
+#include "fp4x_mfma.h"
 #include "../../include/fp4x.h"
 #include <cstdio>
 
 namespace fp4x {
 
 // GEMV launches are instantiated in the fp4x_gemv_*.hip translation units.
-extern template int launch_gemv<FmtBF16, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtMX8, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtW8<false>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtW8<true>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtW6, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtNV4, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtInt2<false, 16>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtInt2<false, 32>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtInt2<false, 0>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtInt2<true, 16>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtInt2<true, 32>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
-extern template int launch_gemv<FmtInt2<true, 0>, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtBF16, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtMX8, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtW8<false>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtW8<true>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtW6, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtNV4, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtInt2<false, 32>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtInt2<false, 0>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtInt2<true, 16>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtInt2<true, 32>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+extern template int launch_gemv_mfma<FmtInt2<true, 0>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 
 static thread_local std::string g_err;
+
+int mfma_grid_target(int kw) {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus * (16 / (kw < 1 ? 1 : kw > 16 ? 16 : kw));
+}
 void set_error(const std::string& msg) { g_err = msg; }
 
 int check_launch(const char* what) {
@@ -119,11 +131,9 @@ int fp4x_layout(int fmt, int k_slice, int* lpr, int* cpl) {
 int fp4x_splitk_sizes(int fmt, int M, int N, int K, int ksplit, int batch, int64_t* part_floats, int64_t* n_tickets) {
   const FmtInfo fi = fmt_info(fmt);
   if (!fi.kpc || ksplit < 1 || K % ksplit || (K / ksplit) % fi.kpc) return fail(FP4X_ERR_ARG, "bad split-K query");
-  const int chunks = (K / ksplit) / fi.kpc;
-  const int lpr = layout_lpr(chunks);
-  const int tile_rows = kWaves * (64 / lpr);   // RPL = 1
-  *part_floats = (int64_t)batch * ksplit * mt_of(M < 1 ? 1 : M) * N;
-  *n_tickets = (int64_t)batch * ((N + tile_rows - 1) / tile_rows);
+  (void)M;
+  *part_floats = (int64_t)batch * ksplit * 16 * N;     // one 16-row slot tile per K slice
+  *n_tickets = (int64_t)batch * ((N + 15) / 16);       // one ticket per 16-row tile
   return FP4X_OK;
 }
 
@@ -136,7 +146,7 @@ int fp4x_mx8_linear(const void* x, int64_t x_stride, const void* w, const void* 
   GemvLaunch p = base_launch(FP4X_FMT_MX8, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
   p.pa.w0 = static_cast<const uint8_t*>(w);
   p.pa.s = static_cast<const uint8_t*>(s);
-  return launch_gemv<FmtMX8, EpiStore>(p, 1, (hipStream_t)stream);
+  return launch_gemv_mfma<FmtMX8, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
 int fp4x_bf16_linear(const void* x, int64_t x_stride, const void* w, void* out, int out_dtype, int M, int N, int K,
@@ -147,7 +157,7 @@ int fp4x_bf16_linear(const void* x, int64_t x_stride, const void* w, void* out, 
   if (M == 0 || N == 0) return FP4X_OK;
   GemvLaunch p = base_launch(FP4X_FMT_BF16, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
   p.pa.w0 = static_cast<const uint8_t*>(w);
-  return launch_gemv<FmtBF16, EpiStore>(p, 1, (hipStream_t)stream);
+  return launch_gemv_mfma<FmtBF16, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
 int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, const void* q, int64_t q_lstride,
@@ -169,8 +179,8 @@ int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, co
   p.w0_bstride = q_lstride;
   p.s_bstride = s_lstride * (s_dtype == FP4X_DT_F16 ? 2 : 4);
   p.out_bstride = out_lstride;
-  if (fmt == FP4X_FMT_W8_F16) return launch_gemv<FmtW8<true>, EpiStore>(p, layers, (hipStream_t)stream);
-  return launch_gemv<FmtW8<false>, EpiStore>(p, layers, (hipStream_t)stream);
+  if (fmt == FP4X_FMT_W8_F16) return launch_gemv_mfma<FmtW8<true>, EpiStore>(p, layers, (hipStream_t)stream);
+  return launch_gemv_mfma<FmtW8<false>, EpiStore>(p, layers, (hipStream_t)stream);
 }
 
 int fp4x_w8_linear(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* out, int out_dtype,
@@ -189,7 +199,7 @@ int fp4x_w6_linear(const void* x, int64_t x_stride, const void* L, const void* H
   p.pa.w0 = static_cast<const uint8_t*>(L);
   p.pa.w1 = static_cast<const uint8_t*>(H);
   p.pa.s = static_cast<const uint8_t*>(S);
-  return launch_gemv<FmtW6, EpiStore>(p, 1, (hipStream_t)stream);
+  return launch_gemv_mfma<FmtW6, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
 int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* S, float gs, void* out, int out_dtype,
@@ -202,7 +212,7 @@ int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* 
   p.pa.w0 = static_cast<const uint8_t*>(P);
   p.pa.s = static_cast<const uint8_t*>(S);
   p.gs = gs;
-  return launch_gemv<FmtNV4, EpiStore>(p, 1, (hipStream_t)stream);
+  return launch_gemv_mfma<FmtNV4, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
 int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
@@ -223,13 +233,13 @@ int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void*
   p.rs = rs;
   hipStream_t st = (hipStream_t)stream;
   if (fmt == FP4X_FMT_INT2_F16) {
-    if (G == 16) return launch_gemv<FmtInt2<false, 16>, EpiStore>(p, 1, st);
-    if (G == 32) return launch_gemv<FmtInt2<false, 32>, EpiStore>(p, 1, st);
-    return launch_gemv<FmtInt2<false, 0>, EpiStore>(p, 1, st);
+    if (G == 16) return launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(p, 1, st);
+    if (G == 32) return launch_gemv_mfma<FmtInt2<false, 32>, EpiStore>(p, 1, st);
+    return launch_gemv_mfma<FmtInt2<false, 0>, EpiStore>(p, 1, st);
   }
-  if (G == 16) return launch_gemv<FmtInt2<true, 16>, EpiStore>(p, 1, st);
-  if (G == 32) return launch_gemv<FmtInt2<true, 32>, EpiStore>(p, 1, st);
-  return launch_gemv<FmtInt2<true, 0>, EpiStore>(p, 1, st);
+  if (G == 16) return launch_gemv_mfma<FmtInt2<true, 16>, EpiStore>(p, 1, st);
+  if (G == 32) return launch_gemv_mfma<FmtInt2<true, 32>, EpiStore>(p, 1, st);
+  return launch_gemv_mfma<FmtInt2<true, 0>, EpiStore>(p, 1, st);
 }
 
 }  // extern "C"

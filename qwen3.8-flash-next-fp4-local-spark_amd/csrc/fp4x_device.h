@@ -63,10 +63,12 @@ template <bool HI>
 __device__ __forceinline__ f32x2_t fp8x2_to_f32x2(uint32_t v, float scale) {
   return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(v, scale, HI);
 }
-// Two OCP e2m1 nibbles (byte `B` of v; low nibble first) -> bf16x2 times scale.
+// Two OCP e2m1 nibbles (byte `B` of v; low nibble first) -> fp32 pair.  The
+// scalef32 converts apply only the exponent of their scale operand (they are
+// built for e8m0 scales), so a general scale is multiplied separately.
 template <int B>
-__device__ __forceinline__ uint32_t fp4x2_to_bf16x2(uint32_t v, float scale) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, scale, B));
+__device__ __forceinline__ f32x2_t fp4x2_to_f32x2(uint32_t v) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v, 1.0f, B);
 }
 
 // ---------------------------------------------------------------- byte ops

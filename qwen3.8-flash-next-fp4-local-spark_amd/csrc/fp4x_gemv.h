@@ -52,6 +52,14 @@ struct PlaneArgs {
 struct FmtMX8 {
   static constexpr int KPC = 16, SUB = 1;
   struct Chunk { uint4 q; uint32_t e; };
+  struct Row { const uint8_t* w; const uint8_t* s; };
+  __device__ static Row row(const PlaneArgs& a, int64_t r) { return {a.w0 + r * a.K, a.s + r * (a.K / 32)}; }
+  __device__ static Chunk load_row(const Row& r, int c) {
+    Chunk ch;
+    ch.q = ld_u128(r.w + c * 16);
+    ch.e = ld_u8(r.s + (c >> 1));
+    return ch;
+  }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
     ch.q = ld_u128(a.w0 + row * a.K + c * 16);
@@ -75,6 +83,17 @@ template <bool F16S>
 struct FmtW8 {
   static constexpr int KPC = 16, SUB = 1;
   struct Chunk { uint4 q; uint32_t s; };
+  struct Row { const uint8_t* w; const uint8_t* s; };
+  __device__ static Row row(const PlaneArgs& a, int64_t r) {
+    return {a.w0 + r * a.K, a.s + r * (a.K / 64) * (F16S ? 2 : 4)};
+  }
+  __device__ static Chunk load_row(const Row& r, int c) {
+    Chunk ch;
+    ch.q = ld_u128(r.w + c * 16);
+    if constexpr (F16S) ch.s = ld_u16(r.s + (c >> 2) * 2);
+    else ch.s = ld_u32(r.s + (c >> 2) * 4);
+    return ch;
+  }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
     ch.q = ld_u128(a.w0 + row * a.K + c * 16);
@@ -113,6 +132,17 @@ struct FmtW8 {
 struct FmtW6 {
   static constexpr int KPC = 32, SUB = 2;
   struct Chunk { uint4 lo; uint2 hi; uint32_t s; };
+  struct Row { const uint8_t* l; const uint8_t* h; const uint8_t* s; };
+  __device__ static Row row(const PlaneArgs& a, int64_t r) {
+    return {a.w0 + r * (a.K / 2), a.w1 + r * (a.K / 4), a.s + r * (a.K / 32) * 2};
+  }
+  __device__ static Chunk load_row(const Row& r, int c) {
+    Chunk ch;
+    ch.lo = ld_u128(r.l + c * 16);
+    ch.hi = ld_u64(r.h + c * 8);
+    ch.s = ld_u16(r.s + c * 2);
+    return ch;
+  }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
     ch.lo = ld_u128(a.w0 + row * (a.K / 2) + c * 16);
@@ -174,6 +204,14 @@ struct FmtW6 {
 struct FmtNV4 {
   static constexpr int KPC = 32, SUB = 2;
   struct Chunk { uint4 q; uint32_t s; };
+  struct Row { const uint8_t* w; const uint8_t* s; };
+  __device__ static Row row(const PlaneArgs& a, int64_t r) { return {a.w0 + r * (a.K / 2), a.s + r * (a.K / 16)}; }
+  __device__ static Chunk load_row(const Row& r, int c) {
+    Chunk ch;
+    ch.q = ld_u128(r.w + c * 16);
+    ch.s = ld_u16(r.s + c * 2);
+    return ch;
+  }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
     ch.q = ld_u128(a.w0 + row * (a.K / 2) + c * 16);
@@ -186,11 +224,14 @@ struct FmtNV4 {
     const float sc = sub ? sc2.y : sc2.x;
     const uint32_t d0 = sub ? ch.q.z : ch.q.x;
     const uint32_t d1 = sub ? ch.q.w : ch.q.y;
-    w[0] = fp4x2_to_bf16x2<0>(d0, sc); w[1] = fp4x2_to_bf16x2<1>(d0, sc);
-    w[2] = fp4x2_to_bf16x2<2>(d0, sc); w[3] = fp4x2_to_bf16x2<3>(d0, sc);
-    w[4] = fp4x2_to_bf16x2<0>(d1, sc); w[5] = fp4x2_to_bf16x2<1>(d1, sc);
-    w[6] = fp4x2_to_bf16x2<2>(d1, sc); w[7] = fp4x2_to_bf16x2<3>(d1, sc);
+    w[0] = pair(fp4x2_to_f32x2<0>(d0), sc); w[1] = pair(fp4x2_to_f32x2<1>(d0), sc);
+    w[2] = pair(fp4x2_to_f32x2<2>(d0), sc); w[3] = pair(fp4x2_to_f32x2<3>(d0), sc);
+    w[4] = pair(fp4x2_to_f32x2<0>(d1), sc); w[5] = pair(fp4x2_to_f32x2<1>(d1), sc);
+    w[6] = pair(fp4x2_to_f32x2<2>(d1), sc); w[7] = pair(fp4x2_to_f32x2<3>(d1), sc);
   }
+  // e2m1 * e4m3 has at most 6 significant bits: the fp32 product and its
+  // bf16 rounding are exact.
+  __device__ static uint32_t pair(f32x2_t v, float sc) { return pack_bf16x2(v.x * sc, v.y * sc); }
 };
 
 // INT2 coarse head: codes P [N, K/4] (element j of each 4-group in bit pair
@@ -201,6 +242,28 @@ template <bool E4M3, int GC>
 struct FmtInt2 {
   static constexpr int KPC = 64, SUB = 4;
   struct Chunk { uint4 q; uint2 s; };
+  struct Row { const uint8_t* w; const uint8_t* s; int G; };
+  __device__ static Row row(const PlaneArgs& a, int64_t r) {
+    return {a.w0 + r * (a.K / 4), a.s + r * (a.K / a.G) * (E4M3 ? 1 : 2), a.G};
+  }
+  __device__ static Chunk load_row(const Row& r, int c) {
+    Chunk ch;
+    ch.q = ld_u128(r.w + c * 16);
+    const uint8_t* sp = r.s;
+    if constexpr (GC == 16) {
+      if constexpr (E4M3) { ch.s.x = ld_u32(sp + c * 4); ch.s.y = 0; }
+      else ch.s = ld_u64(sp + c * 8);
+    } else if constexpr (GC == 32) {
+      if constexpr (E4M3) ch.s.x = ld_u16(sp + c * 2);
+      else ch.s.x = ld_u32(sp + c * 4);
+      ch.s.y = 0;
+    } else {
+      const int g = (c * 64) / r.G;
+      ch.s.x = E4M3 ? ld_u8(sp + g) : ld_u16(sp + g * 2);
+      ch.s.y = 0;
+    }
+    return ch;
+  }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
     ch.q = ld_u128(a.w0 + row * (a.K / 4) + c * 16);
@@ -264,6 +327,14 @@ struct FmtInt2 {
 struct FmtBF16 {
   static constexpr int KPC = 16, SUB = 1;
   struct Chunk { uint4 a, b; };
+  struct Row { const uint8_t* w; };
+  __device__ static Row row(const PlaneArgs& p, int64_t r) { return {p.w0 + r * p.K * 2}; }
+  __device__ static Chunk load_row(const Row& r, int c) {
+    Chunk ch;
+    ch.a = ld_u128(r.w + c * 32);
+    ch.b = ld_u128(r.w + c * 32 + 16);
+    return ch;
+  }
   __device__ static Chunk load(const PlaneArgs& p, int64_t row, int c) {
     Chunk ch;
     const uint8_t* base = p.w0 + row * p.K * 2 + c * 32;
@@ -279,6 +350,21 @@ struct FmtBF16 {
 };
 
 // ------------------------------------------------------------------ core
+// Accumulation step of one (weight pair, activation pair).
+//   AccDot2: v_dot2_f32_bf16 (one instruction per pair; its internal rounding
+//            is the hardware's).
+//   AccFma:  two IEEE fp32 fma, low element first: every rounding is
+//            specified, so the sum can be replayed bit for bit on a CPU.
+struct AccDot2 {
+  __device__ static float step(uint32_t w, uint32_t x, float acc) { return dot2_bf16(w, x, acc); }
+};
+struct AccFma {
+  __device__ static float step(uint32_t w, uint32_t x, float acc) {
+    acc = __builtin_fmaf(bf16_lo(w), bf16_lo(x), acc);
+    return __builtin_fmaf(bf16_hi(w), bf16_hi(x), acc);
+  }
+};
+
 // Load one batch of chunks for RPL rows.  Row r of this lane is rows[r]
 // (negative = no row); chunk j is c0 + lrow + (jb + j) * lpr, and chunks at
 // or past cend (the end of the K slice) are neither loaded nor used.
@@ -304,7 +390,7 @@ __device__ __forceinline__ void load_batch(ChunkBatch<F, RPL>& b, const PlaneArg
 
 // x[m][k] lives at xs[m * xstride + k - kx0] (LDS or global, bf16).
 // Rows m >= M of x are not read (their accumulators stay 0).
-template <class F, int MT, int RPL, class XPtr>
+template <class F, int MT, int RPL, class XPtr, class Acc = AccDot2>
 __device__ __forceinline__ void compute_batch(const ChunkBatch<F, RPL>& b, XPtr xs, int xstride, int kx0, int M,
                                               int c0, int cend, int lrow, int lpr, int jb, int cpl,
                                               float (&acc)[RPL][MT]) {
@@ -330,7 +416,7 @@ __device__ __forceinline__ void compute_batch(const ChunkBatch<F, RPL>& b, XPtr 
         for (int r = 0; r < RPL; ++r) {
           float t = acc[r][m];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) t = dot2_bf16(w[r][i], xv[i], t);
+          for (int i = 0; i < 8; ++i) t = Acc::step(w[r][i], xv[i], t);
           acc[r][m] = t;
         }
       }
@@ -352,18 +438,20 @@ __device__ __forceinline__ void stage_x(uint16_t* lds, const uint16_t* x, int64_
   }
 }
 
-// Split-K slot protocol.  `part` is [ksplit][MT][N] fp32 for this batch entry.
-// Returns true in the (single) last-arriving workgroup of the tile, after all
-// slot writes of the tile are visible to it.
+// Split-K slot protocol.  Partial sums travel through LDS to wave 0, which
+// stores the tile's slot (coalesced), releases it at agent scope and takes the
+// tile ticket.  splitk_arrive returns true in the (single) last-arriving
+// workgroup of the tile, after an agent-scope acquire by every thread, so the
+// plain loads that follow see every slice's slot.
 __device__ __forceinline__ bool splitk_arrive(int* ticket, int ksplit) {
   __shared__ int last;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    const int old = ticket_acq_rel(ticket);
-    last = (old == ksplit - 1);
+  if (threadIdx.x < 64) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (threadIdx.x == 0) last = (__hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                                  ksplit - 1);
   }
   __syncthreads();
+  if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   return last != 0;
 }
 

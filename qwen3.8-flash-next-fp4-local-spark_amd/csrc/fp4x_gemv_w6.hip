@@ -1,7 +1,7 @@
 // Explicit GEMV instantiations (one translation unit per weight format, so
 // the library compiles in parallel).
-#include "fp4x_kernels.h"
+#include "fp4x_mfma.h"
 
 namespace fp4x {
-template int launch_gemv<FmtW6, EpiStore, 1>(const GemvLaunch&, int, hipStream_t);
+template int launch_gemv_mfma<FmtW6, EpiStore>(const GemvLaunch&, int, hipStream_t);
 }  // namespace fp4x

@@ -12,7 +12,7 @@
 // with the same split, scaled-SiLU kernel, W8 GEMV, gate-mean kernel.  Both
 // paths share the GEMV core, the K split and every epilogue function, so they
 // agree bit for bit.
-#include "fp4x_kernels.h"
+#include "fp4x_mfma.h"
 #include "../../include/fp4x.h"
 
 namespace fp4x {
@@ -37,33 +37,51 @@ struct HcUpArgs {
   int M, K, H, hc, bj, lpr, cpl;
 };
 
-template <class F, int MT>
-__global__ __launch_bounds__(1024) void hc_up_kernel(HcUpArgs p) {
-  extern __shared__ __align__(16) uint16_t lds_x[];      // [MT][K] bf16, then [MT][T] fp32 gates
-  const int T = p.hc * p.bj;                              // stored rows per tile
-  float* gl = reinterpret_cast<float*>(lds_x + MT * p.K);
+// The interleaved tile of T = hc*bj stored rows is T/16 MFMA row groups of
+// KW waves each; every group runs the same K mapping, MFMA order and
+// wave-order reduction as gemv_mfma_kernel, so each row's sum equals the one
+// w8_linear gives for that row.
+template <class F>
+__global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
+  extern __shared__ __align__(16) uint16_t lds[];
+  const int T = p.hc * p.bj;
+  const int KW = p.lpr;                                   // waves per 16-row group
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int lpr = p.lpr, lrow = lane & (lpr - 1), slot = lane / lpr, spw = 64 / lpr;
-  const int rt = wave * spw + slot;                       // row within tile
-  const int64_t tile0 = (int64_t)blockIdx.x * T;
-  int64_t rows[1] = {rt < T ? tile0 + rt : -1};
-  float acc[1][MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) acc[0][m] = 0.0f;
-  for (int jb = 0; jb < p.cpl; jb += kCplBatch) {
-    ChunkBatch<F, 1> cb;
-    load_batch<F, 1>(cb, p.pa, rows, 0, p.K / F::KPC, lrow, lpr, jb, p.cpl);
+  const int grp = wave / KW, wv = wave - grp * KW;
+  const int n = lane & 15, g = lane >> 4;
+  const size_t xbytes = ((size_t)p.M * p.K * 2 + 15) & ~(size_t)15;
+  float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + xbytes);
+  float* gl = red + (size_t)(T / 16) * (KW > 1 ? KW - 1 : 0) * 256;
+  const int cend = p.K / F::KPC, cw = wv * 4 + g, cstep = 4 * KW;
+  const int J = (cend + cstep - 1) / cstep;
+  const int64_t row = (int64_t)blockIdx.x * T + grp * 16 + n;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int jb = 0; jb < J; jb += kJ) {
+    MfmaBatch<F> cb;
+    mfma_load<F>(cb, p.pa, row, 0, cend, cw, cstep, jb, J);
     if (jb == 0) {
-      stage_x<MT>(lds_x, p.bot, p.bot_stride, p.M, 0, p.K);
+      const int per_row = p.K / 8;
+      for (int i = threadIdx.x; i < p.M * per_row; i += blockDim.x) {
+        const int m = i / per_row, q = i - m * per_row;
+        reinterpret_cast<uint4*>(lds + m * p.K)[q] = *reinterpret_cast<const uint4*>(p.bot + m * p.bot_stride + q * 8);
+      }
       __syncthreads();
     }
-    compute_batch<F, MT, 1>(cb, (const uint16_t*)lds_x, p.K, 0, MT, 0, p.K / F::KPC, lrow, lpr, jb, p.cpl, acc);
+    mfma_compute<F>(cb, (const uint16_t*)lds, p.K, 0, p.M, true, 0, cend, cw, cstep, jb, J, acc);
   }
+  // wave-order reduction within each row group
+  float* gred = red + (size_t)grp * (KW > 1 ? KW - 1 : 0) * 256;
+  if (wv > 0) reinterpret_cast<f32x4_t*>(gred)[(wv - 1) * 64 + lane] = acc;
+  __syncthreads();
+  if (wv == 0) {
+    for (int w = 1; w < KW; ++w) {
+      const f32x4_t o = reinterpret_cast<const f32x4_t*>(gred)[(w - 1) * 64 + lane];
+      acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
+    }
 #pragma unroll
-  for (int m = 0; m < MT; ++m) acc[0][m] = group_allreduce(acc[0][m], lpr);
-  if (lrow == 0 && rt < T)
-#pragma unroll
-    for (int m = 0; m < MT; ++m) gl[m * T + rt] = round_bf16(acc[0][m]);
+    for (int i = 0; i < 4; ++i)
+      if (g * 4 + i < p.M) gl[(g * 4 + i) * T + grp * 16 + n] = round_bf16(acc[i]);
+  }
   __syncthreads();
   for (int t = threadIdx.x; t < p.M * p.bj; t += blockDim.x) {
     const int m = t / p.bj, jj = t - m * p.bj;
@@ -135,14 +153,11 @@ int fp4x_hc_down(const void* x, int64_t x_stride, const void* q, const void* s, 
   p.M = M;
   p.N = N;
   p.ksplit = ksplit;
-  const int chunks = (K / ksplit) / 16;
-  p.lpr = layout_lpr(chunks);
-  p.cpl = (chunks + p.lpr - 1) / p.lpr;
   p.part = part;
   p.tickets = tickets;
   hipStream_t st = (hipStream_t)stream;
-  if (s_dtype == FP4X_DT_F16) return launch_gemv<FmtW8<true>, EpiHcDown>(p, 1, st);
-  return launch_gemv<FmtW8<false>, EpiHcDown>(p, 1, st);
+  if (s_dtype == FP4X_DT_F16) return launch_gemv_mfma<FmtW8<true>, EpiHcDown>(p, 1, st);
+  return launch_gemv_mfma<FmtW8<false>, EpiHcDown>(p, 1, st);
 }
 
 int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* si, int s_dtype, const void* nrm,
@@ -151,12 +166,12 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
   if (M < 0 || M > 16 || K <= 0 || K % 64 || H <= 0 || hc <= 0 || bj <= 0 || H % bj)
     return hc_fail("hc_up: bad shape (M <= 16, K % 64 == 0, H % bj == 0)");
   const int chunks = K / 16;
-  const int lpr = layout_lpr(chunks), spw = 64 / lpr;
+  const int KW = mfma_kw(chunks);
   const int T = hc * bj;
-  if (T % spw || T / spw > 16) return hc_fail("hc_up: hc*bj must be a multiple of the rows per wave and at most 16 waves");
-  const int mt = mt_of(M < 1 ? 1 : M);
-  const size_t lds = (size_t)mt * K * 2 + (size_t)mt * T * 4;
-  if (lds > 64 * 1024) return hc_fail("hc_up: K too large for the LDS activation stage");
+  if (T % 16 || (T / 16) * KW > 16) return hc_fail("hc_up: hc*bj must be a multiple of 16 with at most 16 waves per tile");
+  const size_t lds = (((size_t)(M < 1 ? 1 : M) * K * 2 + 15) & ~(size_t)15) + (size_t)(T / 16) * (KW - 1) * 256 * 4 +
+                     (size_t)16 * T * 4;
+  if (lds > 96 * 1024) return hc_fail("hc_up: K too large for the LDS activation stage");
   if (M > 0 && (!al(bot, 16) || bot_stride % 8 || bot_stride < K)) return hc_fail("hc_up: bot must be 16-byte aligned, stride % 8 == 0");
   if (!al(qi, 16) || !al(si, s_dtype == FP4X_DT_F16 ? 2 : 4)) return hc_fail("hc_up: misaligned weights");
   if (M == 0) return FP4X_OK;
@@ -170,22 +185,11 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
   p.nrm_stride = nrm_stride;
   p.out = static_cast<uint16_t*>(out);
   p.M = M; p.K = K; p.H = H; p.hc = hc; p.bj = bj;
-  p.lpr = lpr;
-  p.cpl = (chunks + lpr - 1) / lpr;
-  dim3 grid(H / bj), block((T / spw) * 64);
+  p.lpr = KW;
+  dim3 grid(H / bj), block((T / 16) * KW * 64);
   hipStream_t st = (hipStream_t)stream;
-#define FP4X_UP(MT_)                                                                                      \
-  if (s_dtype == FP4X_DT_F16) hipLaunchKernelGGL((hc_up_kernel<FmtW8<true>, MT_>), grid, block, lds, st, p); \
-  else hipLaunchKernelGGL((hc_up_kernel<FmtW8<false>, MT_>), grid, block, lds, st, p);
-  switch (mt) {
-    case 1: FP4X_UP(1) break;
-    case 2: FP4X_UP(2) break;
-    case 3: FP4X_UP(3) break;
-    case 4: FP4X_UP(4) break;
-    case 8: FP4X_UP(8) break;
-    default: FP4X_UP(16) break;
-  }
-#undef FP4X_UP
+  if (s_dtype == FP4X_DT_F16) hipLaunchKernelGGL(hc_up_mfma_kernel<FmtW8<true>>, grid, block, lds, st, p);
+  else hipLaunchKernelGGL(hc_up_mfma_kernel<FmtW8<false>>, grid, block, lds, st, p);
   return check_launch("hc_up");
 }
 

@@ -17,9 +17,10 @@ struct RefineArgs {
   int M, C, K, V, lpr, cpl;
 };
 
-// The candidate rows go through the same chunk layout, dot2 order and lane
-// butterfly as mx8_linear; e4m3 * 2^(e-127) is exact in bf16, so every
-// product equals the fp32 product the reference forms.
+// The candidate rows go through the chunk layout and lane butterfly of
+// mx8_linear, accumulated with IEEE fp32 fma (AccFma) so every rounding is
+// specified; e4m3 * 2^(e-127) is exact in bf16 and in fp32, and its product
+// with a bf16 activation is exact, as in the reference's fp32 dot.
 __global__ __launch_bounds__(kThreads) void refine_mx8_kernel(RefineArgs p) {
   extern __shared__ __align__(16) uint16_t lds_x[];
   const int m = blockIdx.y;
@@ -39,16 +40,30 @@ __global__ __launch_bounds__(kThreads) void refine_mx8_kernel(RefineArgs p) {
       stage_x<1>(lds_x, p.x + (int64_t)m * p.K, p.K, 1, 0, p.K);
       __syncthreads();
     }
-    compute_batch<FmtMX8, 1, 1>(cb, (const uint16_t*)lds_x, p.K, 0, 1, 0, p.K / 16, lrow, lpr, jb, p.cpl, acc);
+    compute_batch<FmtMX8, 1, 1, const uint16_t*, AccFma>(cb, (const uint16_t*)lds_x, p.K, 0, 1, 0, p.K / 16, lrow,
+                                                         lpr, jb, p.cpl, acc);
   }
   const float v = group_allreduce(acc[0][0], lpr);
   if (lrow == 0 && rows[0] >= 0) store_out(p.out, (int64_t)m * p.out_stride + rows[0], p.out_dtype, v);
 }
 
 // ------------------------------------------------------------------ top-k
+// Three launches per call (no grid-wide waits):
+//   A  slice maxima: the row is cut into <= 4096 slices of S elements (S a
+//      multiple of 8); smax[m][i] = largest order key of slice i.  Also zeroes
+//      the row's candidate counter.
+//   B  every workgroup of a row derives T0 = the C-th largest slice maximum
+//      (a lower bound of the C-th largest element: C slices each hold an
+//      element >= T0) and appends its elements with key >= T0 to the row's
+//      candidate list (composite keys, wave-aggregated atomics).
+//   C  one workgroup per row sorts the candidates (at most 4096) by the
+//      total order and writes the first C indices.  Rows with fewer than C
+//      slices, or more than 4096 candidates (massive ties), take the exact
+//      threshold path in C instead.
 constexpr int kTkThreads = 1024;
-constexpr int kTkCap = 4096;     // candidate buffer (composite keys)
-constexpr int kTkSlices = 4096;  // slice maxima
+constexpr int kTkCap = 4096;     // candidates per row
+constexpr int kTkSlices = 4096;  // slice maxima per row
+constexpr int kTkB = 32;         // collecting workgroups per row
 
 // bf16 bits -> 16-bit key increasing with the value; -0 counts as +0 and
 // every NaN as the largest value.
@@ -63,163 +78,178 @@ __device__ __forceinline__ uint64_t tk_comp(uint32_t key, uint32_t i) {
   return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - i);
 }
 
-struct TkShared {
-  uint64_t cand[kTkCap];
-  uint16_t smax[kTkSlices];
+__host__ __device__ inline int tk_slice(int V) { return 8 * ((V + 8 * kTkSlices - 1) / (8 * kTkSlices)); }
+
+struct TkHist {
   uint32_t hist[256];
-  int n;          // candidates appended
-  int sel_bin;    // histogram walk result
-  int sel_above;  // elements in bins above sel_bin
+  int sel_bin, sel_above;
 };
 
-// Walk a 256-bin histogram from the top: returns the bin holding the k-th
-// largest element (k >= 1) and the count of elements in higher bins.
-__device__ void tk_walk(TkShared& sh, int k) {
+// Walk a 256-bin histogram from the top: the bin holding the k-th largest
+// element (k >= 1) and the count of elements in higher bins.
+__device__ void tk_walk(TkHist& h, int k) {
   if (threadIdx.x == 0) {
     int above = 0, b = 255;
     for (; b > 0; --b) {
-      if (above + (int)sh.hist[b] >= k) break;
-      above += sh.hist[b];
+      if (above + (int)h.hist[b] >= k) break;
+      above += h.hist[b];
     }
-    sh.sel_bin = b;
-    sh.sel_above = above;
+    h.sel_bin = b;
+    h.sel_above = above;
   }
   __syncthreads();
 }
 
-// Exact k-th largest key among n keys given by get(i) (two 8-bit rounds).
-// Returns the key; *n_above receives the number of keys strictly above it.
+// Exact k-th largest key among n keys get(i) (two 8-bit rounds); *n_above
+// receives the number of keys strictly above it.
 template <class Get>
-__device__ uint32_t tk_kth(TkShared& sh, Get get, int n, int k, int* n_above) {
-  for (int i = threadIdx.x; i < 256; i += blockDim.x) sh.hist[i] = 0;
+__device__ uint32_t tk_kth(TkHist& h, Get get, int n, int k, int* n_above) {
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) h.hist[i] = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&sh.hist[get(i) >> 8], 1u);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&h.hist[get(i) >> 8], 1u);
   __syncthreads();
-  tk_walk(sh, k);
-  const uint32_t b1 = sh.sel_bin;
-  const int above1 = sh.sel_above;
+  tk_walk(h, k);
+  const uint32_t b1 = h.sel_bin;
+  const int above1 = h.sel_above;
   __syncthreads();
-  for (int i = threadIdx.x; i < 256; i += blockDim.x) sh.hist[i] = 0;
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) h.hist[i] = 0;
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const uint32_t kk = get(i);
-    if ((kk >> 8) == b1) atomicAdd(&sh.hist[kk & 255u], 1u);
+    if ((kk >> 8) == b1) atomicAdd(&h.hist[kk & 255u], 1u);
   }
   __syncthreads();
-  tk_walk(sh, k - above1);
-  const uint32_t t = (b1 << 8) | (uint32_t)sh.sel_bin;
-  *n_above = above1 + sh.sel_above;
+  tk_walk(h, k - above1);
+  const uint32_t t = (b1 << 8) | (uint32_t)h.sel_bin;
+  *n_above = above1 + h.sel_above;
   __syncthreads();
   return t;
 }
 
-// Wave-aggregated append of (flag ? comp : nothing) into sh.cand.
-__device__ __forceinline__ void tk_append(TkShared& sh, bool flag, uint64_t comp) {
+// Wave-aggregated append of comp (when flag) to list[*count]; positions past
+// cap are counted but not written.
+__device__ __forceinline__ void tk_append(uint64_t* list, int* count, int cap, bool flag, uint64_t comp) {
   const uint64_t mask = __ballot(flag);
   if (!mask) return;
   const int lane = threadIdx.x & 63;
-  int base = 0;
   const int leader = __ffsll((unsigned long long)mask) - 1;
-  if (lane == leader) base = atomicAdd(&sh.n, __popcll(mask));
+  int base = 0;
+  if (lane == leader) base = atomicAdd(count, __popcll(mask));
   base = __shfl(base, leader, 64);
   if (flag) {
     const int pos = base + __popcll(mask & ((1ull << lane) - 1ull));
-    if (pos < kTkCap) sh.cand[pos] = comp;
+    if (pos < cap) list[pos] = comp;
   }
 }
 
-// Descending bitonic sort of sh.cand[0, n2), n2 a power of two.
-__device__ void tk_sort(TkShared& sh, int n2) {
+struct TkWork {              // per row, in the caller's workspace
+  uint64_t cand[kTkCap];
+  uint16_t smax[kTkSlices];
+  int count;
+  int pad[3];
+};
+
+__global__ __launch_bounds__(256) void topk_slicemax_kernel(const uint16_t* logits, int64_t stride, int V,
+                                                            TkWork* work) {
+  const int m = blockIdx.y;
+  const uint16_t* row = logits + (int64_t)m * stride;
+  TkWork& w = work[m];
+  const int S = tk_slice(V), ns = (V + S - 1) / S;
+  if (blockIdx.x == 0 && threadIdx.x == 0) w.count = 0;
+  const int sl = blockIdx.x * blockDim.x + threadIdx.x;
+  if (sl >= ns) return;
+  uint32_t mx = 0;
+  const int e0 = sl * S;
+  for (int e = e0; e < e0 + S; e += 8) {
+    if (e + 8 <= V) {
+      const uint4 v = *reinterpret_cast<const uint4*>(row + e);
+      const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) mx = max(mx, max(tk_key(d[q] & 0xffffu), tk_key(d[q] >> 16)));
+    } else {
+      for (int i = e; i < V; ++i) mx = max(mx, tk_key(row[i]));
+    }
+  }
+  w.smax[sl] = (uint16_t)mx;
+}
+
+__global__ __launch_bounds__(256) void topk_collect_kernel(const uint16_t* logits, int64_t stride, int V, int C,
+                                                           TkWork* work) {
+  __shared__ uint16_t smax[kTkSlices];
+  __shared__ TkHist h;
+  const int m = blockIdx.y;
+  const uint16_t* row = logits + (int64_t)m * stride;
+  TkWork& w = work[m];
+  const int S = tk_slice(V), ns = (V + S - 1) / S;
+  for (int i = threadIdx.x; i < ns; i += blockDim.x) smax[i] = w.smax[i];
+  __syncthreads();
+  int above;
+  const uint32_t T0 = tk_kth(h, [&](int i) { return (uint32_t)smax[i]; }, ns, C, &above);
+  // this workgroup's share of the row, in whole 8-element vectors
+  const int nvec = (V + 7) / 8;
+  const int per = (nvec + gridDim.x - 1) / gridDim.x;
+  const int v0 = blockIdx.x * per, v1 = min(nvec, v0 + per);
+  for (int base = v0; base < v1; base += blockDim.x) {
+    const int vi = base + threadIdx.x;
+    uint32_t d[4] = {0, 0, 0, 0};
+    const bool full = vi < v1 && vi * 8 + 8 <= V;
+    if (full) {
+      const uint4 v = *reinterpret_cast<const uint4*>(row + (int64_t)vi * 8);
+      d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = vi * 8 + q;
+      bool ok = vi < v1 && i < V;
+      uint32_t key = 0;
+      if (ok) key = full ? tk_key(q & 1 ? d[q >> 1] >> 16 : d[q >> 1] & 0xffffu) : tk_key(row[i]);
+      tk_append(w.cand, &w.count, kTkCap, ok && key >= T0, tk_comp(key, i));
+    }
+  }
+}
+
+// Descending bitonic sort of a[0, n2), n2 a power of two.
+__device__ void tk_sort(uint64_t* a, int n2) {
   for (int size = 2; size <= n2; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       for (int t = threadIdx.x; t < n2 / 2; t += blockDim.x) {
         const int i = 2 * t - (t & (stride - 1));
         const int j = i + stride;
         const bool desc = (i & size) == 0;
-        const uint64_t a = sh.cand[i], b = sh.cand[j];
-        if ((a < b) == desc) { sh.cand[i] = b; sh.cand[j] = a; }
+        const uint64_t x = a[i], y = a[j];
+        if ((x < y) == desc) { a[i] = y; a[j] = x; }
       }
       __syncthreads();
     }
   }
 }
 
-__global__ __launch_bounds__(kTkThreads) void topk_rows_kernel(const uint16_t* logits, int64_t stride, int V, int C,
-                                                                int64_t* idx_out) {
-  __shared__ TkShared sh;
+__global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const uint16_t* logits, int64_t stride, int V, int C,
+                                                                 TkWork* work, int64_t* idx_out) {
+  __shared__ uint64_t cand[kTkCap];
+  __shared__ TkHist h;
+  __shared__ int n_sh;
   const int m = blockIdx.x;
   const uint16_t* row = logits + (int64_t)m * stride;
   int64_t* out = idx_out + (int64_t)m * C;
-  if (threadIdx.x == 0) sh.n = 0;
-  __syncthreads();
-
-  bool exact = false;  // selection by the exact threshold path
+  const int S = tk_slice(V), ns = (V + S - 1) / S;
+  int n;
   if (V <= kTkCap) {
-    for (int i = threadIdx.x; i < V; i += blockDim.x) sh.cand[i] = tk_comp(tk_key(row[i]), i);
-    if (threadIdx.x == 0) sh.n = V;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) cand[i] = tk_comp(tk_key(row[i]), i);
+    n = V;
+  } else if (ns >= C && work[m].count <= kTkCap) {
+    n = work[m].count;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) cand[i] = work[m].cand[i];
   } else {
-    // Slice maxima: the C-th largest of >= C slice maxima bounds the C-th
-    // largest element from below, so every top-C element is >= T0.
-    const int S = 8 * ((V + 8 * kTkSlices - 1) / (8 * kTkSlices));
-    const int ns = (V + S - 1) / S;
-    if (ns >= C) {
-      for (int sl = threadIdx.x; sl < ns; sl += blockDim.x) {
-        uint32_t mx = 0;
-        const int e0 = sl * S;
-        for (int e = e0; e < e0 + S; e += 8) {
-          if (e + 8 <= V) {
-            const uint4 v = *reinterpret_cast<const uint4*>(row + e);
-            const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              mx = max(mx, tk_key(d[q] & 0xffffu));
-              mx = max(mx, tk_key(d[q] >> 16));
-            }
-          } else {
-            for (int i = e; i < V; ++i) mx = max(mx, tk_key(row[i]));
-          }
-        }
-        sh.smax[sl] = (uint16_t)mx;
-      }
-      __syncthreads();
-      int above;
-      const uint32_t T0 = tk_kth(sh, [&](int i) { return (uint32_t)sh.smax[i]; }, ns, C, &above);
-      // collect every element >= T0
-      const int nvec = V / 8;
-      for (int vi = threadIdx.x; vi < (nvec + blockDim.x - 1) / blockDim.x * blockDim.x; vi += blockDim.x) {
-        uint4 v = make_uint4(0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu);  // -NaN pattern: key 0
-        if (vi < nvec) v = *reinterpret_cast<const uint4*>(row + (int64_t)vi * 8);
-        const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const uint32_t key = vi < nvec ? tk_key(q & 1 ? d[q >> 1] >> 16 : d[q >> 1] & 0xffffu) : 0u;
-          tk_append(sh, vi < nvec && key >= T0, tk_comp(key, vi * 8 + q));
-        }
-      }
-      for (int i = nvec * 8 + threadIdx.x; i < V; i += blockDim.x) {
-        const uint32_t key = tk_key(row[i]);
-        if (key >= T0) {
-          const int pos = atomicAdd(&sh.n, 1);
-          if (pos < kTkCap) sh.cand[pos] = tk_comp(key, i);
-        }
-      }
-      __syncthreads();
-      exact = sh.n > kTkCap;
-    } else {
-      exact = true;
-    }
-  }
-  __syncthreads();
-  if (exact) {
-    // Exact threshold T and the ties at T taken in index order.
-    if (threadIdx.x == 0) sh.n = 0;
+    // exact threshold T, the elements above it, and ties at T in index order
+    if (threadIdx.x == 0) n_sh = 0;
     __syncthreads();
     int above;
-    const uint32_t T = tk_kth(sh, [&](int i) { return tk_key(row[i]); }, V, C, &above);
+    const uint32_t T = tk_kth(h, [&](int i) { return tk_key(row[i]); }, V, C, &above);
     for (int i0 = 0; i0 < V; i0 += blockDim.x) {
       const int i = i0 + threadIdx.x;
       const uint32_t key = i < V ? tk_key(row[i]) : 0u;
-      tk_append(sh, i < V && key > T, tk_comp(key, i));
+      tk_append(cand, &n_sh, kTkCap, i < V && key > T, tk_comp(key, i));
     }
     __syncthreads();
     const int need = C - above;
@@ -230,20 +260,19 @@ __global__ __launch_bounds__(kTkThreads) void topk_rows_kernel(const uint16_t* l
         const bool eq = i < V && tk_key(row[i]) == T;
         const uint64_t mask = __ballot(eq);
         const int pos = taken + __popcll(mask & ((1ull << threadIdx.x) - 1ull));
-        if (eq && pos < need) sh.cand[above + pos] = tk_comp(T, i);
+        if (eq && pos < need) cand[above + pos] = tk_comp(T, i);
         taken += __popcll(mask);
       }
-      if (threadIdx.x == 0) sh.n = C;
     }
-    __syncthreads();
+    n = C;
   }
-  const int n = sh.n;
   int n2 = 1;
   while (n2 < n) n2 <<= 1;
-  for (int i = n + threadIdx.x; i < n2; i += blockDim.x) sh.cand[i] = 0;
   __syncthreads();
-  tk_sort(sh, n2);
-  for (int i = threadIdx.x; i < C; i += blockDim.x) out[i] = (int64_t)(0xffffffffu - (uint32_t)(sh.cand[i] & 0xffffffffu));
+  for (int i = n + threadIdx.x; i < n2; i += blockDim.x) cand[i] = 0;
+  __syncthreads();
+  tk_sort(cand, n2);
+  for (int i = threadIdx.x; i < C; i += blockDim.x) out[i] = (int64_t)(0xffffffffu - (uint32_t)(cand[i] & 0xffffffffu));
 }
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -254,15 +283,29 @@ using namespace fp4x;
 
 extern "C" {
 
-int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int64_t* idx_out, void* stream) {
+int64_t fp4x_topk_workspace_size(int M) { return (int64_t)(M < 0 ? 0 : M) * (int64_t)sizeof(TkWork); }
+
+int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int64_t* idx_out, void* workspace,
+                   int64_t ws_bytes, void* stream) {
   if (M < 0 || V < 1 || C < 1 || C > V || C > 2048) { set_error("topk_rows: need 1 <= C <= min(V, 2048)"); return FP4X_ERR_ARG; }
   if (stride < V || stride % 8 || !al16(logits)) {
     set_error("topk_rows: logits must be 16-byte aligned with a row stride that is a multiple of 8");
     return FP4X_ERR_ARG;
   }
+  if (ws_bytes < fp4x_topk_workspace_size(M) || (M > 0 && !al16(workspace))) {
+    set_error("topk_rows: workspace smaller than fp4x_topk_workspace_size(M) or misaligned");
+    return FP4X_ERR_ARG;
+  }
   if (M == 0) return FP4X_OK;
-  hipLaunchKernelGGL(topk_rows_kernel, dim3(M), dim3(kTkThreads), 0, (hipStream_t)stream,
-                     static_cast<const uint16_t*>(logits), stride, V, C, idx_out);
+  hipStream_t st = (hipStream_t)stream;
+  TkWork* w = static_cast<TkWork*>(workspace);
+  const uint16_t* lg = static_cast<const uint16_t*>(logits);
+  if (V > kTkCap) {
+    const int S = tk_slice(V), ns = (V + S - 1) / S;
+    hipLaunchKernelGGL(topk_slicemax_kernel, dim3((ns + 255) / 256, M), dim3(256), 0, st, lg, stride, V, w);
+    if (ns >= C) hipLaunchKernelGGL(topk_collect_kernel, dim3(kTkB, M), dim3(256), 0, st, lg, stride, V, C, w);
+  }
+  hipLaunchKernelGGL(topk_select_kernel, dim3(M), dim3(kTkThreads), 0, st, lg, stride, V, C, w, idx_out);
   return check_launch("topk_rows");
 }
 

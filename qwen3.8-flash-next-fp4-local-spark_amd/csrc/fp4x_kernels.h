@@ -106,29 +106,47 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvLaunch p) {
     }
     return;
   }
-  // split-K: write this slice's partials, last workgroup of the tile reduces
-  float* part = p.part + (int64_t)b * p.ksplit * MT * p.N;
+  // split-K: the tile's partials go through LDS to wave 0, which writes the
+  // slice's slot; the last workgroup of the tile sums slots 0..ks-1 in order.
+  __shared__ float tile_part[kWaves * 64 * RPL * MT];
+  const int nrow = tile_rows;                       // rows of this tile
   if (lrow == 0) {
 #pragma unroll
     for (int r = 0; r < RPL; ++r)
-      if (rows[r] >= 0)
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-          if (m < p.M) part[((int64_t)split * MT + m) * p.N + rows[r]] = acc[r][m] * p.gs;
+      for (int m = 0; m < MT; ++m)
+        tile_part[m * nrow + wave * spw * RPL + r * spw + slot] = acc[r][m] * p.gs;
+  }
+  __syncthreads();
+  float* part = p.part + (int64_t)b * p.ksplit * MT * p.N;
+  const int64_t tile0 = (int64_t)blockIdx.x * tile_rows;
+  if (threadIdx.x < 64) {
+    for (int i = threadIdx.x; i < p.M * nrow; i += 64) {
+      const int m = i / nrow;
+      const int64_t row = tile0 + (i - m * nrow);
+      if (row < p.N) part[((int64_t)split * MT + m) * p.N + row] = tile_part[i];
+    }
   }
   const int tiles = gridDim.x;
   int* ticket = p.tickets + (int64_t)b * tiles + blockIdx.x;
   if (!splitk_arrive(ticket, p.ksplit)) return;
-  const int64_t tile0 = (int64_t)blockIdx.x * tile_rows;
-  for (int i = threadIdx.x; i < p.M * tile_rows; i += blockDim.x) {
-    const int m = i / tile_rows;
-    const int64_t row = tile0 + (i - m * tile_rows);
+  for (int i = threadIdx.x; i < p.M * nrow; i += blockDim.x) {
+    const int m = i / nrow;
+    const int64_t row = tile0 + (i - m * nrow);
     if (row >= p.N) continue;
-    float v = ld_coherent(part + (int64_t)m * p.N + row);
-    for (int s = 1; s < p.ksplit; ++s) v += ld_coherent(part + ((int64_t)s * MT + m) * p.N + row);
-    Epi::apply(p, b, m, row, v);
+    const float* src = part + (int64_t)m * p.N + row;
+    const int64_t sstride = (int64_t)MT * p.N;
+    float tot = 0.0f;
+    for (int s0 = 0; s0 < p.ksplit; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = s0 + j < p.ksplit ? src[(s0 + j) * sstride] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < p.ksplit) tot = s0 + j == 0 ? v[j] : tot + v[j];
+    }
+    Epi::apply(p, b, m, row, tot);
   }
-  __syncthreads();
   if (threadIdx.x == 0) ticket_reset(ticket);
 }
 

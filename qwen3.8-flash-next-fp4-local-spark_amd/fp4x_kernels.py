@@ -216,12 +216,16 @@ def topk_rows(logits, C):
     _need_cuda(logits)
     if logits.dtype != torch.bfloat16:
         raise TypeError("fp4x: topk_rows takes bf16 logits")
-    if logits.stride(1) != 1 or logits.stride(0) % 8 or logits.data_ptr() % 16:
-        logits = logits.contiguous()
     m, v = logits.shape
+    if logits.stride(1) != 1 or logits.stride(0) % 8 or logits.data_ptr() % 16:
+        padded = torch.empty((m, -(-v // 8) * 8), dtype=logits.dtype, device=logits.device)
+        padded[:, :v] = logits
+        logits = padded
     idx = torch.empty((m, C), dtype=torch.int64, device=logits.device)
-    _L.check(_L.lib().fp4x_topk_rows(_ptr(logits), logits.stride(0), m, v, C, _ptr(idx), _L.stream_of(logits)),
-             "topk_rows")
+    nbytes = _L.lib().fp4x_topk_workspace_size(m)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=logits.device)
+    _L.check(_L.lib().fp4x_topk_rows(_ptr(logits), logits.stride(0), m, v, C, _ptr(idx), _ptr(ws), nbytes,
+                                     _L.stream_of(logits)), "topk_rows")
     return idx
 
 

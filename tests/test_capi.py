@@ -62,7 +62,8 @@ def test_argument_errors_without_gpu(lib):
     assert L.fp4x_w8_linear(None, 100, None, None, 1, None, 0, 1, 8, 100, 1, None, None, None) == _fp4x.ERR_ARG
     assert L.fp4x_w6_linear(None, 2560, None, None, None, None, 0, 1, 8, 2560, 4, None, None, None) == _fp4x.ERR_ARG
     assert L.fp4x_int2_logits(None, 2560, None, None, 2, None, None, 0, 1, 8, 2560, 48, None) == _fp4x.ERR_ARG
-    assert L.fp4x_topk_rows(None, 64, 1, 64, 65, None, None) == _fp4x.ERR_ARG
+    assert L.fp4x_topk_rows(None, 64, 1, 64, 65, None, None, 0, None) == _fp4x.ERR_ARG
+    assert L.fp4x_topk_workspace_size(3) > 3 * 4096 * 8
     assert L.fp4x_hc_up(None, 640, None, None, 1, None, 10240, None, 1, 640, 2560, 4, 3, None) == _fp4x.ERR_ARG
     # empty problems are no-ops
     assert L.fp4x_mx8_linear(None, 2560, None, None, None, 0, 0, 64, 2560, 1, None, None, None) == _fp4x.OK
@@ -71,5 +72,5 @@ def test_argument_errors_without_gpu(lib):
 def test_splitk_sizes():
     import _fp4x
     part, tick = _fp4x.splitk_sizes(_fp4x.FMT_W8_F32, 3, 640, 10240, 16)
-    assert part == 16 * 3 * 640
-    assert tick == 640 // 32                  # 4 waves x 8 rows per tile (lpr 8)
+    assert part == 16 * 16 * 640              # one 16-row slot tile per K slice
+    assert tick == 640 // 16                  # one ticket per 16-row tile

@@ -1,5 +1,10 @@
-"""Pins the rounding of v_dot2_f32_bf16 (the accumulation step of every GEMV)
-against the oracle's model, on crafted and random operands."""
+"""Measures the rounding of v_dot2_f32_bf16 against the oracle's models.
+
+The instruction is not a correctly rounded three-term sum: on random
+operands it agrees with RN(a0*b0 + a1*b1 + c) for about 88% of inputs and
+with chained IEEE fma for about 84%.  No GEMV accumulates with it (the dense
+cores use MFMA, the rescore uses IEEE fma); the test bounds its error by
+2^-23 * (|a0 b0| + |a1 b1| + |c|) and records the agreement rates."""
 import numpy as np
 import pytest
 import torch
@@ -11,8 +16,9 @@ from gpu_helpers import dev
 
 def bits_pair(a0, a1):
     from oracle import formats as fm
-    return (fm.bf16_bits(np.float32(a0)).astype(np.uint32) |
-            (fm.bf16_bits(np.float32(a1)).astype(np.uint32) << 16))
+    lo = int(fm.bf16_bits(np.array([a0], np.float32))[0])
+    hi = int(fm.bf16_bits(np.array([a1], np.float32))[0])
+    return lo | (hi << 16)
 
 
 def operands(rng, n):
@@ -52,5 +58,15 @@ def test_dot2_rounding_model(gpu):
         want = ordered.dot2(a, b, c, mode)
         report[mode] = float(np.mean(got.view(np.uint32) == want.view(np.uint32)))
     print(f"dot2 agreement per model: {report}; crafted gpu={got[:4].tolist()}")
-    want = ordered.dot2(a, b, c)
-    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), report
+    rn = ordered.dot2(a, b, c, 0).astype(np.float64)
+
+    def halves(v):
+        lo = (v & 0xFFFF).astype(np.uint32) << 16
+        hi = v & 0xFFFF0000
+        return lo.view(np.float32).astype(np.float64), hi.view(np.float32).astype(np.float64)
+    a0, a1 = halves(a)
+    b0, b1 = halves(b)
+    l1 = np.abs(a0 * b0) + np.abs(a1 * b1) + np.abs(c.astype(np.float64))
+    err = np.abs(got.astype(np.float64) - rn)
+    assert np.all(err <= 2.0 ** -23 * l1), float((err / (2.0 ** -23 * l1)).max())
+    assert report[0] >= 0.8

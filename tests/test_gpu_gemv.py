@@ -4,7 +4,8 @@
   oracle's dequantize-then-round (all formats, all fp8 codes).
 * GEMV: |y - y_oracle| <= 1e-2 + 2e-3 |y_oracle| against the fp32-accumulated
   oracle, for M = 1..20 (M > 16 runs as 16-row launches), split-K and tails;
-  and bit-exact against the oracle replaying the kernels' summation order.
+  and, in fp32, within the MFMA accumulation bound of the exact (float64)
+  sum (oracle.ordered.mfma_bound).
 """
 import numpy as np
 import pytest
@@ -125,13 +126,12 @@ def test_gemv_parity(gpu, F, fmt, M):
     ref = og.matmul_f32(x, w_op) * np.float32(gs)
     print(f"{fmt} M={M}: max|d| {np.abs(to_f32(y) - ref).max():.3g}")
     assert_tol(to_f32(y), ref, what=f"{fmt} M={M}")
-    # bit-exact against the oracle replaying the kernel's order (16-row blocks)
-    import _fp4x
-    lpr, _ = _fp4x.layout(FMT[fmt], k)
-    wb = fm.bf16_bits(w_op)
-    exact = np.concatenate([ordered.ordered_gemv(xb[m0:m0 + 16], wb, KPC[fmt], lpr, gs=gs)
-                            for m0 in range(0, M, 16)])
-    assert np.array_equal(bf16_bits(y), fm.bf16_bits(exact))
+    # fp32 sums within the MFMA accumulation bound of the exact sum
+    exact = ordered.exact_sum(x, w_op) * gs
+    y32 = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
+    bound = ordered.mfma_bound(x, w_op) * abs(gs)
+    assert np.all(np.abs(y32 - exact) <= bound), (np.abs(y32 - exact) / bound).max()
+    print(f"{fmt} M={M}: max |y - exact| / bound = {(np.abs(y32 - exact) / bound).max():.3g}")
 
 
 @pytest.mark.parametrize("fmt", ["mx8", "w8", "w6", "nv4"])
@@ -142,10 +142,9 @@ def test_gemv_split_k(gpu, F, fmt, ks):
     planes, w_op, gs = prep(fmt, rng, n, k)
     x, xb = act(rng, 3, k)
     y = run(F, fmt, bf16_dev(x), planes, ks, torch.float32)
-    import _fp4x
-    lpr, _ = _fp4x.layout(FMT[fmt], k // ks)
-    exact = ordered.ordered_gemv(xb, fm.bf16_bits(w_op), KPC[fmt], lpr, ksplit=ks, gs=gs)
-    assert np.array_equal(to_f32(y).view(np.uint32), exact.view(np.uint32))
+    exact = ordered.exact_sum(x, w_op) * gs
+    bound = ordered.mfma_bound(x, w_op, ks) * abs(gs)
+    assert np.all(np.abs(to_f32(y) - exact) <= bound), (np.abs(to_f32(y) - exact) / bound).max()
     # repeated calls reuse the re-armed tickets and give identical results
     for _ in range(3):
         y2 = run(F, fmt, bf16_dev(x), planes, ks, torch.float32)

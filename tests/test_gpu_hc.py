@@ -3,8 +3,9 @@
 * fused (hc_down + hc_up) and unfused (W8 GEMV, scaled SiLU, W8 GEMV, gate
   mean) agree bit for bit, over 97 seeded layers at the synthetic shape
   (x [3, 4 x 2560], W_down [640, 10240], W_up [10240, 640], 16 K-splits);
-* both match the oracle: DI exactly against the ordered replay, block_input
-  within bf16 rounding of the oracle's float64-sigmoid epilogue;
+* both match the oracle: DI within the MFMA accumulation bound of the exact
+  sum plus bf16 rounding, block_input within bf16 rounding of the oracle's
+  float64-sigmoid epilogue;
 * the split-K scratch is re-armed: tickets are zero after every call.
 """
 import numpy as np
@@ -64,8 +65,10 @@ def test_fused_equals_unfused_97_layers(gpu, F):
             import _fp4x
             qd, sd, qu, su = (t.cpu().numpy() for t in (qd_t, sd_t, qu_t, su_t))
             lpr, _ = _fp4x.layout(_fp4x.FMT_W8_F32, HC * H // KS)
-            exact = ordered.ordered_gemv(xb, fm.bf16_bits(fm.round_bf16(oq.dequant_w8(qd, sd))), 16, lpr, ksplit=KS)
-            assert np.array_equal(bf16_bits(di), fm.bf16_bits(exact)), f"layer {i} down"
+            wop = fm.round_bf16(oq.dequant_w8(qd, sd))
+            exact = ordered.exact_sum(x, wop)
+            bound = ordered.mfma_bound(x, wop, KS) + np.abs(exact) * 2.0 ** -8
+            assert np.all(np.abs(to_f32(di) - exact) <= bound), f"layer {i} down"
             _, _, bi_ref = ohc.mixer(x, qd, sd, qu, su, LR, HC)
             bot_o = ohc.scaled_silu(to_f32(di)[:, :LR], HC)       # the epilogue alone, from the GPU's di
             assert np.abs(to_f32(bot) - bot_o).max() <= np.abs(bot_o).max() * 2 ** -7
