@@ -254,25 +254,38 @@ def main():
     y1 = F.w8_linear(x3[7], q[7], s[7], (16, 512, 1, 4), torch.float32)
     assert torch.equal(y[7], y1)
 
-    graphs = []
+    # K steps run as replays of one graph holding G consecutive steps (every
+    # weight copy in turn, so launches follow each other without replay gaps),
+    # plus one graph for the K mod G remainder: exactly K launches are timed.
+    G = ncp * 8
     cs = torch.cuda.Stream()
     cs.wait_stream(torch.cuda.current_stream())
+
+    def capture(nsteps):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=cs):
+            for i in range(nsteps):
+                step(i)
+        return gr
+
     with torch.cuda.stream(cs):
         step(0)
         torch.cuda.synchronize()
-        for i in range(ncp):
-            gr = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gr, stream=cs):
-                step(i)
-            graphs.append(gr)
-        for i in range(args.warmup):
-            graphs[i % ncp].replay()
+        g_full = capture(G)
+        rem = args.steps % G
+        g_rem = capture(rem) if rem else None
+        for _ in range(args.warmup // G):
+            g_full.replay()
+        for i in range(args.warmup % G):
+            step(i)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record(cs)
-        for i in range(args.steps):
-            graphs[i % ncp].replay()
+        for _ in range(args.steps // G):
+            g_full.replay()
+        if g_rem is not None:
+            g_rem.replay()
         e1.record(cs)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
@@ -284,7 +297,7 @@ def main():
     sel = set("ABCDE") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
     if "B" in sel:
         bench_gates_single(F, torch, dev, kernels, q, s)
-    del qs, out3, graphs
+    del qs, out3, g_full, g_rem
     torch.cuda.empty_cache()
     if sel & {"A", "C"}:
         bench_dense(F, torch, dev, kernels)

@@ -3,6 +3,7 @@
 #include "fp4x_mfma.h"
 #include "../../include/fp4x.h"
 #include <cstdio>
+#include <cstdlib>
 
 namespace fp4x {
 
@@ -22,7 +23,7 @@ extern template int launch_gemv_mfma<FmtInt2<true, 0>, EpiStore>(const GemvLaunc
 
 static thread_local std::string g_err;
 
-int mfma_grid_target(int kw) {
+int device_cus() {
   static int cus = 0;
   if (!cus) {
     int dev = 0, n = 0;
@@ -31,7 +32,17 @@ int mfma_grid_target(int kw) {
     else
       cus = 256;
   }
-  return cus * (16 / (kw < 1 ? 1 : kw > 16 ? 16 : kw));
+  return cus;
+}
+
+int waves_per_cu_cap() {
+  static int cap = -1;
+  if (cap < 0) {
+    const char* e = getenv("FP4X_WAVES_PER_CU");
+    const int v = e ? atoi(e) : 0;
+    cap = v >= 1 && v <= 64 ? v : 0;
+  }
+  return cap;
 }
 void set_error(const std::string& msg) { g_err = msg; }
 

@@ -52,12 +52,18 @@ struct PlaneArgs {
 struct FmtMX8 {
   static constexpr int KPC = 16, SUB = 1;
   struct Chunk { uint4 q; uint32_t e; };
-  struct Row { const uint8_t* w; const uint8_t* s; };
-  __device__ static Row row(const PlaneArgs& a, int64_t r) { return {a.w0 + r * a.K, a.s + r * (a.K / 32)}; }
-  __device__ static Chunk load_row(const Row& r, int c) {
+  // Lane: pointers at chunk c of row r; at<DC>(L, j) reads chunk c + j*DC
+  // (DC even) at constant offsets.
+  struct Lane { const uint8_t* w; const uint8_t* s; };
+  __device__ static Lane lane(const PlaneArgs& a, int64_t r, int c) {
+    return {a.w0 + r * a.K + c * 16, a.s + r * (a.K / 32) + (c >> 1)};
+  }
+  __device__ static Lane step(const Lane& L, int dc) { return {L.w + dc * 16, L.s + (dc >> 1)}; }
+  template <int DC>
+  __device__ static Chunk at(const Lane& L, int j) {
     Chunk ch;
-    ch.q = ld_u128(r.w + c * 16);
-    ch.e = ld_u8(r.s + (c >> 1));
+    ch.q = ld_u128(L.w + j * DC * 16);
+    ch.e = ld_u8(L.s + j * (DC / 2));
     return ch;
   }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
@@ -83,15 +89,20 @@ template <bool F16S>
 struct FmtW8 {
   static constexpr int KPC = 16, SUB = 1;
   struct Chunk { uint4 q; uint32_t s; };
-  struct Row { const uint8_t* w; const uint8_t* s; };
-  __device__ static Row row(const PlaneArgs& a, int64_t r) {
-    return {a.w0 + r * a.K, a.s + r * (a.K / 64) * (F16S ? 2 : 4)};
+  static constexpr int SB = F16S ? 2 : 4;
+  // Lane: pointers at chunk c of row r; at<DC>(L, j) reads chunk c + j*DC
+  // (DC a multiple of 4, so the g64 scale index moves by DC/4).
+  struct Lane { const uint8_t* w; const uint8_t* s; };
+  __device__ static Lane lane(const PlaneArgs& a, int64_t r, int c) {
+    return {a.w0 + r * a.K + c * 16, a.s + (r * (a.K / 64) + (c >> 2)) * SB};
   }
-  __device__ static Chunk load_row(const Row& r, int c) {
+  __device__ static Lane step(const Lane& L, int dc) { return {L.w + dc * 16, L.s + (dc >> 2) * SB}; }
+  template <int DC>
+  __device__ static Chunk at(const Lane& L, int j) {
     Chunk ch;
-    ch.q = ld_u128(r.w + c * 16);
-    if constexpr (F16S) ch.s = ld_u16(r.s + (c >> 2) * 2);
-    else ch.s = ld_u32(r.s + (c >> 2) * 4);
+    ch.q = ld_u128(L.w + j * DC * 16);
+    if constexpr (F16S) ch.s = ld_u16(L.s + j * (DC / 4) * 2);
+    else ch.s = ld_u32(L.s + j * (DC / 4) * 4);
     return ch;
   }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
@@ -132,15 +143,17 @@ struct FmtW8 {
 struct FmtW6 {
   static constexpr int KPC = 32, SUB = 2;
   struct Chunk { uint4 lo; uint2 hi; uint32_t s; };
-  struct Row { const uint8_t* l; const uint8_t* h; const uint8_t* s; };
-  __device__ static Row row(const PlaneArgs& a, int64_t r) {
-    return {a.w0 + r * (a.K / 2), a.w1 + r * (a.K / 4), a.s + r * (a.K / 32) * 2};
+  struct Lane { const uint8_t* l; const uint8_t* h; const uint8_t* s; };
+  __device__ static Lane lane(const PlaneArgs& a, int64_t r, int c) {
+    return {a.w0 + r * (a.K / 2) + c * 16, a.w1 + r * (a.K / 4) + c * 8, a.s + (r * (a.K / 32) + c) * 2};
   }
-  __device__ static Chunk load_row(const Row& r, int c) {
+  __device__ static Lane step(const Lane& L, int dc) { return {L.l + dc * 16, L.h + dc * 8, L.s + dc * 2}; }
+  template <int DC>
+  __device__ static Chunk at(const Lane& L, int j) {
     Chunk ch;
-    ch.lo = ld_u128(r.l + c * 16);
-    ch.hi = ld_u64(r.h + c * 8);
-    ch.s = ld_u16(r.s + c * 2);
+    ch.lo = ld_u128(L.l + j * DC * 16);
+    ch.hi = ld_u64(L.h + j * DC * 8);
+    ch.s = ld_u16(L.s + j * DC * 2);
     return ch;
   }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
@@ -204,12 +217,16 @@ struct FmtW6 {
 struct FmtNV4 {
   static constexpr int KPC = 32, SUB = 2;
   struct Chunk { uint4 q; uint32_t s; };
-  struct Row { const uint8_t* w; const uint8_t* s; };
-  __device__ static Row row(const PlaneArgs& a, int64_t r) { return {a.w0 + r * (a.K / 2), a.s + r * (a.K / 16)}; }
-  __device__ static Chunk load_row(const Row& r, int c) {
+  struct Lane { const uint8_t* w; const uint8_t* s; };
+  __device__ static Lane lane(const PlaneArgs& a, int64_t r, int c) {
+    return {a.w0 + r * (a.K / 2) + c * 16, a.s + r * (a.K / 16) + c * 2};
+  }
+  __device__ static Lane step(const Lane& L, int dc) { return {L.w + dc * 16, L.s + dc * 2}; }
+  template <int DC>
+  __device__ static Chunk at(const Lane& L, int j) {
     Chunk ch;
-    ch.q = ld_u128(r.w + c * 16);
-    ch.s = ld_u16(r.s + c * 2);
+    ch.q = ld_u128(L.w + j * DC * 16);
+    ch.s = ld_u16(L.s + j * DC * 2);
     return ch;
   }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
@@ -242,24 +259,35 @@ template <bool E4M3, int GC>
 struct FmtInt2 {
   static constexpr int KPC = 64, SUB = 4;
   struct Chunk { uint4 q; uint2 s; };
-  struct Row { const uint8_t* w; const uint8_t* s; int G; };
-  __device__ static Row row(const PlaneArgs& a, int64_t r) {
-    return {a.w0 + r * (a.K / 4), a.s + r * (a.K / a.G) * (E4M3 ? 1 : 2), a.G};
+  // Lane: pointers at chunk c of row r.  GC = 16 / 32: the chunk's group
+  // scales sit at a fixed stride, read at constant offsets.  GC = 0 (G >= 64):
+  // the lane keeps its row's scale base and first chunk, and at() computes
+  // the group index (c * 64) / G.
+  static constexpr int SB = E4M3 ? 1 : 2;
+  struct Lane { const uint8_t* w; const uint8_t* s; int c, G; };
+  __device__ static Lane lane(const PlaneArgs& a, int64_t r, int c) {
+    const uint8_t* srow = a.s + r * (a.K / a.G) * SB;
+    if constexpr (GC == 0) return {a.w0 + r * (a.K / 4) + c * 16, srow, c, a.G};
+    else return {a.w0 + r * (a.K / 4) + c * 16, srow + c * (64 / GC) * SB, c, a.G};
   }
-  __device__ static Chunk load_row(const Row& r, int c) {
+  __device__ static Lane step(const Lane& L, int dc) {
+    if constexpr (GC == 0) return {L.w + dc * 16, L.s, L.c + dc, L.G};
+    else return {L.w + dc * 16, L.s + dc * (64 / GC) * SB, L.c + dc, L.G};
+  }
+  template <int DC>
+  __device__ static Chunk at(const Lane& L, int j) {
     Chunk ch;
-    ch.q = ld_u128(r.w + c * 16);
-    const uint8_t* sp = r.s;
+    ch.q = ld_u128(L.w + j * DC * 16);
     if constexpr (GC == 16) {
-      if constexpr (E4M3) { ch.s.x = ld_u32(sp + c * 4); ch.s.y = 0; }
-      else ch.s = ld_u64(sp + c * 8);
+      if constexpr (E4M3) { ch.s.x = ld_u32(L.s + j * DC * 4); ch.s.y = 0; }
+      else ch.s = ld_u64(L.s + j * DC * 8);
     } else if constexpr (GC == 32) {
-      if constexpr (E4M3) ch.s.x = ld_u16(sp + c * 2);
-      else ch.s.x = ld_u32(sp + c * 4);
+      if constexpr (E4M3) ch.s.x = ld_u16(L.s + j * DC * 2);
+      else ch.s.x = ld_u32(L.s + j * DC * 4);
       ch.s.y = 0;
     } else {
-      const int g = (c * 64) / r.G;
-      ch.s.x = E4M3 ? ld_u8(sp + g) : ld_u16(sp + g * 2);
+      const int g = ((L.c + j * DC) * 64) / L.G;
+      ch.s.x = E4M3 ? ld_u8(L.s + g) : ld_u16(L.s + g * 2);
       ch.s.y = 0;
     }
     return ch;
@@ -327,12 +355,14 @@ struct FmtInt2 {
 struct FmtBF16 {
   static constexpr int KPC = 16, SUB = 1;
   struct Chunk { uint4 a, b; };
-  struct Row { const uint8_t* w; };
-  __device__ static Row row(const PlaneArgs& p, int64_t r) { return {p.w0 + r * p.K * 2}; }
-  __device__ static Chunk load_row(const Row& r, int c) {
+  struct Lane { const uint8_t* w; };
+  __device__ static Lane lane(const PlaneArgs& p, int64_t r, int c) { return {p.w0 + r * p.K * 2 + c * 32}; }
+  __device__ static Lane step(const Lane& L, int dc) { return {L.w + dc * 32}; }
+  template <int DC>
+  __device__ static Chunk at(const Lane& L, int j) {
     Chunk ch;
-    ch.a = ld_u128(r.w + c * 32);
-    ch.b = ld_u128(r.w + c * 32 + 16);
+    ch.a = ld_u128(L.w + j * DC * 32);
+    ch.b = ld_u128(L.w + j * DC * 32 + 16);
     return ch;
   }
   __device__ static Chunk load(const PlaneArgs& p, int64_t row, int c) {

@@ -38,28 +38,32 @@ struct HcUpArgs {
 };
 
 // The interleaved tile of T = hc*bj stored rows is T/16 MFMA row groups of
-// KW waves each; every group runs the same K mapping, MFMA order and
-// wave-order reduction as gemv_mfma_kernel, so each row's sum equals the one
-// w8_linear gives for that row.
-template <class F>
+// KW waves each; every group runs the same K mapping, batches, MFMA order and
+// wave-order reduction as gemv_mfma_kernel<F, KW, FULL, ...>, so each row's
+// sum equals the one w8_linear gives for that row.
+template <class F, int KW, bool FULL>
 __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
+  constexpr int DC = 4 * KW;
   extern __shared__ __align__(16) uint16_t lds[];
   const int T = p.hc * p.bj;
-  const int KW = p.lpr;                                   // waves per 16-row group
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / KW, wv = wave - grp * KW;
   const int n = lane & 15, g = lane >> 4;
   const size_t xbytes = ((size_t)p.M * p.K * 2 + 15) & ~(size_t)15;
   float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + xbytes);
   float* gl = red + (size_t)(T / 16) * (KW > 1 ? KW - 1 : 0) * 256;
-  const int cend = p.K / F::KPC, cw = wv * 4 + g, cstep = 4 * KW;
-  const int J = (cend + cstep - 1) / cstep;
+  const int nch = p.K / F::KPC, cw = wv * 4 + g;
+  const int J = (nch + DC - 1) / DC, nb = (J + kNJ - 1) / kNJ;
   const int64_t row = (int64_t)blockIdx.x * T + grp * 16 + n;
+  const bool xon = n < p.M;
+  const uint16_t* xl0 = lds + (xon ? n : 0) * p.K + cw * F::KPC;
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int jb = 0; jb < J; jb += kJ) {
+  for (int bi = 0; bi < nb; ++bi) {
     MfmaBatch<F> cb;
-    mfma_load<F>(cb, p.pa, row, 0, cend, cw, cstep, jb, J);
-    if (jb == 0) {
+    if constexpr (FULL) mfma_load_full<F, DC>(cb, F::lane(p.pa, row, cw + bi * kNJ * DC));
+    else mfma_load_general<F, DC>(cb, p.pa, row, 0, cw, bi * kNJ, J, nch);
+    if (bi == 0) {
+      // stage the bottleneck activations while the first weight batch is in flight
       const int per_row = p.K / 8;
       for (int i = threadIdx.x; i < p.M * per_row; i += blockDim.x) {
         const int m = i / per_row, q = i - m * per_row;
@@ -67,13 +71,14 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
       }
       __syncthreads();
     }
-    mfma_compute<F>(cb, (const uint16_t*)lds, p.K, 0, p.M, true, 0, cend, cw, cstep, jb, J, acc);
+    mfma_compute<F, DC, FULL>(cb, xl0 + bi * kNJ * DC * F::KPC, xon, true, bi * kNJ, J, cw, nch, acc);
   }
   // wave-order reduction within each row group
   float* gred = red + (size_t)grp * (KW > 1 ? KW - 1 : 0) * 256;
   if (wv > 0) reinterpret_cast<f32x4_t*>(gred)[(wv - 1) * 64 + lane] = acc;
   __syncthreads();
   if (wv == 0) {
+#pragma unroll
     for (int w = 1; w < KW; ++w) {
       const f32x4_t o = reinterpret_cast<const f32x4_t*>(gred)[(w - 1) * 64 + lane];
       acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
@@ -91,6 +96,19 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
     const int64_t H = p.H;
     p.out[(int64_t)m * p.H + j] =
         hc_gate_mean([&](int s) { return gm[s * p.bj]; }, [&](int s) { return bf16_to_f32(nm[s * H]); }, p.hc);
+  }
+}
+
+template <class F>
+static void launch_hc_up(const HcUpArgs& p, int KW, bool full, dim3 grid, size_t lds, hipStream_t st) {
+  const int T = p.hc * p.bj;
+  const dim3 block((T / 16) * KW * 64);
+  if (!full) { hipLaunchKernelGGL((hc_up_mfma_kernel<F, kMaxKW, false>), grid, block, lds, st, p); return; }
+  switch (KW) {
+    case 1: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 1, true>), grid, block, lds, st, p); break;
+    case 2: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 2, true>), grid, block, lds, st, p); break;
+    case 4: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 4, true>), grid, block, lds, st, p); break;
+    default: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 8, true>), grid, block, lds, st, p); break;
   }
 }
 
@@ -166,7 +184,9 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
   if (M < 0 || M > 16 || K <= 0 || K % 64 || H <= 0 || hc <= 0 || bj <= 0 || H % bj)
     return hc_fail("hc_up: bad shape (M <= 16, K % 64 == 0, H % bj == 0)");
   const int chunks = K / 16;
-  const int KW = mfma_kw(chunks);
+  int KW = mfma_kw(chunks);
+  const bool full = mfma_full(chunks, KW);
+  if (!full) KW = kMaxKW;                       // the GEMV core's general path
   const int T = hc * bj;
   if (T % 16 || (T / 16) * KW > 16) return hc_fail("hc_up: hc*bj must be a multiple of 16 with at most 16 waves per tile");
   const size_t lds = (((size_t)(M < 1 ? 1 : M) * K * 2 + 15) & ~(size_t)15) + (size_t)(T / 16) * (KW - 1) * 256 * 4 +
@@ -185,11 +205,10 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
   p.nrm_stride = nrm_stride;
   p.out = static_cast<uint16_t*>(out);
   p.M = M; p.K = K; p.H = H; p.hc = hc; p.bj = bj;
-  p.lpr = KW;
-  dim3 grid(H / bj), block((T / 16) * KW * 64);
+  dim3 grid(H / bj);
   hipStream_t st = (hipStream_t)stream;
-  if (s_dtype == FP4X_DT_F16) hipLaunchKernelGGL(hc_up_mfma_kernel<FmtW8<true>>, grid, block, lds, st, p);
-  else hipLaunchKernelGGL(hc_up_mfma_kernel<FmtW8<false>>, grid, block, lds, st, p);
+  if (s_dtype == FP4X_DT_F16) launch_hc_up<FmtW8<true>>(p, KW, full, grid, lds, st);
+  else launch_hc_up<FmtW8<false>>(p, KW, full, grid, lds, st);
   return check_launch("hc_up");
 }
 

@@ -1,18 +1,31 @@
 // MFMA GEMV core for gfx950: y[m, n] = sum_k x[m, k] * w[n, k], M <= 16.
 //
-// One workgroup owns a tile of 16 weight rows (the n dimension of
-// v_mfma_f32_16x16x32_bf16; the M <= 16 activation rows pad the m dimension)
-// and loops over tiles grid-stride.  Its KW waves split the K slice: lane
-// (n = lane & 15, g = lane >> 4) of wave w streams 16-byte chunks
-// c = w*4 + g + j*4*KW of row n (four lane groups read four consecutive
-// chunks of each row), dequantizes them in registers to the bf16 operand and
-// feeds 8 k-values per MFMA step; the activation fragment of lane (m, g)
-// carries x[m] at the same k.  The KW partial 16x16 tiles are summed in wave
-// order through LDS.
+// One workgroup of KW waves works on tiles of 16 weight rows (the n dimension
+// of v_mfma_f32_16x16x32_bf16; the M <= 16 activation rows pad the m
+// dimension).  Lane (n = lane & 15, g = lane >> 4) of wave w streams 16-byte
+// chunks c = w*4 + g + j*4*KW of row n of its K slice: the four lane groups of
+// a wave read 64 contiguous bytes of each of 16 rows per load instruction.
+// Chunks are dequantized in registers to the bf16 operand and fed 8 k-values
+// per MFMA step; the activation fragment of lane (m, g) carries x[m] at the
+// same k, read from LDS.  The KW partial 16x16 tiles are summed in wave order
+// through LDS.
 //
-// Split-K (ksplit > 1) and the epilogue functors are those of the VALU core
-// (fp4x_kernels.h): one slot per K slice, the last-arriving workgroup sums
-// the slots in slice order.
+// Instruction economy: KW is a template parameter, so a lane's chunks sit at
+// compile-time strides from one base pointer per weight plane (F::Lane) and
+// from one activation address; every load and LDS read of a batch uses a
+// constant offset.  Tile and batch positions advance by counters.
+//
+// Latency hiding: KW is chosen so that a lane's share of a tile (J chunks)
+// fills whole register batches of kNJ chunks, all of a batch's loads are in
+// flight together, and the launch keeps as many workgroups resident as the
+// register and LDS budget allows (each with the same number of tiles), so
+// the memory latency of one workgroup overlaps the work of the others.  The
+// first batch's loads go out before the activations are staged.
+//
+// Split-K (ksplit > 1): one fp32 slot tile per K slice; the last-arriving
+// workgroup of a tile (agent-scope ticket, see splitk_arrive) sums the slots
+// in slice order and applies the epilogue, which keeps results independent
+// of the arrival order.
 #pragma once
 #include "fp4x_kernels.h"
 
@@ -21,14 +34,22 @@ namespace fp4x {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kJ = 4;   // chunks per lane held in registers per batch
+constexpr int kNJ = 5;        // chunks per lane held in one register batch
+constexpr int kMaxKW = 8;     // waves per workgroup at most
 
-// Waves per tile for a K slice of `chunks` 16-byte chunks: at most four
-// chunks per lane where 8 waves allow it.
+// Waves per tile for a K slice of `chunks` chunks: the fewest (a power of
+// two, at most kMaxKW) that keep a lane's share within one batch.
 __host__ __device__ inline int mfma_kw(int chunks) {
-  int want = (chunks + 15) / 16, kw = 1;
-  while (kw < want && kw < 8) kw <<= 1;
+  int kw = 1;
+  while (kw < kMaxKW && (chunks + 4 * kw - 1) / (4 * kw) > kNJ) kw <<= 1;
   return kw;
+}
+
+// True when every lane of every wave gets exactly J chunks in whole batches
+// (the constant-offset path); other slices take the general path.
+__host__ __device__ inline bool mfma_full(int chunks, int kw) {
+  const int dc = 4 * kw;
+  return chunks % dc == 0 && (chunks / dc) % kNJ == 0;
 }
 
 __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
@@ -36,49 +57,64 @@ __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
                                                  0, 0, 0);
 }
 
+// Barrier for LDS hand-offs between the waves of a workgroup.  Only LDS
+// accesses are ordered: outstanding global memory operations (the epilogue's
+// stores) are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <class F>
 struct MfmaBatch {
-  typename F::Chunk ch[kJ];
+  typename F::Chunk ch[kNJ];
 };
 
-// Chunk c of this lane for batch slot j: c = c0 + cw + j * cstep.
-template <class F>
-__device__ __forceinline__ void mfma_load(MfmaBatch<F>& b, const PlaneArgs& a, int64_t row, int c0, int cend, int cw,
-                                          int cstep, int jb, int J) {
-  const typename F::Row r = F::row(a, row < 0 ? 0 : row);
+// Full path: the kNJ chunks of a batch at constant offsets from L.
+template <class F, int DC>
+__device__ __forceinline__ void mfma_load_full(MfmaBatch<F>& b, const typename F::Lane& L) {
 #pragma unroll
-  for (int j = 0; j < kJ; ++j) {
-    const int c = c0 + cw + (jb + j) * cstep;
-    if (jb + j < J && row >= 0 && c < cend) b.ch[j] = F::load_row(r, c);
-    else b.ch[j] = F::zero();
+  for (int j = 0; j < kNJ; ++j) b.ch[j] = F::template at<DC>(L, j);
+}
+
+// General path: slot j holds chunk c0 + cw + (jb + j) * DC when that chunk is
+// inside the slice (jb + j < J and cw + (jb + j) * DC < nch); other slots read
+// chunk c0 of the same row, which is in bounds, and are multiplied as zeros.
+template <class F, int DC>
+__device__ __forceinline__ void mfma_load_general(MfmaBatch<F>& b, const PlaneArgs& a, int64_t row, int c0, int cw,
+                                                  int jb, int J, int nch) {
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j) {
+    const int jj = jb + j;
+    const bool live = jj < J && cw + jj * DC < nch;
+    b.ch[j] = F::template at<DC>(F::lane(a, row, live ? c0 + cw + jj * DC : c0), 0);
   }
 }
 
-// MFMA steps over one batch.  xs: x[m][k] at xs[m * xstride + k - kx0] for
-// m < M (LDS or global); lanes with m >= M feed zeros.
-template <class F, class XPtr>
-__device__ __forceinline__ void mfma_compute(const MfmaBatch<F>& b, XPtr xs, int xstride, int kx0, int M, bool wrow,
-                                             int c0, int cend, int cw, int cstep, int jb, int J, f32x4_t& acc) {
-  const int lane = threadIdx.x & 63;
-  const int xm = lane & 15;
+// MFMA steps over one batch.  xl points at x[m][k] of this lane's slot 0
+// (LDS or global, m = lane & 15); slot j's activations are DC*KPC elements
+// further.  xon: m < M.  won: the lane's weight row exists.  Every slot is
+// consumed (dead slots multiply zeros), so no path leaves a batch load
+// outstanding past its compute.
+template <class F, int DC, bool FULL, class XPtr>
+__device__ __forceinline__ void mfma_compute(const MfmaBatch<F>& b, XPtr xl, bool xon, bool won, int jb, int J,
+                                             int cw, int nch, f32x4_t& acc) {
 #pragma unroll
-  for (int j = 0; j < kJ; ++j) {
-    if (jb + j >= J) break;
-    const int c = c0 + cw + (jb + j) * cstep;
-    const bool live = c < cend;                     // lane group's chunk exists (uniform per 16 lanes)
+  for (int j = 0; j < kNJ; ++j) {
+    const bool live = FULL || (jb + j < J && cw + (jb + j) * DC < nch);   // uniform per 16 lanes
 #pragma unroll
     for (int sub = 0; sub < F::SUB; ++sub) {
       uint32_t w[8];
       F::deq16(b.ch[j], sub, w);
-      const int k = c * F::KPC + sub * 16;
       uint4 xa = make_uint4(0, 0, 0, 0), xb = xa;
-      if (live && xm < M) {
-        const uint4* xp = reinterpret_cast<const uint4*>(xs + (int64_t)xm * xstride + (k - kx0));
+      if (xon && live) {
+        const uint4* xp = reinterpret_cast<const uint4*>(xl + j * DC * F::KPC + sub * 16);
         xa = xp[0];
         xb = xp[1];
       }
       uint4 wa = make_uint4(w[0], w[1], w[2], w[3]), wb = make_uint4(w[4], w[5], w[6], w[7]);
-      if (!live || !wrow) { wa = make_uint4(0, 0, 0, 0); wb = wa; }
+      if (!(won && live)) { wa = make_uint4(0, 0, 0, 0); wb = wa; }
       acc = mfma16(xa, wa, acc);
       acc = mfma16(xb, wb, acc);
     }
@@ -86,134 +122,231 @@ __device__ __forceinline__ void mfma_compute(const MfmaBatch<F>& b, XPtr xs, int
 }
 
 // Sum the KW waves' 16x16 tiles in wave order; the result is valid in wave 0.
-template <int KWMAX>
-__device__ __forceinline__ f32x4_t mfma_wave_reduce(f32x4_t acc, int KW, float* red) {
+template <int KW>
+__device__ __forceinline__ f32x4_t mfma_wave_reduce(f32x4_t acc, float* red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (KW == 1) return acc;
+  if constexpr (KW == 1) return acc;
   if (wave > 0) reinterpret_cast<f32x4_t*>(red)[(wave - 1) * 64 + lane] = acc;
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {
+#pragma unroll
     for (int w = 1; w < KW; ++w) {
       const f32x4_t o = reinterpret_cast<const f32x4_t*>(red)[(w - 1) * 64 + lane];
       acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
     }
   }
-  __syncthreads();
+  lds_barrier();
   return acc;
 }
 
-// LDS layout: [x: M x ks bf16 (XL only)] [red: (KW-1) x 64 x 4 fp32] [slot tile: 16 x 16 fp32]
+// Activation rows in LDS are padded by 16 bytes so that the 16 rows of an
+// MFMA fragment fall into different banks.
+__host__ __device__ inline int mfma_xstride(int ks) { return ks + 8; }
+
+// LDS layout: [x: M x xstride bf16 (XL only)] [red: (KW-1) x 64 x 4 fp32]
 __host__ __device__ inline size_t mfma_lds_bytes(int M, int ks, int KW, bool xl) {
-  size_t x = xl ? (size_t)M * ks * 2 : 0;
+  size_t x = xl ? (size_t)M * mfma_xstride(ks) * 2 : 0;
   x = (x + 15) & ~(size_t)15;
-  return x + (size_t)(KW > 1 ? KW - 1 : 0) * 64 * 16 + 16 * 16 * 4;
+  return x + (size_t)(KW > 1 ? KW - 1 : 0) * 64 * 16;
 }
 
-template <class F, bool XL, class Epi>
-__global__ __launch_bounds__(512) void gemv_mfma_kernel(GemvLaunch p) {
-  extern __shared__ __align__(16) uint16_t lds[];
-  const int b = blockIdx.z, split = blockIdx.y;
+// Finish tile t: wave reduce, then the epilogue (ksplit == 1) or the split-K
+// slot write and last-arrival reduction.
+template <int KW, class Epi>
+__device__ __forceinline__ void mfma_finish(const GemvLaunch& p, int b, int split, int t, f32x4_t acc, float* red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int KW = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
-  PlaneArgs pa = p.pa;
-  pa.w0 += b * p.w0_bstride;
-  if (pa.w1) pa.w1 += b * p.w1_bstride;
-  pa.s += b * p.s_bstride;
-  const int ks = pa.K / p.ksplit, k0 = split * ks, c0 = k0 / F::KPC, cend = c0 + ks / F::KPC;
-  const int cw = wave * 4 + g, cstep = 4 * KW;
-  const int J = (ks / F::KPC + cstep - 1) / cstep;     // chunks per lane per tile
-  const uint16_t* xg = p.x + b * p.x_bstride;
-  size_t xbytes = XL ? (((size_t)p.M * ks * 2 + 15) & ~(size_t)15) : 0;
-  float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + xbytes);
-  float* slot = red + (KW > 1 ? KW - 1 : 0) * 64 * 4;
+  const int64_t row = (int64_t)t * 16 + n;
+  const bool wrow = row < p.N;
+  acc = mfma_wave_reduce<KW>(acc, red);
+  // lane of wave 0 holds D[m = g*4 + i][n]
+  if (p.ksplit == 1) {
+    if (wave == 0 && wrow) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (g * 4 + i < p.M) Epi::apply(p, b, g * 4 + i, row, acc[i] * p.gs);
+    }
+    return;
+  }
+  float* part = p.part + (int64_t)b * p.ksplit * 16 * p.N;
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = g * 4 + i;
+      if (m < p.M && wrow) part[((int64_t)split * 16 + m) * p.N + row] = acc[i] * p.gs;
+    }
+  }
   const int tiles = (p.N + 15) / 16;
-  int t = blockIdx.x;
-  if (t >= tiles) return;
-
-  if constexpr (XL) {
-    // stage x[0:M, k0:k0+ks]
-    const int per_row = ks / 8;
-    for (int i = threadIdx.x; i < p.M * per_row; i += blockDim.x) {
-      const int m = i / per_row, q = i - m * per_row;
-      reinterpret_cast<uint4*>(lds + m * ks)[q] = *reinterpret_cast<const uint4*>(xg + m * p.x_stride + k0 + q * 8);
-    }
-    __syncthreads();
-  }
-
-  for (; t < tiles; t += gridDim.x) {
-    const int64_t row = (int64_t)t * 16 + n;
-    const bool wrow = row < p.N;
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int jb = 0; jb < J; jb += kJ) {
-      MfmaBatch<F> cur;
-      mfma_load<F>(cur, pa, wrow ? row : -1, c0, cend, cw, cstep, jb, J);
-      if constexpr (XL) mfma_compute<F>(cur, (const uint16_t*)lds, ks, k0, p.M, wrow, c0, cend, cw, cstep, jb, J, acc);
-      else mfma_compute<F>(cur, xg, (int)p.x_stride, 0, p.M, wrow, c0, cend, cw, cstep, jb, J, acc);
-    }
-    acc = mfma_wave_reduce<8>(acc, KW, red);
-    // lane holds D[m = g*4 + i][n]
-    if (p.ksplit == 1) {
-      if (wave == 0 && wrow) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (g * 4 + i < p.M) Epi::apply(p, b, g * 4 + i, row, acc[i] * p.gs);
-      }
-      continue;
-    }
-    // split-K: wave 0 writes this slice's slot tile, the last workgroup reduces
-    float* part = p.part + (int64_t)b * p.ksplit * 16 * p.N;
+  int* ticket = p.tickets + (int64_t)b * tiles + t;
+  if (splitk_arrive(ticket, p.ksplit)) {
     const int64_t tile0 = (int64_t)t * 16;
-    if (wave == 0) {
+    for (int i = threadIdx.x; i < p.M * 16; i += blockDim.x) {
+      const int m = i >> 4;
+      const int64_t r = tile0 + (i & 15);
+      if (r >= p.N) continue;
+      const float* src = part + (int64_t)m * p.N + r;
+      const int64_t sstride = (int64_t)16 * p.N;
+      float tot = 0.0f;
+      for (int s0 = 0; s0 < p.ksplit; s0 += 8) {
+        float v[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = g * 4 + i;
-        if (m < p.M && wrow) part[((int64_t)split * 16 + m) * p.N + row] = acc[i] * p.gs;
+        for (int jj = 0; jj < 8; ++jj) v[jj] = s0 + jj < p.ksplit ? src[(s0 + jj) * sstride] : 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          if (s0 + jj < p.ksplit) tot = s0 + jj == 0 ? v[jj] : tot + v[jj];
       }
+      Epi::apply(p, b, m, r, tot);
     }
-    int* ticket = p.tickets + (int64_t)b * tiles + t;
-    if (splitk_arrive(ticket, p.ksplit)) {
-      for (int i = threadIdx.x; i < p.M * 16; i += blockDim.x) {
-        const int m = i >> 4;
-        const int64_t r = tile0 + (i & 15);
-        if (r >= p.N) continue;
-        const float* src = part + (int64_t)m * p.N + r;
-        const int64_t sstride = (int64_t)16 * p.N;
-        float tot = 0.0f;
-        for (int s0 = 0; s0 < p.ksplit; s0 += 8) {
-          float v[8];
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) v[jj] = s0 + jj < p.ksplit ? src[(s0 + jj) * sstride] : 0.0f;
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj)
-            if (s0 + jj < p.ksplit) tot = s0 + jj == 0 ? v[jj] : tot + v[jj];
-        }
-        Epi::apply(p, b, m, r, tot);
-      }
-      if (threadIdx.x == 0) ticket_reset(ticket);
-    }
-    __syncthreads();
+    if (threadIdx.x == 0) ticket_reset(ticket);
   }
-  (void)slot;
+  __syncthreads();
 }
 
-// Workgroups to launch so that each CU holds about 16 waves of KW-wave groups.
-int mfma_grid_target(int kw);
+// Stage x[0:M, k0:k0+ks] (bf16) into LDS rows of xs elements.  Four 16-byte
+// loads per thread are issued before their LDS writes; the first round is
+// straight-line code, so its loads are not held back by a loop-entry wait on
+// weight loads already in flight.  Rows of x and of the stage are 16-byte
+// aligned (strides and k0 are multiples of 8 elements).
+__device__ __forceinline__ void mfma_stage_x(uint16_t* lds, const uint16_t* xg, int64_t x_stride, int M, int k0,
+                                             int ks, int xs) {
+  const int per_row = ks / 8, total = M * per_row;
+  const uint4* xg4 = reinterpret_cast<const uint4*>(xg + k0);
+  const int64_t xrow4 = x_stride / 8;
+  uint4* lds4 = reinterpret_cast<uint4*>(lds);
+  const int lrow4 = xs / 8;
+  auto stage4 = [&](int i0) {
+    const int i1 = i0 + blockDim.x, i2 = i1 + blockDim.x, i3 = i2 + blockDim.x;
+    const int j0 = i0 < total ? i0 : total - 1, j1 = i1 < total ? i1 : total - 1,
+              j2 = i2 < total ? i2 : total - 1, j3 = i3 < total ? i3 : total - 1;
+    const uint4 v0 = xg4[(j0 / per_row) * xrow4 + j0 % per_row];
+    const uint4 v1 = xg4[(j1 / per_row) * xrow4 + j1 % per_row];
+    const uint4 v2 = xg4[(j2 / per_row) * xrow4 + j2 % per_row];
+    const uint4 v3 = xg4[(j3 / per_row) * xrow4 + j3 % per_row];
+    if (i0 < total) lds4[(i0 / per_row) * lrow4 + i0 % per_row] = v0;
+    if (i1 < total) lds4[(i1 / per_row) * lrow4 + i1 % per_row] = v1;
+    if (i2 < total) lds4[(i2 / per_row) * lrow4 + i2 % per_row] = v2;
+    if (i3 < total) lds4[(i3 / per_row) * lrow4 + i3 % per_row] = v3;
+  };
+  stage4(threadIdx.x);
+  for (int i0 = threadIdx.x + 4 * blockDim.x; i0 < total; i0 += 4 * blockDim.x) stage4(i0);
+}
+
+// Work items are (batch entry, 16-row tile) pairs, numbered entry-major;
+// workgroup x of K slice y takes items [x * per_wg, (x + 1) * per_wg).  The
+// host sizes per_wg so that every workgroup of the launch is resident at once
+// and all carry the same number of items.  The activations of an entry are
+// staged once per run of items of that entry.  p.J: chunks per lane per
+// tile, p.nb: register batches per tile.
+template <class F, int KW, bool FULL, bool XL, class Epi>
+__global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
+  constexpr int DC = 4 * KW;                // chunks between a lane's consecutive chunks
+  extern __shared__ __align__(16) uint16_t lds[];
+  const int split = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int tiles = (p.N + 15) / 16, items = p.batch * tiles;
+  int it = blockIdx.x * p.per_wg;
+  const int iend = it + p.per_wg < items ? it + p.per_wg : items;
+  if (it >= iend) return;
+  const int ks = p.pa.K / p.ksplit, k0 = split * ks, nch = ks / F::KPC, c0 = k0 / F::KPC;
+  const int cw = wave * 4 + g;              // this lane's first chunk within the slice
+  const int J = p.J, nb = p.nb;
+  const int xs = mfma_xstride(ks);
+  const size_t xbytes = XL ? (((size_t)p.M * xs * 2 + 15) & ~(size_t)15) : 0;
+  float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + xbytes);
+  const bool xon = n < p.M;
+  const int xrow = xon ? n : 0;
+  int cur_b = -1;
+  for (; it < iend; ++it) {
+    const int b = it / tiles, t = it - b * tiles;
+    PlaneArgs pa = p.pa;
+    pa.w0 += b * p.w0_bstride;
+    if (pa.w1) pa.w1 += b * p.w1_bstride;
+    pa.s += b * p.s_bstride;
+    const int64_t row = (int64_t)t * 16 + n;
+    const int64_t rowc = row < p.N ? row : p.N - 1;     // rows past N read row N-1 (in bounds) as zeros
+    const bool won = row < p.N;
+    const uint16_t* xg = p.x + b * p.x_bstride;
+    const uint16_t* xl0 = XL ? lds + xrow * xs + cw * F::KPC : xg + xrow * p.x_stride + k0 + cw * F::KPC;
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int bi = 0; bi < nb; ++bi) {
+      MfmaBatch<F> A;
+      if constexpr (FULL) mfma_load_full<F, DC>(A, F::lane(pa, rowc, c0 + cw + bi * kNJ * DC));
+      else mfma_load_general<F, DC>(A, pa, rowc, c0, cw, bi * kNJ, J, nch);
+      if constexpr (XL) {
+        if (b != cur_b) {
+          // new batch entry: stage its activations while the weight loads are in flight
+          if (cur_b >= 0) __syncthreads();               // every wave is done with the previous entry's x
+          mfma_stage_x(lds, xg, p.x_stride, p.M, k0, ks, xs);
+          __syncthreads();
+          cur_b = b;
+        }
+      }
+      mfma_compute<F, DC, FULL>(A, xl0 + bi * kNJ * DC * F::KPC, xon, won, bi * kNJ, J, cw, nch, acc);
+    }
+    mfma_finish<KW, Epi>(p, b, split, t, acc, red);
+  }
+}
+
+// Compute units of the current device (cached).
+int device_cus();
+// Optional cap on resident waves per CU from FP4X_WAVES_PER_CU (0: none).
+int waves_per_cu_cap();
+
+template <class F, int KW, bool FULL, bool XL, class Epi>
+void launch_mfma_kw(GemvLaunch p, int batch, size_t lds, hipStream_t st) {
+  auto kern = gemv_mfma_kernel<F, KW, FULL, XL, Epi>;
+  // resident workgroups per CU for this kernel and LDS size (cached per LDS size)
+  static int occ_cache[97];
+  const int key = (int)((lds + 1023) / 1024);
+  int occ = key < 97 ? occ_cache[key] : 0;
+  if (occ <= 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(kern), 64 * KW, lds) !=
+            hipSuccess || occ < 1)
+      occ = 1;
+    if (key < 97) occ_cache[key] = occ;
+  }
+  const int cap = waves_per_cu_cap();
+  if (cap > 0 && occ * KW > cap) occ = cap / KW > 0 ? cap / KW : 1;
+  const int tiles = (p.N + 15) / 16;
+  const int64_t items = (int64_t)batch * tiles;
+  int64_t slots = (int64_t)device_cus() * occ / p.ksplit;
+  if (slots < 1) slots = 1;
+  const int64_t per = (items + slots - 1) / slots;
+  p.batch = batch;
+  p.per_wg = (int)per;
+  const int gx = (int)((items + per - 1) / per);
+  hipLaunchKernelGGL(kern, dim3(gx, p.ksplit, 1), dim3(64 * KW), lds, st, p);
+}
+
+template <class F, int KW, bool FULL, class Epi>
+void launch_mfma_xl(const GemvLaunch& p, int batch, size_t lds, bool xl, hipStream_t st) {
+  if (xl) launch_mfma_kw<F, KW, FULL, true, Epi>(p, batch, lds, st);
+  else launch_mfma_kw<F, KW, FULL, false, Epi>(p, batch, lds, st);
+}
 
 template <class F, class Epi>
 int launch_gemv_mfma(const GemvLaunch& p0, int batch, hipStream_t st) {
   GemvLaunch p = p0;
   const int ks = p.pa.K / p.ksplit;
   const int chunks = ks / F::KPC;
-  const int KW = mfma_kw(chunks);
-  const int tiles = (p.N + 15) / 16;
-  const int per_batch = (mfma_grid_target(KW) + batch * p.ksplit - 1) / (batch * p.ksplit);
-  const int gx = tiles < per_batch ? tiles : (per_batch < 1 ? 1 : per_batch);
+  int KW = mfma_kw(chunks);
+  const bool full = mfma_full(chunks, KW);
+  if (!full) KW = kMaxKW;                               // general path: one instantiation
+  p.J = (chunks + 4 * KW - 1) / (4 * KW);
+  p.nb = (p.J + kNJ - 1) / kNJ;
   const bool xl = mfma_lds_bytes(p.M, ks, KW, true) <= 96 * 1024;
   const size_t lds = mfma_lds_bytes(p.M, ks, KW, xl);
-  dim3 grid(gx, p.ksplit, batch), block(64 * KW);
-  if (xl) hipLaunchKernelGGL((gemv_mfma_kernel<F, true, Epi>), grid, block, lds, st, p);
-  else hipLaunchKernelGGL((gemv_mfma_kernel<F, false, Epi>), grid, block, lds, st, p);
+  if (!full) {
+    launch_mfma_xl<F, kMaxKW, false, Epi>(p, batch, lds, xl, st);
+  } else {
+    switch (KW) {
+      case 1: launch_mfma_xl<F, 1, true, Epi>(p, batch, lds, xl, st); break;
+      case 2: launch_mfma_xl<F, 2, true, Epi>(p, batch, lds, xl, st); break;
+      case 4: launch_mfma_xl<F, 4, true, Epi>(p, batch, lds, xl, st); break;
+      default: launch_mfma_xl<F, 8, true, Epi>(p, batch, lds, xl, st); break;
+    }
+  }
   return check_launch("gemv_mfma");
 }
 

@@ -15,6 +15,7 @@ import torch
 from oracle import formats as fm
 from oracle import gemv as og
 from oracle import head as oh
+from oracle import ordered
 from oracle import quant as oq
 
 from gpu_helpers import act, assert_tol, bf16_bits, bf16_dev, dev, to_f32
@@ -140,7 +141,15 @@ def test_fast_head_full_size_exact(gpu, F):
     diff = coarse_bits != o_coarse
     print(f"fast head: coarse bf16 differing from the ordered replay: {int(diff.sum())} of {diff.size}")
     assert diff.mean() <= 1e-3
-    assert np.all(np.abs(coarse_bits.astype(np.int32) - o_coarse.astype(np.int32))[diff] <= 1)   # one bf16 ulp
+    # every coarse value (MFMA-accumulated, then rounded to bf16) lies within
+    # the accumulation bound plus half a bf16 ulp of the exact sum
+    w_op = fm.bf16_to_f32(ordered.int2_operand_bits(Pn, Sn, 16))
+    xf = fm.bf16_to_f32(xb)
+    exact_c = ordered.exact_sum(xf, w_op)
+    cf = fm.bf16_to_f32(coarse_bits).astype(np.float64)
+    bound = ordered.mfma_bound(xf, w_op) + np.abs(cf) * 2.0 ** -8
+    assert np.all(np.abs(cf - exact_c) <= bound), float((np.abs(cf - exact_c) / bound).max())
+    del w_op, exact_c, bound
     sel = idx.cpu().numpy()
     # selection is exact on the kernel's own coarse logits ...
     assert np.array_equal(sel, oh.topk_total_order(coarse_bits, C))
