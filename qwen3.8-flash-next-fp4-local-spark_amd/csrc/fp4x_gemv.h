@@ -66,6 +66,15 @@ struct FmtMX8 {
     ch.e = ld_u8(L.s + j * (DC / 2));
     return ch;
   }
+  // Chunks c, c + 1 (c = lane chunk + j*DC, even): 32 contiguous bytes and
+  // their shared e8m0 scale.
+  static constexpr int AUX_ALIGN = 1;
+  template <int DC>
+  __device__ static void pair(const Lane& L, int j, Chunk& a, Chunk& b) {
+    a.q = ld_u128(L.w + j * DC * 16);
+    b.q = ld_u128(L.w + j * DC * 16 + 16);
+    a.e = b.e = ld_u8(L.s + j * (DC / 2));
+  }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
     ch.q = ld_u128(a.w0 + row * a.K + c * 16);
@@ -104,6 +113,15 @@ struct FmtW8 {
     if constexpr (F16S) ch.s = ld_u16(L.s + j * (DC / 4) * 2);
     else ch.s = ld_u32(L.s + j * (DC / 4) * 4);
     return ch;
+  }
+  // Chunks c, c + 1 (c even): one g64 group, one scale.
+  static constexpr int AUX_ALIGN = SB;
+  template <int DC>
+  __device__ static void pair(const Lane& L, int j, Chunk& a, Chunk& b) {
+    a.q = ld_u128(L.w + j * DC * 16);
+    b.q = ld_u128(L.w + j * DC * 16 + 16);
+    if constexpr (F16S) a.s = b.s = ld_u16(L.s + j * (DC / 4) * 2);
+    else a.s = b.s = ld_u32(L.s + j * (DC / 4) * 4);
   }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
@@ -155,6 +173,19 @@ struct FmtW6 {
     ch.hi = ld_u64(L.h + j * DC * 8);
     ch.s = ld_u16(L.s + j * DC * 2);
     return ch;
+  }
+  // Chunks c, c + 1 (c even): 32 bytes of L, 16 of H, two scales in a dword.
+  static constexpr int AUX_ALIGN = 4;
+  template <int DC>
+  __device__ static void pair(const Lane& L, int j, Chunk& a, Chunk& b) {
+    a.lo = ld_u128(L.l + j * DC * 16);
+    b.lo = ld_u128(L.l + j * DC * 16 + 16);
+    const uint4 h = ld_u128(L.h + j * DC * 8);
+    a.hi = make_uint2(h.x, h.y);
+    b.hi = make_uint2(h.z, h.w);
+    const uint32_t sc = ld_u32(L.s + j * DC * 2);
+    a.s = sc & 0xffffu;
+    b.s = sc >> 16;
   }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
@@ -229,6 +260,16 @@ struct FmtNV4 {
     ch.s = ld_u16(L.s + j * DC * 2);
     return ch;
   }
+  // Chunks c, c + 1 (c even): 32 bytes of codes, four e4m3 scales in a dword.
+  static constexpr int AUX_ALIGN = 4;
+  template <int DC>
+  __device__ static void pair(const Lane& L, int j, Chunk& a, Chunk& b) {
+    a.q = ld_u128(L.w + j * DC * 16);
+    b.q = ld_u128(L.w + j * DC * 16 + 16);
+    const uint32_t sc = ld_u32(L.s + j * DC * 2);
+    a.s = sc & 0xffffu;
+    b.s = sc >> 16;
+  }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
     ch.q = ld_u128(a.w0 + row * (a.K / 2) + c * 16);
@@ -291,6 +332,39 @@ struct FmtInt2 {
       ch.s.y = 0;
     }
     return ch;
+  }
+  // Chunks c, c + 1 (c even): 32 bytes of codes; with G = 16 / 32 the group
+  // scales of both chunks in one load.
+  static constexpr int AUX_ALIGN = GC == 16 ? (E4M3 ? 8 : 16) : GC == 32 ? (E4M3 ? 4 : 8) : SB;
+  template <int DC>
+  __device__ static void pair(const Lane& L, int j, Chunk& a, Chunk& b) {
+    a.q = ld_u128(L.w + j * DC * 16);
+    b.q = ld_u128(L.w + j * DC * 16 + 16);
+    if constexpr (GC == 16) {
+      if constexpr (E4M3) {
+        const uint2 v = ld_u64(L.s + j * DC * 4);
+        a.s = make_uint2(v.x, 0);
+        b.s = make_uint2(v.y, 0);
+      } else {
+        const uint4 v = ld_u128(L.s + j * DC * 8);
+        a.s = make_uint2(v.x, v.y);
+        b.s = make_uint2(v.z, v.w);
+      }
+    } else if constexpr (GC == 32) {
+      if constexpr (E4M3) {
+        const uint32_t v = ld_u32(L.s + j * DC * 2);
+        a.s = make_uint2(v & 0xffffu, 0);
+        b.s = make_uint2(v >> 16, 0);
+      } else {
+        const uint2 v = ld_u64(L.s + j * DC * 4);
+        a.s = make_uint2(v.x, 0);
+        b.s = make_uint2(v.y, 0);
+      }
+    } else {
+      const int g0 = ((L.c + j * DC) * 64) / L.G, g1 = ((L.c + j * DC + 1) * 64) / L.G;
+      a.s = make_uint2(E4M3 ? ld_u8(L.s + g0) : ld_u16(L.s + g0 * 2), 0);
+      b.s = make_uint2(E4M3 ? ld_u8(L.s + g1) : ld_u16(L.s + g1 * 2), 0);
+    }
   }
   __device__ static Chunk load(const PlaneArgs& a, int64_t row, int c) {
     Chunk ch;
@@ -364,6 +438,13 @@ struct FmtBF16 {
     ch.a = ld_u128(L.w + j * DC * 32);
     ch.b = ld_u128(L.w + j * DC * 32 + 16);
     return ch;
+  }
+  static constexpr int AUX_ALIGN = 1;
+  template <int DC>
+  __device__ static void pair(const Lane& L, int j, Chunk& a, Chunk& b) {
+    a = at<DC>(L, j);
+    b.a = ld_u128(L.w + j * DC * 32 + 32);
+    b.b = ld_u128(L.w + j * DC * 32 + 48);
   }
   __device__ static Chunk load(const PlaneArgs& p, int64_t row, int c) {
     Chunk ch;

@@ -39,11 +39,12 @@ struct HcUpArgs {
 
 // The interleaved tile of T = hc*bj stored rows is T/16 MFMA row groups of
 // KW waves each; every group runs the same K mapping, batches, MFMA order and
-// wave-order reduction as gemv_mfma_kernel<F, KW, FULL, ...>, so each row's
+// wave-order reduction as gemv_mfma_kernel<F, KW, CPS, FULL, ...>, so each row's
 // sum equals the one w8_linear gives for that row.
-template <class F, int KW, bool FULL>
+template <class F, int KW, int CPS, bool FULL>
 __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
-  constexpr int DC = 4 * KW;
+  constexpr int DP = 4 * KW;
+  constexpr int NJ = kNJ;
   extern __shared__ __align__(16) uint16_t lds[];
   const int T = p.hc * p.bj;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -53,15 +54,15 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
   float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + xbytes);
   float* gl = red + (size_t)(T / 16) * (KW > 1 ? KW - 1 : 0) * 256;
   const int nch = p.K / F::KPC, cw = wv * 4 + g;
-  const int J = (nch + DC - 1) / DC, nb = (J + kNJ - 1) / kNJ;
+  const int J = ((nch + CPS - 1) / CPS + DP - 1) / DP, nb = (J + NJ - 1) / NJ;
   const int64_t row = (int64_t)blockIdx.x * T + grp * 16 + n;
   const bool xon = n < p.M;
-  const uint16_t* xl0 = lds + (xon ? n : 0) * p.K + cw * F::KPC;
+  const uint16_t* xl0 = lds + (xon ? n : 0) * p.K + CPS * cw * F::KPC;
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int bi = 0; bi < nb; ++bi) {
-    MfmaBatch<F> cb;
-    if constexpr (FULL) mfma_load_full<F, DC>(cb, F::lane(p.pa, row, cw + bi * kNJ * DC));
-    else mfma_load_general<F, DC>(cb, p.pa, row, 0, cw, bi * kNJ, J, nch);
+    MfmaBatch<F, CPS> cb;
+    if constexpr (FULL) mfma_load_full<F, DP, CPS>(cb, F::lane(p.pa, row, CPS * (cw + bi * NJ * DP)));
+    else mfma_load_general<F, DP, CPS>(cb, p.pa, row, 0, cw, bi * NJ, J, nch);
     if (bi == 0) {
       // stage the bottleneck activations while the first weight batch is in flight
       const int per_row = p.K / 8;
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
       }
       __syncthreads();
     }
-    mfma_compute<F, DC, FULL>(cb, xl0 + bi * kNJ * DC * F::KPC, xon, true, bi * kNJ, J, cw, nch, acc);
+    mfma_compute<F, DP, CPS, FULL>(cb, xl0 + bi * NJ * CPS * DP * F::KPC, xon, true, bi * NJ, J, cw, nch, acc);
   }
   // wave-order reduction within each row group
   float* gred = red + (size_t)grp * (KW > 1 ? KW - 1 : 0) * 256;
@@ -99,17 +100,23 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
   }
 }
 
+template <class F, int CPS>
+static void launch_hc_up_full(const HcUpArgs& p, int KW, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+  switch (KW) {
+    case 1: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 1, CPS, true>), grid, block, lds, st, p); break;
+    case 2: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 2, CPS, true>), grid, block, lds, st, p); break;
+    case 4: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 4, CPS, true>), grid, block, lds, st, p); break;
+    default: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 8, CPS, true>), grid, block, lds, st, p); break;
+  }
+}
+
 template <class F>
-static void launch_hc_up(const HcUpArgs& p, int KW, bool full, dim3 grid, size_t lds, hipStream_t st) {
+static void launch_hc_up(const HcUpArgs& p, int KW, int cps, bool full, dim3 grid, size_t lds, hipStream_t st) {
   const int T = p.hc * p.bj;
   const dim3 block((T / 16) * KW * 64);
-  if (!full) { hipLaunchKernelGGL((hc_up_mfma_kernel<F, kMaxKW, false>), grid, block, lds, st, p); return; }
-  switch (KW) {
-    case 1: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 1, true>), grid, block, lds, st, p); break;
-    case 2: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 2, true>), grid, block, lds, st, p); break;
-    case 4: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 4, true>), grid, block, lds, st, p); break;
-    default: hipLaunchKernelGGL((hc_up_mfma_kernel<F, 8, true>), grid, block, lds, st, p); break;
-  }
+  if (!full) hipLaunchKernelGGL((hc_up_mfma_kernel<F, kMaxKW, 1, false>), grid, block, lds, st, p);
+  else if (cps == 2) launch_hc_up_full<F, 2>(p, KW, grid, block, lds, st);
+  else launch_hc_up_full<F, 1>(p, KW, grid, block, lds, st);
 }
 
 __global__ __launch_bounds__(256) void hc_scaled_silu_kernel(const uint16_t* d, int64_t d_stride, uint16_t* bot,
@@ -184,8 +191,14 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
   if (M < 0 || M > 16 || K <= 0 || K % 64 || H <= 0 || hc <= 0 || bj <= 0 || H % bj)
     return hc_fail("hc_up: bad shape (M <= 16, K % 64 == 0, H % bj == 0)");
   const int chunks = K / 16;
-  int KW = mfma_kw(chunks);
-  const bool full = mfma_full(chunks, KW);
+  // the same slot shape, wave count and path as launch_gemv_mfma picks for W8
+  GemvLaunch q{};
+  q.pa.w0 = static_cast<const uint8_t*>(qi);
+  q.pa.s = static_cast<const uint8_t*>(si);
+  const bool pal = s_dtype == FP4X_DT_F16 ? mfma_pair_aligned<FmtW8<true>>(q, 1) : mfma_pair_aligned<FmtW8<false>>(q, 1);
+  const int cps = mfma_cps<FmtW8<false>>(chunks) == 2 && pal ? 2 : 1;
+  int KW = mfma_kw(chunks, cps);
+  const bool full = mfma_full(chunks, KW, cps);
   if (!full) KW = kMaxKW;                       // the GEMV core's general path
   const int T = hc * bj;
   if (T % 16 || (T / 16) * KW > 16) return hc_fail("hc_up: hc*bj must be a multiple of 16 with at most 16 waves per tile");
@@ -207,8 +220,8 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
   p.M = M; p.K = K; p.H = H; p.hc = hc; p.bj = bj;
   dim3 grid(H / bj);
   hipStream_t st = (hipStream_t)stream;
-  if (s_dtype == FP4X_DT_F16) launch_hc_up<FmtW8<true>>(p, KW, full, grid, lds, st);
-  else launch_hc_up<FmtW8<false>>(p, KW, full, grid, lds, st);
+  if (s_dtype == FP4X_DT_F16) launch_hc_up<FmtW8<true>>(p, KW, cps, full, grid, lds, st);
+  else launch_hc_up<FmtW8<false>>(p, KW, cps, full, grid, lds, st);
   return check_launch("hc_up");
 }
 

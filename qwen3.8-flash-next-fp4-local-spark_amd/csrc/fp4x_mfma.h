@@ -2,25 +2,27 @@
 //
 // One workgroup of KW waves works on tiles of 16 weight rows (the n dimension
 // of v_mfma_f32_16x16x32_bf16; the M <= 16 activation rows pad the m
-// dimension).  Lane (n = lane & 15, g = lane >> 4) of wave w streams 16-byte
-// chunks c = w*4 + g + j*4*KW of row n of its K slice: the four lane groups of
-// a wave read 64 contiguous bytes of each of 16 rows per load instruction.
-// Chunks are dequantized in registers to the bf16 operand and fed 8 k-values
-// per MFMA step; the activation fragment of lane (m, g) carries x[m] at the
-// same k, read from LDS.  The KW partial 16x16 tiles are summed in wave order
-// through LDS.
+// dimension).  The K slice of a row is cut into 16-byte chunks (KPC weights
+// each) taken in pairs: lane (n = lane & 15, g = lane >> 4) of wave w holds
+// pair slots p = w*4 + g + j*4*KW of row n, i.e. chunks 2p and 2p + 1, so the
+// four lane groups of a wave read 128 contiguous bytes of each of 16 rows per
+// pair of load instructions, and one scale (or auxiliary-plane) load serves
+// both chunks.  Chunks are dequantized in registers to the bf16 operand and
+// fed 8 k-values per MFMA step; the activation fragment of lane (m, g)
+// carries x[m] at the same k, read from LDS.  The KW partial 16x16 tiles are
+// summed in wave order through LDS.
 //
 // Instruction economy: KW is a template parameter, so a lane's chunks sit at
 // compile-time strides from one base pointer per weight plane (F::Lane) and
 // from one activation address; every load and LDS read of a batch uses a
-// constant offset.  Tile and batch positions advance by counters.
+// constant offset.
 //
-// Latency hiding: KW is chosen so that a lane's share of a tile (J chunks)
-// fills whole register batches of kNJ chunks, all of a batch's loads are in
-// flight together, and the launch keeps as many workgroups resident as the
-// register and LDS budget allows (each with the same number of tiles), so
-// the memory latency of one workgroup overlaps the work of the others.  The
-// first batch's loads go out before the activations are staged.
+// Latency hiding: KW is chosen so that a lane's share of a tile (J pair
+// slots) fills whole register batches of NJ slots, all of a batch's loads
+// are in flight together, and the launch keeps as many workgroups resident
+// as the register and LDS budget allows (each with the same number of
+// tiles), so the memory latency of one workgroup overlaps the work of the
+// others.  The first batch's loads go out before the activations are staged.
 //
 // Split-K (ksplit > 1): one fp32 slot tile per K slice; the last-arriving
 // workgroup of a tile (agent-scope ticket, see splitk_arrive) sums the slots
@@ -34,22 +36,34 @@ namespace fp4x {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kNJ = 5;        // chunks per lane held in one register batch
 constexpr int kMaxKW = 8;     // waves per workgroup at most
+
+// A lane's register batch holds NJ slots of CPS chunks each: CPS = 1, or 2
+// for the pair layout (32 contiguous bytes per lane and one scale load shared
+// by both chunks).  Measured on MI355X: pairs pay off for W8 slices of at
+// least 128 chunks (K = 2560 router gates); single chunks win everywhere
+// else (MXFP8, W6, NVFP4, INT2, and the K = 640 mixer slices).
+constexpr int kNJ = 5;
+template <class F> struct MfmaTune { static constexpr bool PAIRS = false; };
+template <bool F16S> struct MfmaTune<FmtW8<F16S>> { static constexpr bool PAIRS = true; };
+
+template <class F>
+__host__ __device__ inline int mfma_cps(int chunks) { return MfmaTune<F>::PAIRS && chunks >= 128 ? 2 : 1; }
 
 // Waves per tile for a K slice of `chunks` chunks: the fewest (a power of
 // two, at most kMaxKW) that keep a lane's share within one batch.
-__host__ __device__ inline int mfma_kw(int chunks) {
+__host__ __device__ inline int mfma_kw(int chunks, int cps) {
+  const int slots = (chunks + cps - 1) / cps;
   int kw = 1;
-  while (kw < kMaxKW && (chunks + 4 * kw - 1) / (4 * kw) > kNJ) kw <<= 1;
+  while (kw < kMaxKW && (slots + 4 * kw - 1) / (4 * kw) > kNJ) kw <<= 1;
   return kw;
 }
 
-// True when every lane of every wave gets exactly J chunks in whole batches
+// True when every lane of every wave gets exactly J slots in whole batches
 // (the constant-offset path); other slices take the general path.
-__host__ __device__ inline bool mfma_full(int chunks, int kw) {
-  const int dc = 4 * kw;
-  return chunks % dc == 0 && (chunks / dc) % kNJ == 0;
+__host__ __device__ inline bool mfma_full(int chunks, int kw, int cps) {
+  const int dp = 4 * kw;
+  return chunks % (cps * dp) == 0 && (chunks / (cps * dp)) % kNJ == 0;
 }
 
 __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
@@ -66,59 +80,68 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <class F>
+template <class F, int CPS>
 struct MfmaBatch {
-  typename F::Chunk ch[kNJ];
+  typename F::Chunk ch[kNJ][CPS];
 };
 
-// Full path: the kNJ chunks of a batch at constant offsets from L.
-template <class F, int DC>
-__device__ __forceinline__ void mfma_load_full(MfmaBatch<F>& b, const typename F::Lane& L) {
-#pragma unroll
-  for (int j = 0; j < kNJ; ++j) b.ch[j] = F::template at<DC>(L, j);
-}
-
-// General path: slot j holds chunk c0 + cw + (jb + j) * DC when that chunk is
-// inside the slice (jb + j < J and cw + (jb + j) * DC < nch); other slots read
-// chunk c0 of the same row, which is in bounds, and are multiplied as zeros.
-template <class F, int DC>
-__device__ __forceinline__ void mfma_load_general(MfmaBatch<F>& b, const PlaneArgs& a, int64_t row, int c0, int cw,
-                                                  int jb, int J, int nch) {
+// Full path: the NJ slots of a batch at constant offsets from L (L at the
+// slot-0 chunk CPS*p, DP = 4*KW slots between a lane's slots).
+template <class F, int DP, int CPS>
+__device__ __forceinline__ void mfma_load_full(MfmaBatch<F, CPS>& b, const typename F::Lane& L) {
 #pragma unroll
   for (int j = 0; j < kNJ; ++j) {
-    const int jj = jb + j;
-    const bool live = jj < J && cw + jj * DC < nch;
-    b.ch[j] = F::template at<DC>(F::lane(a, row, live ? c0 + cw + jj * DC : c0), 0);
+    if constexpr (CPS == 2) F::template pair<2 * DP>(L, j, b.ch[j][0], b.ch[j][1]);
+    else b.ch[j][0] = F::template at<DP>(L, j);
   }
 }
 
-// MFMA steps over one batch.  xl points at x[m][k] of this lane's slot 0
-// (LDS or global, m = lane & 15); slot j's activations are DC*KPC elements
-// further.  xon: m < M.  won: the lane's weight row exists.  Every slot is
-// consumed (dead slots multiply zeros), so no path leaves a batch load
-// outstanding past its compute.
-template <class F, int DC, bool FULL, class XPtr>
-__device__ __forceinline__ void mfma_compute(const MfmaBatch<F>& b, XPtr xl, bool xon, bool won, int jb, int J,
+// General path: chunk (slot j, half h) is c0 + CPS * (cw + (jb + j) * DP) + h
+// when it is inside the slice (jb + j < J and the chunk index < nch); other
+// chunks read chunk c0 of the same row, which is in bounds, and are
+// multiplied as zeros.
+template <class F, int DP, int CPS>
+__device__ __forceinline__ void mfma_load_general(MfmaBatch<F, CPS>& b, const PlaneArgs& a, int64_t row, int c0,
+                                                  int cw, int jb, int J, int nch) {
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j)
+#pragma unroll
+    for (int h = 0; h < CPS; ++h) {
+      const int jj = jb + j, c = CPS * (cw + jj * DP) + h;
+      const bool live = jj < J && c < nch;
+      b.ch[j][h] = F::template at<CPS * DP>(F::lane(a, row, live ? c0 + c : c0), 0);
+    }
+}
+
+// MFMA steps over one batch.  xl points at x[m][k] of this lane's slot-0
+// chunk (LDS or global, m = lane & 15); slot j's activations are CPS*DP*KPC
+// elements further, chunk h of a slot h*KPC further.  xon: m < M.  won: the
+// lane's weight row exists.  Every chunk is consumed (dead chunks multiply
+// zeros), so no path leaves a batch load outstanding past its compute.
+template <class F, int DP, int CPS, bool FULL, class XPtr>
+__device__ __forceinline__ void mfma_compute(const MfmaBatch<F, CPS>& b, XPtr xl, bool xon, bool won, int jb, int J,
                                              int cw, int nch, f32x4_t& acc) {
 #pragma unroll
-  for (int j = 0; j < kNJ; ++j) {
-    const bool live = FULL || (jb + j < J && cw + (jb + j) * DC < nch);   // uniform per 16 lanes
+  for (int j = 0; j < kNJ; ++j)
 #pragma unroll
-    for (int sub = 0; sub < F::SUB; ++sub) {
-      uint32_t w[8];
-      F::deq16(b.ch[j], sub, w);
-      uint4 xa = make_uint4(0, 0, 0, 0), xb = xa;
-      if (xon && live) {
-        const uint4* xp = reinterpret_cast<const uint4*>(xl + j * DC * F::KPC + sub * 16);
-        xa = xp[0];
-        xb = xp[1];
+    for (int h = 0; h < CPS; ++h) {
+      const bool live = FULL || (jb + j < J && CPS * (cw + (jb + j) * DP) + h < nch);   // uniform per 16 lanes
+#pragma unroll
+      for (int sub = 0; sub < F::SUB; ++sub) {
+        uint32_t w[8];
+        F::deq16(b.ch[j][h], sub, w);
+        uint4 xa = make_uint4(0, 0, 0, 0), xb = xa;
+        if (xon && live) {
+          const uint4* xp = reinterpret_cast<const uint4*>(xl + (j * CPS * DP + h) * F::KPC + sub * 16);
+          xa = xp[0];
+          xb = xp[1];
+        }
+        uint4 wa = make_uint4(w[0], w[1], w[2], w[3]), wb = make_uint4(w[4], w[5], w[6], w[7]);
+        if (!(won && live)) { wa = make_uint4(0, 0, 0, 0); wb = wa; }
+        acc = mfma16(xa, wa, acc);
+        acc = mfma16(xb, wb, acc);
       }
-      uint4 wa = make_uint4(w[0], w[1], w[2], w[3]), wb = make_uint4(w[4], w[5], w[6], w[7]);
-      if (!(won && live)) { wa = make_uint4(0, 0, 0, 0); wb = wa; }
-      acc = mfma16(xa, wa, acc);
-      acc = mfma16(xb, wb, acc);
     }
-  }
 }
 
 // Sum the KW waves' 16x16 tiles in wave order; the result is valid in wave 0.
@@ -236,10 +259,11 @@ __device__ __forceinline__ void mfma_stage_x(uint16_t* lds, const uint16_t* xg, 
 // host sizes per_wg so that every workgroup of the launch is resident at once
 // and all carry the same number of items.  The activations of an entry are
 // staged once per run of items of that entry.  p.J: chunks per lane per
-// tile, p.nb: register batches per tile.
-template <class F, int KW, bool FULL, bool XL, class Epi>
+// tile (slots), p.nb: register batches per tile.
+template <class F, int KW, int CPS, bool FULL, bool XL, class Epi>
 __global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
-  constexpr int DC = 4 * KW;                // chunks between a lane's consecutive chunks
+  constexpr int DP = 4 * KW;                // slots between a lane's consecutive slots
+  constexpr int NJ = kNJ;
   extern __shared__ __align__(16) uint16_t lds[];
   const int split = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -249,7 +273,7 @@ __global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
   const int iend = it + p.per_wg < items ? it + p.per_wg : items;
   if (it >= iend) return;
   const int ks = p.pa.K / p.ksplit, k0 = split * ks, nch = ks / F::KPC, c0 = k0 / F::KPC;
-  const int cw = wave * 4 + g;              // this lane's first chunk within the slice
+  const int cw = wave * 4 + g;              // this lane's first slot within the slice
   const int J = p.J, nb = p.nb;
   const int xs = mfma_xstride(ks);
   const size_t xbytes = XL ? (((size_t)p.M * xs * 2 + 15) & ~(size_t)15) : 0;
@@ -267,12 +291,12 @@ __global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
     const int64_t rowc = row < p.N ? row : p.N - 1;     // rows past N read row N-1 (in bounds) as zeros
     const bool won = row < p.N;
     const uint16_t* xg = p.x + b * p.x_bstride;
-    const uint16_t* xl0 = XL ? lds + xrow * xs + cw * F::KPC : xg + xrow * p.x_stride + k0 + cw * F::KPC;
+    const uint16_t* xl0 = XL ? lds + xrow * xs + CPS * cw * F::KPC : xg + xrow * p.x_stride + k0 + CPS * cw * F::KPC;
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int bi = 0; bi < nb; ++bi) {
-      MfmaBatch<F> A;
-      if constexpr (FULL) mfma_load_full<F, DC>(A, F::lane(pa, rowc, c0 + cw + bi * kNJ * DC));
-      else mfma_load_general<F, DC>(A, pa, rowc, c0, cw, bi * kNJ, J, nch);
+      MfmaBatch<F, CPS> A;
+      if constexpr (FULL) mfma_load_full<F, DP, CPS>(A, F::lane(pa, rowc, c0 + CPS * (cw + bi * NJ * DP)));
+      else mfma_load_general<F, DP, CPS>(A, pa, rowc, c0, cw, bi * NJ, J, nch);
       if constexpr (XL) {
         if (b != cur_b) {
           // new batch entry: stage its activations while the weight loads are in flight
@@ -282,7 +306,7 @@ __global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
           cur_b = b;
         }
       }
-      mfma_compute<F, DC, FULL>(A, xl0 + bi * kNJ * DC * F::KPC, xon, won, bi * kNJ, J, cw, nch, acc);
+      mfma_compute<F, DP, CPS, FULL>(A, xl0 + bi * NJ * CPS * DP * F::KPC, xon, won, bi * NJ, J, cw, nch, acc);
     }
     mfma_finish<KW, Epi>(p, b, split, t, acc, red);
   }
@@ -293,9 +317,9 @@ int device_cus();
 // Optional cap on resident waves per CU from FP4X_WAVES_PER_CU (0: none).
 int waves_per_cu_cap();
 
-template <class F, int KW, bool FULL, bool XL, class Epi>
+template <class F, int KW, int CPS, bool FULL, bool XL, class Epi>
 void launch_mfma_kw(GemvLaunch p, int batch, size_t lds, hipStream_t st) {
-  auto kern = gemv_mfma_kernel<F, KW, FULL, XL, Epi>;
+  auto kern = gemv_mfma_kernel<F, KW, CPS, FULL, XL, Epi>;
   // resident workgroups per CU for this kernel and LDS size (cached per LDS size)
   static int occ_cache[97];
   const int key = (int)((lds + 1023) / 1024);
@@ -319,10 +343,32 @@ void launch_mfma_kw(GemvLaunch p, int batch, size_t lds, hipStream_t st) {
   hipLaunchKernelGGL(kern, dim3(gx, p.ksplit, 1), dim3(64 * KW), lds, st, p);
 }
 
-template <class F, int KW, bool FULL, class Epi>
+template <class F, int KW, int CPS, bool FULL, class Epi>
 void launch_mfma_xl(const GemvLaunch& p, int batch, size_t lds, bool xl, hipStream_t st) {
-  if (xl) launch_mfma_kw<F, KW, FULL, true, Epi>(p, batch, lds, st);
-  else launch_mfma_kw<F, KW, FULL, false, Epi>(p, batch, lds, st);
+  if (xl) launch_mfma_kw<F, KW, CPS, FULL, true, Epi>(p, batch, lds, st);
+  else launch_mfma_kw<F, KW, CPS, FULL, false, Epi>(p, batch, lds, st);
+}
+
+template <class F, int CPS, class Epi>
+void launch_mfma_full(const GemvLaunch& p, int KW, int batch, size_t lds, bool xl, hipStream_t st) {
+  switch (KW) {
+    case 1: launch_mfma_xl<F, 1, CPS, true, Epi>(p, batch, lds, xl, st); break;
+    case 2: launch_mfma_xl<F, 2, CPS, true, Epi>(p, batch, lds, xl, st); break;
+    case 4: launch_mfma_xl<F, 4, CPS, true, Epi>(p, batch, lds, xl, st); break;
+    default: launch_mfma_xl<F, 8, CPS, true, Epi>(p, batch, lds, xl, st); break;
+  }
+}
+
+// Pair loads of the full path read 16-byte main-plane pieces and
+// F::AUX_ALIGN-byte scale pieces: every plane base (and batch stride) must
+// allow them, else the general path runs.
+template <class F>
+bool mfma_pair_aligned(const GemvLaunch& p, int batch) {
+  auto al = [](const void* q, int n) { return (reinterpret_cast<uintptr_t>(q) & (uintptr_t)(n - 1)) == 0; };
+  bool ok = al(p.pa.w0, 16) && al(p.pa.s, F::AUX_ALIGN) && (!p.pa.w1 || al(p.pa.w1, 16));
+  if (batch > 1)
+    ok = ok && p.w0_bstride % 16 == 0 && p.s_bstride % F::AUX_ALIGN == 0 && (!p.pa.w1 || p.w1_bstride % 16 == 0);
+  return ok;
 }
 
 template <class F, class Epi>
@@ -330,22 +376,21 @@ int launch_gemv_mfma(const GemvLaunch& p0, int batch, hipStream_t st) {
   GemvLaunch p = p0;
   const int ks = p.pa.K / p.ksplit;
   const int chunks = ks / F::KPC;
-  int KW = mfma_kw(chunks);
-  const bool full = mfma_full(chunks, KW);
-  if (!full) KW = kMaxKW;                               // general path: one instantiation
-  p.J = (chunks + 4 * KW - 1) / (4 * KW);
+  const int cps = mfma_cps<F>(chunks) == 2 && mfma_pair_aligned<F>(p, batch) ? 2 : 1;
+  int KW = mfma_kw(chunks, cps);
+  const bool full = mfma_full(chunks, KW, cps);
+  if (!full) KW = kMaxKW;                               // general path (single chunks): one instantiation
+  const int cpsu = full ? cps : 1;
+  p.J = ((chunks + cpsu - 1) / cpsu + 4 * KW - 1) / (4 * KW);
   p.nb = (p.J + kNJ - 1) / kNJ;
   const bool xl = mfma_lds_bytes(p.M, ks, KW, true) <= 96 * 1024;
   const size_t lds = mfma_lds_bytes(p.M, ks, KW, xl);
-  if (!full) {
-    launch_mfma_xl<F, kMaxKW, false, Epi>(p, batch, lds, xl, st);
+  if (!full) launch_mfma_xl<F, kMaxKW, 1, false, Epi>(p, batch, lds, xl, st);
+  else if constexpr (MfmaTune<F>::PAIRS) {
+    if (cps == 2) launch_mfma_full<F, 2, Epi>(p, KW, batch, lds, xl, st);
+    else launch_mfma_full<F, 1, Epi>(p, KW, batch, lds, xl, st);
   } else {
-    switch (KW) {
-      case 1: launch_mfma_xl<F, 1, true, Epi>(p, batch, lds, xl, st); break;
-      case 2: launch_mfma_xl<F, 2, true, Epi>(p, batch, lds, xl, st); break;
-      case 4: launch_mfma_xl<F, 4, true, Epi>(p, batch, lds, xl, st); break;
-      default: launch_mfma_xl<F, 8, true, Epi>(p, batch, lds, xl, st); break;
-    }
+    launch_mfma_full<F, 1, Epi>(p, KW, batch, lds, xl, st);
   }
   return check_launch("gemv_mfma");
 }
