@@ -114,13 +114,20 @@ __device__ __forceinline__ void mfma_load_general(MfmaBatch<F, CPS>& b, const Pl
 }
 
 // MFMA steps over one batch.  xl points at x[m][k] of this lane's slot-0
-// chunk (LDS or global, m = lane & 15); slot j's activations are CPS*DP*KPC
-// elements further, chunk h of a slot h*KPC further.  xon: m < M.  won: the
-// lane's weight row exists.  Every chunk is consumed (dead chunks multiply
-// zeros), so no path leaves a batch load outstanding past its compute.
+// chunk (LDS or global, m = lane & 15, or a valid row for m >= M); slot j's
+// activations are CPS*DP*KPC elements further, chunk h of a slot h*KPC
+// further.
+//
+// Output row m of the 16x16 tile depends only on activation row m, and
+// column n only on weight row n.  Lanes of rows m >= M and of weight rows
+// past N therefore feed whatever their (valid, in-bounds) addresses hold:
+// their outputs are never stored.  Only dead chunks of the general path
+// (outside the K slice) would reach stored outputs, so only they are zeroed.
+// Every chunk is consumed, so no path leaves a batch load outstanding past
+// its compute.
 template <class F, int DP, int CPS, bool FULL, class XPtr>
-__device__ __forceinline__ void mfma_compute(const MfmaBatch<F, CPS>& b, XPtr xl, bool xon, bool won, int jb, int J,
-                                             int cw, int nch, f32x4_t& acc) {
+__device__ __forceinline__ void mfma_compute(const MfmaBatch<F, CPS>& b, XPtr xl, int jb, int J, int cw, int nch,
+                                             f32x4_t& acc) {
 #pragma unroll
   for (int j = 0; j < kNJ; ++j)
 #pragma unroll
@@ -130,14 +137,24 @@ __device__ __forceinline__ void mfma_compute(const MfmaBatch<F, CPS>& b, XPtr xl
       for (int sub = 0; sub < F::SUB; ++sub) {
         uint32_t w[8];
         F::deq16(b.ch[j][h], sub, w);
-        uint4 xa = make_uint4(0, 0, 0, 0), xb = xa;
-        if (xon && live) {
+        uint4 wa = make_uint4(w[0], w[1], w[2], w[3]), wb = make_uint4(w[4], w[5], w[6], w[7]);
+        uint4 xa, xb;
+        if constexpr (FULL) {
           const uint4* xp = reinterpret_cast<const uint4*>(xl + (j * CPS * DP + h) * F::KPC + sub * 16);
           xa = xp[0];
           xb = xp[1];
+        } else {
+          xa = make_uint4(0, 0, 0, 0);
+          xb = xa;
+          if (live) {
+            const uint4* xp = reinterpret_cast<const uint4*>(xl + (j * CPS * DP + h) * F::KPC + sub * 16);
+            xa = xp[0];
+            xb = xp[1];
+          } else {
+            wa = xa;
+            wb = xa;
+          }
         }
-        uint4 wa = make_uint4(w[0], w[1], w[2], w[3]), wb = make_uint4(w[4], w[5], w[6], w[7]);
-        if (!(won && live)) { wa = make_uint4(0, 0, 0, 0); wb = wa; }
         acc = mfma16(xa, wa, acc);
         acc = mfma16(xb, wb, acc);
       }
@@ -289,7 +306,6 @@ __global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
     pa.s += b * p.s_bstride;
     const int64_t row = (int64_t)t * 16 + n;
     const int64_t rowc = row < p.N ? row : p.N - 1;     // rows past N read row N-1 (in bounds) as zeros
-    const bool won = row < p.N;
     const uint16_t* xg = p.x + b * p.x_bstride;
     const uint16_t* xl0 = XL ? lds + xrow * xs + CPS * cw * F::KPC : xg + xrow * p.x_stride + k0 + CPS * cw * F::KPC;
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -306,7 +322,7 @@ __global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
           cur_b = b;
         }
       }
-      mfma_compute<F, DP, CPS, FULL>(A, xl0 + bi * NJ * CPS * DP * F::KPC, xon, won, bi * NJ, J, cw, nch, acc);
+      mfma_compute<F, DP, CPS, FULL>(A, xl0 + bi * NJ * CPS * DP * F::KPC, bi * NJ, J, cw, nch, acc);
     }
     mfma_finish<KW, Epi>(p, b, split, t, acc, red);
   }
