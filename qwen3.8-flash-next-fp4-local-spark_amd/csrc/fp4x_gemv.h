@@ -400,6 +400,30 @@ struct FmtInt2 {
       return f16_to_f32((uint16_t)(h & 0xffffu));
     }
   }
+  // Transposed dequant for the MFMA core: the 16 weights of sub-block `sub`
+  // in k order [0,4,8,12, 1,5,9,13, 2,6,10,14, 3,7,11,15] (a 4x4 transpose
+  // within the block), matching activations staged in the same order.  Each
+  // code word W_t (element t of every 4-group) selects the low and the high
+  // bytes of four values at once; two more byte permutes interleave them.
+  static constexpr bool XPERM = true;
+  __device__ static void deq16t(const Chunk& ch, int sub, uint32_t (&w)[8]) {
+    const float s = group_scale(ch, sub);
+    const float p = 0.5f * s, q = 1.5f * s;       // exact in fp32
+    const uint32_t B = pack_bf16x2(p, q);         // [lo p, hi p, lo q, hi q]
+    // value of code c: -q, -p, p, q; negation flips the sign bit of the high byte
+    const uint32_t lut_lo = perm_b32(B, B, 0x02000002u);
+    const uint32_t lut_hi = perm_b32(B, B, 0x03010103u) ^ 0x00008080u;
+    const uint32_t cw = sub == 0 ? ch.q.x : sub == 1 ? ch.q.y : sub == 2 ? ch.q.z : ch.q.w;
+    const uint32_t W[4] = {cw & 0x03030303u, (cw >> 4) & 0x03030303u, (cw >> 2) & 0x03030303u,
+                           (cw >> 6) & 0x03030303u};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t lo = perm_b32(lut_lo, lut_lo, W[t]);
+      const uint32_t hi = perm_b32(lut_hi, lut_hi, W[t]);
+      w[2 * t] = perm_b32(hi, lo, 0x05010400u);       // k = t, 4 + t
+      w[2 * t + 1] = perm_b32(hi, lo, 0x07030602u);   // k = 8 + t, 12 + t
+    }
+  }
   __device__ static void deq16(const Chunk& ch, int sub, uint32_t (&w)[8]) {
     const float s = group_scale(ch, sub);
     const float p = 0.5f * s, q = 1.5f * s;       // exact in fp32

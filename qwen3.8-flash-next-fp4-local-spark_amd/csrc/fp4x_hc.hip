@@ -72,7 +72,7 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
       }
       __syncthreads();
     }
-    mfma_compute<F, DP, CPS, FULL>(cb, xl0 + bi * NJ * CPS * DP * F::KPC, bi * NJ, J, cw, nch, acc);
+    mfma_compute<F, DP, CPS, FULL, false>(cb, xl0 + bi * NJ * CPS * DP * F::KPC, bi * NJ, J, cw, nch, acc);
   }
   // wave-order reduction within each row group
   float* gred = red + (size_t)grp * (KW > 1 ? KW - 1 : 0) * 256;

@@ -45,6 +45,12 @@ constexpr int kMaxKW = 8;     // waves per workgroup at most
 // else (MXFP8, W6, NVFP4, INT2, and the K = 640 mixer slices).
 constexpr int kNJ = 5;
 template <class F> struct MfmaTune { static constexpr bool PAIRS = false; };
+
+// Formats whose MFMA operand is produced in a permuted k order within each
+// 16-element block (F::deq16t) declare XPERM; their activations are staged
+// with the same permutation.
+template <class F, class = void> struct HasXPerm { static constexpr bool value = false; };
+template <class F> struct HasXPerm<F, decltype(void(F::XPERM))> { static constexpr bool value = F::XPERM; };
 template <bool F16S> struct MfmaTune<FmtW8<F16S>> { static constexpr bool PAIRS = true; };
 
 template <class F>
@@ -125,7 +131,7 @@ __device__ __forceinline__ void mfma_load_general(MfmaBatch<F, CPS>& b, const Pl
 // (outside the K slice) would reach stored outputs, so only they are zeroed.
 // Every chunk is consumed, so no path leaves a batch load outstanding past
 // its compute.
-template <class F, int DP, int CPS, bool FULL, class XPtr>
+template <class F, int DP, int CPS, bool FULL, bool XP, class XPtr>
 __device__ __forceinline__ void mfma_compute(const MfmaBatch<F, CPS>& b, XPtr xl, int jb, int J, int cw, int nch,
                                              f32x4_t& acc) {
 #pragma unroll
@@ -136,7 +142,8 @@ __device__ __forceinline__ void mfma_compute(const MfmaBatch<F, CPS>& b, XPtr xl
 #pragma unroll
       for (int sub = 0; sub < F::SUB; ++sub) {
         uint32_t w[8];
-        F::deq16(b.ch[j][h], sub, w);
+        if constexpr (XP) F::deq16t(b.ch[j][h], sub, w);
+        else F::deq16(b.ch[j][h], sub, w);
         uint4 wa = make_uint4(w[0], w[1], w[2], w[3]), wb = make_uint4(w[4], w[5], w[6], w[7]);
         uint4 xa, xb;
         if constexpr (FULL) {
@@ -271,6 +278,32 @@ __device__ __forceinline__ void mfma_stage_x(uint16_t* lds, const uint16_t* xg, 
   for (int i0 = threadIdx.x + 4 * blockDim.x; i0 < total; i0 += 4 * blockDim.x) stage4(i0);
 }
 
+// The same staging with the k order of F::deq16t: a 4x4 transpose within each
+// 16-element block (position i holds element (i % 4) * 4 + i / 4).
+__device__ __forceinline__ void mfma_stage_x_t4(uint16_t* lds, const uint16_t* xg, int64_t x_stride, int M, int k0,
+                                                int ks, int xs) {
+  const int per_row = ks / 16, total = M * per_row;
+  const uint4* xg4 = reinterpret_cast<const uint4*>(xg + k0);
+  const int64_t xrow4 = x_stride / 8;
+  uint4* lds4 = reinterpret_cast<uint4*>(lds);
+  const int lrow4 = xs / 8;
+  for (int i = threadIdx.x; i < total; i += blockDim.x) {
+    const int m = i / per_row, q = i - m * per_row;
+    const uint4 a = xg4[m * xrow4 + 2 * q], b = xg4[m * xrow4 + 2 * q + 1];   // elements 0-7, 8-15
+    uint4 o, r;
+    o.x = perm_b32(a.z, a.x, 0x05040100u);   // x0, x4
+    o.y = perm_b32(b.z, b.x, 0x05040100u);   // x8, x12
+    o.z = perm_b32(a.z, a.x, 0x07060302u);   // x1, x5
+    o.w = perm_b32(b.z, b.x, 0x07060302u);   // x9, x13
+    r.x = perm_b32(a.w, a.y, 0x05040100u);   // x2, x6
+    r.y = perm_b32(b.w, b.y, 0x05040100u);   // x10, x14
+    r.z = perm_b32(a.w, a.y, 0x07060302u);   // x3, x7
+    r.w = perm_b32(b.w, b.y, 0x07060302u);   // x11, x15
+    lds4[m * lrow4 + 2 * q] = o;
+    lds4[m * lrow4 + 2 * q + 1] = r;
+  }
+}
+
 // Work items are (batch entry, 16-row tile) pairs, numbered entry-major;
 // workgroup x of K slice y takes items [x * per_wg, (x + 1) * per_wg).  The
 // host sizes per_wg so that every workgroup of the launch is resident at once
@@ -317,12 +350,14 @@ __global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
         if (b != cur_b) {
           // new batch entry: stage its activations while the weight loads are in flight
           if (cur_b >= 0) __syncthreads();               // every wave is done with the previous entry's x
-          mfma_stage_x(lds, xg, p.x_stride, p.M, k0, ks, xs);
+          if constexpr (HasXPerm<F>::value) mfma_stage_x_t4(lds, xg, p.x_stride, p.M, k0, ks, xs);
+          else mfma_stage_x(lds, xg, p.x_stride, p.M, k0, ks, xs);
           __syncthreads();
           cur_b = b;
         }
       }
-      mfma_compute<F, DP, CPS, FULL>(A, xl0 + bi * NJ * CPS * DP * F::KPC, bi * NJ, J, cw, nch, acc);
+      mfma_compute<F, DP, CPS, FULL, XL && HasXPerm<F>::value>(A, xl0 + bi * NJ * CPS * DP * F::KPC, bi * NJ, J, cw,
+                                                                nch, acc);
     }
     mfma_finish<KW, Epi>(p, b, split, t, acc, red);
   }
