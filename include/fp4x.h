@@ -114,7 +114,9 @@ int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void*
  * [torch.topk(coarse, C) in the fast head, x/fp4patch.py:377] */
 int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int64_t* idx_out, void* workspace,
                    int64_t ws_bytes, void* stream);
-/* Bytes of device workspace fp4x_topk_rows needs for M rows (16-byte aligned). */
+/* Bytes of device workspace fp4x_topk_rows needs for M rows (16-byte
+ * aligned, no initial contents required).  Calls that share a workspace must
+ * be stream-ordered. */
 int64_t fp4x_topk_workspace_size(int M);
 
 /* In place: out[m, idx[m, c]] = cast(sum_k float(e4m3(w)*2^(s-127)) * float(x[m, k])).

@@ -48,22 +48,24 @@ __global__ __launch_bounds__(kThreads) void refine_mx8_kernel(RefineArgs p) {
 }
 
 // ------------------------------------------------------------------ top-k
-// Three launches per call (no grid-wide waits):
+// Three launches per call, which exchange data only across launch
+// boundaries (no grid-wide waits, no cross-workgroup fences):
 //   A  slice maxima: the row is cut into <= 4096 slices of S elements (S a
 //      multiple of 8); smax[m][i] = largest order key of slice i.  Also zeroes
 //      the row's candidate counter.
 //   B  every workgroup of a row derives T0 = the C-th largest slice maximum
 //      (a lower bound of the C-th largest element: C slices each hold an
-//      element >= T0) and appends its elements with key >= T0 to the row's
-//      candidate list (composite keys, wave-aggregated atomics).
+//      element >= T0), gathers its elements with key >= T0 in LDS and
+//      appends them to the row's candidate list with one global atomic.
 //   C  one workgroup per row sorts the candidates (at most 4096) by the
 //      total order and writes the first C indices.  Rows with fewer than C
 //      slices, or more than 4096 candidates (massive ties), take the exact
-//      threshold path in C instead.
+//      threshold path in C instead.  Rows of at most 4096 elements skip A and
+//      B: C sorts the whole row.
 constexpr int kTkThreads = 1024;
 constexpr int kTkCap = 4096;     // candidates per row
 constexpr int kTkSlices = 4096;  // slice maxima per row
-constexpr int kTkB = 32;         // collecting workgroups per row
+constexpr int kTkB = 16;         // collecting workgroups per row (kTkThreads each)
 
 // bf16 bits -> 16-bit key increasing with the value; -0 counts as +0 and
 // every NaN as the largest value.
@@ -86,18 +88,56 @@ struct TkHist {
 };
 
 // Walk a 256-bin histogram from the top: the bin holding the k-th largest
-// element (k >= 1) and the count of elements in higher bins.
+// element (k >= 1) and the count of elements in higher bins (bin 0 if the
+// count never reaches k).  Wave 0 holds four bins per lane, top bins first,
+// scans the lane sums and picks the first lane whose running count reaches k.
 __device__ void tk_walk(TkHist& h, int k) {
-  if (threadIdx.x == 0) {
-    int above = 0, b = 255;
-    for (; b > 0; --b) {
-      if (above + (int)h.hist[b] >= k) break;
-      above += h.hist[b];
+  if (threadIdx.x < 64) {
+    const int l = threadIdx.x;
+    uint32_t c[4], sum = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      c[r] = h.hist[255 - 4 * l - r];
+      sum += c[r];
     }
-    h.sel_bin = b;
-    h.sel_above = above;
+    uint32_t incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t v = __shfl_up(incl, d, 64);
+      if (l >= d) incl += v;
+    }
+    const uint64_t hit = __ballot(incl >= (uint32_t)k);
+    const int L = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
+    if (l == L) {
+      uint32_t above = incl - sum;
+      int b = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int bin = 255 - 4 * l - r;
+        if (above + c[r] >= (uint32_t)k || bin == 0) { b = bin; break; }
+        above += c[r];
+      }
+      h.sel_bin = b;
+      h.sel_above = (int)above;
+    }
   }
   __syncthreads();
+}
+
+// hist[bin] += 1 for every lane with valid set: lanes holding the same bin
+// add together (one LDS atomic per distinct bin per wave), so the high bytes
+// of a skewed key set (the slice maxima, logits) do not serialize on one
+// address.
+__device__ __forceinline__ void tk_hist_add(uint32_t* hist, uint32_t bin, bool valid) {
+  const int lane = threadIdx.x & 63;
+  uint64_t active = __ballot(valid);
+  while (active) {
+    const int leader = __ffsll((unsigned long long)active) - 1;
+    const uint32_t lb = __shfl(bin, leader, 64);
+    const uint64_t same = __ballot(valid && bin == lb) & active;
+    if (lane == leader) atomicAdd(&hist[lb], (uint32_t)__popcll(same));
+    active &= ~same;
+  }
 }
 
 // Exact k-th largest key among n keys get(i) (two 8-bit rounds); *n_above
@@ -106,7 +146,10 @@ template <class Get>
 __device__ uint32_t tk_kth(TkHist& h, Get get, int n, int k, int* n_above) {
   for (int i = threadIdx.x; i < 256; i += blockDim.x) h.hist[i] = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&h.hist[get(i) >> 8], 1u);
+  for (int i0 = 0; i0 < n; i0 += blockDim.x) {
+    const int i = i0 + threadIdx.x;
+    tk_hist_add(h.hist, i < n ? get(i) >> 8 : 0u, i < n);
+  }
   __syncthreads();
   tk_walk(h, k);
   const uint32_t b1 = h.sel_bin;
@@ -115,6 +158,7 @@ __device__ uint32_t tk_kth(TkHist& h, Get get, int n, int k, int* n_above) {
   for (int i = threadIdx.x; i < 256; i += blockDim.x) h.hist[i] = 0;
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    // low bytes within one high-byte bin are spread out: plain atomics
     const uint32_t kk = get(i);
     if ((kk >> 8) == b1) atomicAdd(&h.hist[kk & 255u], 1u);
   }
@@ -145,7 +189,7 @@ __device__ __forceinline__ void tk_append(uint64_t* list, int* count, int cap, b
 struct TkWork {              // per row, in the caller's workspace
   uint64_t cand[kTkCap];
   uint16_t smax[kTkSlices];
-  int count;
+  int count;                 // candidates appended (beyond kTkCap: exact path)
   int pad[3];
 };
 
@@ -173,41 +217,6 @@ __global__ __launch_bounds__(256) void topk_slicemax_kernel(const uint16_t* logi
   w.smax[sl] = (uint16_t)mx;
 }
 
-__global__ __launch_bounds__(256) void topk_collect_kernel(const uint16_t* logits, int64_t stride, int V, int C,
-                                                           TkWork* work) {
-  __shared__ uint16_t smax[kTkSlices];
-  __shared__ TkHist h;
-  const int m = blockIdx.y;
-  const uint16_t* row = logits + (int64_t)m * stride;
-  TkWork& w = work[m];
-  const int S = tk_slice(V), ns = (V + S - 1) / S;
-  for (int i = threadIdx.x; i < ns; i += blockDim.x) smax[i] = w.smax[i];
-  __syncthreads();
-  int above;
-  const uint32_t T0 = tk_kth(h, [&](int i) { return (uint32_t)smax[i]; }, ns, C, &above);
-  // this workgroup's share of the row, in whole 8-element vectors
-  const int nvec = (V + 7) / 8;
-  const int per = (nvec + gridDim.x - 1) / gridDim.x;
-  const int v0 = blockIdx.x * per, v1 = min(nvec, v0 + per);
-  for (int base = v0; base < v1; base += blockDim.x) {
-    const int vi = base + threadIdx.x;
-    uint32_t d[4] = {0, 0, 0, 0};
-    const bool full = vi < v1 && vi * 8 + 8 <= V;
-    if (full) {
-      const uint4 v = *reinterpret_cast<const uint4*>(row + (int64_t)vi * 8);
-      d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int i = vi * 8 + q;
-      bool ok = vi < v1 && i < V;
-      uint32_t key = 0;
-      if (ok) key = full ? tk_key(q & 1 ? d[q >> 1] >> 16 : d[q >> 1] & 0xffffu) : tk_key(row[i]);
-      tk_append(w.cand, &w.count, kTkCap, ok && key >= T0, tk_comp(key, i));
-    }
-  }
-}
-
 // Descending bitonic sort of a[0, n2), n2 a power of two.
 __device__ void tk_sort(uint64_t* a, int n2) {
   for (int size = 2; size <= n2; size <<= 1) {
@@ -224,55 +233,164 @@ __device__ void tk_sort(uint64_t* a, int n2) {
   }
 }
 
+// The exact path: T = the C-th largest key of the row, the elements above
+// it, then ties at T in index order; n = C on return in cand[0, C).
+__device__ void tk_exact(const uint16_t* row, int V, int C, uint64_t* cand, TkHist& h, int* n_sh) {
+  if (threadIdx.x == 0) *n_sh = 0;
+  __syncthreads();
+  int above;
+  const uint32_t T = tk_kth(h, [&](int i) { return tk_key(row[i]); }, V, C, &above);
+  for (int i0 = 0; i0 < V; i0 += blockDim.x) {
+    const int i = i0 + threadIdx.x;
+    const uint32_t key = i < V ? tk_key(row[i]) : 0u;
+    tk_append(cand, n_sh, kTkCap, i < V && key > T, tk_comp(key, i));
+  }
+  __syncthreads();
+  const int need = C - above;
+  if (threadIdx.x < 64) {
+    int taken = 0;
+    for (int i0 = 0; i0 < V && taken < need; i0 += 64) {
+      const int i = i0 + threadIdx.x;
+      const bool eq = i < V && tk_key(row[i]) == T;
+      const uint64_t mask = __ballot(eq);
+      const int pos = taken + __popcll(mask & ((1ull << threadIdx.x) - 1ull));
+      if (eq && pos < need) cand[above + pos] = tk_comp(T, i);
+      taken += __popcll(mask);
+    }
+  }
+  __syncthreads();
+}
+
+// Descending bitonic sort of n2 <= blockDim.x keys (n2 a power of two), one
+// per thread in a register: stages with partners in the same wave exchange by
+// shuffles, the others (stride >= 64) through xch[] in LDS.  Thread t < n2
+// holds element t and ends with the t-th largest; threads past n2 sort their
+// own values among themselves.  Every thread of the workgroup must call it.
+__device__ uint64_t tk_sort_regs(uint64_t a, int n2, uint64_t* xch) {
+  const int t = threadIdx.x;
+  for (int size = 2; size <= n2; size <<= 1) {
+    const bool desc = (t & size) == 0;
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      uint64_t b;
+      if (stride >= 64) {
+        xch[t] = a;
+        __syncthreads();
+        b = xch[t ^ stride];
+        __syncthreads();
+      } else {
+        b = __shfl_xor(a, stride, 64);
+      }
+      const bool lower = (t & stride) == 0;        // t is the first of the pair
+      const bool keep_max = lower == desc;
+      a = keep_max ? (a > b ? a : b) : (a < b ? a : b);
+    }
+  }
+  return a;
+}
+
+// Sort cand[0, n) descending and write the first C indices.
+__device__ void tk_finish(uint64_t* cand, int n, int C, int64_t* out) {
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  if (n2 <= (int)blockDim.x && n2 >= 64) {
+    const int t = threadIdx.x;
+    const uint64_t a = t < n ? cand[t] : 0ull;
+    __syncthreads();                                // cand doubles as the exchange buffer
+    const uint64_t r = tk_sort_regs(a, n2, cand);   // every thread takes part in the barriers
+    if (t < C) out[t] = (int64_t)(0xffffffffu - (uint32_t)(r & 0xffffffffu));
+    return;
+  }
+  for (int i = n + threadIdx.x; i < n2; i += blockDim.x) cand[i] = 0;
+  __syncthreads();
+  tk_sort(cand, n2);
+  for (int i = threadIdx.x; i < C; i += blockDim.x) out[i] = (int64_t)(0xffffffffu - (uint32_t)(cand[i] & 0xffffffffu));
+}
+
+// Elements per collecting thread, held in registers while T0 is derived.
+constexpr int kTkVecs = 2;   // 8-element vectors per thread per round
+
+__global__ __launch_bounds__(kTkThreads) void topk_collect_kernel(const uint16_t* logits, int64_t stride, int V, int C,
+                                                                  TkWork* work) {
+  __shared__ uint64_t buf[kTkCap];     // this workgroup's candidates
+  __shared__ uint16_t smax[kTkSlices];
+  __shared__ TkHist h;
+  __shared__ int n_loc, base_sh;
+  const int m = blockIdx.y;
+  const uint16_t* row = logits + (int64_t)m * stride;
+  TkWork& w = work[m];
+  const int S = tk_slice(V), ns = (V + S - 1) / S;
+  // this workgroup's share of the row, in whole 8-element vectors
+  const int nvec = (V + 7) / 8;
+  const int per = (nvec + gridDim.x - 1) / gridDim.x;
+  const int v0 = blockIdx.x * per, v1 = min(nvec, v0 + per);
+  // first round of row vectors: loads issued before the slice maxima
+  uint4 d[kTkVecs];
+#pragma unroll
+  for (int r = 0; r < kTkVecs; ++r) {
+    const int vi = v0 + r * blockDim.x + threadIdx.x;
+    d[r] = vi < v1 && vi * 8 + 8 <= V ? *reinterpret_cast<const uint4*>(row + (int64_t)vi * 8) : make_uint4(0, 0, 0, 0);
+  }
+  if (threadIdx.x == 0) n_loc = 0;
+  for (int i = threadIdx.x; i < ns; i += blockDim.x) smax[i] = w.smax[i];
+  __syncthreads();
+  int above;
+  const uint32_t T0 = tk_kth(h, [&](int i) { return (uint32_t)smax[i]; }, ns, C, &above);
+  for (int base = v0; base < v1; base += kTkVecs * blockDim.x) {
+    if (base != v0) {
+#pragma unroll
+      for (int r = 0; r < kTkVecs; ++r) {
+        const int vi = base + r * blockDim.x + threadIdx.x;
+        d[r] = vi < v1 && vi * 8 + 8 <= V ? *reinterpret_cast<const uint4*>(row + (int64_t)vi * 8)
+                                          : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kTkVecs; ++r) {
+      const int vi = base + r * blockDim.x + threadIdx.x;
+      const bool full = vi < v1 && vi * 8 + 8 <= V;
+      const uint32_t dd[4] = {d[r].x, d[r].y, d[r].z, d[r].w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = vi * 8 + q;
+        const bool ok = vi < v1 && i < V;
+        uint32_t key = 0;
+        if (ok) key = full ? tk_key(q & 1 ? dd[q >> 1] >> 16 : dd[q >> 1] & 0xffffu) : tk_key(row[i]);
+        tk_append(buf, &n_loc, kTkCap, ok && key >= T0, tk_comp(key, i));
+      }
+    }
+  }
+  __syncthreads();
+  const int nl = n_loc;
+  if (threadIdx.x == 0) base_sh = nl ? atomicAdd(&w.count, nl) : 0;   // nl > kTkCap pushes count past it
+  __syncthreads();
+  for (int i = threadIdx.x; i < nl && i < kTkCap; i += blockDim.x)
+    if (base_sh + i < kTkCap) w.cand[base_sh + i] = buf[i];
+}
+
 __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const uint16_t* logits, int64_t stride, int V, int C,
-                                                                 TkWork* work, int64_t* idx_out) {
+                                                                 const TkWork* work, int64_t* idx_out) {
   __shared__ uint64_t cand[kTkCap];
   __shared__ TkHist h;
   __shared__ int n_sh;
   const int m = blockIdx.x;
   const uint16_t* row = logits + (int64_t)m * stride;
   int64_t* out = idx_out + (int64_t)m * C;
-  const int S = tk_slice(V), ns = (V + S - 1) / S;
-  int n;
   if (V <= kTkCap) {
     for (int i = threadIdx.x; i < V; i += blockDim.x) cand[i] = tk_comp(tk_key(row[i]), i);
-    n = V;
-  } else if (ns >= C && work[m].count <= kTkCap) {
-    n = work[m].count;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) cand[i] = work[m].cand[i];
-  } else {
-    // exact threshold T, the elements above it, and ties at T in index order
-    if (threadIdx.x == 0) n_sh = 0;
     __syncthreads();
-    int above;
-    const uint32_t T = tk_kth(h, [&](int i) { return tk_key(row[i]); }, V, C, &above);
-    for (int i0 = 0; i0 < V; i0 += blockDim.x) {
-      const int i = i0 + threadIdx.x;
-      const uint32_t key = i < V ? tk_key(row[i]) : 0u;
-      tk_append(cand, &n_sh, kTkCap, i < V && key > T, tk_comp(key, i));
-    }
-    __syncthreads();
-    const int need = C - above;
-    if (threadIdx.x < 64) {
-      int taken = 0;
-      for (int i0 = 0; i0 < V && taken < need; i0 += 64) {
-        const int i = i0 + threadIdx.x;
-        const bool eq = i < V && tk_key(row[i]) == T;
-        const uint64_t mask = __ballot(eq);
-        const int pos = taken + __popcll(mask & ((1ull << threadIdx.x) - 1ull));
-        if (eq && pos < need) cand[above + pos] = tk_comp(T, i);
-        taken += __popcll(mask);
-      }
-    }
-    n = C;
+    tk_finish(cand, V, C, out);
+    return;
   }
-  int n2 = 1;
-  while (n2 < n) n2 <<= 1;
-  __syncthreads();
-  for (int i = n + threadIdx.x; i < n2; i += blockDim.x) cand[i] = 0;
-  __syncthreads();
-  tk_sort(cand, n2);
-  for (int i = threadIdx.x; i < C; i += blockDim.x) out[i] = (int64_t)(0xffffffffu - (uint32_t)(cand[i] & 0xffffffffu));
+  const int S = tk_slice(V), ns = (V + S - 1) / S;
+  const int n = ns >= C ? work[m].count : kTkCap + 1;
+  if (n <= kTkCap) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) cand[i] = work[m].cand[i];
+    __syncthreads();
+    tk_finish(cand, n, C, out);
+  } else {
+    tk_exact(row, V, C, cand, h, &n_sh);
+    tk_finish(cand, C, C, out);
+  }
 }
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -303,7 +421,7 @@ int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int6
   if (V > kTkCap) {
     const int S = tk_slice(V), ns = (V + S - 1) / S;
     hipLaunchKernelGGL(topk_slicemax_kernel, dim3((ns + 255) / 256, M), dim3(256), 0, st, lg, stride, V, w);
-    if (ns >= C) hipLaunchKernelGGL(topk_collect_kernel, dim3(kTkB, M), dim3(256), 0, st, lg, stride, V, C, w);
+    if (ns >= C) hipLaunchKernelGGL(topk_collect_kernel, dim3(kTkB, M), dim3(kTkThreads), 0, st, lg, stride, V, C, w);
   }
   hipLaunchKernelGGL(topk_select_kernel, dim3(M), dim3(kTkThreads), 0, st, lg, stride, V, C, w, idx_out);
   return check_launch("topk_rows");

@@ -223,10 +223,24 @@ def topk_rows(logits, C):
         logits = padded
     idx = torch.empty((m, C), dtype=torch.int64, device=logits.device)
     nbytes = _L.lib().fp4x_topk_workspace_size(m)
-    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=logits.device)
+    ws = _topk_workspace(logits.device, nbytes)
     _L.check(_L.lib().fp4x_topk_rows(_ptr(logits), logits.stride(0), m, v, C, _ptr(idx), _ptr(ws), nbytes,
                                      _L.stream_of(logits)), "topk_rows")
     return idx
+
+
+_TOPK_WS = {}
+
+
+def _topk_workspace(device, nbytes):
+    """Top-k workspace per device, grown on demand and reused (calls on one
+    device must be stream-ordered)."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _TOPK_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=device)
+        _TOPK_WS[key] = ws
+    return ws
 
 
 def refine_mx8_(out, x, idx, w8, s_u8, BC=16, BK=256, nw=4):

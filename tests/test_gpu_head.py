@@ -58,6 +58,24 @@ def test_topk_all_equal_exact_path(gpu, F):
     assert got[0].tolist() == list(range(C)) and got[1, 0] == 123456
 
 
+def test_topk_rearms_across_calls_and_paths(gpu, F):
+    """The arrival counters in the shared workspace re-arm after every call:
+    alternating candidate-path and exact-path rows (and row counts) on one
+    workspace keeps every result exact."""
+    rng = np.random.default_rng(77)
+    V, C = 248320, 512
+    normal = fm.bf16_bits(fm.round_bf16(rng.standard_normal((3, V)).astype(np.float32)))
+    ties = np.full((2, V), fm.bf16_bits(np.array([0.75], np.float32))[0], np.uint16)
+    want_n = oh.topk_total_order(normal, C)
+    want_t = oh.topk_total_order(ties, C)
+    tn = dev(normal.view(np.int16)).view(torch.bfloat16)
+    tt = dev(ties.view(np.int16)).view(torch.bfloat16)
+    for _ in range(3):
+        assert np.array_equal(F.topk_rows(tn, C).cpu().numpy(), want_n)
+        assert np.array_equal(F.topk_rows(tt, C).cpu().numpy(), want_t)
+        assert np.array_equal(F.topk_rows(tn[1:2], C).cpu().numpy(), want_n[1:2])
+
+
 # ------------------------------------------------------------------ refine
 def test_refine_mx8_exact(gpu, F):
     rng = np.random.default_rng(21)
