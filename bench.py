@@ -38,7 +38,21 @@ def parse():
     ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (--steps times): the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     return ap.parse_args()
+
+
+def calibrate_copy(mib, steps):
+    import torch
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": steps}), flush=True)
 
 
 # ------------------------------------------------------------------ timing
@@ -224,9 +238,12 @@ def cpu_baseline(seconds):
 # ------------------------------------------------------------------ main
 def main():
     args = parse()
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy, args.steps)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU; the sharded layouts are documented in DESIGN.md "
-              "and no multi-GPU figure is produced", file=sys.stderr)
+        print("bench.py: only --gpus 1 is supported: these kernels are measured on one GPU and no "
+              "multi-GPU figure is produced", file=sys.stderr)
         sys.exit(2)
     import torch
     import fp4x_kernels as F

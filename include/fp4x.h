@@ -60,7 +60,9 @@ enum {
 const char* fp4x_last_error(void);
 int fp4x_abi_version(void);
 
-/* Lane layout of a K slice: lanes per row and 16-byte chunks per lane. */
+/* Lane layout of the rescore kernel (fp4x_refine_mx8) for a row of k_slice
+ * weights: lanes per row and 16-byte chunks per lane.  (The GEMV entry
+ * points choose their MFMA tiling internally.) */
 int fp4x_layout(int fmt, int k_slice, int* lpr, int* cpl);
 
 /* Scratch needed by a split-K call: fp32 slots and int32 tickets. */
@@ -158,9 +160,10 @@ int fp4x_dequant_bf16(int fmt, const void* w0, const void* w1, const void* s, in
 /* fp32 MXFP8 dequant, out [N, K].  [mx8_dequant, x/fp4x_kernels.py:261-267] */
 int fp4x_mx8_dequant(const void* w, const void* s, int N, int K, float* out, void* stream);
 
-/* out[i] = a[i].lo*b[i].lo + a[i].hi*b[i].hi + c[i] with v_dot2_f32_bf16, the
- * accumulation step of every GEMV here.  No counterpart in the reference:
- * exposed so tests can pin the step's rounding against the oracle's model. */
+/* out[i] = a[i].lo*b[i].lo + a[i].hi*b[i].hi + c[i] with v_dot2_f32_bf16.
+ * No counterpart in the reference: exposed so tests can measure the
+ * instruction's rounding (it is not IEEE; the GEMVs accumulate with MFMA and
+ * the rescore with IEEE fp32 fma instead). */
 int fp4x_dot2_bf16(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n, void* stream);
 
 #ifdef __cplusplus
