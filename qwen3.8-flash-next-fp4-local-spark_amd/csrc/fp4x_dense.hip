@@ -12,6 +12,9 @@ extern template int launch_gemv_mfma<FmtBF16, EpiStore>(const GemvLaunch&, int, 
 extern template int launch_gemv_mfma<FmtMX8, EpiStore>(const GemvLaunch&, int, hipStream_t);
 extern template int launch_gemv_mfma<FmtW8<false>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 extern template int launch_gemv_mfma<FmtW8<true>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+template <bool F16S> bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st);
+extern template bool launch_w8_stream<false>(GemvLaunch, int, hipStream_t);
+extern template bool launch_w8_stream<true>(GemvLaunch, int, hipStream_t);
 extern template int launch_gemv_mfma<FmtW6, EpiStore>(const GemvLaunch&, int, hipStream_t);
 extern template int launch_gemv_mfma<FmtNV4, EpiStore>(const GemvLaunch&, int, hipStream_t);
 extern template int launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(const GemvLaunch&, int, hipStream_t);
@@ -190,7 +193,12 @@ int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, co
   p.w0_bstride = q_lstride;
   p.s_bstride = s_lstride * (s_dtype == FP4X_DT_F16 ? 2 : 4);
   p.out_bstride = out_lstride;
-  if (fmt == FP4X_FMT_W8_F16) return launch_gemv_mfma<FmtW8<true>, EpiStore>(p, layers, (hipStream_t)stream);
+  // long runs of tiles (layer-batched gates) stream through LDS; other shapes use the MFMA core
+  if (fmt == FP4X_FMT_W8_F16) {
+    if (launch_w8_stream<true>(p, layers, (hipStream_t)stream)) return check_launch("w8_stream");
+    return launch_gemv_mfma<FmtW8<true>, EpiStore>(p, layers, (hipStream_t)stream);
+  }
+  if (launch_w8_stream<false>(p, layers, (hipStream_t)stream)) return check_launch("w8_stream");
   return launch_gemv_mfma<FmtW8<false>, EpiStore>(p, layers, (hipStream_t)stream);
 }
 

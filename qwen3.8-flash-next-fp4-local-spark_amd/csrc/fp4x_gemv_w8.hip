@@ -1,8 +1,11 @@
 // Explicit GEMV instantiations (one translation unit per weight format, so
 // the library compiles in parallel).
 #include "fp4x_mfma.h"
+#include "fp4x_stream.h"
 
 namespace fp4x {
 template int launch_gemv_mfma<FmtW8<false>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 template int launch_gemv_mfma<FmtW8<true>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+template bool launch_w8_stream<false>(GemvLaunch, int, hipStream_t);
+template bool launch_w8_stream<true>(GemvLaunch, int, hipStream_t);
 }  // namespace fp4x

@@ -20,6 +20,7 @@ struct GemvLaunch {
   int M, N, ksplit, lpr, cpl;  // cpl = chunks per lane per K slice
   int J, nb;             // MFMA core: chunks per lane per tile, register batches per tile
   int batch, per_wg;     // MFMA core: batch entries, (entry, tile) items per workgroup
+  int xbufs;             // streaming W8 kernel: activation buffers staged in LDS
   float* part;           // split-K slots [batch][ksplit][MT][N]
   int* tickets;          // split-K tickets [batch][tiles], zero between calls
   // mixer-down epilogue

@@ -1,0 +1,285 @@
+// Streaming W8 g64 GEMV for long runs of 16-row tiles (the layer-batched
+// router gates: many independent [N, K] int8 matrices, one launch).
+//
+// y[m, n] = sum_k x[m, k] * bf16(q[n, k] * s[n, k / 64]), fp32 accumulation,
+// the semantics of the plugin's _w8 kernel (x/fp4x_kernels.py:116-135).
+//
+// Design (one workgroup per CU, every tile of the launch in one pass):
+//   * A workgroup runs T tile slots x KW waves.  The KW waves of a slot split
+//     the K range of their 16-row tile into KW contiguous parts; a part is a
+//     sequence of "units" of 128 bytes of each of the 16 rows.
+//   * Each wave streams its units through a private ring of D unit buffers in
+//     LDS, filled by direct global->LDS loads (global_load_lds_dwordx4 /
+//     _dword, which need no registers): per unit two 16-byte loads per lane
+//     (8 rows x one full 128-byte line each) and one 4-byte load per lane for
+//     the unit's group scales.  The wave waits on its own load counter for the
+//     oldest unit, computes it, and refills that buffer with the unit D ahead,
+//     so about D units per wave are always in flight while it computes.
+//   * All LDS accesses after the first direct load are inline assembly: the
+//     compiler cannot tell the ring from other LDS data and would otherwise
+//     wait for every outstanding direct load before each LDS access.  Each
+//     asm read block ends with its own LDS wait, so no use of a loaded
+//     register can be scheduled before the data arrives.  vmcnt waits count
+//     at most the loads issued after the awaited unit, so stores or other
+//     memory operations in between only make a wait stricter.
+//   * Dequant: v_cvt_f32_i32 with a sign-extended byte select (SDWA), the fp32
+//     product q * s (the reference's rounding), packed to bf16 with RNE; MFMA
+//     v_mfma_f32_16x16x32_bf16 accumulates one tile part per wave.
+//   * The KW parts of a tile are summed in part order through LDS, then stored.
+//   * The activations of the one or two batch entries a workgroup touches
+//     are staged once into LDS by direct loads of 1 KB rows pieces.
+#pragma once
+#include <cstdlib>
+#include "fp4x_mfma.h"
+
+namespace fp4x {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_ptr_t)p; }
+
+// Direct global -> LDS loads: lane l writes its bytes at l * size from the
+// (wave-uniform) LDS address.
+__device__ __forceinline__ void dma_b128(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)l, 16, 0, 0);
+}
+__device__ __forceinline__ void dma_b32(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)l, 4, 0, 0);
+}
+
+// Wait until at most N vector memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Workgroup barrier without a memory fence (LDS data is waited for by the
+// asm blocks that produce it).
+__device__ __forceinline__ void wg_barrier_raw() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ void lds_put_f32x4(uint32_t a, f32x4_t v) {
+  asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(a), "v"(v) : "memory");
+}
+__device__ __forceinline__ f32x4_t lds_get_f32x4(uint32_t a) {
+  f32x4_t v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a) : "memory");
+  return v;
+}
+
+// One unit's operands for lane (n, g): weight chunks g and g + 4 of row n (at
+// wa, wb), the two scale dwords (sa, sa + 64), and the activations of both
+// chunks (xa: 32 bytes of chunk g; chunk g + 4 is 128 bytes further).
+__device__ __forceinline__ void stream_read_unit(uint32_t wa, uint32_t wb, uint32_t sa, uint32_t xa, uint4& q0,
+                                                 uint4& q1, uint32_t& s0, uint32_t& s1, uint4& x0a, uint4& x0b,
+                                                 uint4& x1a, uint4& x1b) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %9\n\t"
+      "ds_read_b32 %2, %10\n\t"
+      "ds_read_b32 %3, %10 offset:64\n\t"
+      "ds_read_b128 %4, %11\n\t"
+      "ds_read_b128 %5, %11 offset:16\n\t"
+      "ds_read_b128 %6, %11 offset:128\n\t"
+      "ds_read_b128 %7, %11 offset:144\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(q0), "=&v"(q1), "=&v"(s0), "=&v"(s1), "=&v"(x0a), "=&v"(x0b), "=&v"(x1a), "=&v"(x1b)
+      : "v"(wa), "v"(wb), "v"(sa), "v"(xa)
+      : "memory");
+}
+
+// bf16(q * s) for 16 int8 weights; q * s is the fp32 product, then RNE.
+__device__ __forceinline__ uint32_t w8_pair_bf16(uint32_t d, int sh, float s) {
+  const float a = (float)(int8_t)(d >> sh), b = (float)(int8_t)(d >> (sh + 8));
+  return pack_bf16x2(a * s, b * s);
+}
+__device__ __forceinline__ void w8_chunk_bf16(uint4 q, float s, uint32_t (&w)[8]) {
+  w[0] = w8_pair_bf16(q.x, 0, s); w[1] = w8_pair_bf16(q.x, 16, s);
+  w[2] = w8_pair_bf16(q.y, 0, s); w[3] = w8_pair_bf16(q.y, 16, s);
+  w[4] = w8_pair_bf16(q.z, 0, s); w[5] = w8_pair_bf16(q.z, 16, s);
+  w[6] = w8_pair_bf16(q.w, 0, s); w[7] = w8_pair_bf16(q.w, 16, s);
+}
+
+constexpr int kStreamUnit = 2048 + 256;     // LDS bytes of one unit: 16 rows x 128 B + scale dwords
+
+// Geometry shared by host and device.
+struct StreamGeom {
+  int T, KW, D;
+  __host__ __device__ static int xrow_bytes(int K) { return mfma_xstride(K) * 2; }
+  __host__ __device__ static int xbuf_bytes(int M, int K) { return (M * xrow_bytes(K) + 15) & ~15; }
+};
+
+template <bool F16S, int T, int KW, int D>
+__global__ __launch_bounds__(64 * T * KW) void w8_stream_kernel(GemvLaunch p) {
+  constexpr int NW = T * KW;
+  extern __shared__ __align__(16) uint16_t lds[];
+  char* base = reinterpret_cast<char*>(lds);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slot = wave / KW, part = wave - slot * KW;
+  const int n = lane & 15, g = lane >> 4;
+  const int tiles = (p.N + 15) / 16, items = p.batch * tiles;
+  const int K = p.pa.K, JW = K / 128 / KW;           // units per wave per tile
+  const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
+  const int wg0 = blockIdx.x * p.per_wg;
+  const int wgend = wg0 + p.per_wg < items ? wg0 + p.per_wg : items;
+  if (wg0 >= wgend) return;
+  const int R = (wgend - wg0 + T - 1) / T;           // rounds of T tiles
+  const int b0 = wg0 / tiles, nbuf = (wgend - 1) / tiles - b0 + 1;
+  char* part_base = base + p.xbufs * xbuf;
+  char* ring = part_base + T * (KW - 1) * 1024 + wave * D * kStreamUnit;
+
+  // Activations of the workgroup's batch entries: 1 KB pieces of each row.
+  const int bpr = K * 2 / 1024, nblk = nbuf * p.M * bpr;
+  for (int i = wave; i < nblk; i += NW) {
+    const int bi = i / (p.M * bpr), r = i - bi * (p.M * bpr), m = r / bpr, blk = r - m * bpr;
+    const uint16_t* xg = p.x + (int64_t)(b0 + bi) * p.x_bstride + (int64_t)m * p.x_stride + blk * 512 + lane * 8;
+    dma_b128(xg, base + bi * xbuf + m * xrow + blk * 1024);
+  }
+
+  // DMA lane l of weight load h reads row 8h + (l >> 3) of the tile, chunk
+  // (l & 7) ^ (row >> 1) of the unit: 8 lanes cover one 128-byte line, and the
+  // XOR makes the 16 lanes of a quarter-wave read 16 different LDS bank
+  // groups when the operands are read back.
+  const int dr = lane >> 3, dc = lane & 7;
+  const int cA = dc ^ (dr >> 1), cB = dc ^ (4 + (dr >> 1));
+  // Scale lane: fp32, row n, group 2j + ((l >> 4) & 1); fp16, row n, the
+  // dword holding groups 2j and 2j + 1.
+  const int sg = F16S ? 0 : (lane >> 4) & 1;
+  const int U = R * JW;
+  int ir = 0, ij = 0, is = 0, issued = 0;
+  const uint8_t* iw = nullptr;
+  const uint8_t* isb = nullptr;
+  uint32_t o0 = 0, o1 = 0, os = 0;
+  auto set_tile = [&](int rr) {
+    int it = wg0 + rr * T + slot;
+    if (it >= wgend) it = wgend - 1;                 // idle slot of the last round: reload a valid tile
+    const int b = it / tiles, t = it - b * tiles;
+    const int lim = p.N - 1 - t * 16;                // rows past N read row N - 1
+    iw = p.pa.w0 + b * p.w0_bstride + (int64_t)t * 16 * K + part * JW * 128;
+    isb = p.pa.s + b * p.s_bstride + ((int64_t)t * 16 * (K / 64) + part * JW * 2) * (F16S ? 2 : 4);
+    const int rA = dr < lim ? dr : lim, rB = dr + 8 < lim ? dr + 8 : lim, rS = n < lim ? n : lim;
+    o0 = (uint32_t)(rA * K + cA * 16);
+    o1 = (uint32_t)(rB * K + cB * 16);
+    os = (uint32_t)((rS * (K / 64) + sg) * (F16S ? 2 : 4));
+  };
+  set_tile(0);
+  auto issue_next = [&]() {
+    char* l = ring + is * kStreamUnit;
+    const uint8_t* u0 = iw + ij * 128;
+    dma_b128(u0 + o0, l);
+    dma_b128(u0 + o1, l + 1024);
+    dma_b32(isb + ij * (F16S ? 4 : 8) + os, l + 2048);
+    if (++is == D) is = 0;
+    ++issued;
+    if (++ij == JW) {
+      ij = 0;
+      if (++ir < R) set_tile(ir);
+    }
+  };
+  const int pro = U < D ? U : D;
+  for (int u = 0; u < pro; ++u) issue_next();
+  // the activation loads went out first: wait for them only
+  if (pro == D) wait_vmcnt<3 * D>();
+  else wait_vmcnt<0>();
+  wg_barrier_raw();
+
+  const int xr = n < p.M ? n : 0;                    // rows m >= M: never stored
+  const uint32_t rl = lds_addr(ring);
+  const uint32_t wlA = rl + n * 128 + ((g ^ (n >> 1)) * 16), wlB = rl + n * 128 + (((g + 4) ^ (n >> 1)) * 16);
+  const uint32_t sl = rl + 2048 + n * 4;
+  const uint32_t pl = lds_addr(part_base) + slot * (KW - 1) * 1024 + lane * 16;
+  int cs = 0, u = 0;
+  for (int r = 0; r < R; ++r) {
+    const int it = wg0 + r * T + slot;
+    const int itc = it < wgend ? it : wgend - 1;
+    const int b = itc / tiles, t = itc - b * tiles;
+    const uint32_t xl = lds_addr(base + (b - b0) * xbuf) + xr * xrow + part * JW * 256 + g * 32;
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < JW; ++j, ++u) {
+      if (issued - 1 - u >= D - 1) wait_vmcnt<3 * (D - 1)>();
+      else wait_vmcnt<0>();
+      uint4 q0, q1, x0a, x0b, x1a, x1b;
+      uint32_t s0, s1;
+      const uint32_t so = cs * kStreamUnit;
+      stream_read_unit(wlA + so, wlB + so, sl + so, xl + j * 256, q0, q1, s0, s1, x0a, x0b, x1a, x1b);
+      float sc0, sc1;
+      if constexpr (F16S) {
+        sc0 = f16_to_f32((uint16_t)s0);
+        sc1 = f16_to_f32((uint16_t)(s0 >> 16));
+      } else {
+        sc0 = __uint_as_float(s0);
+        sc1 = __uint_as_float(s1);
+      }
+      uint32_t w[8];
+      w8_chunk_bf16(q0, sc0, w);
+      acc = mfma16(x0a, make_uint4(w[0], w[1], w[2], w[3]), acc);
+      acc = mfma16(x0b, make_uint4(w[4], w[5], w[6], w[7]), acc);
+      w8_chunk_bf16(q1, sc1, w);
+      acc = mfma16(x1a, make_uint4(w[0], w[1], w[2], w[3]), acc);
+      acc = mfma16(x1b, make_uint4(w[4], w[5], w[6], w[7]), acc);
+      if (++cs == D) cs = 0;
+      if (issued < U) issue_next();
+    }
+    if constexpr (KW > 1) {
+      if (part > 0) lds_put_f32x4(pl + (part - 1) * 1024, acc);
+      wg_barrier_raw();
+      if (part == 0) {
+#pragma unroll
+        for (int h = 1; h < KW; ++h) {
+          const f32x4_t o = lds_get_f32x4(pl + (h - 1) * 1024);
+          acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
+        }
+      }
+      wg_barrier_raw();
+    }
+    if (part == 0 && it < wgend) {
+      const int64_t row = (int64_t)t * 16 + n;       // lane (n, g) holds D[m = 4g + i][n]
+      if (row < p.N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (g * 4 + i < p.M) EpiStore::apply(p, b, g * 4 + i, row, acc[i] * p.gs);
+      }
+    }
+  }
+}
+
+// Launch the streaming kernel when the call fits it; returns false (and
+// launches nothing) otherwise, or when the environment sets FP4X_W8_STREAM=0.
+// Conditions: no split-K, K a multiple of 512
+// (whole 1 KB activation pieces and whole units per part), scales and their
+// batch stride 4-byte aligned, enough tiles for a full round on every CU, and
+// the LDS plan within the CU's 160 KB.
+template <bool F16S>
+bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
+  constexpr int T = 6, KW = 2, D = 3;
+  const char* env = getenv("FP4X_W8_STREAM");          // "0": always use the MFMA core (read per call)
+  if (env && env[0] == '0') return false;
+  const int K = p.pa.K, tiles = (p.N + 15) / 16;
+  if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / 128) % KW != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(p.pa.s) & 3) || (batch > 1 && (p.s_bstride & 3))) return false;
+  const int64_t items = (int64_t)batch * tiles;
+  const int cus = device_cus();
+  if (items < (int64_t)cus * T) return false;
+  const int64_t per = (items + (int64_t)cus * T - 1) / ((int64_t)cus * T) * T;
+  // batch entries one workgroup can span: its first and last tile
+  const int64_t span = (per + tiles - 1) / tiles + 1;
+  if (span > 2) return false;
+  const size_t lds = (size_t)span * StreamGeom::xbuf_bytes(p.M, K) + (size_t)T * (KW - 1) * 1024 +
+                     (size_t)T * KW * D * kStreamUnit;
+  if (lds > 160 * 1024) return false;
+  auto kern = w8_stream_kernel<F16S, T, KW, D>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess)
+      return false;
+    attr_set = true;
+  }
+  p.batch = batch;
+  p.per_wg = (int)per;
+  p.xbufs = (int)span;
+  const int gx = (int)((items + per - 1) / per);
+  hipLaunchKernelGGL(kern, dim3(gx), dim3(64 * T * KW), lds, st, p);
+  return true;
+}
+
+}  // namespace fp4x

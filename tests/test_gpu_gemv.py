@@ -191,3 +191,46 @@ def test_w8_fp16_scales_and_layers(gpu, F):
             assert_tol(to_f32(y[i]), ref, what=f"layer {i}")
             single = F.w8_linear(x3[i], q3[i], s3[i], (16, 512, 1, 4), torch.float32)
             assert torch.equal(single, y[i])
+
+
+# ------------------------------------------------------------------ streaming W8 (layer-batched gates)
+@pytest.mark.parametrize("case", [
+    # layers, N, K, M, scale dtype
+    (48, 512, 2560, 3, np.float16),    # the router-gate workload: one round of 6 tiles per CU
+    (48, 512, 2560, 3, np.float32),
+    (48, 512, 2560, 1, np.float32),
+    (40, 512, 2560, 5, np.float16),    # fewer tiles than CUs x 6: falls back to the MFMA core
+    (96, 512, 2560, 3, np.float16),    # two rounds per workgroup: the ring crosses tiles
+    (25, 1000, 2560, 3, np.float32),   # N tail (rows past N) and idle slots in the last round
+    (48, 512, 1024, 2, np.float16),    # K = 1024: 4 units per wave
+])
+def test_w8_stream_layers(gpu, F, case, monkeypatch):
+    Ly, n, k, M, s_dtype = case
+    rng = np.random.default_rng(1000 + Ly + n + k + M)
+    q3n = np.empty((Ly, n, k), np.int8)
+    s3n = np.empty((Ly, n, k // 64), np.float32)
+    for i in range(Ly):
+        q3n[i], s3n[i] = oq.quantize_w8(weights(rng, n, k))
+    s3n = s3n.astype(s_dtype)
+    x3n = np.stack([act(rng, M, k)[0] for _ in range(Ly)])
+    q3, s3, x3 = dev(q3n), dev(s3n), bf16_dev(x3n)
+    y = to_f32(F.w8_linear_layers(x3, q3, s3, torch.float32))
+    monkeypatch.setenv("FP4X_W8_STREAM", "0")
+    y_core = to_f32(F.w8_linear_layers(x3, q3, s3, torch.float32))
+    monkeypatch.delenv("FP4X_W8_STREAM")
+    worst = 0.0
+    for i in range(Ly):
+        w_op = og.operand("w8", q3n[i], s3n[i].astype(np.float32))
+        ref = og.matmul_f32(x3n[i], w_op)
+        assert_tol(y[i], ref, what=f"layer {i}")
+        exact = ordered.exact_sum(x3n[i], w_op)
+        bound = ordered.mfma_bound(x3n[i], w_op)
+        assert np.all(np.abs(y[i] - exact) <= bound), (i, (np.abs(y[i] - exact) / bound).max())
+        assert np.all(np.abs(y_core[i] - exact) <= bound)
+        worst = max(worst, float((np.abs(y[i] - exact) / bound).max()))
+    streamed = not np.array_equal(y.view(np.uint32), y_core.view(np.uint32))
+    print(f"layers={Ly} N={n} K={k} M={M} {np.dtype(s_dtype).name}: streamed={streamed}, "
+          f"max |y - exact| / bound = {worst:.3g}")
+    # the workload shapes above the CUs x 6 tile threshold take the streaming kernel (a different
+    # K decomposition, so its fp32 sums differ from the core's in the last bits)
+    assert streamed == (Ly * ((n + 15) // 16) >= 6 * torch.cuda.get_device_properties(0).multi_processor_count)
