@@ -15,6 +15,7 @@ extern template int launch_gemv_mfma<FmtW8<true>, EpiStore>(const GemvLaunch&, i
 template <bool F16S> bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st);
 extern template bool launch_w8_stream<false>(GemvLaunch, int, hipStream_t);
 extern template bool launch_w8_stream<true>(GemvLaunch, int, hipStream_t);
+bool launch_int2_stream_f16(GemvLaunch p, hipStream_t st);
 extern template int launch_gemv_mfma<FmtW6, EpiStore>(const GemvLaunch&, int, hipStream_t);
 extern template int launch_gemv_mfma<FmtNV4, EpiStore>(const GemvLaunch&, int, hipStream_t);
 extern template int launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(const GemvLaunch&, int, hipStream_t);
@@ -252,7 +253,10 @@ int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void*
   p.rs = rs;
   hipStream_t st = (hipStream_t)stream;
   if (fmt == FP4X_FMT_INT2_F16) {
-    if (G == 16) return launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(p, 1, st);
+    if (G == 16) {
+      if (launch_int2_stream_f16(p, st)) return check_launch("int2_stream");   // large heads
+      return launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(p, 1, st);
+    }
     if (G == 32) return launch_gemv_mfma<FmtInt2<false, 32>, EpiStore>(p, 1, st);
     return launch_gemv_mfma<FmtInt2<false, 0>, EpiStore>(p, 1, st);
   }

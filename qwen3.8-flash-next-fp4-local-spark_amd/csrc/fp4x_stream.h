@@ -283,3 +283,212 @@ bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
 }
 
 }  // namespace fp4x
+
+namespace fp4x {
+
+// ---------------------------------------------------------------------------
+// Streaming INT2 coarse head (2-bit codes, one fp16 scale per 16 K values):
+// logits[m, n] = sum_k x[m, k] * bf16((code - 1.5) * s) (x/fp4x_kernels.py:304-325),
+// optionally times rs[n].
+//
+// One wave per 16-row tile, no cross-wave reduction: the tiles of the matrix
+// are split into contiguous, equal (+-1) ranges over every wave of the grid
+// (one workgroup of W waves per CU), and each wave streams its tiles' units
+// through a private LDS ring of D buffers.  A unit is 128 bytes of codes
+// (512 weights) and the 64 bytes of their scales, for each of the 16 rows:
+// two 16-byte direct loads per lane for the codes (the W8 lane pattern) and
+// one for the scales (lane l: row l >> 2, 16-byte piece (l & 3) ^ ((row >> 2) & 3),
+// so that the 8-byte scale reads of a quarter-wave hit distinct banks).  The
+// activations are staged once per workgroup in the 4x4-transposed k order of
+// FmtInt2::deq16t (one byte permute per weight).
+constexpr int kInt2Unit = 2048 + 1024;
+
+__device__ __forceinline__ void int2_read_unit(uint32_t wa, uint32_t wb, uint32_t sa, uint32_t sb, uint4& q0,
+                                               uint4& q1, uint2& s0, uint2& s1) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %5\n\t"
+      "ds_read_b64 %2, %6\n\t"
+      "ds_read_b64 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(q0), "=&v"(q1), "=&v"(s0), "=&v"(s1)
+      : "v"(wa), "v"(wb), "v"(sa), "v"(sb)
+      : "memory");
+}
+// The activations of one 64-weight chunk: 4 sub-blocks x 2 operand halves.
+__device__ __forceinline__ void int2_read_x(uint32_t xa, uint4 (&x)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %8 offset:16\n\t"
+      "ds_read_b128 %2, %8 offset:32\n\t"
+      "ds_read_b128 %3, %8 offset:48\n\t"
+      "ds_read_b128 %4, %8 offset:64\n\t"
+      "ds_read_b128 %5, %8 offset:80\n\t"
+      "ds_read_b128 %6, %8 offset:96\n\t"
+      "ds_read_b128 %7, %8 offset:112\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]), "=&v"(x[6]), "=&v"(x[7])
+      : "v"(xa)
+      : "memory");
+}
+__device__ __forceinline__ void lds_put_u128(uint32_t a, uint4 v) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t w = {v.x, v.y, v.z, v.w};
+  asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(w) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int W, int D>
+__global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
+  using F = FmtInt2<false, 16>;
+  extern __shared__ __align__(16) uint16_t lds[];
+  char* base = reinterpret_cast<char*>(lds);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int K = p.pa.K, J = K / 512;                 // units per tile
+  const int64_t tiles = (p.N + 15) / 16;
+  const int64_t nw = (int64_t)gridDim.x * W, gw = (int64_t)blockIdx.x * W + wave;
+  const int64_t t0 = gw * tiles / nw, t1 = (gw + 1) * tiles / nw;
+  const int nt = (int)(t1 - t0);                     // >= 2 (host condition), so U >= D
+  const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
+  char* ring = base + xbuf + wave * D * kInt2Unit;
+  const int cb = K / 4, sbr = K / 8;                 // code and scale bytes per row
+
+  // DMA lanes (codes as in the W8 kernel; scales: row l >> 2, piece (l & 3) ^ ((row >> 2) & 3))
+  const int dr = lane >> 3, dc = lane & 7;
+  const int cA = dc ^ (dr >> 1), cB = dc ^ (4 + (dr >> 1));
+  const int sr = lane >> 2, sp = (lane & 3) ^ ((sr >> 2) & 3);
+  const int U = nt * J;
+  int iq = 0, ij = 0, is = 0, issued = 0;
+  const uint8_t* iw = nullptr;
+  const uint8_t* isb = nullptr;
+  uint32_t o0 = 0, o1 = 0, os = 0;
+  auto set_tile = [&](int q) {
+    int64_t t = t0 + q;
+    if (t >= t1) t = t1 - 1 >= 0 ? t1 - 1 : 0;      // beyond the range: reload the last tile (not consumed)
+    const int64_t lim64 = (int64_t)p.N - 1 - t * 16;
+    const int lim = (int)(lim64 < 15 ? lim64 : 15);
+    iw = p.pa.w0 + t * 16 * cb;
+    isb = p.pa.s + t * 16 * sbr;
+    const int rA = dr < lim ? dr : lim, rB = dr + 8 < lim ? dr + 8 : lim, rS = sr < lim ? sr : lim;
+    o0 = (uint32_t)(rA * cb + cA * 16);
+    o1 = (uint32_t)(rB * cb + cB * 16);
+    os = (uint32_t)(rS * sbr + sp * 16);
+  };
+  set_tile(0);
+  auto issue_next = [&]() {
+    char* l = ring + is * kInt2Unit;
+    dma_b128(iw + ij * 128 + o0, l);
+    dma_b128(iw + ij * 128 + o1, l + 1024);
+    dma_b128(isb + ij * 64 + os, l + 2048);
+    if (++is == D) is = 0;
+    ++issued;
+    if (++ij == J) {
+      ij = 0;
+      set_tile(++iq);
+    }
+  };
+  // D units go out first (units past the wave's range reload its last tile
+  // and are never read), then the activations are staged while they fly.
+#pragma unroll
+  for (int u = 0; u < D; ++u) issue_next();
+  {
+    const int per_row = K / 16, total = p.M * per_row;
+    const uint4* xg4 = reinterpret_cast<const uint4*>(p.x);
+    const int64_t xrow4 = p.x_stride / 8;
+    const uint32_t xl0 = lds_addr(base);
+    for (int i = threadIdx.x; i < total; i += 64 * W) {
+      const int m = i / per_row, qb = i - m * per_row;
+      const uint4 a = xg4[m * xrow4 + 2 * qb], b = xg4[m * xrow4 + 2 * qb + 1];   // elements 0-7, 8-15
+      uint4 o, r;
+      o.x = perm_b32(a.z, a.x, 0x05040100u);   // x0, x4
+      o.y = perm_b32(b.z, b.x, 0x05040100u);   // x8, x12
+      o.z = perm_b32(a.z, a.x, 0x07060302u);   // x1, x5
+      o.w = perm_b32(b.z, b.x, 0x07060302u);   // x9, x13
+      r.x = perm_b32(a.w, a.y, 0x05040100u);   // x2, x6
+      r.y = perm_b32(b.w, b.y, 0x05040100u);   // x10, x14
+      r.z = perm_b32(a.w, a.y, 0x07060302u);   // x3, x7
+      r.w = perm_b32(b.w, b.y, 0x07060302u);   // x11, x15
+      const uint32_t la = xl0 + m * xrow + qb * 32;
+      lds_put_u128(la, o);
+      lds_put_u128(la + 16, r);
+    }
+    wait_lgkm0_barrier();
+  }
+  const int xr = n < p.M ? n : 0;
+  const uint32_t rl = lds_addr(ring);
+  const uint32_t wlA = rl + n * 128 + ((g ^ (n >> 1)) * 16), wlB = rl + n * 128 + (((g + 4) ^ (n >> 1)) * 16);
+  const int sx = (n >> 2) & 3;
+  const uint32_t slA = rl + 2048 + n * 64 + (((g >> 1) ^ sx) * 16) + (g & 1) * 8;
+  const uint32_t slB = rl + 2048 + n * 64 + (((2 + (g >> 1)) ^ sx) * 16) + (g & 1) * 8;
+  const uint32_t xl = lds_addr(base) + xr * xrow + g * 128;   // chunk g of unit 0
+  int cs = 0, u = 0;
+  for (int q = 0; q < nt; ++q) {
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < J; ++j, ++u) {
+      if (issued - 1 - u >= D - 1) wait_vmcnt<3 * (D - 1)>();
+      else wait_vmcnt<0>();
+      const uint32_t so = cs * kInt2Unit;
+      typename F::Chunk ch[2];
+      int2_read_unit(wlA + so, wlB + so, slA + so, slB + so, ch[0].q, ch[1].q, ch[0].s, ch[1].s);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint4 x[8];
+        int2_read_x(xl + j * 1024 + h * 512, x);
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+          uint32_t w[8];
+          F::deq16t(ch[h], sub, w);
+          acc = mfma16(x[2 * sub], make_uint4(w[0], w[1], w[2], w[3]), acc);
+          acc = mfma16(x[2 * sub + 1], make_uint4(w[4], w[5], w[6], w[7]), acc);
+        }
+      }
+      if (++cs == D) cs = 0;
+      if (issued < U) issue_next();
+    }
+    const int64_t row = (t0 + q) * 16 + n;           // lane (n, g) holds D[m = 4g + i][n]
+    if (row < p.N) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (g * 4 + i < p.M) EpiStore::apply(p, 0, g * 4 + i, row, acc[i] * p.gs);
+    }
+  }
+  wait_vmcnt<0>();                                   // no load of the prologue outlives the wave
+}
+
+// The INT2 head (fp16 scales, G = 16) through the streaming kernel when the
+// matrix has at least 2 tiles per wave of the grid; false otherwise (or when
+// FP4X_INT2_STREAM=0).  16 waves per CU (ring depth 3) when the staged
+// activations leave room, else 8 waves with the deepest ring that fits.
+template <int W, int D>
+bool launch_int2_stream_wd(GemvLaunch p, size_t lds, hipStream_t st) {
+  auto kern = int2_stream_kernel<W, D>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess)
+      return false;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(device_cus()), dim3(64 * W), lds, st, p);
+  return true;
+}
+
+inline bool launch_int2_stream(GemvLaunch p, hipStream_t st) {
+  const char* env = getenv("FP4X_INT2_STREAM");
+  if (env && env[0] == '0') return false;
+  const int K = p.pa.K;
+  if (p.pa.G != 16 || K % 512 != 0 || p.M > 16 || p.ksplit != 1) return false;
+  if ((reinterpret_cast<uintptr_t>(p.pa.w0) & 15) || (reinterpret_cast<uintptr_t>(p.pa.s) & 15)) return false;
+  const int64_t tiles = (p.N + 15) / 16;
+  const size_t xb = (size_t)StreamGeom::xbuf_bytes(p.M, K);
+  auto fits = [&](int W, int D) { return xb + (size_t)W * D * kInt2Unit <= 160 * 1024 &&
+                                         tiles >= (int64_t)device_cus() * W * 2; };
+  if (fits(16, 3)) return launch_int2_stream_wd<16, 3>(p, xb + (size_t)16 * 3 * kInt2Unit, st);
+  if (fits(8, 6)) return launch_int2_stream_wd<8, 6>(p, xb + (size_t)8 * 6 * kInt2Unit, st);
+  if (fits(8, 4)) return launch_int2_stream_wd<8, 4>(p, xb + (size_t)8 * 4 * kInt2Unit, st);
+  if (fits(8, 3)) return launch_int2_stream_wd<8, 3>(p, xb + (size_t)8 * 3 * kInt2Unit, st);
+  return false;
+}
+
+}  // namespace fp4x

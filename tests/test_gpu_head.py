@@ -184,3 +184,41 @@ def test_fast_head_full_size_exact(gpu, F):
     # the exact full-vocabulary MXFP8 argmax agrees (true argmax inside the top-512)
     full = F.mx8_linear(xt, q, s, (32, 512, 1, 4), torch.float32)
     assert np.array_equal(am, full.argmax(-1).cpu().numpy())
+
+
+# ------------------------------------------------------------------ INT2 streaming kernel
+@pytest.mark.parametrize("M,rs", [(3, False), (16, False), (3, True)])
+def test_int2_stream(gpu, F, M, rs, monkeypatch):
+    """Heads of at least 4 tiles per wave of the grid take the streaming kernel
+    (one wave per tile, LDS ring of direct loads); N tail of 40 rows."""
+    rng = np.random.default_rng(77 + M + rs)
+    K = 2560
+    V = 4 * 8 * 16 * torch.cuda.get_device_properties(0).multi_processor_count + 40
+    w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    P, S = oq.quantize_int2(w, group=16)
+    del w
+    R = (rng.random(V) + 0.5).astype(np.float32) if rs else None
+    x, xb = act(rng, M, K)
+    args = (bf16_dev(x), dev(P), dev(S), V)
+    kw = {"RS": dev(R)} if rs else {}
+    y = F.int2_logits(*args, **kw).cpu().numpy()
+    monkeypatch.setenv("FP4X_INT2_STREAM", "0")
+    y_core = F.int2_logits(*args, **kw).cpu().numpy()
+    monkeypatch.delenv("FP4X_INT2_STREAM")
+    assert not np.array_equal(y.view(np.uint32), y_core.view(np.uint32)), "streaming kernel not taken"
+    worst = 0.0
+    for r0 in range(0, V, 16384):
+        r1 = min(V, r0 + 16384)
+        wop = og.operand("int2", P[r0:r1], S[r0:r1])
+        exact = ordered.exact_sum(x, wop)
+        bound = ordered.mfma_bound(x, wop)
+        if rs:
+            exact = exact * R[r0:r1]
+            bound = bound * R[r0:r1] * (1 + 2.0 ** -23) + np.abs(exact) * 2.0 ** -23
+        for got in (y[:, r0:r1], y_core[:, r0:r1]):
+            assert np.all(np.abs(got - exact) <= bound), float((np.abs(got - exact) / bound).max())
+        worst = max(worst, float((np.abs(y[:, r0:r1] - exact) / bound).max()))
+    print(f"int2 stream V={V} M={M} rs={rs}: max |y - exact| / bound = {worst:.3g}")
+    # bf16 logits round the same sums
+    yb = F.int2_logits(*args, out_dtype=torch.bfloat16, **kw)
+    assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
