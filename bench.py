@@ -91,15 +91,18 @@ def entry(us, nbytes):
 
 
 # ------------------------------------------------------------------ workloads
-def gate_weights(F, torch, dev, layers=48, n=512, k=2560, seed=0):
-    """Symmetric int8 gates with one fp16 scale per 64 K values: the scale is
-    amax / 127 rounded to fp16, and q = round(w / s) against that scale."""
-    g = torch.Generator(device=dev).manual_seed(seed)
-    w = torch.randn((layers, n, k), generator=g, device=dev) * 0.02
-    grp = w.reshape(layers, n, k // 64, 64)
+def w8_f16(torch, w):
+    """Symmetric int8 with one fp16 scale per 64 K values (last dim): the
+    scale is amax / 127 rounded to fp16, and q = round(w / s) against it."""
+    grp = w.reshape(*w.shape[:-1], w.shape[-1] // 64, 64)
     s16 = (grp.abs().amax(-1).clamp_min(1e-12) / 127.0).half()
-    q = torch.round(grp / s16.float().unsqueeze(-1)).clamp(-127, 127).to(torch.int8).reshape(layers, n, k)
+    q = torch.round(grp / s16.float().unsqueeze(-1)).clamp(-127, 127).to(torch.int8).reshape(w.shape)
     return q.contiguous(), s16.contiguous()
+
+
+def gate_weights(F, torch, dev, layers=48, n=512, k=2560, seed=0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return w8_f16(torch, torch.randn((layers, n, k), generator=g, device=dev) * 0.02)
 
 
 def gate_bytes(layers, M, n, k, s_bytes=2, out_bytes=4):
@@ -150,13 +153,13 @@ def bench_hc(F, torch, dev, out, layers=97):
     fx = F.HCFused(dev, n_down=ND, max_ksplit=KS)
     mix = []
     for _ in range(layers):
-        qd, sd = F.quantize_w8(torch.randn((ND, HC * H), generator=g, device=dev) * 0.02)
-        qu, su = F.quantize_w8(torch.randn((HC * H, LR), generator=g, device=dev) * 0.02)
+        qd, sd = w8_f16(torch, torch.randn((ND, HC * H), generator=g, device=dev) * 0.02)
+        qu, su = w8_f16(torch, torch.randn((HC * H, LR), generator=g, device=dev) * 0.02)
         qi, si = F.HCFused.interleave_up(qu, su, HC, 8)
         mix.append((qd, sd, qi, si))
     x = torch.randn((M, HC * H), generator=g, device=dev).to(torch.bfloat16)
-    down_b = ND * HC * H + ND * (HC * H // 64) * 4 + M * HC * H * 2 + M * ND * 2 + M * LR * 2
-    up_b = HC * H * LR + HC * H * (LR // 64) * 4 + M * LR * 2 + M * HC * H * 2 + M * H * 2
+    down_b = ND * HC * H + ND * (HC * H // 64) * 2 + M * HC * H * 2 + M * ND * 2 + M * LR * 2
+    up_b = HC * H * LR + HC * H * (LR // 64) * 2 + M * LR * 2 + M * HC * H * 2 + M * H * 2
     bots = [fx.down(x, qd, sd, LR, HC, (32, 256, KS, 4))[1] for qd, sd, _, _ in mix]
     us_down = graph_time([lambda m=m: fx.down(x, m[0], m[1], LR, HC, (32, 256, KS, 4)) for m in mix], replays=5)
     us_up = graph_time([lambda m=m, b=b: F.HCFused.up(b, m[2], m[3], x, HC, (8, 64, 4)) for m, b in zip(mix, bots)],

@@ -16,6 +16,9 @@ template <bool F16S> bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t 
 extern template bool launch_w8_stream<false>(GemvLaunch, int, hipStream_t);
 extern template bool launch_w8_stream<true>(GemvLaunch, int, hipStream_t);
 bool launch_int2_stream_f16(GemvLaunch p, hipStream_t st);
+template <bool F16S, class Epi> bool launch_w8_ktile(GemvLaunch p, hipStream_t st);
+extern template bool launch_w8_ktile<false, EpiStore>(GemvLaunch, hipStream_t);
+extern template bool launch_w8_ktile<true, EpiStore>(GemvLaunch, hipStream_t);
 extern template int launch_gemv_mfma<FmtW6, EpiStore>(const GemvLaunch&, int, hipStream_t);
 extern template int launch_gemv_mfma<FmtNV4, EpiStore>(const GemvLaunch&, int, hipStream_t);
 extern template int launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(const GemvLaunch&, int, hipStream_t);
@@ -194,13 +197,18 @@ int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, co
   p.w0_bstride = q_lstride;
   p.s_bstride = s_lstride * (s_dtype == FP4X_DT_F16 ? 2 : 4);
   p.out_bstride = out_lstride;
-  // long runs of tiles (layer-batched gates) stream through LDS; other shapes use the MFMA core
+  // long runs of tiles (layer-batched gates) stream through LDS; split-K calls of
+  // few tiles split K over the waves of one workgroup per tile (the mixer's
+  // down projection takes the same path); other shapes use the MFMA core
+  hipStream_t st = (hipStream_t)stream;
   if (fmt == FP4X_FMT_W8_F16) {
-    if (launch_w8_stream<true>(p, layers, (hipStream_t)stream)) return check_launch("w8_stream");
-    return launch_gemv_mfma<FmtW8<true>, EpiStore>(p, layers, (hipStream_t)stream);
+    if (launch_w8_stream<true>(p, layers, st)) return check_launch("w8_stream");
+    if (layers == 1 && launch_w8_ktile<true, EpiStore>(p, st)) return check_launch("w8_ktile");
+    return launch_gemv_mfma<FmtW8<true>, EpiStore>(p, layers, st);
   }
-  if (launch_w8_stream<false>(p, layers, (hipStream_t)stream)) return check_launch("w8_stream");
-  return launch_gemv_mfma<FmtW8<false>, EpiStore>(p, layers, (hipStream_t)stream);
+  if (launch_w8_stream<false>(p, layers, st)) return check_launch("w8_stream");
+  if (layers == 1 && launch_w8_ktile<false, EpiStore>(p, st)) return check_launch("w8_ktile");
+  return launch_gemv_mfma<FmtW8<false>, EpiStore>(p, layers, st);
 }
 
 int fp4x_w8_linear(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* out, int out_dtype,

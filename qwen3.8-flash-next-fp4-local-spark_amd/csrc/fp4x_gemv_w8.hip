@@ -8,4 +8,6 @@ template int launch_gemv_mfma<FmtW8<false>, EpiStore>(const GemvLaunch&, int, hi
 template int launch_gemv_mfma<FmtW8<true>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 template bool launch_w8_stream<false>(GemvLaunch, int, hipStream_t);
 template bool launch_w8_stream<true>(GemvLaunch, int, hipStream_t);
+template bool launch_w8_ktile<false, EpiStore>(GemvLaunch, hipStream_t);
+template bool launch_w8_ktile<true, EpiStore>(GemvLaunch, hipStream_t);
 }  // namespace fp4x

@@ -13,6 +13,7 @@
 // paths share the GEMV core, the K split and every epilogue function, so they
 // agree bit for bit.
 #include "fp4x_mfma.h"
+#include "fp4x_stream.h"
 #include "../../include/fp4x.h"
 
 namespace fp4x {
@@ -181,7 +182,12 @@ int fp4x_hc_down(const void* x, int64_t x_stride, const void* q, const void* s, 
   p.part = part;
   p.tickets = tickets;
   hipStream_t st = (hipStream_t)stream;
-  if (s_dtype == FP4X_DT_F16) return launch_gemv_mfma<FmtW8<true>, EpiHcDown>(p, 1, st);
+  // the split-K decomposition fp4x_w8_linear takes for the same (M, N, K, ksplit)
+  if (s_dtype == FP4X_DT_F16) {
+    if (launch_w8_ktile<true, EpiHcDown>(p, st)) return check_launch("hc_down");
+    return launch_gemv_mfma<FmtW8<true>, EpiHcDown>(p, 1, st);
+  }
+  if (launch_w8_ktile<false, EpiHcDown>(p, st)) return check_launch("hc_down");
   return launch_gemv_mfma<FmtW8<false>, EpiHcDown>(p, 1, st);
 }
 

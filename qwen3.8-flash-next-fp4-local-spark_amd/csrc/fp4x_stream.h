@@ -108,7 +108,7 @@ struct StreamGeom {
   __host__ __device__ static int xbuf_bytes(int M, int K) { return (M * xrow_bytes(K) + 15) & ~15; }
 };
 
-template <bool F16S, int T, int KW, int D>
+template <bool F16S, int T, int KW, int D, class Epi>
 __global__ __launch_bounds__(64 * T * KW) void w8_stream_kernel(GemvLaunch p) {
   constexpr int NW = T * KW;
   extern __shared__ __align__(16) uint16_t lds[];
@@ -236,10 +236,24 @@ __global__ __launch_bounds__(64 * T * KW) void w8_stream_kernel(GemvLaunch p) {
       if (row < p.N) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (g * 4 + i < p.M) EpiStore::apply(p, b, g * 4 + i, row, acc[i] * p.gs);
+          if (g * 4 + i < p.M) Epi::apply(p, b, g * 4 + i, row, acc[i] * p.gs);
       }
     }
   }
+}
+
+template <bool F16S, int T, int KW, int D, class Epi>
+bool launch_w8_stream_cfg(GemvLaunch p, size_t lds, int gx, hipStream_t st) {
+  auto kern = w8_stream_kernel<F16S, T, KW, D, Epi>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess)
+      return false;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(gx), dim3(64 * T * KW), lds, st, p);
+  return true;
 }
 
 // Launch the streaming kernel when the call fits it; returns false (and
@@ -266,20 +280,40 @@ bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
   const size_t lds = (size_t)span * StreamGeom::xbuf_bytes(p.M, K) + (size_t)T * (KW - 1) * 1024 +
                      (size_t)T * KW * D * kStreamUnit;
   if (lds > 160 * 1024) return false;
-  auto kern = w8_stream_kernel<F16S, T, KW, D>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024) != hipSuccess)
-      return false;
-    attr_set = true;
-  }
   p.batch = batch;
   p.per_wg = (int)per;
   p.xbufs = (int)span;
   const int gx = (int)((items + per - 1) / per);
-  hipLaunchKernelGGL(kern, dim3(gx), dim3(64 * T * KW), lds, st, p);
-  return true;
+  return launch_w8_stream_cfg<F16S, T, KW, D, EpiStore>(p, lds, gx, st);
+}
+
+// Split-K W8 GEMVs of few tiles (the mixer's down projection, N = 640,
+// K = 10240): one workgroup per 16-row tile whose KW = 16 waves split K into
+// contiguous parts and sum them in part order through LDS, then run the
+// epilogue: no workspace, tickets or cross-workgroup fences.  The caller's
+// ksplit > 1 selects this decomposition (whatever its value); taken when
+// K / 128 is a multiple of 16 with at least 2 units per wave, the tiles do
+// not exceed two per CU, and the activations fit in LDS beside the rings
+// (M <= 3 at K = 10240).  Returns false otherwise (or with FP4X_W8_STREAM=0),
+// launching nothing.  Every entry point deciding on the same (M, N, K,
+// ksplit) takes the same path, which keeps the fused mixer bit-identical to
+// the unfused GEMV + epilogue kernels.
+template <bool F16S, class Epi>
+bool launch_w8_ktile(GemvLaunch p, hipStream_t st) {
+  constexpr int KW = 16, D = 2;
+  const char* env = getenv("FP4X_W8_STREAM");
+  if (env && env[0] == '0') return false;
+  const int K = p.pa.K, tiles = (p.N + 15) / 16;
+  if (p.ksplit < 2 || K % 512 != 0 || p.M > 16 || (K / 128) % KW != 0 || K / 128 / KW < D) return false;
+  if (reinterpret_cast<uintptr_t>(p.pa.s) & 3) return false;
+  if (tiles > 2 * device_cus()) return false;
+  const size_t lds = (size_t)StreamGeom::xbuf_bytes(p.M, K) + (size_t)(KW - 1) * 1024 + (size_t)KW * D * kStreamUnit;
+  if (lds > 160 * 1024) return false;
+  p.batch = 1;
+  p.per_wg = 1;
+  p.xbufs = 1;
+  p.ksplit = 1;                                      // one slice per workgroup: the parts live in its waves
+  return launch_w8_stream_cfg<F16S, 1, KW, D, Epi>(p, lds, tiles, st);
 }
 
 }  // namespace fp4x
