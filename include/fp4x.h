@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 1
+#define FP4X_ABI_VERSION 2
 
 enum {
   FP4X_OK = 0,
@@ -116,10 +116,20 @@ int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void*
  * [torch.topk(coarse, C) in the fast head, x/fp4patch.py:377] */
 int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int64_t* idx_out, void* workspace,
                    int64_t ws_bytes, void* stream);
-/* Bytes of device workspace fp4x_topk_rows needs for M rows (16-byte
- * aligned, no initial contents required).  Calls that share a workspace must
- * be stream-ordered. */
-int64_t fp4x_topk_workspace_size(int M);
+/* Bytes of device workspace fp4x_topk_rows and fp4x_int2_topk need for M
+ * rows of V elements (16-byte aligned, no initial contents required).  Calls
+ * that share a workspace must be stream-ordered. */
+int64_t fp4x_topk_workspace_size(int M, int V);
+
+/* The fast head's coarse stage in one call: fp4x_int2_logits into bf16
+ * coarse [M, N] (row stride coarse_stride, a multiple of 8), then
+ * fp4x_topk_rows of it into idx_out [M, C], with the top-k's slice maxima
+ * written by the coarse kernel's epilogue where it streams.  Results equal
+ * the two calls made separately.
+ * [int2_logits then torch.topk(coarse, C) in the fast head, x/fp4patch.py:371-377] */
+int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
+                   void* coarse, int64_t coarse_stride, int M, int N, int K, int G, int C, int64_t* idx_out,
+                   void* workspace, int64_t ws_bytes, void* stream);
 
 /* In place: out[m, idx[m, c]] = cast(sum_k float(e4m3(w)*2^(s-127)) * float(x[m, k])).
  * out is [M, V] in out_dtype, x bf16 [M, K] contiguous, idx int64 [M, C].

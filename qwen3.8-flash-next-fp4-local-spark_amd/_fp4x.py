@@ -31,7 +31,8 @@ _SIGS = {
     "fp4x_nv4_linear": ([_P, _I64, _P, _P, _F, _P, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "fp4x_int2_logits": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P], _I),
     "fp4x_topk_rows": ([_P, _I64, _I, _I, _I, _P, _P, _I64, _P], _I),
-    "fp4x_topk_workspace_size": ([_I], _I64),
+    "fp4x_topk_workspace_size": ([_I, _I], _I64),
+    "fp4x_int2_topk": ([_P, _I64, _P, _P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _I64, _P], _I),
     "fp4x_refine_mx8": ([_P, _I, _I64, _P, _P, _I, _I, _P, _P, _I, _I, _P], _I),
     "fp4x_hc_down": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "fp4x_hc_up": ([_P, _I64, _P, _P, _I, _P, _I64, _P, _I, _I, _I, _I, _I, _P], _I),
@@ -41,7 +42,7 @@ _SIGS = {
     "fp4x_mx8_dequant": ([_P, _P, _I, _I, _P, _P], _I),
     "fp4x_dot2_bf16": ([_P, _P, _P, _P, _I, _P], _I),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _LIB = None
 

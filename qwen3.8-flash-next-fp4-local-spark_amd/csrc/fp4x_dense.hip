@@ -16,6 +16,11 @@ template <bool F16S> bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t 
 extern template bool launch_w8_stream<false>(GemvLaunch, int, hipStream_t);
 extern template bool launch_w8_stream<true>(GemvLaunch, int, hipStream_t);
 bool launch_int2_stream_f16(GemvLaunch p, hipStream_t st);
+int topk_check(const void* logits, int64_t stride, int M, int V, int C, void* workspace, int64_t ws_bytes);
+int topk_launch(const uint16_t* lg, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
+                bool have_smax, hipStream_t st);
+int topk_slice_len(int V);
+int64_t topk_smax_stride(int V);
 template <bool F16S, class Epi> bool launch_w8_ktile(GemvLaunch p, hipStream_t st);
 extern template bool launch_w8_ktile<false, EpiStore>(GemvLaunch, hipStream_t);
 extern template bool launch_w8_ktile<true, EpiStore>(GemvLaunch, hipStream_t);
@@ -243,8 +248,16 @@ int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* 
   return launch_gemv_mfma<FmtNV4, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
-int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
-                     void* out, int out_dtype, int M, int N, int K, int G, void* stream) {
+}  // extern "C"
+
+namespace fp4x {
+// INT2 coarse logits [M, N] at out (row stride out_stride); with smax set, the
+// streaming kernel also writes the 16-element slice maxima of the stored
+// logits and the function returns 1 (0 when another kernel ran and smax was
+// not written), or a negative error.
+static int int2_coarse(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
+                       void* out, int out_dtype, int64_t out_stride, int M, int N, int K, int G, uint16_t* smax,
+                       int64_t smax_stride, hipStream_t st) {
   const int fmt = s_fmt == FP4X_DT_E4M3 ? FP4X_FMT_INT2_E4M3 : FP4X_FMT_INT2_F16;
   if (s_fmt != FP4X_DT_E4M3 && s_fmt != FP4X_DT_F16) return fail(FP4X_ERR_ARG, "int2: scale format %lld", s_fmt);
   int rc = validate(fmt, x, x_stride, M, N, K, 1, nullptr, nullptr);
@@ -253,24 +266,62 @@ int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void*
     return fail(FP4X_ERR_ARG, "int2: group size G=%lld must be 16, 32 or a multiple of 64 dividing K=%lld", G, K);
   if (!aligned(P, 16) || !aligned(S, s_fmt == FP4X_DT_E4M3 ? (G == 16 ? 4 : 1) : (G == 16 ? 8 : 2)))
     return fail(FP4X_ERR_ARG, "int2: misaligned planes");
-  if (M == 0 || N == 0) return FP4X_OK;
-  GemvLaunch p = base_launch(fmt, x, x_stride, out, out_dtype, N, M, N, K, 1, nullptr, nullptr);
+  if (M == 0 || N == 0) return 0;
+  GemvLaunch p = base_launch(fmt, x, x_stride, out, out_dtype, out_stride, M, N, K, 1, nullptr, nullptr);
   p.pa.w0 = static_cast<const uint8_t*>(P);
   p.pa.s = static_cast<const uint8_t*>(S);
   p.pa.G = G;
   p.rs = rs;
-  hipStream_t st = (hipStream_t)stream;
+  p.smax = smax;
+  p.smax_stride = smax_stride;
   if (fmt == FP4X_FMT_INT2_F16) {
     if (G == 16) {
-      if (launch_int2_stream_f16(p, st)) return check_launch("int2_stream");   // large heads
-      return launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(p, 1, st);
+      if (launch_int2_stream_f16(p, st)) {                 // large heads
+        rc = check_launch("int2_stream");
+        return rc ? rc : (smax ? 1 : 0);
+      }
+      p.smax = nullptr;
+      rc = launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(p, 1, st);
+    } else {
+      p.smax = nullptr;
+      rc = G == 32 ? launch_gemv_mfma<FmtInt2<false, 32>, EpiStore>(p, 1, st)
+                   : launch_gemv_mfma<FmtInt2<false, 0>, EpiStore>(p, 1, st);
     }
-    if (G == 32) return launch_gemv_mfma<FmtInt2<false, 32>, EpiStore>(p, 1, st);
-    return launch_gemv_mfma<FmtInt2<false, 0>, EpiStore>(p, 1, st);
+    return rc;
   }
+  p.smax = nullptr;
   if (G == 16) return launch_gemv_mfma<FmtInt2<true, 16>, EpiStore>(p, 1, st);
   if (G == 32) return launch_gemv_mfma<FmtInt2<true, 32>, EpiStore>(p, 1, st);
   return launch_gemv_mfma<FmtInt2<true, 0>, EpiStore>(p, 1, st);
+}
+}  // namespace fp4x
+
+extern "C" {
+
+int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
+                     void* out, int out_dtype, int M, int N, int K, int G, void* stream) {
+  const int rc = int2_coarse(x, x_stride, P, S, s_fmt, rs, out, out_dtype, N, M, N, K, G, nullptr, 0,
+                             (hipStream_t)stream);
+  return rc < 0 ? rc : FP4X_OK;
+}
+
+int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
+                   void* coarse, int64_t coarse_stride, int M, int N, int K, int G, int C, int64_t* idx_out,
+                   void* workspace, int64_t ws_bytes, void* stream) {
+  if (coarse_stride < N || coarse_stride % 8 || !aligned(coarse, 16))
+    return fail(FP4X_ERR_ARG, "int2_topk: coarse logits need 16-byte aligned rows with a stride (%lld) that is a "
+                "multiple of 8 and >= N (%lld)", coarse_stride, N);
+  int rc = topk_check(coarse, coarse_stride, M, N, C, workspace, ws_bytes);
+  if (rc) return rc;
+  if (M == 0) return FP4X_OK;
+  hipStream_t st = (hipStream_t)stream;
+  uint16_t* smax = static_cast<uint16_t*>(workspace);
+  // the streaming kernel's per-tile maxima are the top-k's slices when they are 16 elements
+  const bool fuse = topk_slice_len(N) == 16;
+  rc = int2_coarse(x, x_stride, P, S, s_fmt, rs, coarse, FP4X_DT_BF16, coarse_stride, M, N, K, G,
+                   fuse ? smax : nullptr, topk_smax_stride(N), st);
+  if (rc < 0) return rc;
+  return topk_launch(static_cast<const uint16_t*>(coarse), coarse_stride, M, N, C, idx_out, smax, rc == 1, st);
 }
 
 }  // extern "C"

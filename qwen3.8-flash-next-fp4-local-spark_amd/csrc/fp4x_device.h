@@ -46,6 +46,17 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
+// ---------------------------------------------------------------- order keys
+// bf16 bits -> 16-bit key increasing with the value; -0 counts as +0 and
+// every NaN as the largest value.  Key 0 lies below every value (the key of
+// -inf is 0x7f), so it marks "no element".
+__device__ __forceinline__ uint32_t tk_key(uint32_t b) {
+  b &= 0xffffu;
+  if ((b & 0x7fffu) == 0) b = 0;
+  else if ((b & 0x7f80u) == 0x7f80u && (b & 0x7fu)) b = 0x7fc0u;
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+
 // ---------------------------------------------------------------- fp8 / fp4
 // e8m0 shared exponent -> fp32 2^(e-127).  e = 0 gives the fp32 denormal
 // 2^-127, e = 255 gives +inf (the value exp2(255 - 127) rounds to).

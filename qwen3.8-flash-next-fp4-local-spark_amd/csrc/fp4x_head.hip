@@ -48,39 +48,39 @@ __global__ __launch_bounds__(kThreads) void refine_mx8_kernel(RefineArgs p) {
 }
 
 // ------------------------------------------------------------------ top-k
-// Three launches per call, which exchange data only across launch
-// boundaries (no grid-wide waits, no cross-workgroup fences):
-//   A  slice maxima: the row is cut into <= 4096 slices of S elements (S a
-//      multiple of 8); smax[m][i] = largest order key of slice i.  Also zeroes
-//      the row's candidate counter.
-//   B  every workgroup of a row derives T0 = the C-th largest slice maximum
-//      (a lower bound of the C-th largest element: C slices each hold an
-//      element >= T0), gathers its elements with key >= T0 in LDS and
-//      appends them to the row's candidate list with one global atomic.
-//   C  one workgroup per row sorts the candidates (at most 4096) by the
-//      total order and writes the first C indices.  Rows with fewer than C
-//      slices, or more than 4096 candidates (massive ties), take the exact
-//      threshold path in C instead.  Rows of at most 4096 elements skip A and
-//      B: C sorts the whole row.
+// Two launches per call, which exchange data only across the launch boundary
+// (no grid-wide waits, no cross-workgroup fences):
+//   A  slice maxima: smax[m][s] = largest order key of slice s of row m, the
+//      elements [S*s, S*s + S) (S = 16 for rows up to 2^19 elements, else the
+//      next power of two keeping at most 32768 slices).  The streaming INT2
+//      head writes them from its epilogue (fp4x_int2_topk), so A is then free.
+//   B  one workgroup per row: T0 = the C-th largest slice maximum (a lower
+//      bound of the C-th largest element: C slices each hold an element
+//      >= T0); the slices whose maximum reaches T0 (about C of them) are the
+//      only ones read back; their elements with key >= T0 are sorted by the
+//      total order (value desc, index asc) and the first C indices written.
+//      More than 4096 such slices or candidates (massive ties), or fewer than
+//      C slices, take the exact threshold path over the whole row instead;
+//      rows of at most 4096 elements sort the whole row.
 constexpr int kTkThreads = 1024;
-constexpr int kTkCap = 4096;     // candidates per row
-constexpr int kTkSlices = 4096;  // slice maxima per row
-constexpr int kTkB = 16;         // collecting workgroups per row (kTkThreads each)
+constexpr int kTkCap = 4096;      // candidates (and candidate slices) per row
+constexpr int kTkMaxSlices = 32768;
 
-// bf16 bits -> 16-bit key increasing with the value; -0 counts as +0 and
-// every NaN as the largest value.
-__device__ __forceinline__ uint32_t tk_key(uint32_t b) {
-  b &= 0xffffu;
-  if ((b & 0x7fffu) == 0) b = 0;
-  else if ((b & 0x7f80u) == 0x7f80u && (b & 0x7fu)) b = 0x7fc0u;
-  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
-}
 // Composite order key: larger = larger value, then smaller index.
 __device__ __forceinline__ uint64_t tk_comp(uint32_t key, uint32_t i) {
   return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - i);
 }
 
-__host__ __device__ inline int tk_slice(int V) { return 8 * ((V + 8 * kTkSlices - 1) / (8 * kTkSlices)); }
+// Slice length for a row of V elements (a power of two >= 16).
+__host__ __device__ inline int tk_slice(int V) {
+  int S = 16;
+  while ((V + S - 1) / S > kTkMaxSlices) S <<= 1;
+  return S;
+}
+__host__ __device__ inline int64_t tk_smax_stride(int V) {
+  const int ns = (V + tk_slice(V) - 1) / tk_slice(V);
+  return (ns + 7) & ~7;
+}
 
 struct TkHist {
   uint32_t hist[256];
@@ -170,9 +170,10 @@ __device__ uint32_t tk_kth(TkHist& h, Get get, int n, int k, int* n_above) {
   return t;
 }
 
-// Wave-aggregated append of comp (when flag) to list[*count]; positions past
+// Wave-aggregated append of v (when flag) to list[*count]; positions past
 // cap are counted but not written.
-__device__ __forceinline__ void tk_append(uint64_t* list, int* count, int cap, bool flag, uint64_t comp) {
+template <class T>
+__device__ __forceinline__ void tk_append(T* list, int* count, int cap, bool flag, T v) {
   const uint64_t mask = __ballot(flag);
   if (!mask) return;
   const int lane = threadIdx.x & 63;
@@ -182,24 +183,16 @@ __device__ __forceinline__ void tk_append(uint64_t* list, int* count, int cap, b
   base = __shfl(base, leader, 64);
   if (flag) {
     const int pos = base + __popcll(mask & ((1ull << lane) - 1ull));
-    if (pos < cap) list[pos] = comp;
+    if (pos < cap) list[pos] = v;
   }
 }
 
-struct TkWork {              // per row, in the caller's workspace
-  uint64_t cand[kTkCap];
-  uint16_t smax[kTkSlices];
-  int count;                 // candidates appended (beyond kTkCap: exact path)
-  int pad[3];
-};
-
+// A: slice maxima of rows whose slices are S elements (S a multiple of 16).
 __global__ __launch_bounds__(256) void topk_slicemax_kernel(const uint16_t* logits, int64_t stride, int V,
-                                                            TkWork* work) {
+                                                            uint16_t* smax, int64_t sstride) {
   const int m = blockIdx.y;
   const uint16_t* row = logits + (int64_t)m * stride;
-  TkWork& w = work[m];
   const int S = tk_slice(V), ns = (V + S - 1) / S;
-  if (blockIdx.x == 0 && threadIdx.x == 0) w.count = 0;
   const int sl = blockIdx.x * blockDim.x + threadIdx.x;
   if (sl >= ns) return;
   uint32_t mx = 0;
@@ -214,7 +207,7 @@ __global__ __launch_bounds__(256) void topk_slicemax_kernel(const uint16_t* logi
       for (int i = e; i < V; ++i) mx = max(mx, tk_key(row[i]));
     }
   }
-  w.smax[sl] = (uint16_t)mx;
+  smax[(int64_t)m * sstride + sl] = (uint16_t)mx;
 }
 
 // Descending bitonic sort of a[0, n2), n2 a power of two.
@@ -243,7 +236,7 @@ __device__ void tk_exact(const uint16_t* row, int V, int C, uint64_t* cand, TkHi
   for (int i0 = 0; i0 < V; i0 += blockDim.x) {
     const int i = i0 + threadIdx.x;
     const uint32_t key = i < V ? tk_key(row[i]) : 0u;
-    tk_append(cand, n_sh, kTkCap, i < V && key > T, tk_comp(key, i));
+    tk_append<uint64_t>(cand, n_sh, kTkCap, i < V && key > T, tk_comp(key, i));
   }
   __syncthreads();
   const int need = C - above;
@@ -306,72 +299,206 @@ __device__ void tk_finish(uint64_t* cand, int n, int C, int64_t* out) {
   for (int i = threadIdx.x; i < C; i += blockDim.x) out[i] = (int64_t)(0xffffffffu - (uint32_t)(cand[i] & 0xffffffffu));
 }
 
-// Elements per collecting thread, held in registers while T0 is derived.
-constexpr int kTkVecs = 2;   // 8-element vectors per thread per round
+// ---- B: one workgroup of 16 waves per row, no cross-wave atomics ----------
+constexpr int kRsThreads = 1024;
+constexpr int kRsWaves = kRsThreads / 64;
+constexpr int kRsVpt = kTkMaxSlices / 8 / kRsThreads;   // 8-slice vectors per thread (registers)
+constexpr int kRsIpt = 2;                                // candidate 8-element items per thread per round
+constexpr int kRsSortThreads = 256;                      // the sort runs on the first 4 waves
 
-__global__ __launch_bounds__(kTkThreads) void topk_collect_kernel(const uint16_t* logits, int64_t stride, int V, int C,
-                                                                  TkWork* work) {
-  __shared__ uint64_t buf[kTkCap];     // this workgroup's candidates
-  __shared__ uint16_t smax[kTkSlices];
-  __shared__ TkHist h;
-  __shared__ int n_loc, base_sh;
-  const int m = blockIdx.y;
-  const uint16_t* row = logits + (int64_t)m * stride;
-  TkWork& w = work[m];
-  const int S = tk_slice(V), ns = (V + S - 1) / S;
-  // this workgroup's share of the row, in whole 8-element vectors
-  const int nvec = (V + 7) / 8;
-  const int per = (nvec + gridDim.x - 1) / gridDim.x;
-  const int v0 = blockIdx.x * per, v1 = min(nvec, v0 + per);
-  // first round of row vectors: loads issued before the slice maxima
-  uint4 d[kTkVecs];
-#pragma unroll
-  for (int r = 0; r < kTkVecs; ++r) {
-    const int vi = v0 + r * blockDim.x + threadIdx.x;
-    d[r] = vi < v1 && vi * 8 + 8 <= V ? *reinterpret_cast<const uint4*>(row + (int64_t)vi * 8) : make_uint4(0, 0, 0, 0);
-  }
-  if (threadIdx.x == 0) n_loc = 0;
-  for (int i = threadIdx.x; i < ns; i += blockDim.x) smax[i] = w.smax[i];
-  __syncthreads();
-  int above;
-  const uint32_t T0 = tk_kth(h, [&](int i) { return (uint32_t)smax[i]; }, ns, C, &above);
-  for (int base = v0; base < v1; base += kTkVecs * blockDim.x) {
-    if (base != v0) {
-#pragma unroll
-      for (int r = 0; r < kTkVecs; ++r) {
-        const int vi = base + r * blockDim.x + threadIdx.x;
-        d[r] = vi < v1 && vi * 8 + 8 <= V ? *reinterpret_cast<const uint4*>(row + (int64_t)vi * 8)
-                                          : make_uint4(0, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < kTkVecs; ++r) {
-      const int vi = base + r * blockDim.x + threadIdx.x;
-      const bool full = vi < v1 && vi * 8 + 8 <= V;
-      const uint32_t dd[4] = {d[r].x, d[r].y, d[r].z, d[r].w};
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int i = vi * 8 + q;
-        const bool ok = vi < v1 && i < V;
-        uint32_t key = 0;
-        if (ok) key = full ? tk_key(q & 1 ? dd[q >> 1] >> 16 : dd[q >> 1] & 0xffffu) : tk_key(row[i]);
-        tk_append(buf, &n_loc, kTkCap, ok && key >= T0, tk_comp(key, i));
-      }
-    }
-  }
-  __syncthreads();
-  const int nl = n_loc;
-  if (threadIdx.x == 0) base_sh = nl ? atomicAdd(&w.count, nl) : 0;   // nl > kTkCap pushes count past it
-  __syncthreads();
-  for (int i = threadIdx.x; i < nl && i < kTkCap; i += blockDim.x)
-    if (base_sh + i < kTkCap) w.cand[base_sh + i] = buf[i];
+// Inclusive prefix sum over the 64 lanes of a wave, by DPP: row shifts build
+// the prefix within each row of 16 lanes, row broadcasts carry rows 0-1 and
+// 2 into rows 1-3.
+__device__ __forceinline__ int rs_wave_scan(int v) {
+  int x = v;
+  x += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, v, 0x113, 0xF, 0xF, true);   // row_shr:3  (sums of 4)
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xE, false);  // row_shr:4 into lanes 4-15 of a row
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xC, false);  // row_shr:8 into lanes 8-15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return x;
 }
 
-__global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const uint16_t* logits, int64_t stride, int V, int C,
-                                                                 const TkWork* work, int64_t* idx_out) {
-  __shared__ uint64_t cand[kTkCap];
+// Exclusive prefix of v over the workgroup in thread order; *total = sum.
+// Two barriers; slots: kRsWaves ints.
+__device__ __forceinline__ int rs_scan(int v, int* slots, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int incl = rs_wave_scan(v);
+  if (lane == 63) slots[wave] = incl;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kRsWaves; ++w) {
+    const int sw = slots[w];
+    before += w < wave ? sw : 0;
+    tot += sw;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + incl - v;
+}
+
+// The bin holding the k-th largest element of a 256-bin histogram (k >= 1)
+// and the count in higher bins (bin 0 if the count never reaches k): wave 0,
+// four bins per lane, top bins first, DPP scan of the lane sums.
+__device__ void rs_walk(TkHist& h, int k) {
+  if (threadIdx.x < 64) {
+    const int l = threadIdx.x;
+    uint32_t c[4], sum = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      c[r] = h.hist[255 - 4 * l - r];
+      sum += c[r];
+    }
+    const uint32_t incl = (uint32_t)rs_wave_scan((int)sum);
+    const uint64_t hit = __ballot(incl >= (uint32_t)k);
+    const int L = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
+    if (l == L) {
+      uint32_t above = incl - sum;
+      int b = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int bin = 255 - 4 * l - r;
+        if (above + c[r] >= (uint32_t)k || bin == 0) { b = bin; break; }
+        above += c[r];
+      }
+      h.sel_bin = b;
+      h.sel_above = (int)above;
+    }
+  }
+  __syncthreads();
+}
+
+// Value of lane (lane ^ s) of the wave, s = 1 .. 32 (a constant after unrolling).
+__device__ __forceinline__ uint32_t rs_xor_lane(uint32_t v, int s) {
+  if (s == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);    // quad_perm [1,0,3,2]
+  if (s == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);    // quad_perm [2,3,0,1]
+  if (s == 4) {
+    // lane i of an 8-group: half mirror gives 7 - i, a quad reversal then (7 - i) ^ 3 = i ^ 4
+    const uint32_t h = __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(h, 0x1B, 0xF, 0xF, false);
+  }
+  if (s == 8) return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);   // row_ror:8 = xor 8 within 16
+  if (s == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401F);               // xor 16 within 32 lanes
+  return __shfl_xor(v, 32, 64);
+}
+
+// Descending bitonic sort of 1024 32-bit keys, 4 per thread on threads
+// t < kRsSortThreads (element 4t + r in a[r]): strides 1 and 2 in registers,
+// 4 .. 128 across lanes of a wave, 256 and 512 through xch[1024] in LDS.  Every
+// thread of the workgroup calls it (the barriers); the others only wait.
+__device__ __forceinline__ void rs_sort1024(uint32_t (&a)[4], uint32_t* xch) {
+  const int t = threadIdx.x;
+  const bool on = t < kRsSortThreads;
+#pragma unroll
+  for (int size = 2; size <= 1024; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride <= 2) {
+        if (!on) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (r & stride) continue;
+          const int e = 4 * t + r;
+          const bool desc = (e & size) == 0;
+          const uint32_t x = a[r], y = a[r + stride];
+          const uint32_t hi = max(x, y), lo = min(x, y);
+          a[r] = desc ? hi : lo;
+          a[r + stride] = desc ? lo : hi;
+        }
+      } else {
+        uint32_t b[4];
+        if (stride <= 128) {
+          if (!on) continue;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) b[r] = rs_xor_lane(a[r], stride >> 2);
+        } else {
+          if (on) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) xch[4 * t + r] = a[r];
+          }
+          __syncthreads();
+          if (on) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) b[r] = xch[4 * (t ^ (stride >> 2)) + r];
+          }
+          __syncthreads();
+          if (!on) continue;
+        }
+        const bool keep_max = ((4 * t & stride) == 0) == ((4 * t & size) == 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[r] = keep_max ? max(a[r], b[r]) : min(a[r], b[r]);
+      }
+    }
+  }
+}
+
+// Descending bitonic sort of a[0, n2) of 32-bit keys in LDS.
+__device__ void tk_sort32(uint32_t* a, int n2) {
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = threadIdx.x; t < n2 / 2; t += blockDim.x) {
+        const int i = 2 * t - (t & (stride - 1));
+        const int j = i + stride;
+        const bool desc = (i & size) == 0;
+        const uint32_t x = a[i], y = a[j];
+        if ((x < y) == desc) { a[i] = y; a[j] = x; }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// k-th largest (k >= 1) of the keys held N per thread (0 = none), two 8-bit
+// rounds over per-wave histograms (no atomics across waves).
+template <int N>
+__device__ uint32_t rs_kth(const uint32_t (&key)[N], int k, uint32_t* wh, TkHist& h) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t* mine = wh + wave * 256;
+  uint32_t prefix = 0;
+  int kk = k;
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mine[lane * 4 + j] = 0;
+    // (LDS operations of one wave complete in order: the zeros land before the adds)
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const uint32_t kj = key[j];
+      const bool in = kj != 0 && (round == 0 || (kj >> 8) == prefix);
+      if (in) atomicAdd(&mine[round == 0 ? kj >> 8 : kj & 255u], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      const int b = threadIdx.x;
+      uint32_t tot = 0;
+#pragma unroll
+      for (int w = 0; w < kRsWaves; ++w) tot += wh[w * 256 + b];
+      h.hist[b] = tot;
+    }
+    __syncthreads();
+    rs_walk(h, kk);
+    const uint32_t bin = h.sel_bin;
+    kk -= h.sel_above;
+    __syncthreads();
+    prefix = round == 0 ? bin : (prefix << 8) | bin;
+  }
+  return prefix;
+}
+
+__global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t* logits, int64_t stride, int V, int C,
+                                                                 const uint16_t* smax, int64_t sstride,
+                                                                 int64_t* idx_out) {
+  __shared__ uint64_t cand[kTkCap];   // exact and short-row paths
+  __shared__ uint32_t ck[kTkCap];     // candidate sort keys: key << 16 | (0xffff - position)
+  __shared__ int cidx[kTkCap];        // candidate element indices, increasing
+  __shared__ int slist[kTkCap];       // candidate slices, increasing
+  __shared__ uint32_t wh[kRsWaves * 256];
   __shared__ TkHist h;
-  __shared__ int n_sh;
+  __shared__ int slots[kRsWaves];
+  __shared__ int n_x;
   const int m = blockIdx.x;
   const uint16_t* row = logits + (int64_t)m * stride;
   int64_t* out = idx_out + (int64_t)m * C;
@@ -382,14 +509,125 @@ __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const uint16_t*
     return;
   }
   const int S = tk_slice(V), ns = (V + S - 1) / S;
-  const int n = ns >= C ? work[m].count : kTkCap + 1;
-  if (n <= kTkCap) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) cand[i] = work[m].cand[i];
+  int n_c = 0;
+  bool exact = ns < C;
+  if (!exact) {
+    // thread t holds the 8-slice vectors [t * vpt, t * vpt + vpt) of the row's
+    // slice maxima (the padding past ns is never written: masked)
+    const int nv = (ns + 7) / 8, vpt = (nv + kRsThreads - 1) / kRsThreads;
+    const uint4* src = reinterpret_cast<const uint4*>(smax + (int64_t)m * sstride);
+    uint32_t sk[kRsVpt * 8];
+#pragma unroll
+    for (int j = 0; j < kRsVpt; ++j) {
+      const int vi = threadIdx.x * vpt + j;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (j < vpt && vi < nv) v = src[vi];
+      const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t kq = q & 1 ? d[q >> 1] >> 16 : d[q >> 1] & 0xffffu;
+        sk[j * 8 + q] = j < vpt && vi * 8 + q < ns ? kq : 0u;
+      }
+    }
+    // T0: the C-th largest maximum of 4-slice groups (a lower bound of the
+    // C-th largest element: C groups each hold an element >= T0)
+    uint32_t key[kRsVpt * 2];
+#pragma unroll
+    for (int j = 0; j < kRsVpt * 2; ++j)
+      key[j] = max(max(sk[4 * j], sk[4 * j + 1]), max(sk[4 * j + 2], sk[4 * j + 3]));
+    const int ng = (ns + 3) / 4;
+    const uint32_t T0 = ng >= C ? rs_kth(key, C, wh, h) : 1u;
+    // candidate slices (maximum >= T0), in increasing order: one scan
+    int cc = 0;
+#pragma unroll
+    for (int j = 0; j < kRsVpt * 8; ++j) cc += sk[j] >= T0 ? 1 : 0;
+    int nsl;
+    int pos = rs_scan(cc, slots, &nsl);
+#pragma unroll
+    for (int j = 0; j < kRsVpt * 8; ++j)
+      if (sk[j] >= T0) {
+        if (pos < kTkCap) slist[pos] = (threadIdx.x * vpt + (j >> 3)) * 8 + (j & 7);
+        ++pos;
+      }
     __syncthreads();
-    tk_finish(cand, n, C, out);
-  } else {
-    tk_exact(row, V, C, cand, h, &n_sh);
+    exact = nsl > kTkCap;
+    if (!exact) {
+      // their elements >= T0 in increasing index order: thread t takes
+      // contiguous items (8 elements each) of a round, one scan per round
+      const int per = S / 8, tot = nsl * per;
+      for (int r0 = 0; r0 < tot; r0 += kRsThreads * kRsIpt) {
+        const int nr = min(tot - r0, kRsThreads * kRsIpt);
+        const int ipt = (nr + kRsThreads - 1) / kRsThreads;
+        uint4 v[kRsIpt];
+        int e[kRsIpt];
+#pragma unroll
+        for (int j = 0; j < kRsIpt; ++j) {
+          const int it = r0 + threadIdx.x * ipt + j;
+          const bool ok = j < ipt && it < r0 + nr;
+          e[j] = ok ? slist[it / per] * S + (it % per) * 8 : -1;
+          v[j] = make_uint4(0, 0, 0, 0);
+          if (ok && e[j] + 8 <= V) v[j] = *reinterpret_cast<const uint4*>(row + e[j]);
+        }
+        uint32_t k8[kRsIpt * 8];
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < kRsIpt; ++j) {
+          const uint32_t d[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            uint32_t kq = 0;
+            if (e[j] >= 0 && e[j] + q < V)
+              kq = e[j] + 8 <= V ? tk_key(q & 1 ? d[q >> 1] >> 16 : d[q >> 1] & 0xffffu) : tk_key(row[e[j] + q]);
+            k8[j * 8 + q] = kq;
+            cnt += kq >= T0 ? 1 : 0;
+          }
+        }
+        int step;
+        int p2 = n_c + rs_scan(cnt, slots, &step);
+#pragma unroll
+        for (int j = 0; j < kRsIpt * 8; ++j)
+          if (k8[j] >= T0) {
+            if (p2 < kTkCap) {
+              ck[p2] = (k8[j] << 16) | (uint32_t)(0xffff - p2);
+              cidx[p2] = e[j >> 3] + (j & 7);
+            }
+            ++p2;
+          }
+        n_c += step;
+      }
+      __syncthreads();
+      exact = n_c > kTkCap;
+    }
+  }
+  if (exact) {
+    tk_exact(row, V, C, cand, h, &n_x);
     tk_finish(cand, C, C, out);
+    return;
+  }
+  // sort the candidates (positions follow the index order, so ties sort by index)
+  if (n_c <= 1024) {
+    uint32_t a[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = 4 * (int)threadIdx.x + r;
+      a[r] = threadIdx.x < kRsSortThreads && e < n_c ? ck[e] : 0u;
+    }
+    __syncthreads();
+    rs_sort1024(a, ck);
+    if (threadIdx.x < kRsSortThreads) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int e = 4 * threadIdx.x + r;
+        if (e < C) out[e] = (int64_t)cidx[0xffff - (a[r] & 0xffffu)];
+      }
+    }
+  } else {
+    int n2 = 2048;
+    while (n2 < n_c) n2 <<= 1;
+    for (int i = n_c + threadIdx.x; i < n2; i += blockDim.x) ck[i] = 0;
+    __syncthreads();
+    tk_sort32(ck, n2);
+    for (int i = threadIdx.x; i < C; i += blockDim.x) out[i] = (int64_t)cidx[0xffff - (ck[i] & 0xffffu)];
   }
 }
 
@@ -401,30 +639,50 @@ using namespace fp4x;
 
 extern "C" {
 
-int64_t fp4x_topk_workspace_size(int M) { return (int64_t)(M < 0 ? 0 : M) * (int64_t)sizeof(TkWork); }
+int64_t fp4x_topk_workspace_size(int M, int V) {
+  if (M <= 0 || V <= 0) return 0;
+  return (int64_t)M * tk_smax_stride(V) * 2;
+}
+
+}  // extern "C"
+
+namespace fp4x {
+int topk_slice_len(int V) { return tk_slice(V); }
+int64_t topk_smax_stride(int V) { return tk_smax_stride(V); }
+
+int topk_check(const void* logits, int64_t stride, int M, int V, int C, void* workspace, int64_t ws_bytes) {
+  if (M < 0 || V < 1 || C < 1 || C > V || C > 2048) { set_error("topk: need 1 <= C <= min(V, 2048)"); return FP4X_ERR_ARG; }
+  if (stride < V || stride % 8 || !al16(logits)) {
+    set_error("topk: logits must be 16-byte aligned with a row stride that is a multiple of 8");
+    return FP4X_ERR_ARG;
+  }
+  if (ws_bytes < fp4x_topk_workspace_size(M, V) || (M > 0 && !al16(workspace))) {
+    set_error("topk: workspace smaller than fp4x_topk_workspace_size(M, V) or misaligned");
+    return FP4X_ERR_ARG;
+  }
+  return FP4X_OK;
+}
+
+// B (and A unless the slice maxima are already in the workspace).
+int topk_launch(const uint16_t* lg, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
+                       bool have_smax, hipStream_t st) {
+  const int S = tk_slice(V), ns = (V + S - 1) / S;
+  const int64_t ss = tk_smax_stride(V);
+  if (V > kTkCap && ns >= C && !have_smax)
+    hipLaunchKernelGGL(topk_slicemax_kernel, dim3((ns + 255) / 256, M), dim3(256), 0, st, lg, stride, V, smax, ss);
+  hipLaunchKernelGGL(topk_rowsel_kernel, dim3(M), dim3(kRsThreads), 0, st, lg, stride, V, C, smax, ss, idx_out);
+  return check_launch("topk");
+}
+}  // namespace fp4x
+
+extern "C" {
 
 int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int64_t* idx_out, void* workspace,
                    int64_t ws_bytes, void* stream) {
-  if (M < 0 || V < 1 || C < 1 || C > V || C > 2048) { set_error("topk_rows: need 1 <= C <= min(V, 2048)"); return FP4X_ERR_ARG; }
-  if (stride < V || stride % 8 || !al16(logits)) {
-    set_error("topk_rows: logits must be 16-byte aligned with a row stride that is a multiple of 8");
-    return FP4X_ERR_ARG;
-  }
-  if (ws_bytes < fp4x_topk_workspace_size(M) || (M > 0 && !al16(workspace))) {
-    set_error("topk_rows: workspace smaller than fp4x_topk_workspace_size(M) or misaligned");
-    return FP4X_ERR_ARG;
-  }
-  if (M == 0) return FP4X_OK;
-  hipStream_t st = (hipStream_t)stream;
-  TkWork* w = static_cast<TkWork*>(workspace);
-  const uint16_t* lg = static_cast<const uint16_t*>(logits);
-  if (V > kTkCap) {
-    const int S = tk_slice(V), ns = (V + S - 1) / S;
-    hipLaunchKernelGGL(topk_slicemax_kernel, dim3((ns + 255) / 256, M), dim3(256), 0, st, lg, stride, V, w);
-    if (ns >= C) hipLaunchKernelGGL(topk_collect_kernel, dim3(kTkB, M), dim3(kTkThreads), 0, st, lg, stride, V, C, w);
-  }
-  hipLaunchKernelGGL(topk_select_kernel, dim3(M), dim3(kTkThreads), 0, st, lg, stride, V, C, w, idx_out);
-  return check_launch("topk_rows");
+  int rc = topk_check(logits, stride, M, V, C, workspace, ws_bytes);
+  if (rc || M == 0) return rc;
+  return topk_launch(static_cast<const uint16_t*>(logits), stride, M, V, C, idx_out, static_cast<uint16_t*>(workspace),
+                     false, (hipStream_t)stream);
 }
 
 int fp4x_refine_mx8(void* out, int out_dtype, int64_t out_stride, const void* x, const int64_t* idx, int M, int C,

@@ -21,6 +21,8 @@ struct GemvLaunch {
   int J, nb;             // MFMA core: chunks per lane per tile, register batches per tile
   int batch, per_wg;     // MFMA core: batch entries, (entry, tile) items per workgroup
   int xbufs;             // streaming W8 kernel: activation buffers staged in LDS
+  uint16_t* smax;        // streaming INT2 head: per-tile maximum order key of each row m (or null)
+  int64_t smax_stride;   //   elements between rows m of smax
   float* part;           // split-K slots [batch][ksplit][MT][N]
   int* tickets;          // split-K tickets [batch][tiles], zero between calls
   // mixer-down epilogue

@@ -486,6 +486,22 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
       for (int i = 0; i < 4; ++i)
         if (g * 4 + i < p.M) EpiStore::apply(p, 0, g * 4 + i, row, acc[i] * p.gs);
     }
+    if (p.smax) {
+      // the largest order key of the tile's 16 stored (bf16) logits of each row m:
+      // the 16-element slice maxima of the top-k (rows past N: key 0, below all)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = acc[i] * p.gs;
+        if (p.rs) v = v * p.rs[row < p.N ? row : p.N - 1];
+        uint32_t key = row < p.N ? tk_key(f32_to_bf16(v)) : 0u;
+        // maximum over the 16 lanes n of this g (one DPP row): quad swaps, half mirror, mirror
+        key = max(key, (uint32_t)__builtin_amdgcn_mov_dpp((int)key, 0xB1, 0xF, 0xF, false));
+        key = max(key, (uint32_t)__builtin_amdgcn_mov_dpp((int)key, 0x4E, 0xF, 0xF, false));
+        key = max(key, (uint32_t)__builtin_amdgcn_mov_dpp((int)key, 0x141, 0xF, 0xF, false));
+        key = max(key, (uint32_t)__builtin_amdgcn_mov_dpp((int)key, 0x140, 0xF, 0xF, false));
+        if (n == 0 && g * 4 + i < p.M) p.smax[(int64_t)(g * 4 + i) * p.smax_stride + t0 + q] = (uint16_t)key;
+      }
+    }
   }
   wait_vmcnt<0>();                                   // no load of the prologue outlives the wave
 }

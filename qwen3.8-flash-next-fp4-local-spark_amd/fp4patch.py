@@ -293,11 +293,12 @@ def _patch_fast_head():
     def fast(self, h):
         if st["int2"]:
             P, S = st["coarse"]
-            coarse = F.int2_logits(h, P, S, st["w"].shape[0], out_dtype=torch.bfloat16)
+            # int2_logits + top-C in one call (the coarse kernel also yields the top-k's slice maxima)
+            coarse, idx = F.int2_topk(h, P, S, st["w"].shape[0], C)
         else:
             P, S, gs = st["coarse"]
             coarse = F.nv4_linear(h, P, S, gs, (32, 256, 4))
-        idx = F.topk_rows(coarse, C)
+            idx = F.topk_rows(coarse, C)
         return F.refine_mx8_(coarse, h, idx, st["w"], st["s"])
 
     def compute_logits(self, hidden_states):

@@ -21,7 +21,7 @@ import _fp4x as _L
 
 __all__ = [
     "mx8_linear", "bf16_linear", "nv4_linear", "w8_linear", "w6_linear", "int2_logits", "refine_mx8_",
-    "topk_rows", "w8_linear_layers", "HCFused", "hc_scaled_silu", "hc_gate_mean",
+    "topk_rows", "int2_topk", "w8_linear_layers", "HCFused", "hc_scaled_silu", "hc_gate_mean",
     "quantize_w8", "quantize_w6", "quantize_nv4", "quantize_int2", "quantize_mx8",
     "mx8_dequant", "dequant_int2", "dequant_nv4", "dequant_operand", "ORDER",
 ]
@@ -209,6 +209,29 @@ def int2_logits(x, P, S, N, BN=64, BK=512, nw=4, RS=None, out_dtype=torch.float3
     return out
 
 
+def int2_topk(x, P, S, N, C, RS=None):
+    """The fast head's coarse stage: (coarse bf16 [M, N], idx int64 [M, C]) =
+    (int2_logits(x, P, S, N, RS=RS, out_dtype=bfloat16), topk_rows(coarse, C)),
+    in one call that lets the coarse kernel produce the top-k's slice maxima."""
+    _need_cuda(x, P, S)
+    x = x.to(torch.bfloat16).contiguous()
+    m, k = x.shape
+    G = k // S.shape[1]
+    sfmt = _L.DT_E4M3 if S.dtype == torch.float8_e4m3fn else _L.DT_F16
+    ld = -(-N // 8) * 8
+    coarse = torch.empty((m, ld), dtype=torch.bfloat16, device=x.device)[:, :N]
+    idx = torch.empty((m, C), dtype=torch.int64, device=x.device)
+    st = _L.stream_of(x)
+    for m0 in _rows_blocks(m):
+        mb = min(MAX_M, m - m0)
+        nbytes = _L.lib().fp4x_topk_workspace_size(mb, N)
+        ws = _topk_workspace(x.device, nbytes)
+        _L.check(_L.lib().fp4x_int2_topk(_ptr(x[m0:]), k, _ptr(P), _ptr(S), sfmt,
+                                         _ptr(RS) if RS is not None else None, _ptr(coarse[m0:]), ld, mb, N, k, G,
+                                         C, _ptr(idx[m0:]), _ptr(ws), nbytes, st), "int2_topk")
+    return coarse, idx
+
+
 def topk_rows(logits, C):
     """Indices [M, C] (int64) of the C largest bf16 logits of each row, in
     the order (value desc, index asc) — the selection the fast head takes
@@ -222,7 +245,7 @@ def topk_rows(logits, C):
         padded[:, :v] = logits
         logits = padded
     idx = torch.empty((m, C), dtype=torch.int64, device=logits.device)
-    nbytes = _L.lib().fp4x_topk_workspace_size(m)
+    nbytes = _L.lib().fp4x_topk_workspace_size(m, v)
     ws = _topk_workspace(logits.device, nbytes)
     _L.check(_L.lib().fp4x_topk_rows(_ptr(logits), logits.stride(0), m, v, C, _ptr(idx), _ptr(ws), nbytes,
                                      _L.stream_of(logits)), "topk_rows")

@@ -59,7 +59,7 @@ def test_topk_all_equal_exact_path(gpu, F):
 
 
 def test_topk_rearms_across_calls_and_paths(gpu, F):
-    """The arrival counters in the shared workspace re-arm after every call:
+    """The shared workspace carries no state from one call to the next:
     alternating candidate-path and exact-path rows (and row counts) on one
     workspace keeps every result exact."""
     rng = np.random.default_rng(77)
@@ -74,6 +74,19 @@ def test_topk_rearms_across_calls_and_paths(gpu, F):
         assert np.array_equal(F.topk_rows(tn, C).cpu().numpy(), want_n)
         assert np.array_equal(F.topk_rows(tt, C).cpu().numpy(), want_t)
         assert np.array_equal(F.topk_rows(tn[1:2], C).cpu().numpy(), want_n[1:2])
+
+
+def test_topk_ignores_stale_workspace(gpu, F):
+    """A row of 12,503 slices (not a multiple of the 8-slice padding): the
+    workspace's padding entries, never written, hold 0xff from an earlier call
+    and must not raise the threshold."""
+    rng = np.random.default_rng(5)
+    V, C = 200040, 512
+    bits = fm.bf16_bits(fm.round_bf16(rng.standard_normal((2, V)).astype(np.float32)))
+    t = dev(bits.view(np.int16)).view(torch.bfloat16)
+    ws = F._topk_workspace(t.device, 16 << 20)
+    ws.fill_(255)
+    assert np.array_equal(F.topk_rows(t, C).cpu().numpy(), oh.topk_total_order(bits, C))
 
 
 # ------------------------------------------------------------------ refine
@@ -222,3 +235,27 @@ def test_int2_stream(gpu, F, M, rs, monkeypatch):
     # bf16 logits round the same sums
     yb = F.int2_logits(*args, out_dtype=torch.bfloat16, **kw)
     assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
+
+
+# ------------------------------------------------------------------ fused coarse + top-k
+@pytest.mark.parametrize("V,M,rs", [(248320, 3, False), (248320, 16, False), (200040, 3, True), (50000, 3, False)])
+def test_int2_topk_fused_equals_separate(gpu, F, V, M, rs):
+    """int2_topk (slice maxima from the streaming coarse kernel's epilogue where
+    it streams, else a slice-max launch) equals int2_logits + topk_rows bit for
+    bit, and its selection is the oracle's total order on its own logits."""
+    K, C = 2560, 512
+    g = torch.Generator(device=gpu).manual_seed(V + M)
+    w = torch.randn((V, K), generator=g, device=gpu) * 0.02
+    w[torch.randperm(V, generator=g, device=gpu)[:64]] *= 4
+    P, S = F.quantize_int2(w, group=16)
+    del w
+    R = (torch.rand(V, generator=g, device=gpu) + 0.5) if rs else None
+    rng = np.random.default_rng(V + M)
+    x, _ = act(rng, M, K)
+    xt = bf16_dev(x)
+    coarse, idx = F.int2_topk(xt, P, S, V, C, RS=R)
+    coarse2 = F.int2_logits(xt, P, S, V, RS=R, out_dtype=torch.bfloat16)
+    idx2 = F.topk_rows(coarse2, C)
+    assert np.array_equal(bf16_bits(coarse), bf16_bits(coarse2))
+    assert torch.equal(idx, idx2)
+    assert np.array_equal(idx.cpu().numpy(), oh.topk_total_order(bf16_bits(coarse), C))
