@@ -203,8 +203,9 @@ int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, co
   p.s_bstride = s_lstride * (s_dtype == FP4X_DT_F16 ? 2 : 4);
   p.out_bstride = out_lstride;
   // long runs of tiles (layer-batched gates) stream through LDS; split-K calls of
-  // few tiles split K over the waves of one workgroup per tile (the mixer's
-  // down projection takes the same path); other shapes use the MFMA core
+  // few tiles spread each tile's K over several workgroups (or over the waves
+  // of one workgroup), the mixer's down projection taking the same path; other
+  // shapes use the MFMA core
   hipStream_t st = (hipStream_t)stream;
   if (fmt == FP4X_FMT_W8_F16) {
     if (launch_w8_stream<true>(p, layers, st)) return check_launch("w8_stream");

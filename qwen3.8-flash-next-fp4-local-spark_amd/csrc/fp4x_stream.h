@@ -242,6 +242,148 @@ __global__ __launch_bounds__(64 * T * KW) void w8_stream_kernel(GemvLaunch p) {
   }
 }
 
+// The activations of one unit for lane (n, g): 32 bytes of chunk g and 32 of
+// chunk g + 4 (128 bytes further).
+__device__ __forceinline__ void stream_read_x(uint32_t xa, uint4& x0a, uint4& x0b, uint4& x1a, uint4& x1b) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %4 offset:16\n\t"
+      "ds_read_b128 %2, %4 offset:128\n\t"
+      "ds_read_b128 %3, %4 offset:144\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x0a), "=&v"(x0b), "=&v"(x1a), "=&v"(x1b)
+      : "v"(xa)
+      : "memory");
+}
+
+// Split-K W8 GEMV of few 16-row tiles (the mixer's down projection, N = 640,
+// K = 10240): C workgroups per tile, each of WPG waves owning JW units of 128
+// K values (so C = K / (128 * WPG * JW)), which spreads a 40-tile matrix over
+// C x 40 CUs.  A CU streams only some 20 GB/s of its own, so the CU count, not
+// the depth of one CU's queue, bounds a GEMV this small.
+//   * Every wave issues its weight and scale loads (lane (n, g): chunks g and
+//     g + 4 of row n per unit, and the unit's scale dword) right after the
+//     workgroup's activation slice, waits once, and computes from registers.
+//   * The WPG wave parts are summed in wave order through LDS; wave 0 stores
+//     the workgroup's [M x 16] partial to slot c of the tile with agent-scope
+//     (device-coherent) stores, waits for them to complete, and takes a ticket
+//     on the tile; the workgroup drawing ticket C - 1 reads the C slots with
+//     agent-scope loads, sums them in slot order (so the result does not
+//     depend on arrival order), runs the epilogue and re-arms the ticket.
+//     Ordering comes from the explicit completion wait between the slot
+//     stores and the ticket, and from the loads depending on the ticket value;
+//     no cache-wide write-back or invalidate is needed because every access to
+//     the slots and the ticket is device-coherent.
+template <bool F16S, int WPG, int JW, class Epi>
+__global__ __launch_bounds__(64 * WPG) void w8_splitk_kernel(GemvLaunch p, int C) {
+  constexpr int UW = WPG * JW;                       // units per workgroup
+  constexpr int XR = UW * 256 + 64;                  // LDS bytes per activation row
+  static_assert(UW % 4 == 0, "activation slice in whole 1 KB pieces");
+  extern __shared__ __align__(16) uint16_t lds[];
+  char* base = reinterpret_cast<char*>(lds);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int K = p.pa.K, t = blockIdx.x / C, c = blockIdx.x - t * C;
+  char* part_base = base + ((p.M * XR + 15) & ~15);
+
+  // activation slice [M, c * UW * 128, + UW * 128): 1 KB pieces
+  constexpr int PPR = UW / 4;                        // pieces per row
+  for (int i = wave; i < p.M * PPR; i += WPG) {
+    const int m = i / PPR, u = i - m * PPR;
+    dma_b128(p.x + (int64_t)m * p.x_stride + (int64_t)(c * UW + u * 4) * 128 + lane * 8, base + m * XR + u * 1024);
+  }
+  const int lim = p.N - 1 - t * 16;                  // rows past N read row N - 1
+  const int64_t row = (int64_t)t * 16 + (n < lim ? n : lim);
+  const int u0 = c * UW + wave * JW;
+  const uint8_t* wr = p.pa.w0 + row * K + u0 * 128 + g * 16;
+  const uint8_t* sr = p.pa.s + (row * (K / 64) + u0 * 2) * (F16S ? 2 : 4);
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  u32x4_t qa[JW], qb[JW];
+  uint32_t sa[JW], sb[JW];
+#pragma unroll
+  for (int j = 0; j < JW; ++j) {
+    qa[j] = *reinterpret_cast<const u32x4_t*>(wr + j * 128);
+    qb[j] = *reinterpret_cast<const u32x4_t*>(wr + j * 128 + 64);
+    if constexpr (F16S) {
+      sa[j] = *reinterpret_cast<const uint32_t*>(sr + j * 4);
+      sb[j] = 0;
+    } else {
+      sa[j] = *reinterpret_cast<const uint32_t*>(sr + j * 8);
+      sb[j] = *reinterpret_cast<const uint32_t*>(sr + j * 8 + 4);
+    }
+  }
+  wait_vmcnt<0>();
+  wg_barrier_raw();
+
+  const int xr = n < p.M ? n : 0;                    // rows m >= M: never stored
+  const uint32_t xl = lds_addr(base) + xr * XR + wave * JW * 256 + g * 32;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < JW; ++j) {
+    uint4 x0a, x0b, x1a, x1b;
+    stream_read_x(xl + j * 256, x0a, x0b, x1a, x1b);
+    float sc0, sc1;
+    if constexpr (F16S) {
+      sc0 = f16_to_f32((uint16_t)sa[j]);
+      sc1 = f16_to_f32((uint16_t)(sa[j] >> 16));
+    } else {
+      sc0 = __uint_as_float(sa[j]);
+      sc1 = __uint_as_float(sb[j]);
+    }
+    uint32_t w[8];
+    w8_chunk_bf16(make_uint4(qa[j].x, qa[j].y, qa[j].z, qa[j].w), sc0, w);
+    acc = mfma16(x0a, make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x0b, make_uint4(w[4], w[5], w[6], w[7]), acc);
+    w8_chunk_bf16(make_uint4(qb[j].x, qb[j].y, qb[j].z, qb[j].w), sc1, w);
+    acc = mfma16(x1a, make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x1b, make_uint4(w[4], w[5], w[6], w[7]), acc);
+  }
+  if constexpr (WPG > 1) {
+    const uint32_t pl = lds_addr(part_base) + lane * 16;
+    if (wave > 0) lds_put_f32x4(pl + (wave - 1) * 1024, acc);
+    wg_barrier_raw();
+    if (wave > 0) return;
+#pragma unroll
+    for (int h = 1; h < WPG; ++h) {
+      const f32x4_t o = lds_get_f32x4(pl + (h - 1) * 1024);
+      acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
+    }
+  }
+  // wave 0: slot c of tile t holds [M][16] fp32 partials
+  float* slots = p.part + (int64_t)t * C * p.M * 16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (g * 4 + i < p.M)
+      __hip_atomic_store(slots + (c * p.M + g * 4 + i) * 16 + n, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_vmcnt<0>();                                   // the slot stores have completed
+  int tk = 0;
+  if (lane == 0) tk = __hip_atomic_fetch_add(p.tickets + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  tk = __builtin_amdgcn_readfirstlane(tk);
+  if (tk != C - 1) return;
+  for (int e = lane; e < p.M * 16; e += 64) {        // e = m * 16 + n
+    const float* src = slots + e;
+    float tot = ld_coherent(src);
+    for (int cc = 1; cc < C; ++cc) tot += ld_coherent(src + cc * p.M * 16);
+    const int64_t orow = (int64_t)t * 16 + (e & 15);
+    if (orow < p.N) Epi::apply(p, 0, e >> 4, orow, tot * p.gs);
+  }
+  if (lane == 0) ticket_reset(p.tickets + t);
+}
+
+template <bool F16S, int WPG, int JW, class Epi>
+bool launch_w8_splitk(GemvLaunch p, int C, size_t lds, int gx, hipStream_t st) {
+  auto kern = w8_splitk_kernel<F16S, WPG, JW, Epi>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess)
+      return false;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(gx), dim3(64 * WPG), lds, st, p, C);
+  return true;
+}
+
 template <bool F16S, int T, int KW, int D, class Epi>
 bool launch_w8_stream_cfg(GemvLaunch p, size_t lds, int gx, hipStream_t st) {
   auto kern = w8_stream_kernel<F16S, T, KW, D, Epi>;
@@ -288,30 +430,43 @@ bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
 }
 
 // Split-K W8 GEMVs of few tiles (the mixer's down projection, N = 640,
-// K = 10240): one workgroup per 16-row tile whose KW = 16 waves split K into
-// contiguous parts and sum them in part order through LDS, then run the
-// epilogue: no workspace, tickets or cross-workgroup fences.  The caller's
-// ksplit > 1 selects this decomposition (whatever its value); taken when
-// K / 128 is a multiple of 16 with at least 2 units per wave, the tiles do
-// not exceed two per CU, and the activations fit in LDS beside the rings
-// (M <= 3 at K = 10240).  Returns false otherwise (or with FP4X_W8_STREAM=0),
-// launching nothing.  Every entry point deciding on the same (M, N, K,
-// ksplit) takes the same path, which keeps the fused mixer bit-identical to
-// the unfused GEMV + epilogue kernels.
+// K = 10240).  The caller's ksplit > 1 selects split-K (whatever its value);
+// this library picks the decomposition from (M, N, K, ksplit) alone, so every
+// entry point deciding on the same shape takes the same path, which keeps the
+// fused mixer bit-identical to the unfused GEMV + epilogue kernels:
+//   * w8_splitk_kernel when K is a multiple of 2048 (8 waves x 2 units per
+//     workgroup, C = K / 2048 >= 2 workgroups per tile) and the caller's
+//     scratch (ksplit x 16 x N floats, one ticket per tile) holds the
+//     tiles x C x M x 16 partial slots;
+//   * else the ring kernel with one workgroup per tile whose KW = 16 waves
+//     split K and sum in part order through LDS (no scratch), when K / 128 is
+//     a multiple of 16 with at least 2 units per wave and the activations fit
+//     in LDS beside the rings (M <= 3 at K = 10240).
+// Both need at most two tiles per CU.  Returns false otherwise (or with
+// FP4X_W8_STREAM=0), launching nothing.
 template <bool F16S, class Epi>
 bool launch_w8_ktile(GemvLaunch p, hipStream_t st) {
   constexpr int KW = 16, D = 2;
+  constexpr int SW = 8, SJ = 2, SU = SW * SJ;
   const char* env = getenv("FP4X_W8_STREAM");
   if (env && env[0] == '0') return false;
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
-  if (p.ksplit < 2 || K % 512 != 0 || p.M > 16 || (K / 128) % KW != 0 || K / 128 / KW < D) return false;
+  if (p.ksplit < 2 || K % 512 != 0 || p.M > 16) return false;
   if (reinterpret_cast<uintptr_t>(p.pa.s) & 3) return false;
   if (tiles > 2 * device_cus()) return false;
-  const size_t lds = (size_t)StreamGeom::xbuf_bytes(p.M, K) + (size_t)(KW - 1) * 1024 + (size_t)KW * D * kStreamUnit;
-  if (lds > 160 * 1024) return false;
+  const int units = K / 128;
   p.batch = 1;
   p.per_wg = 1;
   p.xbufs = 1;
+  if (units % SU == 0 && units / SU >= 2 && p.part && p.tickets) {
+    const int C = units / SU;
+    const int64_t slots = (int64_t)tiles * C * p.M * 16, have = (int64_t)p.ksplit * 16 * p.N;
+    const size_t lds = (size_t)((p.M * (SU * 256 + 64) + 15) & ~15) + (size_t)(SW - 1) * 1024;
+    if (slots <= have && lds <= 160 * 1024) return launch_w8_splitk<F16S, SW, SJ, Epi>(p, C, lds, tiles * C, st);
+  }
+  if (units % KW != 0 || units / KW < D) return false;
+  const size_t lds = (size_t)StreamGeom::xbuf_bytes(p.M, K) + (size_t)(KW - 1) * 1024 + (size_t)KW * D * kStreamUnit;
+  if (lds > 160 * 1024) return false;
   p.ksplit = 1;                                      // one slice per workgroup: the parts live in its waves
   return launch_w8_stream_cfg<F16S, 1, KW, D, Epi>(p, lds, tiles, st);
 }

@@ -151,6 +151,41 @@ def test_gemv_split_k(gpu, F, fmt, ks):
         assert torch.equal(y, y2)
 
 
+@pytest.mark.parametrize("case", [
+    # N, K, M, ksplit, scale dtype, split over workgroups
+    (640, 10240, 3, 4, np.float16, True),    # the mixer's down projection: 5 workgroups per tile
+    (640, 10240, 1, 4, np.float32, True),
+    (1000, 4096, 5, 2, np.float32, True),    # N tail (rows past N), M > 4, 2 workgroups per tile
+    (520, 8192, 16, 8, np.float16, True),    # M = 16 (the last workgroup sums 256 outputs)
+    (520, 8192, 16, 4, np.float16, False),   # the slots exceed ksplit = 4's scratch: the MFMA core
+])
+def test_w8_splitk_workgroups(gpu, F, case, monkeypatch):
+    """W8 split-K of few tiles with K a multiple of 2048: each tile's K spread over
+    several workgroups, partials summed in slot order by the last one to arrive."""
+    n, k, M, ks, s_dtype, split = case
+    rng = np.random.default_rng(2000 + n + k + M + ks)
+    q, s = oq.quantize_w8(weights(rng, n, k))
+    s = s.astype(s_dtype)
+    x, _ = act(rng, M, k)
+    qd, sd, xd = dev(q), dev(s), bf16_dev(x)
+    y = F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32)
+    w_op = og.operand("w8", q, s.astype(np.float32))
+    exact = ordered.exact_sum(x, w_op)
+    bound = ordered.mfma_bound(x, w_op, max(ks, k // 2048))
+    assert np.all(np.abs(to_f32(y) - exact) <= bound), (np.abs(to_f32(y) - exact) / bound).max()
+    assert_tol(to_f32(y), og.matmul_f32(x, w_op), what=str(case))
+    for _ in range(3):                        # re-armed tickets, arrival order does not matter
+        assert torch.equal(y, F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32))
+    monkeypatch.setenv("FP4X_W8_STREAM", "0")
+    y_core = F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32)
+    monkeypatch.delenv("FP4X_W8_STREAM")
+    assert np.all(np.abs(to_f32(y_core) - exact) <= bound)
+    # another K decomposition than the core's: its fp32 sums differ in the last bits
+    assert (not torch.equal(y, y_core)) == split
+    print(f"N={n} K={k} M={M} ksplit={ks}: split={split}, max |y - exact| / bound = "
+          f"{(np.abs(to_f32(y) - exact) / bound).max():.3g}")
+
+
 def test_gemv_out_dtypes_and_strided_x(gpu, F):
     rng = np.random.default_rng(5)
     planes, w_op, _ = prep("mx8", rng, 256, 512)
