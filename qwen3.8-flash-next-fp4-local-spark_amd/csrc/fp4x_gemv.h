@@ -574,19 +574,20 @@ __device__ __forceinline__ void stage_x(uint16_t* lds, const uint16_t* x, int64_
 }
 
 // Split-K slot protocol.  Partial sums travel through LDS to wave 0, which
-// stores the tile's slot (coalesced), releases it at agent scope and takes the
-// tile ticket.  splitk_arrive returns true in the (single) last-arriving
-// workgroup of the tile, after an agent-scope acquire by every thread, so the
-// plain loads that follow see every slice's slot.
+// stores the tile's slot with device-coherent (agent-scope atomic) stores,
+// waits for them to complete and takes the tile ticket.  splitk_arrive
+// returns true in the (single) last-arriving workgroup of the tile, whose
+// threads then read the slots with device-coherent loads (ld_coherent): the
+// loads follow the ticket's return through the barrier, and no cache-wide
+// write-back or invalidate (an agent-scope fence on a multi-XCD GPU) is needed.
 __device__ __forceinline__ bool splitk_arrive(int* ticket, int ksplit) {
   __shared__ int last;
   if (threadIdx.x < 64) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // wave 0's slot stores have completed
     if (threadIdx.x == 0) last = (__hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                                   ksplit - 1);
   }
   __syncthreads();
-  if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   return last != 0;
 }
 

@@ -220,7 +220,9 @@ __device__ __forceinline__ void mfma_finish(const GemvLaunch& p, int b, int spli
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = g * 4 + i;
-      if (m < p.M && wrow) part[((int64_t)split * 16 + m) * p.N + row] = acc[i] * p.gs;
+      if (m < p.M && wrow)
+        __hip_atomic_store(part + ((int64_t)split * 16 + m) * p.N + row, acc[i] * p.gs, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   const int tiles = (p.N + 15) / 16;
@@ -237,7 +239,7 @@ __device__ __forceinline__ void mfma_finish(const GemvLaunch& p, int b, int spli
       for (int s0 = 0; s0 < p.ksplit; s0 += 8) {
         float v[8];
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) v[jj] = s0 + jj < p.ksplit ? src[(s0 + jj) * sstride] : 0.0f;
+        for (int jj = 0; jj < 8; ++jj) v[jj] = s0 + jj < p.ksplit ? ld_coherent(src + (s0 + jj) * sstride) : 0.0f;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
           if (s0 + jj < p.ksplit) tot = s0 + jj == 0 ? v[jj] : tot + v[jj];
