@@ -251,58 +251,85 @@ __device__ __forceinline__ void mfma_finish(const GemvLaunch& p, int b, int spli
   __syncthreads();
 }
 
-// Stage x[0:M, k0:k0+ks] (bf16) into LDS rows of xs elements.  Four 16-byte
-// loads per thread are issued before their LDS writes; the first round is
-// straight-line code, so its loads are not held back by a loop-entry wait on
-// weight loads already in flight.  Rows of x and of the stage are 16-byte
-// aligned (strides and k0 are multiples of 8 elements).
-__device__ __forceinline__ void mfma_stage_x(uint16_t* lds, const uint16_t* xg, int64_t x_stride, int M, int k0,
-                                             int ks, int xs) {
-  const int per_row = ks / 8, total = M * per_row;
+// Activation staging in two halves around the weight batch loads: the first
+// round's global loads (up to four 16-byte pieces per thread) go out before
+// the weights, so that the wait for them before their LDS writes leaves the
+// younger weight loads in flight (the wait counter counts in issue order).
+// Rows of x and of the stage are 16-byte aligned (strides and k0 are
+// multiples of 8 elements).
+typedef uint32_t xs_u32x4 __attribute__((ext_vector_type(4)));
+struct XStage {
+  xs_u32x4 v0, v1, v2, v3;
+};
+__device__ __forceinline__ xs_u32x4 xs_ld(const uint4* p) { return *reinterpret_cast<const xs_u32x4*>(p); }
+__device__ __forceinline__ uint4 xs_u4(xs_u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
+__device__ __forceinline__ void mfma_xfirst_load(XStage& r, const uint16_t* xg, int64_t x_stride, int M, int k0,
+                                                 int ks, bool t4) {
   const uint4* xg4 = reinterpret_cast<const uint4*>(xg + k0);
   const int64_t xrow4 = x_stride / 8;
-  uint4* lds4 = reinterpret_cast<uint4*>(lds);
-  const int lrow4 = xs / 8;
-  auto stage4 = [&](int i0) {
-    const int i1 = i0 + blockDim.x, i2 = i1 + blockDim.x, i3 = i2 + blockDim.x;
-    const int j0 = i0 < total ? i0 : total - 1, j1 = i1 < total ? i1 : total - 1,
-              j2 = i2 < total ? i2 : total - 1, j3 = i3 < total ? i3 : total - 1;
-    const uint4 v0 = xg4[(j0 / per_row) * xrow4 + j0 % per_row];
-    const uint4 v1 = xg4[(j1 / per_row) * xrow4 + j1 % per_row];
-    const uint4 v2 = xg4[(j2 / per_row) * xrow4 + j2 % per_row];
-    const uint4 v3 = xg4[(j3 / per_row) * xrow4 + j3 % per_row];
-    if (i0 < total) lds4[(i0 / per_row) * lrow4 + i0 % per_row] = v0;
-    if (i1 < total) lds4[(i1 / per_row) * lrow4 + i1 % per_row] = v1;
-    if (i2 < total) lds4[(i2 / per_row) * lrow4 + i2 % per_row] = v2;
-    if (i3 < total) lds4[(i3 / per_row) * lrow4 + i3 % per_row] = v3;
-  };
-  stage4(threadIdx.x);
-  for (int i0 = threadIdx.x + 4 * blockDim.x; i0 < total; i0 += 4 * blockDim.x) stage4(i0);
+  if (!t4) {
+    const int per_row = ks / 8, total = M * per_row;
+    auto at = [&](int h) {
+      const int i = threadIdx.x + h * blockDim.x, j = i < total ? i : total - 1;
+      return xs_ld(xg4 + (j / per_row) * xrow4 + j % per_row);
+    };
+    r.v0 = at(0); r.v1 = at(1); r.v2 = at(2); r.v3 = at(3);
+  } else {
+    const int per_row = ks / 16, total = M * per_row;
+    auto at = [&](int h, int e) {
+      const int i = threadIdx.x + h * blockDim.x, j = i < total ? i : total - 1;
+      const int m = j / per_row, q = j - m * per_row;
+      return xs_ld(xg4 + m * xrow4 + 2 * q + e);
+    };
+    r.v0 = at(0, 0); r.v1 = at(0, 1); r.v2 = at(1, 0); r.v3 = at(1, 1);
+  }
 }
-
-// The same staging with the k order of F::deq16t: a 4x4 transpose within each
-// 16-element block (position i holds element (i % 4) * 4 + i / 4).
-__device__ __forceinline__ void mfma_stage_x_t4(uint16_t* lds, const uint16_t* xg, int64_t x_stride, int M, int k0,
-                                                int ks, int xs) {
-  const int per_row = ks / 16, total = M * per_row;
+__device__ __forceinline__ void mfma_x_t4_pack(uint4 a, uint4 b, uint4& o, uint4& r) {
+  o.x = perm_b32(a.z, a.x, 0x05040100u);   // x0, x4
+  o.y = perm_b32(b.z, b.x, 0x05040100u);   // x8, x12
+  o.z = perm_b32(a.z, a.x, 0x07060302u);   // x1, x5
+  o.w = perm_b32(b.z, b.x, 0x07060302u);   // x9, x13
+  r.x = perm_b32(a.w, a.y, 0x05040100u);   // x2, x6
+  r.y = perm_b32(b.w, b.y, 0x05040100u);   // x10, x14
+  r.z = perm_b32(a.w, a.y, 0x07060302u);   // x3, x7
+  r.w = perm_b32(b.w, b.y, 0x07060302u);   // x11, x15
+}
+// Store the first round, then stage the remaining rounds (loads and stores).
+__device__ __forceinline__ void mfma_xrest(const XStage& r, uint16_t* lds, const uint16_t* xg, int64_t x_stride, int M,
+                                           int k0, int ks, int xs, bool t4) {
   const uint4* xg4 = reinterpret_cast<const uint4*>(xg + k0);
   const int64_t xrow4 = x_stride / 8;
   uint4* lds4 = reinterpret_cast<uint4*>(lds);
   const int lrow4 = xs / 8;
-  for (int i = threadIdx.x; i < total; i += blockDim.x) {
-    const int m = i / per_row, q = i - m * per_row;
-    const uint4 a = xg4[m * xrow4 + 2 * q], b = xg4[m * xrow4 + 2 * q + 1];   // elements 0-7, 8-15
-    uint4 o, r;
-    o.x = perm_b32(a.z, a.x, 0x05040100u);   // x0, x4
-    o.y = perm_b32(b.z, b.x, 0x05040100u);   // x8, x12
-    o.z = perm_b32(a.z, a.x, 0x07060302u);   // x1, x5
-    o.w = perm_b32(b.z, b.x, 0x07060302u);   // x9, x13
-    r.x = perm_b32(a.w, a.y, 0x05040100u);   // x2, x6
-    r.y = perm_b32(b.w, b.y, 0x05040100u);   // x10, x14
-    r.z = perm_b32(a.w, a.y, 0x07060302u);   // x3, x7
-    r.w = perm_b32(b.w, b.y, 0x07060302u);   // x11, x15
-    lds4[m * lrow4 + 2 * q] = o;
-    lds4[m * lrow4 + 2 * q + 1] = r;
+  if (!t4) {
+    const int per_row = ks / 8, total = M * per_row;
+    auto put = [&](int h, xs_u32x4 v) {
+      const int i = threadIdx.x + h * blockDim.x;
+      if (i < total) lds4[(i / per_row) * lrow4 + i % per_row] = xs_u4(v);
+    };
+    put(0, r.v0); put(1, r.v1); put(2, r.v2); put(3, r.v3);
+    for (int i = threadIdx.x + 4 * blockDim.x; i < total; i += blockDim.x)
+      lds4[(i / per_row) * lrow4 + i % per_row] = xg4[(i / per_row) * xrow4 + i % per_row];
+  } else {
+    const int per_row = ks / 16, total = M * per_row;
+    auto put = [&](int h, xs_u32x4 a, xs_u32x4 b) {
+      const int i = threadIdx.x + h * blockDim.x;
+      if (i < total) {
+        const int m = i / per_row, q = i - m * per_row;
+        uint4 o, rr;
+        mfma_x_t4_pack(xs_u4(a), xs_u4(b), o, rr);
+        lds4[m * lrow4 + 2 * q] = o;
+        lds4[m * lrow4 + 2 * q + 1] = rr;
+      }
+    };
+    put(0, r.v0, r.v1); put(1, r.v2, r.v3);
+    for (int i = threadIdx.x + 2 * blockDim.x; i < total; i += blockDim.x) {
+      const int m = i / per_row, q = i - m * per_row;
+      uint4 o, rr;
+      mfma_x_t4_pack(xg4[m * xrow4 + 2 * q], xg4[m * xrow4 + 2 * q + 1], o, rr);
+      lds4[m * lrow4 + 2 * q] = o;
+      lds4[m * lrow4 + 2 * q + 1] = rr;
+    }
   }
 }
 
@@ -344,20 +371,33 @@ __global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
     const uint16_t* xg = p.x + b * p.x_bstride;
     const uint16_t* xl0 = XL ? lds + xrow * xs + CPS * cw * F::KPC : xg + xrow * p.x_stride + k0 + CPS * cw * F::KPC;
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int bi = 0; bi < nb; ++bi) {
+    // The activations' first round of loads goes out ahead of the first weight
+    // batch of every item (unconditionally: a load under a branch would be
+    // waited for at the branch's join), and is written to LDS, for a new batch
+    // entry, while the weights are in flight.
+    {
+      XStage xr;
+      if constexpr (XL) {
+        mfma_xfirst_load(xr, xg, p.x_stride, p.M, k0, ks, HasXPerm<F>::value);
+        asm volatile("" ::: "memory");                  // keep the issue order: activations, then weights
+      }
       MfmaBatch<F, CPS> A;
-      if constexpr (FULL) mfma_load_full<F, DP, CPS>(A, F::lane(pa, rowc, c0 + CPS * (cw + bi * NJ * DP)));
-      else mfma_load_general<F, DP, CPS>(A, pa, rowc, c0, cw, bi * NJ, J, nch);
+      if constexpr (FULL) mfma_load_full<F, DP, CPS>(A, F::lane(pa, rowc, c0 + CPS * cw));
+      else mfma_load_general<F, DP, CPS>(A, pa, rowc, c0, cw, 0, J, nch);
       if constexpr (XL) {
         if (b != cur_b) {
-          // new batch entry: stage its activations while the weight loads are in flight
           if (cur_b >= 0) __syncthreads();               // every wave is done with the previous entry's x
-          if constexpr (HasXPerm<F>::value) mfma_stage_x_t4(lds, xg, p.x_stride, p.M, k0, ks, xs);
-          else mfma_stage_x(lds, xg, p.x_stride, p.M, k0, ks, xs);
+          mfma_xrest(xr, lds, xg, p.x_stride, p.M, k0, ks, xs, HasXPerm<F>::value);
           __syncthreads();
           cur_b = b;
         }
       }
+      mfma_compute<F, DP, CPS, FULL, XL && HasXPerm<F>::value>(A, xl0, 0, J, cw, nch, acc);
+    }
+    for (int bi = 1; bi < nb; ++bi) {
+      MfmaBatch<F, CPS> A;
+      if constexpr (FULL) mfma_load_full<F, DP, CPS>(A, F::lane(pa, rowc, c0 + CPS * (cw + bi * NJ * DP)));
+      else mfma_load_general<F, DP, CPS>(A, pa, rowc, c0, cw, bi * NJ, J, nch);
       mfma_compute<F, DP, CPS, FULL, XL && HasXPerm<F>::value>(A, xl0 + bi * NJ * CPS * DP * F::KPC, bi * NJ, J, cw,
                                                                 nch, acc);
     }
