@@ -60,19 +60,23 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
   const bool xon = n < p.M;
   const uint16_t* xl0 = lds + (xon ? n : 0) * p.K + CPS * cw * F::KPC;
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int bi = 0; bi < nb; ++bi) {
+  {
+    // the bottleneck activations' first staging round goes out ahead of the
+    // first weight batch and is written to LDS while the weights are in flight
+    XStage xr;
+    mfma_xfirst_load(xr, p.bot, p.bot_stride, p.M, 0, p.K, false);
+    asm volatile("" ::: "memory");                    // keep the issue order: activations, then weights
+    MfmaBatch<F, CPS> cb;
+    if constexpr (FULL) mfma_load_full<F, DP, CPS>(cb, F::lane(p.pa, row, CPS * cw));
+    else mfma_load_general<F, DP, CPS>(cb, p.pa, row, 0, cw, 0, J, nch);
+    mfma_xrest(xr, lds, p.bot, p.bot_stride, p.M, 0, p.K, p.K, false);
+    __syncthreads();
+    mfma_compute<F, DP, CPS, FULL, false>(cb, xl0, 0, J, cw, nch, acc);
+  }
+  for (int bi = 1; bi < nb; ++bi) {
     MfmaBatch<F, CPS> cb;
     if constexpr (FULL) mfma_load_full<F, DP, CPS>(cb, F::lane(p.pa, row, CPS * (cw + bi * NJ * DP)));
     else mfma_load_general<F, DP, CPS>(cb, p.pa, row, 0, cw, bi * NJ, J, nch);
-    if (bi == 0) {
-      // stage the bottleneck activations while the first weight batch is in flight
-      const int per_row = p.K / 8;
-      for (int i = threadIdx.x; i < p.M * per_row; i += blockDim.x) {
-        const int m = i / per_row, q = i - m * per_row;
-        reinterpret_cast<uint4*>(lds + m * p.K)[q] = *reinterpret_cast<const uint4*>(p.bot + m * p.bot_stride + q * 8);
-      }
-      __syncthreads();
-    }
     mfma_compute<F, DP, CPS, FULL, false>(cb, xl0 + bi * NJ * CPS * DP * F::KPC, bi * NJ, J, cw, nch, acc);
   }
   // wave-order reduction within each row group
