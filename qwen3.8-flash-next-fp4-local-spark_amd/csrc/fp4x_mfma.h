@@ -168,10 +168,12 @@ __device__ __forceinline__ void mfma_compute(const MfmaBatch<F, CPS>& b, XPtr xl
     }
 }
 
-// Sum the KW waves' 16x16 tiles in wave order; the result is valid in wave 0.
+// Sum the KW waves' 16x16 tiles in wave order; the result is valid in wave 0
+// (wave: the index within the tile's group of KW waves, red: the group's
+// reduction buffer).  Every wave of the workgroup takes part in the barriers.
 template <int KW>
-__device__ __forceinline__ f32x4_t mfma_wave_reduce(f32x4_t acc, float* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ f32x4_t mfma_wave_reduce(f32x4_t acc, float* red, int wave) {
+  const int lane = threadIdx.x & 63;
   if constexpr (KW == 1) return acc;
   if (wave > 0) reinterpret_cast<f32x4_t*>(red)[(wave - 1) * 64 + lane] = acc;
   lds_barrier();
@@ -190,22 +192,25 @@ __device__ __forceinline__ f32x4_t mfma_wave_reduce(f32x4_t acc, float* red) {
 // MFMA fragment fall into different banks.
 __host__ __device__ inline int mfma_xstride(int ks) { return ks + 8; }
 
-// LDS layout: [x: M x xstride bf16 (XL only)] [red: (KW-1) x 64 x 4 fp32]
-__host__ __device__ inline size_t mfma_lds_bytes(int M, int ks, int KW, bool xl) {
+// LDS layout: [x: M x xstride bf16 (XL only)] [red: G x (KW-1) x 64 x 4 fp32]
+__host__ __device__ inline size_t mfma_lds_bytes(int M, int ks, int KW, bool xl, int G = 1) {
   size_t x = xl ? (size_t)M * mfma_xstride(ks) * 2 : 0;
   x = (x + 15) & ~(size_t)15;
-  return x + (size_t)(KW > 1 ? KW - 1 : 0) * 64 * 16;
+  return x + (size_t)G * (KW > 1 ? KW - 1 : 0) * 64 * 16;
 }
 
 // Finish tile t: wave reduce, then the epilogue (ksplit == 1) or the split-K
 // slot write and last-arrival reduction.
+// With several tile groups per workgroup (ksplit == 1 only), wave is the index
+// within the group and live is false for a group's padding round.
 template <int KW, class Epi>
-__device__ __forceinline__ void mfma_finish(const GemvLaunch& p, int b, int split, int t, f32x4_t acc, float* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ void mfma_finish(const GemvLaunch& p, int b, int split, int t, f32x4_t acc, float* red,
+                                            int wave, bool live) {
+  const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int64_t row = (int64_t)t * 16 + n;
-  const bool wrow = row < p.N;
-  acc = mfma_wave_reduce<KW>(acc, red);
+  const bool wrow = row < p.N && live;
+  acc = mfma_wave_reduce<KW>(acc, red, wave);
   // lane of wave 0 holds D[m = g*4 + i][n]
   if (p.ksplit == 1) {
     if (wave == 0 && wrow) {
@@ -339,29 +344,39 @@ __device__ __forceinline__ void mfma_xrest(const XStage& r, uint16_t* lds, const
 // and all carry the same number of items.  The activations of an entry are
 // staged once per run of items of that entry.  p.J: chunks per lane per
 // tile (slots), p.nb: register batches per tile.
-template <class F, int KW, int CPS, bool FULL, bool XL, class Epi>
-__global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
+//
+// G > 1 (single matrix, ksplit == 1): the workgroup's waves form G groups of
+// KW that work on G items at once, sharing one activation stage: for large
+// M * K the stage limits a CU to one workgroup, whose tiles would otherwise
+// run one after another, each with its memory latency exposed.  Every group
+// runs the same number of rounds; a round past the workgroup's items
+// recomputes its last item and stores nothing.
+template <class F, int KW, int CPS, bool FULL, bool XL, class Epi, int G = 1>
+__global__ __launch_bounds__(64 * KW * G) void gemv_mfma_kernel(GemvLaunch p) {
   constexpr int DP = 4 * KW;                // slots between a lane's consecutive slots
   constexpr int NJ = kNJ;
   extern __shared__ __align__(16) uint16_t lds[];
   const int split = blockIdx.y;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave_all = threadIdx.x >> 6;
+  const int grp = G > 1 ? wave_all / KW : 0, wave = wave_all - grp * KW;
   const int n = lane & 15, g = lane >> 4;
   const int tiles = (p.N + 15) / 16, items = p.batch * tiles;
-  int it = blockIdx.x * p.per_wg;
-  const int iend = it + p.per_wg < items ? it + p.per_wg : items;
-  if (it >= iend) return;
+  const int it0 = blockIdx.x * p.per_wg;
+  const int iend = it0 + p.per_wg < items ? it0 + p.per_wg : items;
+  if (it0 >= iend) return;
   const int ks = p.pa.K / p.ksplit, k0 = split * ks, nch = ks / F::KPC, c0 = k0 / F::KPC;
   const int cw = wave * 4 + g;              // this lane's first slot within the slice
   const int J = p.J, nb = p.nb;
   const int xs = mfma_xstride(ks);
   const size_t xbytes = XL ? (((size_t)p.M * xs * 2 + 15) & ~(size_t)15) : 0;
-  float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + xbytes);
+  float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + xbytes) + grp * (KW > 1 ? KW - 1 : 0) * 256;
   const bool xon = n < p.M;
   const int xrow = xon ? n : 0;
   int cur_b = -1;
-  for (; it < iend; ++it) {
-    const int b = it / tiles, t = it - b * tiles;
+  for (int it = it0 + grp; it - grp < iend; it += G) {
+    const bool live = it < iend;
+    const int itc = live ? it : iend - 1;
+    const int b = itc / tiles, t = itc - b * tiles;
     PlaneArgs pa = p.pa;
     pa.w0 += b * p.w0_bstride;
     if (pa.w1) pa.w1 += b * p.w1_bstride;
@@ -401,7 +416,7 @@ __global__ __launch_bounds__(64 * KW) void gemv_mfma_kernel(GemvLaunch p) {
       mfma_compute<F, DP, CPS, FULL, XL && HasXPerm<F>::value>(A, xl0 + bi * NJ * CPS * DP * F::KPC, bi * NJ, J, cw,
                                                                 nch, acc);
     }
-    mfma_finish<KW, Epi>(p, b, split, t, acc, red);
+    mfma_finish<KW, Epi>(p, b, split, t, acc, red, wave, live);
   }
 }
 
@@ -410,21 +425,21 @@ int device_cus();
 // Optional cap on resident waves per CU from FP4X_WAVES_PER_CU (0: none).
 int waves_per_cu_cap();
 
-template <class F, int KW, int CPS, bool FULL, bool XL, class Epi>
+template <class F, int KW, int CPS, bool FULL, bool XL, class Epi, int G = 1>
 void launch_mfma_kw(GemvLaunch p, int batch, size_t lds, hipStream_t st) {
-  auto kern = gemv_mfma_kernel<F, KW, CPS, FULL, XL, Epi>;
+  auto kern = gemv_mfma_kernel<F, KW, CPS, FULL, XL, Epi, G>;
   // resident workgroups per CU for this kernel and LDS size (cached per LDS size)
   static int occ_cache[97];
   const int key = (int)((lds + 1023) / 1024);
   int occ = key < 97 ? occ_cache[key] : 0;
   if (occ <= 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(kern), 64 * KW, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(kern), 64 * KW * G, lds) !=
             hipSuccess || occ < 1)
       occ = 1;
     if (key < 97) occ_cache[key] = occ;
   }
   const int cap = waves_per_cu_cap();
-  if (cap > 0 && occ * KW > cap) occ = cap / KW > 0 ? cap / KW : 1;
+  if (cap > 0 && occ * KW * G > cap) occ = cap / (KW * G) > 0 ? cap / (KW * G) : 1;
   const int tiles = (p.N + 15) / 16;
   const int64_t items = (int64_t)batch * tiles;
   int64_t slots = (int64_t)device_cus() * occ / p.ksplit;
@@ -433,7 +448,22 @@ void launch_mfma_kw(GemvLaunch p, int batch, size_t lds, hipStream_t st) {
   p.batch = batch;
   p.per_wg = (int)per;
   const int gx = (int)((items + per - 1) / per);
-  hipLaunchKernelGGL(kern, dim3(gx, p.ksplit, 1), dim3(64 * KW), lds, st, p);
+  hipLaunchKernelGGL(kern, dim3(gx, p.ksplit, 1), dim3(64 * KW * G), lds, st, p);
+}
+
+// Tile groups (see gemv_mfma_kernel): single matrix, ksplit == 1, full slots,
+// single chunks, activations staged in LDS.
+// At most 8 waves per workgroup (KW * G <= 8): 16-wave groupings spill.
+template <class F, class Epi>
+void launch_mfma_grouped(const GemvLaunch& p, int KW, int G, size_t lds, hipStream_t st) {
+  if (G == 4) {
+    if (KW == 1) launch_mfma_kw<F, 1, 1, true, true, Epi, 4>(p, 1, lds, st);
+    else launch_mfma_kw<F, 2, 1, true, true, Epi, 4>(p, 1, lds, st);
+  } else {
+    if (KW == 1) launch_mfma_kw<F, 1, 1, true, true, Epi, 2>(p, 1, lds, st);
+    else if (KW == 2) launch_mfma_kw<F, 2, 1, true, true, Epi, 2>(p, 1, lds, st);
+    else launch_mfma_kw<F, 4, 1, true, true, Epi, 2>(p, 1, lds, st);
+  }
 }
 
 template <class F, int KW, int CPS, bool FULL, class Epi>
@@ -477,7 +507,20 @@ int launch_gemv_mfma(const GemvLaunch& p0, int batch, hipStream_t st) {
   p.J = ((chunks + cpsu - 1) / cpsu + 4 * KW - 1) / (4 * KW);
   p.nb = (p.J + kNJ - 1) / kNJ;
   const bool xl = mfma_lds_bytes(p.M, ks, KW, true) <= 96 * 1024;
-  const size_t lds = mfma_lds_bytes(p.M, ks, KW, xl);
+  // Tile groups when the activation stage leaves room for one workgroup per
+  // CU and the tiles outnumber the CUs: G tiles at once, G <= 4, KW * G <= 8.
+  int G = 1;
+  if (full && xl && cps == 1 && batch == 1 && p.ksplit == 1 && mfma_lds_bytes(p.M, ks, KW, true) > 80 * 1024) {
+    const int64_t tiles = (p.N + 15) / 16, cus = device_cus();
+    const int64_t per_cu = (tiles + cus - 1) / cus;
+    while (G < 4 && 2 * G <= per_cu && KW * 2 * G <= 8 && mfma_lds_bytes(p.M, ks, KW, true, 2 * G) <= 160 * 1024)
+      G *= 2;
+  }
+  const size_t lds = mfma_lds_bytes(p.M, ks, KW, xl, G);
+  if (G > 1) {
+    launch_mfma_grouped<F, Epi>(p, KW, G, lds, st);
+    return check_launch("gemv_mfma");
+  }
   if (!full) launch_mfma_xl<F, kMaxKW, 1, false, Epi>(p, batch, lds, xl, st);
   else if constexpr (MfmaTune<F>::PAIRS) {
     if (cps == 2) launch_mfma_full<F, 2, Epi>(p, KW, batch, lds, xl, st);

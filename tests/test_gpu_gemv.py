@@ -151,6 +151,26 @@ def test_gemv_split_k(gpu, F, fmt, ks):
         assert torch.equal(y, y2)
 
 
+@pytest.mark.parametrize("fmt", ["mx8", "w8", "w6", "nv4"])
+@pytest.mark.parametrize("M", [16, 12])
+def test_gemv_tile_groups(gpu, F, fmt, M):
+    """Wide matrices at M = 16, where the activation stage leaves room for one
+    workgroup per CU and each workgroup runs several tiles at once in wave
+    groups (N = 8232: 515 tiles, so the last round of a workgroup has a
+    padding group); M = 12 is the single-group control."""
+    rng = np.random.default_rng(300 + M)
+    n, k = 8232, 2560
+    planes, w_op, gs = prep(fmt, rng, n, k)
+    x, _ = act(rng, M, k)
+    y = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
+    exact = ordered.exact_sum(x, w_op) * gs
+    bound = ordered.mfma_bound(x, w_op) * abs(gs)
+    assert np.all(np.abs(y - exact) <= bound), (np.abs(y - exact) / bound).max()
+    assert_tol(y, og.matmul_f32(x, w_op) * np.float32(gs), what=f"{fmt} M={M}")
+    y2 = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+
+
 @pytest.mark.parametrize("case", [
     # N, K, M, ksplit, scale dtype, split over workgroups
     (640, 10240, 3, 4, np.float16, True),    # the mixer's down projection: 5 workgroups per tile
