@@ -63,7 +63,7 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
   {
     // the bottleneck activations' first staging round goes out ahead of the
     // first weight batch and is written to LDS while the weights are in flight
-    XStage xr;
+    XStage<4> xr;
     mfma_xfirst_load(xr, p.bot, p.bot_stride, p.M, 0, p.K, false);
     asm volatile("" ::: "memory");                    // keep the issue order: activations, then weights
     MfmaBatch<F, CPS> cb;

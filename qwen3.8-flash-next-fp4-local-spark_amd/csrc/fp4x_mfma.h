@@ -263,30 +263,35 @@ __device__ __forceinline__ void mfma_finish(const GemvLaunch& p, int b, int spli
 // Rows of x and of the stage are 16-byte aligned (strides and k0 are
 // multiples of 8 elements).
 typedef uint32_t xs_u32x4 __attribute__((ext_vector_type(4)));
+// XR: 16-byte pieces per thread in the first round (plain layout; the 4x4
+// transposed layout takes XR / 2 blocks of two pieces).
+template <int XR>
 struct XStage {
-  xs_u32x4 v0, v1, v2, v3;
+  xs_u32x4 v[XR];
 };
 __device__ __forceinline__ xs_u32x4 xs_ld(const uint4* p) { return *reinterpret_cast<const xs_u32x4*>(p); }
 __device__ __forceinline__ uint4 xs_u4(xs_u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
-__device__ __forceinline__ void mfma_xfirst_load(XStage& r, const uint16_t* xg, int64_t x_stride, int M, int k0,
+template <int XR>
+__device__ __forceinline__ void mfma_xfirst_load(XStage<XR>& r, const uint16_t* xg, int64_t x_stride, int M, int k0,
                                                  int ks, bool t4) {
   const uint4* xg4 = reinterpret_cast<const uint4*>(xg + k0);
   const int64_t xrow4 = x_stride / 8;
   if (!t4) {
     const int per_row = ks / 8, total = M * per_row;
-    auto at = [&](int h) {
+#pragma unroll
+    for (int h = 0; h < XR; ++h) {
       const int i = threadIdx.x + h * blockDim.x, j = i < total ? i : total - 1;
-      return xs_ld(xg4 + (j / per_row) * xrow4 + j % per_row);
-    };
-    r.v0 = at(0); r.v1 = at(1); r.v2 = at(2); r.v3 = at(3);
+      r.v[h] = xs_ld(xg4 + (j / per_row) * xrow4 + j % per_row);
+    }
   } else {
     const int per_row = ks / 16, total = M * per_row;
-    auto at = [&](int h, int e) {
+#pragma unroll
+    for (int h = 0; h < XR / 2; ++h) {
       const int i = threadIdx.x + h * blockDim.x, j = i < total ? i : total - 1;
       const int m = j / per_row, q = j - m * per_row;
-      return xs_ld(xg4 + m * xrow4 + 2 * q + e);
-    };
-    r.v0 = at(0, 0); r.v1 = at(0, 1); r.v2 = at(1, 0); r.v3 = at(1, 1);
+      r.v[2 * h] = xs_ld(xg4 + m * xrow4 + 2 * q);
+      r.v[2 * h + 1] = xs_ld(xg4 + m * xrow4 + 2 * q + 1);
+    }
   }
 }
 __device__ __forceinline__ void mfma_x_t4_pack(uint4 a, uint4 b, uint4& o, uint4& r) {
@@ -300,35 +305,36 @@ __device__ __forceinline__ void mfma_x_t4_pack(uint4 a, uint4 b, uint4& o, uint4
   r.w = perm_b32(b.w, b.y, 0x07060302u);   // x11, x15
 }
 // Store the first round, then stage the remaining rounds (loads and stores).
-__device__ __forceinline__ void mfma_xrest(const XStage& r, uint16_t* lds, const uint16_t* xg, int64_t x_stride, int M,
-                                           int k0, int ks, int xs, bool t4) {
+template <int XR>
+__device__ __forceinline__ void mfma_xrest(const XStage<XR>& r, uint16_t* lds, const uint16_t* xg, int64_t x_stride,
+                                           int M, int k0, int ks, int xs, bool t4) {
   const uint4* xg4 = reinterpret_cast<const uint4*>(xg + k0);
   const int64_t xrow4 = x_stride / 8;
   uint4* lds4 = reinterpret_cast<uint4*>(lds);
   const int lrow4 = xs / 8;
   if (!t4) {
     const int per_row = ks / 8, total = M * per_row;
-    auto put = [&](int h, xs_u32x4 v) {
+#pragma unroll
+    for (int h = 0; h < XR; ++h) {
       const int i = threadIdx.x + h * blockDim.x;
-      if (i < total) lds4[(i / per_row) * lrow4 + i % per_row] = xs_u4(v);
-    };
-    put(0, r.v0); put(1, r.v1); put(2, r.v2); put(3, r.v3);
-    for (int i = threadIdx.x + 4 * blockDim.x; i < total; i += blockDim.x)
+      if (i < total) lds4[(i / per_row) * lrow4 + i % per_row] = xs_u4(r.v[h]);
+    }
+    for (int i = threadIdx.x + XR * blockDim.x; i < total; i += blockDim.x)
       lds4[(i / per_row) * lrow4 + i % per_row] = xg4[(i / per_row) * xrow4 + i % per_row];
   } else {
     const int per_row = ks / 16, total = M * per_row;
-    auto put = [&](int h, xs_u32x4 a, xs_u32x4 b) {
+#pragma unroll
+    for (int h = 0; h < XR / 2; ++h) {
       const int i = threadIdx.x + h * blockDim.x;
       if (i < total) {
         const int m = i / per_row, q = i - m * per_row;
         uint4 o, rr;
-        mfma_x_t4_pack(xs_u4(a), xs_u4(b), o, rr);
+        mfma_x_t4_pack(xs_u4(r.v[2 * h]), xs_u4(r.v[2 * h + 1]), o, rr);
         lds4[m * lrow4 + 2 * q] = o;
         lds4[m * lrow4 + 2 * q + 1] = rr;
       }
-    };
-    put(0, r.v0, r.v1); put(1, r.v2, r.v3);
-    for (int i = threadIdx.x + 2 * blockDim.x; i < total; i += blockDim.x) {
+    }
+    for (int i = threadIdx.x + (XR / 2) * blockDim.x; i < total; i += blockDim.x) {
       const int m = i / per_row, q = i - m * per_row;
       uint4 o, rr;
       mfma_x_t4_pack(xg4[m * xrow4 + 2 * q], xg4[m * xrow4 + 2 * q + 1], o, rr);
@@ -391,7 +397,9 @@ __global__ __launch_bounds__(64 * KW * G) void gemv_mfma_kernel(GemvLaunch p) {
     // waited for at the branch's join), and is written to LDS, for a new batch
     // entry, while the weights are in flight.
     {
-      XStage xr;
+      // first-round pieces per thread: 12 with tile groups (chosen for large
+      // activation stages: M = 16, K = 2560 in one round of 8 waves), else 4
+      XStage<(G > 1 ? 12 : 4)> xr;
       if constexpr (XL) {
         mfma_xfirst_load(xr, xg, p.x_stride, p.M, k0, ks, HasXPerm<F>::value);
         asm volatile("" ::: "memory");                  // keep the issue order: activations, then weights
