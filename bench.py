@@ -169,10 +169,15 @@ def bench_hc(F, torch, dev, out, layers=97):
         _, bot = fx.down(x, m[0], m[1], LR, HC, (32, 256, KS, 4))
         F.HCFused.up(bot, m[2], m[3], x, HC, (8, 64, 4))
     us_pair = graph_time([lambda m=m: both(m) for m in mix], replays=5)
+    # the whole mixer as one call (one launch per mixer at this shape)
+    us_mix = graph_time([lambda m=m: fx.mix(x, m[0], m[1], LR, HC, m[2], m[3], x, (32, 256, KS, 4)) for m in mix],
+                        replays=5)
     out["D_hc_down_640x10240_M3"] = entry(us_down, down_b)
     out["D_hc_up_10240x640_M3"] = entry(us_up, up_b)
     out["D_hc_mixer_97_layers_M3"] = entry(us_pair * layers, (down_b + up_b) * layers)
     out["D_hc_mixer_97_layers_M3"]["us_per_mixer"] = round(us_pair, 3)
+    out["D_hc_mix_one_call_97_layers_M3"] = entry(us_mix * layers, (down_b + up_b) * layers)
+    out["D_hc_mix_one_call_97_layers_M3"]["us_per_mixer"] = round(us_mix, 3)
 
 
 def bench_head(F, torch, dev, out, vectors=1000):

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 2
+#define FP4X_ABI_VERSION 3
 
 enum {
   FP4X_OK = 0,
@@ -150,6 +150,22 @@ int fp4x_hc_down(const void* x, int64_t x_stride, const void* q, const void* s, 
  * [HCFused.up -> _hc_up, x/fp4x_kernels.py:519-526, :470-493] */
 int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* si, int s_dtype, const void* nrm,
                int64_t nrm_stride, void* out, int M, int K, int H, int hc, int bj, void* stream);
+
+/* Whole mixer, fp4x_hc_down followed by fp4x_hc_up on its bottleneck
+ * (bot [M, lr] contiguous, up K = lr, one scale dtype for both), with results
+ * bit-identical to those two calls.  When both halves take their planned
+ * decompositions it runs as one launch (the up weights stream while the down
+ * projection runs); otherwise it makes the two calls.  tickets: n_tickets
+ * int32, zero before the first call and re-armed by every call; the single
+ * launch needs at least round_up(ceil(N / 16), 64) + 32 * (CUs + 1) (a count
+ * and one 128-byte flag line per workgroup, after the tile tickets) and makes
+ * the two calls with fewer.  FP4X_HC_MIX=0 forces the two calls.
+ * [HCFused.down then HCFused.up as the plugin's fused mixer calls them,
+ *  x/fp4patch.py:217-218 (_mix_fused); x/fp4x_kernels.py:503-526] */
+int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* di, void* bot,
+                int M, int N, int K, int lr, int hc, int ksplit, float* part, int* tickets, int n_tickets,
+                const void* qi, const void* si, const void* nrm, int64_t nrm_stride, void* out, int H, int bj,
+                void* stream);
 
 /* Unfused mixer epilogues (the b12x run_scaled_silu / run_gate_mean ops the
  * plugin calls, x/fp4patch.py:238-246, at the rounding points of

@@ -36,13 +36,15 @@ _SIGS = {
     "fp4x_refine_mx8": ([_P, _I, _I64, _P, _P, _I, _I, _P, _P, _I, _I, _P], _I),
     "fp4x_hc_down": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "fp4x_hc_up": ([_P, _I64, _P, _P, _I, _P, _I64, _P, _I, _I, _I, _I, _I, _P], _I),
+    "fp4x_hc_mix": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P, _I64, _P, _I, _I,
+                     _P], _I),
     "fp4x_hc_scaled_silu": ([_P, _I64, _P, _I, _I, _I, _P], _I),
     "fp4x_hc_gate_mean": ([_P, _I64, _P, _I64, _P, _I, _I, _I, _P], _I),
     "fp4x_dequant_bf16": ([_I, _P, _P, _P, _I, _I, _I, _P, _P], _I),
     "fp4x_mx8_dequant": ([_P, _P, _I, _I, _P, _P], _I),
     "fp4x_dot2_bf16": ([_P, _P, _P, _P, _I, _P], _I),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _LIB = None
 

@@ -151,6 +151,164 @@ static int hc_fail(const char* msg) {
 
 static bool al(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
 
+
+// ---------------------------------------------------------------------------
+// Single-launch mixer: the down projection (split over C workgroups per tile,
+// exactly w8_splitk_kernel's decomposition) and the up projection with its
+// gate/stream-mean epilogue (exactly hc_up_mfma_kernel's per-row sums) in one
+// launch, so a mixer pays one launch and the up weights stream while the down
+// projection runs.
+//   * Workgroups 0..D-1 (D = down tiles x C) run one down item each.  The
+//     last arriver of a down tile stores di and, device-coherently, the
+//     bottleneck, waits for those stores and counts the tile in sync[0].
+//   * Every workgroup (8 waves) then issues the weight loads of its R up
+//     tiles (R = 8 / waves per up tile), which stream while it waits.
+//     (Issued first, they would share each CU's bandwidth with the down
+//     loads and lengthen the critical path.)
+//   * The workgroup whose count completes the down tiles re-arms the count
+//     and raises one flag per workgroup, each on a 128-byte line of its own.
+//     One lane per workgroup waits for its flag (s_sleep between reads, at
+//     most spin_limit reads) and lowers it; the workgroup then stages the
+//     bottleneck with device-coherent loads and runs its up tiles.  (200
+//     workgroups polling one shared counter instead made a hot spot that cost
+//     about 13 us per mixer.)
+//   * The down items sit in the lowest workgroup indices, which the hardware
+//     dispatches first, so the wait never depends on a workgroup that could
+//     not get a CU; the grid is at most one workgroup per CU.
+//   * A wait that reaches spin_limit (which would need another kernel
+//     holding the CUs for about a second) writes NaN to that workgroup's
+//     outputs.
+constexpr int kMixFlagStride = 32;               // int32 between flags: one 128-byte line each
+
+struct HcMixArgs {
+  GemvLaunch d;          // down: x, q, s, di (out), bot (out2), lr, hc, split-K slots and tickets
+  HcUpArgs u;            // up: bot [M, lr] contiguous, interleaved q/s, normalized, out
+  int* sync;             // [0] down tiles done, [kMixFlagStride * (w + 1)] flag of workgroup w; zero between calls
+  int C, D, tiles_d, R, spin_limit;
+};
+
+template <bool F16S, int KW, int CPS>
+__global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
+  using F = FmtW8<F16S>;
+  constexpr int DP = 4 * KW;
+  extern __shared__ __align__(16) uint16_t lds[];
+  __shared__ int s_ok;
+  char* base = reinterpret_cast<char*>(lds);
+  const HcUpArgs& u = a.u;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int T = u.hc * u.bj, WT = (T / 16) * KW;
+  const int slot = wave / WT, ws = wave - slot * WT, grp = ws / KW, wv = ws - grp * KW;
+  const int ntu = u.H / u.bj, tu = blockIdx.x * a.R + slot;
+  const int tuc = tu < ntu ? tu : ntu - 1;          // padding slots recompute the last tile, store nothing
+  const int nch = u.K / F::KPC, cw = wv * 4 + g;
+  const int J = ((nch + CPS - 1) / CPS + DP - 1) / DP;
+  const int64_t urow = (int64_t)tuc * T + grp * 16 + n;
+
+  // 1. one down item in each of the first D workgroups (the critical path:
+  //    its loads go out first)
+  if ((int)blockIdx.x < a.D) {
+    const int t = blockIdx.x / a.C, c = blockIdx.x - t * a.C;
+    if (w8_splitk_item<F16S, 8, 2, EpiHcDownShared>(a.d, a.C, t, c, base)) {
+      wait_vmcnt<0>();                              // the tile's bottleneck stores have completed
+      int old = 0;
+      if (lane == 0) old = __hip_atomic_fetch_add(a.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __builtin_amdgcn_readfirstlane(old);
+      if (old == a.tiles_d - 1) {                   // the last down tile: re-arm the count, raise every flag
+        if (lane == 0) __hip_atomic_store(a.sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int w = lane; w < (int)gridDim.x; w += 64)
+          __hip_atomic_store(a.sync + kMixFlagStride * (w + 1), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+
+  // 2. the up tiles' weights (one batch per lane) stream during the wait
+  MfmaBatch<F, CPS> cb;
+  mfma_load_full<F, DP, CPS>(cb, F::lane(u.pa, urow, CPS * cw));
+  __syncthreads();
+
+  // 3. wait for this workgroup's flag, then lower it for the next call
+  if (threadIdx.x == 0) {
+    int* flag = a.sync + kMixFlagStride * (blockIdx.x + 1);
+    int f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int it = 0; f == 0 && it < a.spin_limit; ++it) {
+      __builtin_amdgcn_s_sleep(4);
+      f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    s_ok = f != 0;
+    __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  const bool ok = s_ok != 0;
+
+  // 4. the bottleneck [M, K] (K = lr), device-coherent loads, into LDS rows of K
+  const int K = u.K;
+  if (ok) {
+    const uint32_t* bg = reinterpret_cast<const uint32_t*>(u.bot);
+    uint32_t* bl = reinterpret_cast<uint32_t*>(lds);
+    for (int i = threadIdx.x; i < u.M * K / 2; i += blockDim.x)
+      bl[i] = __hip_atomic_load(bg + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+
+  // 5. up tiles: the MFMA order and wave-order reduction of hc_up_mfma_kernel
+  const size_t xbytes = ((size_t)u.M * K * 2 + 15) & ~(size_t)15;
+  float* red = reinterpret_cast<float*>(base + xbytes);
+  float* gl = red + (size_t)a.R * (T / 16) * (KW > 1 ? KW - 1 : 0) * 256;
+  const bool xon = n < u.M;
+  const uint16_t* xl0 = lds + (xon ? n : 0) * K + CPS * cw * F::KPC;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  mfma_compute<F, DP, CPS, true, false>(cb, xl0, 0, J, cw, nch, acc);
+  float* gred = red + ((size_t)slot * (T / 16) + grp) * (KW > 1 ? KW - 1 : 0) * 256;
+  if (wv > 0) reinterpret_cast<f32x4_t*>(gred)[(wv - 1) * 64 + lane] = acc;
+  __syncthreads();
+  if (wv == 0) {
+#pragma unroll
+    for (int w = 1; w < KW; ++w) {
+      const f32x4_t o = reinterpret_cast<const f32x4_t*>(gred)[(w - 1) * 64 + lane];
+      acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
+    }
+    float* gls = gl + (size_t)slot * u.M * T;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (g * 4 + i < u.M) gls[(g * 4 + i) * T + grp * 16 + n] = round_bf16(acc[i]);
+  }
+  __syncthreads();
+  const int per_slot = u.M * u.bj;
+  for (int e = threadIdx.x; e < a.R * per_slot; e += blockDim.x) {
+    const int sl = e / per_slot, r = e - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
+    const int tsl = blockIdx.x * a.R + sl;
+    if (tsl >= ntu) continue;
+    const int64_t j = (int64_t)tsl * u.bj + jj;
+    const float* gm = gl + (size_t)sl * u.M * T + m * T + jj;
+    const uint16_t* nm = u.nrm + m * u.nrm_stride + j;
+    const int64_t H = u.H;
+    u.out[(int64_t)m * u.H + j] =
+        ok ? hc_gate_mean([&](int s) { return gm[s * u.bj]; }, [&](int s) { return bf16_to_f32(nm[s * H]); }, u.hc)
+           : (uint16_t)0x7fc0u;
+  }
+}
+
+
+// The plan keeps the dynamic LDS within 150 KB (the kernel also has a few
+// bytes of static LDS); a failed attribute call is cleared so that the
+// two-launch fallback does not report it.
+template <bool F16S, int KW>
+static bool launch_hc_mix(const HcMixArgs& a, int P, size_t lds, hipStream_t st) {
+  auto kern = hc_mix_kernel<F16S, KW, 1>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            150 * 1024) != hipSuccess) {
+      (void)hipGetLastError();
+      return false;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(P), dim3(512), lds, st, a);
+  return true;
+}
+
 }  // namespace fp4x
 
 using namespace fp4x;
@@ -233,6 +391,98 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
   if (s_dtype == FP4X_DT_F16) launch_hc_up<FmtW8<true>>(p, KW, cps, full, grid, lds, st);
   else launch_hc_up<FmtW8<false>>(p, KW, cps, full, grid, lds, st);
   return check_launch("hc_up");
+}
+
+int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* di, void* bot,
+                int M, int N, int K, int lr, int hc, int ksplit, float* part, int* tickets, int n_tickets,
+                const void* qi, const void* si, const void* nrm, int64_t nrm_stride, void* out, int H, int bj,
+                void* stream) {
+  // one launch when both halves take the planned decompositions; else the two entry points
+  auto two = [&]() {
+    int rc = fp4x_hc_down(x, x_stride, q, s, s_dtype, di, bot, M, N, K, lr, hc, ksplit, part, tickets, stream);
+    if (rc != FP4X_OK) return rc;
+    return fp4x_hc_up(bot, lr, qi, si, s_dtype, nrm, nrm_stride, out, M, lr, H, hc, bj, stream);
+  };
+  const char* env = getenv("FP4X_HC_MIX");
+  if ((env && env[0] == '0') || M < 1 || M > 16 || N <= 0 || K <= 0 || K % 64 || lr <= 0 || lr > N || lr % 64 ||
+      hc <= 0 || bj <= 0 || H <= 0 || H % bj || ksplit < 2 || ksplit > 64 || K % ksplit || (K / ksplit) % 16 ||
+      !part || !tickets || (s_dtype != FP4X_DT_F32 && s_dtype != FP4X_DT_F16))
+    return two();
+  if (!al(x, 16) || x_stride % 8 || x_stride < K || !al(q, 16) || !al(s, 4) || !al(qi, 16) || !al(si, 4) ||
+      !al(bot, 4))
+    return two();
+  GemvLaunch d{};
+  d.x = static_cast<const uint16_t*>(x);
+  d.x_stride = x_stride;
+  d.pa.w0 = static_cast<const uint8_t*>(q);
+  d.pa.s = static_cast<const uint8_t*>(s);
+  d.pa.K = K;
+  d.out = di;
+  d.out_dtype = FP4X_DT_BF16;
+  d.out_stride = N;
+  d.out2 = bot;
+  d.lr = lr;
+  d.hc = hc;
+  d.gs = 1.0f;
+  d.M = M;
+  d.N = N;
+  d.ksplit = ksplit;
+  d.part = part;
+  d.tickets = tickets;
+  d.batch = 1;
+  d.per_wg = 1;
+  d.xbufs = 1;
+  int C = 0;
+  size_t lds_d = 0;
+  const int tiles_d = (N + 15) / 16;
+  const int sync_at = (tiles_d + 63) & ~63;          // the count and the flags, away from the tile tickets
+  if (!w8_splitk_plan(d, C, lds_d)) return two();
+  // the up projection's shape, as fp4x_hc_up plans it
+  const int chunks = lr / 16;
+  GemvLaunch qq{};
+  qq.pa.w0 = static_cast<const uint8_t*>(qi);
+  qq.pa.s = static_cast<const uint8_t*>(si);
+  const bool pal = s_dtype == FP4X_DT_F16 ? mfma_pair_aligned<FmtW8<true>>(qq, 1) : mfma_pair_aligned<FmtW8<false>>(qq, 1);
+  const int cps = mfma_cps<FmtW8<false>>(chunks) == 2 && pal ? 2 : 1;
+  const int KW = mfma_kw(chunks, cps);
+  const int T = hc * bj;
+  if (cps != 1 || !mfma_full(chunks, KW, cps) || (chunks + 4 * KW - 1) / (4 * KW) > kNJ || T % 16) return two();
+  const int WT = (T / 16) * KW;
+  if (WT > 8 || 8 % WT || (KW != 1 && KW != 2 && KW != 4)) return two();
+  const int R = 8 / WT, ntu = H / bj, D = tiles_d * C;
+  const int P = D > (ntu + R - 1) / R ? D : (ntu + R - 1) / R;
+  if (P > device_cus() || (int64_t)n_tickets < (int64_t)sync_at + (int64_t)kMixFlagStride * (P + 1)) return two();
+  const size_t lds_u = (((size_t)M * lr * 2 + 15) & ~(size_t)15) + (size_t)R * (T / 16) * (KW - 1) * 1024 +
+                       (size_t)R * M * T * 4;
+  const size_t lds = lds_d > lds_u ? lds_d : lds_u;
+  if (lds > 150 * 1024) return two();
+  HcMixArgs a{};
+  a.d = d;
+  a.u.bot = static_cast<const uint16_t*>(bot);
+  a.u.bot_stride = lr;
+  a.u.pa.w0 = static_cast<const uint8_t*>(qi);
+  a.u.pa.s = static_cast<const uint8_t*>(si);
+  a.u.pa.K = lr;
+  a.u.nrm = static_cast<const uint16_t*>(nrm);
+  a.u.nrm_stride = nrm_stride;
+  a.u.out = static_cast<uint16_t*>(out);
+  a.u.M = M; a.u.K = lr; a.u.H = H; a.u.hc = hc; a.u.bj = bj;
+  a.sync = tickets + sync_at;
+  a.C = C;
+  a.D = D;
+  a.tiles_d = tiles_d;
+  a.R = R;
+  a.spin_limit = 1 << 22;
+  hipStream_t st = (hipStream_t)stream;
+  bool launched;
+  if (s_dtype == FP4X_DT_F16)
+    launched = KW == 1 ? launch_hc_mix<true, 1>(a, P, lds, st) : KW == 2 ? launch_hc_mix<true, 2>(a, P, lds, st)
+                                                                    : launch_hc_mix<true, 4>(a, P, lds, st);
+  else
+    launched = KW == 1 ? launch_hc_mix<false, 1>(a, P, lds, st) : KW == 2 ? launch_hc_mix<false, 2>(a, P, lds, st)
+                                                                     : launch_hc_mix<false, 4>(a, P, lds, st);
+  if (!launched) return two();
+  return check_launch("hc_mix");
 }
 
 int fp4x_hc_scaled_silu(const void* d, int64_t d_stride, void* bot, int M, int lr, int hc, void* stream) {

@@ -55,6 +55,18 @@ struct EpiHcDown {
   }
 };
 
+// The same epilogue for the single-launch mixer: BOT is stored device-coherently,
+// since other workgroups of the same launch read it.
+struct EpiHcDownShared {
+  __device__ static void apply(const GemvLaunch& p, int, int m, int64_t row, float v) {
+    const uint16_t d = f32_to_bf16(v);
+    reinterpret_cast<uint16_t*>(p.out)[m * p.out_stride + row] = d;
+    if (row < p.lr)
+      __hip_atomic_store(reinterpret_cast<uint16_t*>(p.out2) + (int64_t)m * p.lr + row,
+                         hc_scaled_silu(bf16_to_f32(d), p.hc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+};
+
 // Host-side launch plumbing ---------------------------------------------------
 void set_error(const std::string& msg);
 int check_launch(const char* what);

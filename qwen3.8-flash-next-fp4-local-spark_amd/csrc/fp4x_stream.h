@@ -274,16 +274,18 @@ __device__ __forceinline__ void stream_read_x(uint32_t xa, uint4& x0a, uint4& x0
 //     stores and the ticket, and from the loads depending on the ticket value;
 //     no cache-wide write-back or invalidate is needed because every access to
 //     the slots and the ticket is device-coherent.
+//
+// w8_splitk_item runs one (tile t, part c) item with the workgroup's WPG waves
+// and LDS at base; it returns true in the wave that ran the tile's epilogue
+// (wave 0 of the last-arriving workgroup), false elsewhere.
 template <bool F16S, int WPG, int JW, class Epi>
-__global__ __launch_bounds__(64 * WPG) void w8_splitk_kernel(GemvLaunch p, int C) {
+__device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t, int c, char* base) {
   constexpr int UW = WPG * JW;                       // units per workgroup
   constexpr int XR = UW * 256 + 64;                  // LDS bytes per activation row
   static_assert(UW % 4 == 0, "activation slice in whole 1 KB pieces");
-  extern __shared__ __align__(16) uint16_t lds[];
-  char* base = reinterpret_cast<char*>(lds);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int K = p.pa.K, t = blockIdx.x / C, c = blockIdx.x - t * C;
+  const int K = p.pa.K;
   char* part_base = base + ((p.M * XR + 15) & ~15);
 
   // activation slice [M, c * UW * 128, + UW * 128): 1 KB pieces
@@ -342,7 +344,7 @@ __global__ __launch_bounds__(64 * WPG) void w8_splitk_kernel(GemvLaunch p, int C
     const uint32_t pl = lds_addr(part_base) + lane * 16;
     if (wave > 0) lds_put_f32x4(pl + (wave - 1) * 1024, acc);
     wg_barrier_raw();
-    if (wave > 0) return;
+    if (wave > 0) return false;
 #pragma unroll
     for (int h = 1; h < WPG; ++h) {
       const f32x4_t o = lds_get_f32x4(pl + (h - 1) * 1024);
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(64 * WPG) void w8_splitk_kernel(GemvLaunch p, int C
   int tk = 0;
   if (lane == 0) tk = __hip_atomic_fetch_add(p.tickets + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   tk = __builtin_amdgcn_readfirstlane(tk);
-  if (tk != C - 1) return;
+  if (tk != C - 1) return false;
   for (int e = lane; e < p.M * 16; e += 64) {        // e = m * 16 + n
     const float* src = slots + e;
     float tot = ld_coherent(src);
@@ -368,6 +370,14 @@ __global__ __launch_bounds__(64 * WPG) void w8_splitk_kernel(GemvLaunch p, int C
     if (orow < p.N) Epi::apply(p, 0, e >> 4, orow, tot * p.gs);
   }
   if (lane == 0) ticket_reset(p.tickets + t);
+  return true;
+}
+
+template <bool F16S, int WPG, int JW, class Epi>
+__global__ __launch_bounds__(64 * WPG) void w8_splitk_kernel(GemvLaunch p, int C) {
+  extern __shared__ __align__(16) uint16_t lds[];
+  const int t = blockIdx.x / C, c = blockIdx.x - t * C;
+  w8_splitk_item<F16S, WPG, JW, Epi>(p, C, t, c, reinterpret_cast<char*>(lds));
 }
 
 template <bool F16S, int WPG, int JW, class Epi>
@@ -444,10 +454,27 @@ bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
 //     in LDS beside the rings (M <= 3 at K = 10240).
 // Both need at most two tiles per CU.  Returns false otherwise (or with
 // FP4X_W8_STREAM=0), launching nothing.
+constexpr int kSplitWaves = 8, kSplitUnits = 2;     // w8_splitk_kernel: waves per workgroup, units per wave
+
+// The split-over-workgroups plan of a W8 split-K call: true with C (workgroups
+// per tile) and the LDS bytes when w8_splitk_kernel takes it.
+inline bool w8_splitk_plan(const GemvLaunch& p, int& C, size_t& lds) {
+  constexpr int SU = kSplitWaves * kSplitUnits;
+  const char* env = getenv("FP4X_W8_STREAM");
+  if (env && env[0] == '0') return false;
+  const int K = p.pa.K, tiles = (p.N + 15) / 16, units = K / 128;
+  if (p.ksplit < 2 || K % 512 != 0 || p.M > 16) return false;
+  if (reinterpret_cast<uintptr_t>(p.pa.s) & 3) return false;
+  if (tiles > 2 * device_cus() || units % SU != 0 || units / SU < 2 || !p.part || !p.tickets) return false;
+  C = units / SU;
+  const int64_t slots = (int64_t)tiles * C * p.M * 16, have = (int64_t)p.ksplit * 16 * p.N;
+  lds = (size_t)((p.M * (SU * 256 + 64) + 15) & ~15) + (size_t)(kSplitWaves - 1) * 1024;
+  return slots <= have && lds <= 160 * 1024;
+}
+
 template <bool F16S, class Epi>
 bool launch_w8_ktile(GemvLaunch p, hipStream_t st) {
   constexpr int KW = 16, D = 2;
-  constexpr int SW = 8, SJ = 2, SU = SW * SJ;
   const char* env = getenv("FP4X_W8_STREAM");
   if (env && env[0] == '0') return false;
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
@@ -458,12 +485,10 @@ bool launch_w8_ktile(GemvLaunch p, hipStream_t st) {
   p.batch = 1;
   p.per_wg = 1;
   p.xbufs = 1;
-  if (units % SU == 0 && units / SU >= 2 && p.part && p.tickets) {
-    const int C = units / SU;
-    const int64_t slots = (int64_t)tiles * C * p.M * 16, have = (int64_t)p.ksplit * 16 * p.N;
-    const size_t lds = (size_t)((p.M * (SU * 256 + 64) + 15) & ~15) + (size_t)(SW - 1) * 1024;
-    if (slots <= have && lds <= 160 * 1024) return launch_w8_splitk<F16S, SW, SJ, Epi>(p, C, lds, tiles * C, st);
-  }
+  int C = 0;
+  size_t slds = 0;
+  if (w8_splitk_plan(p, C, slds))
+    return launch_w8_splitk<F16S, kSplitWaves, kSplitUnits, Epi>(p, C, slds, tiles * C, st);
   if (units % KW != 0 || units / KW < D) return false;
   const size_t lds = (size_t)StreamGeom::xbuf_bytes(p.M, K) + (size_t)(KW - 1) * 1024 + (size_t)KW * D * kStreamUnit;
   if (lds > 160 * 1024) return false;

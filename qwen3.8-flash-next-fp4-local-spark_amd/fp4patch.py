@@ -192,8 +192,9 @@ def _patch_hc():
                 if len(qu) in (1, 97):
                     _log(f"HC fused: prepared {len(qu)} mixers")
         x = normalized.contiguous()
-        di, bot = fx[0].down(x, *q8[kd], self.lora_rank, self.hc_count, HC_DOWN_CFG)
-        block_input = F.HCFused.up(bot, *qu[ku], x, self.hc_count, (8, 64, 4))
+        # HCFused.down then HCFused.up (x/fp4patch.py:217-218), in one launch where the shapes allow
+        di, bot, block_input = fx[0].mix(x, *q8[kd], self.lora_rank, self.hc_count, *qu[ku], x, HC_DOWN_CFG,
+                                         (8, 64, 4))
         injection = di[:, self.lora_rank: self.lora_rank + self.hc_count] if self.use_combine else None
         return block_input, injection
 

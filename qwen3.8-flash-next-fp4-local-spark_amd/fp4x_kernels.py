@@ -289,7 +289,10 @@ class HCFused:
     def __init__(self, device, n_down=336, max_m=16, bn=32, max_ksplit=16):
         self.n_down, self.max_m, self.max_ksplit = n_down, max_m, max_ksplit
         self.part = torch.empty(max_ksplit * MAX_M * n_down, dtype=torch.float32, device=device)
-        self.tickets = torch.zeros(max(n_down, 1), dtype=torch.int32, device=device)
+        # one ticket per 16-row tile, then the single-launch mixer's count and one
+        # 128-byte flag line per workgroup (at most one workgroup per CU)
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+        self.tickets = torch.zeros(max(n_down, 1) + 64 + 32 * (cus + 1), dtype=torch.int32, device=device)
 
     def down(self, x, q, s, lr, hc, cfg=(32, 512, 4, 4)):
         """(di bf16 [M, N], bot bf16 [M, lr]) = split-K W8 GEMV + cast + scaled SiLU."""
@@ -307,6 +310,33 @@ class HCFused:
         _L.check(_L.lib().fp4x_hc_down(_ptr(x), x.stride(0), _ptr(q), _ptr(s), sdt, _ptr(di), _ptr(bot), m, n, k, lr,
                                        hc, KS, _ptr(self.part), _ptr(self.tickets), _L.stream_of(x)), "hc_down")
         return di, bot
+
+    def mix(self, x, qd, sd, lr, hc, qi, si, normalized, cfg=(32, 256, 4, 4), up_cfg=(8, 64, 4)):
+        """(di, bot, block_input) = down(...) then up(bot, ...), bit-identical to the two calls
+        (x/fp4patch.py:217-218), in one launch when both halves take their planned decompositions."""
+        _need_cuda(x, qd, sd, qi, si, normalized)
+        KS, BJ = cfg[2], up_cfg[0]
+        x = _act(x)
+        m, k = x.shape
+        n = qd.shape[0]
+        if m > min(self.max_m, MAX_M) or n > self.n_down or KS > self.max_ksplit:
+            raise ValueError(f"fp4x HCFused.mix: M={m} N={n} KSPLIT={KS} exceed the scratch "
+                             f"(max_m={self.max_m}, n_down={self.n_down}, max_ksplit={self.max_ksplit})")
+        if qi.shape[1] != lr or sd.dtype != si.dtype:
+            raise ValueError("fp4x HCFused.mix: up weights must have K = lr and the down weights' scale dtype")
+        nh = qi.shape[0]
+        h = nh // hc
+        if normalized.stride(1) != 1:
+            normalized = normalized.contiguous()
+        di = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+        bot = torch.empty((m, lr), dtype=torch.bfloat16, device=x.device)
+        out = torch.empty((m, h), dtype=torch.bfloat16, device=x.device)
+        sdt = _L.DT_F16 if sd.dtype == torch.float16 else _L.DT_F32
+        _L.check(_L.lib().fp4x_hc_mix(_ptr(x), x.stride(0), _ptr(qd), _ptr(sd), sdt, _ptr(di), _ptr(bot), m, n, k, lr,
+                                      hc, KS, _ptr(self.part), _ptr(self.tickets), self.tickets.numel(), _ptr(qi),
+                                      _ptr(si), _ptr(normalized), normalized.stride(0), _ptr(out), h, BJ,
+                                      _L.stream_of(x)), "hc_mix")
+        return di, bot, out
 
     @staticmethod
     def interleave_up(q, s, hc, bj):

@@ -6,7 +6,9 @@
 * both match the oracle: DI within the MFMA accumulation bound of the exact
   sum plus bf16 rounding, block_input within bf16 rounding of the oracle's
   float64-sigmoid epilogue;
-* the split-K scratch is re-armed: tickets are zero after every call.
+* the split-K scratch is re-armed: tickets are zero after every call;
+* the whole mixer in one call (HCFused.mix, one launch where the shapes allow)
+  equals down + up bit for bit and re-arms its counters.
 """
 import numpy as np
 import pytest
@@ -61,6 +63,9 @@ def test_fused_equals_unfused_97_layers(gpu, F):
         di2, bot2, bi2 = unfused(F, x_t, qd_t, sd_t, qu_t, su_t, LR, KS)
         assert torch.equal(di, di2) and torch.equal(bot, bot2) and torch.equal(bi, bi2), f"layer {i}"
         assert int(fx.tickets.abs().sum()) == 0
+        di3, bot3, bi3 = fx.mix(x_t, qd_t, sd_t, LR, HC, qi, si, x_t, (32, 256, KS, 4))
+        assert torch.equal(di, di3) and torch.equal(bot, bot3) and torch.equal(bi, bi3), f"layer {i} mix"
+        assert int(fx.tickets.abs().sum()) == 0
         if i % 24 == 0:
             import _fp4x
             qd, sd, qu, su = (t.cpu().numpy() for t in (qd_t, sd_t, qu_t, su_t))
@@ -90,6 +95,10 @@ def test_mixer_served_shape(gpu, F, M):
     bi = F.HCFused.up(bot, qi, si, x_t, HC, (8, 64, 4))
     di2, bot2, bi2 = unfused(F, x_t, dev(qd), dev(sd), dev(qu), dev(su), 320, 8)
     assert torch.equal(di, di2) and torch.equal(bot, bot2) and torch.equal(bi, bi2)
+    for _ in range(3):                                # one launch, counters re-armed every call
+        di3, bot3, bi3 = fx.mix(x_t, dev(qd), dev(sd), 320, HC, qi, si, x_t, (32, 256, 8, 4))
+        assert torch.equal(di, di3) and torch.equal(bot, bot3) and torch.equal(bi, bi3)
+        assert int(fx.tickets.abs().sum()) == 0
     di_ref, _, bi_ref = ohc.mixer(x, qd, sd, qu, su, 320, HC)
     assert_tol(to_f32(di), di_ref, what="di")
     assert_tol(to_f32(bi), bi_ref, rel=2e-2, abs_=2e-2, what="block_input")
@@ -108,3 +117,35 @@ def test_epilogue_kernels_vs_oracle(gpu, F):
     ref = ohc.gate_mean(nrm, g, HC)
     assert (bf16_bits(out) == fm.bf16_bits(ref)).mean() > 0.99
     assert_tol(to_f32(out), ref, rel=1e-2, abs_=1e-2, what="gate_mean")
+
+
+def test_mix_fallback_and_fp16_scales(gpu, F, monkeypatch):
+    """The two-call fallback (FP4X_HC_MIX=0) and the single launch agree, with
+    fp16 scales, across repeated calls sharing one scratch."""
+    rng = np.random.default_rng(77)
+    gen = torch.Generator(device=gpu).manual_seed(77)
+    wd = torch.randn((336, HC * H), generator=gen, device=gpu) * 0.02
+    wu = torch.randn((HC * H, 320), generator=gen, device=gpu) * 0.02
+
+    def f16(w):
+        g = w.reshape(w.shape[0], -1, 64)
+        s16 = (g.abs().amax(-1).clamp_min(1e-12) / 127.0).half()
+        q = torch.round(g / s16.float().unsqueeze(-1)).clamp(-127, 127).to(torch.int8).reshape(w.shape)
+        return q.contiguous(), s16.contiguous()
+
+    qd, sd = f16(wd)
+    qu, su = f16(wu)
+    qi, si = F.HCFused.interleave_up(qu, su, HC, 8)
+    fx = F.HCFused(gpu)
+    for M in (3, 16, 1):
+        x_t = bf16_dev(act(rng, M, HC * H)[0])
+        one = fx.mix(x_t, qd, sd, 320, HC, qi, si, x_t, (32, 256, 8, 4))
+        monkeypatch.setenv("FP4X_HC_MIX", "0")
+        two = fx.mix(x_t, qd, sd, 320, HC, qi, si, x_t, (32, 256, 8, 4))
+        monkeypatch.delenv("FP4X_HC_MIX")
+        di, bot = fx.down(x_t, qd, sd, 320, HC, (32, 256, 8, 4))
+        bi = F.HCFused.up(bot, qi, si, x_t, HC, (8, 64, 4))
+        for a, b, c in zip(one, two, (di, bot, bi)):
+            assert torch.equal(a, b) and torch.equal(a, c), M
+        assert not torch.isnan(one[2].float()).any()
+        assert int(fx.tickets.abs().sum()) == 0
