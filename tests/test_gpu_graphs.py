@@ -1,0 +1,110 @@
+"""Entry points with state kept across calls (split-K tickets, the single-launch
+mixer's count and flags, the top-k workspace) replayed from HIP graphs, as the
+plugin runs them under vLLM's decode-graph capture: every replay, with eager
+work and synchronizations between replays, equals the eager results bit for
+bit, and the scratch is re-armed after each replay."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import act, bf16_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def F():
+    import fp4x_kernels
+    return fp4x_kernels
+
+
+def replay_and_check(fn, expected, eager_between):
+    """Capture fn() once, replay it three times; after each replay check every
+    output against the eager results, then run eager work before the next."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()                                       # warm-up outside the capture (allocations, workspaces)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            outs = fn()
+    torch.cuda.synchronize()
+    for r in range(3):
+        for o in outs:
+            o.fill_(0)                             # a stale value cannot pass for a replayed one
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, expected)):
+            assert torch.equal(o, e), f"replay {r} output {i}"
+        eager_between()
+        torch.cuda.synchronize()
+
+
+def test_graph_mixer_one_launch(gpu, F):
+    HC, H, LR, ND = 4, 2560, 320, 336
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    fx = F.HCFused(gpu)
+    layers = []
+    for _ in range(4):
+        qd, sd = F.quantize_w8(torch.randn((ND, HC * H), generator=gen, device=gpu) * 0.02)
+        qu, su = F.quantize_w8(torch.randn((HC * H, LR), generator=gen, device=gpu) * 0.02)
+        qi, si = F.HCFused.interleave_up(qu, su, HC, 8)
+        layers.append((qd, sd, qi, si))
+    x = bf16_dev(act(np.random.default_rng(5), 3, HC * H)[0])
+    cfg = (32, 256, 8, 4)
+
+    def run():
+        outs = []
+        for qd, sd, qi, si in layers:
+            outs += list(fx.mix(x, qd, sd, LR, HC, qi, si, x, cfg))
+        return outs
+
+    expected = []
+    for qd, sd, qi, si in layers:                 # the two-call reference, eagerly
+        di, bot = fx.down(x, qd, sd, LR, HC, cfg)
+        expected += [di, bot, F.HCFused.up(bot, qi, si, x, HC, (8, 64, 4))]
+    torch.cuda.synchronize()
+
+    def eager():
+        fx.mix(x, *layers[0][:2], LR, HC, *layers[0][2:], x, cfg)
+        assert int(fx.tickets.abs().sum()) == 0
+
+    replay_and_check(run, expected, eager)
+    assert int(fx.tickets.abs().sum()) == 0
+
+
+def test_graph_splitk_and_gates(gpu, F):
+    gen = torch.Generator(device=gpu).manual_seed(6)
+    q, s = F.quantize_w8(torch.randn((640, 10240), generator=gen, device=gpu) * 0.02)
+    x = torch.randn((3, 10240), generator=gen, device=gpu).to(torch.bfloat16)
+    qg, sg = F.quantize_w8(torch.randn((48 * 512, 2560), generator=gen, device=gpu) * 0.02)
+    qg, sg = qg.view(48, 512, 2560), sg.view(48, 512, 40).half()
+    xg = torch.randn((48, 3, 2560), generator=gen, device=gpu).to(torch.bfloat16)
+
+    def run():
+        return [F.w8_linear(x, q, s, (32, 256, 4, 4), torch.float32),
+                F.w8_linear_layers(xg, qg, sg, torch.float32)]
+
+    expected = run()
+    torch.cuda.synchronize()
+    replay_and_check(run, [e.clone() for e in expected],
+                     lambda: F.w8_linear(x[:1], q, s, (32, 256, 4, 4), torch.float32))
+
+
+def test_graph_int2_topk(gpu, F):
+    V, K, C = 248320, 2560, 512
+    gen = torch.Generator(device=gpu).manual_seed(7)
+    w = torch.randn((V, K), generator=gen, device=gpu) * 0.02
+    P, S = F.quantize_int2(w, group=16)
+    del w
+    x = torch.randn((3, K), generator=gen, device=gpu).to(torch.bfloat16)
+
+    def run():
+        coarse, idx = F.int2_topk(x, P, S, V, C)
+        return [coarse, idx]
+
+    expected = [e.clone() for e in run()]
+    torch.cuda.synchronize()
+    replay_and_check(run, expected, lambda: F.topk_rows(expected[0], C))
