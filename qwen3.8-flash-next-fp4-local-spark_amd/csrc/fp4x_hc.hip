@@ -199,7 +199,9 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   const int n = lane & 15, g = lane >> 4;
   const int T = u.hc * u.bj, WT = (T / 16) * KW;
   const int slot = wave / WT, ws = wave - slot * WT, grp = ws / KW, wv = ws - grp * KW;
-  const int ntu = u.H / u.bj, tu = blockIdx.x * a.R + slot;
+  // up tiles fill the workgroups from the last one down, so that workgroups
+  // without a down item take them first (they issue the loads at once)
+  const int ntu = u.H / u.bj, tu = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + slot;
   const int tuc = tu < ntu ? tu : ntu - 1;          // padding slots recompute the last tile, store nothing
   const int nch = u.K / F::KPC, cw = wv * 4 + g;
   const int J = ((nch + CPS - 1) / CPS + DP - 1) / DP;
@@ -222,7 +224,8 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
     }
   }
 
-  // 2. the up tiles' weights (one batch per lane) stream during the wait
+  // 2. the up tiles' weights (one batch per lane) stream during the wait (at
+  //    once in a workgroup without a down item)
   MfmaBatch<F, CPS> cb;
   mfma_load_full<F, DP, CPS>(cb, F::lane(u.pa, urow, CPS * cw));
   __syncthreads();
@@ -277,7 +280,7 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   const int per_slot = u.M * u.bj;
   for (int e = threadIdx.x; e < a.R * per_slot; e += blockDim.x) {
     const int sl = e / per_slot, r = e - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
-    const int tsl = blockIdx.x * a.R + sl;
+    const int tsl = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + sl;
     if (tsl >= ntu) continue;
     const int64_t j = (int64_t)tsl * u.bj + jj;
     const float* gm = gl + (size_t)sl * u.M * T + m * T + jj;
@@ -449,9 +452,14 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   if (cps != 1 || !mfma_full(chunks, KW, cps) || (chunks + 4 * KW - 1) / (4 * KW) > kNJ || T % 16) return two();
   const int WT = (T / 16) * KW;
   if (WT > 8 || 8 % WT || (KW != 1 && KW != 2 && KW != 4)) return two();
-  const int R = 8 / WT, ntu = H / bj, D = tiles_d * C;
-  const int P = D > (ntu + R - 1) / R ? D : (ntu + R - 1) / R;
-  if (P > device_cus() || (int64_t)n_tickets < (int64_t)sync_at + (int64_t)kMixFlagStride * (P + 1)) return two();
+  // grid: when the CUs allow, the down items and then separate workgroups for
+  // all up tiles (which load them at once); otherwise max(D, up workgroups),
+  // the up tiles sharing workgroups with down items (measured: spreading only
+  // part of the up tiles to extra workgroups is slower than not at all)
+  const int R = 8 / WT, ntu = H / bj, D = tiles_d * C, cus = device_cus();
+  const int need_u = (ntu + R - 1) / R;
+  const int P = D + need_u <= cus ? D + need_u : (D > need_u ? D : need_u);
+  if (P > cus || (int64_t)n_tickets < (int64_t)sync_at + (int64_t)kMixFlagStride * (P + 1)) return two();
   const size_t lds_u = (((size_t)M * lr * 2 + 15) & ~(size_t)15) + (size_t)R * (T / 16) * (KW - 1) * 1024 +
                        (size_t)R * M * T * 4;
   const size_t lds = lds_d > lds_u ? lds_d : lds_u;
