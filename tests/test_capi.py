@@ -27,7 +27,8 @@ def test_header_declares_entry_points():
     names = declared()
     for must in ("fp4x_mx8_linear", "fp4x_w8_linear", "fp4x_w6_linear", "fp4x_nv4_linear", "fp4x_int2_logits",
                  "fp4x_topk_rows", "fp4x_refine_mx8", "fp4x_hc_down", "fp4x_hc_up", "fp4x_hc_scaled_silu",
-                 "fp4x_hc_gate_mean", "fp4x_bf16_linear", "fp4x_w8_linear_layers", "fp4x_mx8_dequant"):
+                 "fp4x_hc_gate_mean", "fp4x_bf16_linear", "fp4x_w8_linear_layers", "fp4x_mx8_dequant",
+                 "fp4x_hc_mix", "fp4x_int2_topk"):
         assert must in names
 
 
@@ -70,6 +71,13 @@ def test_argument_errors_without_gpu(lib):
                             None) == _fp4x.ERR_ARG                             # coarse stride < N
     assert b"int2_topk" in L.fp4x_last_error()
     assert L.fp4x_hc_up(None, 640, None, None, 1, None, 10240, None, 1, 640, 2560, 4, 3, None) == _fp4x.ERR_ARG
+    # the whole mixer: shapes it cannot take reach the down projection's checks (M = 17; split-K without scratch)
+    assert L.fp4x_hc_mix(None, 10240, None, None, 1, None, None, 17, 336, 10240, 320, 4, 8, None, None, 0, None,
+                         None, None, 10240, None, 2560, 8, None) == _fp4x.ERR_ARG
+    assert b"hc_down" in L.fp4x_last_error()
+    assert L.fp4x_hc_mix(None, 10240, None, None, 1, None, None, 3, 336, 10240, 320, 4, 8, None, None, 0, None,
+                         None, None, 10240, None, 2560, 8, None) == _fp4x.ERR_ARG
+    assert b"scratch" in L.fp4x_last_error()
     # empty problems are no-ops
     assert L.fp4x_mx8_linear(None, 2560, None, None, None, 0, 0, 64, 2560, 1, None, None, None) == _fp4x.OK
 
