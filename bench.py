@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E")
+    ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E,F")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -226,6 +226,36 @@ def bench_head(F, torch, dev, out, vectors=1000):
 
 
 # ------------------------------------------------------------------ CPU baseline
+def bench_draft(F, torch, dev, out):
+    """The MTP draft head over a 65,197-token subset of a 248,320-token NVFP4
+    head (x/fp4patch.py:279-334): INT2 coarse + top-64 + exact NVFP4 rescore,
+    and the NVFP4 GEMV over the whole subset."""
+    sys.path.insert(0, os.path.join(ROOT, "qwen3.8-flash-next-fp4-local-spark_amd"))
+    import fp4patch
+    V, K, M, NS, DC = 248320, 2560, 3, 65197, 64
+    g = torch.Generator(device=dev).manual_seed(4)
+    P = torch.randint(0, 256, (V, K // 2), generator=g, device=dev, dtype=torch.uint8)
+    S = (torch.randint(0x28, 0x40, (V, K // 16), generator=g, device=dev, dtype=torch.uint8)).view(torch.float8_e4m3fn)
+    ids = torch.sort(torch.randperm(V, generator=g, device=dev)[:NS]).values
+    st = fp4patch._draft_prepare(F, P, S, 1.0e-3, ids, DC)
+    del P, S
+    x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    int2_b = NS * (K // 4) + NS * (K // 16) * 2 + M * K * 2
+    ncp = copies_for(int2_b)
+    copies = [dict(st, c=(st["c"][0].clone(), st["c"][1].clone())) for _ in range(ncp)]
+    us = graph_time([lambda c=c: fp4patch._draft_logits(F, x, c, V, DC) for c in copies], 10)
+    out["F_draft_head_65k_int2_top64_nv4_M3"] = entry(us, int2_b + M * DC * (K // 2 + K // 16 + 8) + M * V * 2)
+    cand = F.int2_topk(x, *st["c"], NS, DC)[1]
+    us = graph_time([lambda: F.refine_nv4(x, cand, st["w"], st["s"], st["gs"])] * 4, 10)
+    out["F_refine_nv4_3x64_M3"] = entry(us, M * DC * (K // 2 + K // 16 + 8) + M * K * 2 + M * DC * 4)
+    nv4_b = NS * (K // 2 + K // 16) + M * K * 2 + M * NS * 2
+    ncp = copies_for(nv4_b)
+    wc = [(st["w"].clone(), st["s"].clone()) for _ in range(ncp)]
+    us = graph_time([lambda c=c: F.nv4_linear(x, c[0], c[1], st["gs"], (32, 256, 4)) for c in wc], 10)
+    out["F_draft_subset_nv4_65197x2560_M3"] = entry(us, nv4_b)
+    del copies, wc, st
+
+
 def cpu_baseline(seconds):
     """The oracle's dequantize-then-matmul router gates (numpy, all host
     cores) on a bounded sample: whole 48-layer passes at M = 3."""
@@ -328,7 +358,7 @@ def main():
 
     kernels = {}
     kernels["B_w8_gates_48_layers_M3"] = entry(ms_step * 1e3, step_bytes)
-    sel = set("ABCDE") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
+    sel = set("ABCDEF") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
     if "B" in sel:
         bench_gates_single(F, torch, dev, kernels, q, s)
     del qs, out3, g_full, g_rem
@@ -340,6 +370,9 @@ def main():
         torch.cuda.empty_cache()
     if "E" in sel:
         bench_head(F, torch, dev, kernels)
+        torch.cuda.empty_cache()
+    if "F" in sel:
+        bench_draft(F, torch, dev, kernels)
         torch.cuda.empty_cache()
 
     traffic = None

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 3
+#define FP4X_ABI_VERSION 4
 
 enum {
   FP4X_OK = 0,
@@ -136,6 +136,15 @@ int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S
  * [refine_mx8_ -> _refine_mx8, x/fp4x_kernels.py:384-388, :367-381] */
 int fp4x_refine_mx8(void* out, int out_dtype, int64_t out_stride, const void* x, const int64_t* idx, int M, int C,
                     const void* w, const void* s, int K, int V, void* stream);
+
+/* Exact NVFP4 logits of candidate rows: out [M, C] fp32,
+ * out[m, c] = (sum_k float(bf16(e2m1(wp) * e4m3(s))) * float(x[m, k])) * gs,
+ * in the rescore kernel's specified fma order; NaN where idx[m, c] is outside
+ * [0, V).  wp [V, K/2] (low nibble = even k), s [V, K/16] e4m3, K % 32 == 0.
+ * [refine_nv4 -> _refine_nv4, x/fp4x_kernels.py:410-415, :391-407; the draft
+ *  head, x/fp4patch.py:316] */
+int fp4x_refine_nv4(float* out, const void* x, const int64_t* idx, int M, int C, const void* wp, const void* s, float gs,
+                    int K, int V, void* stream);
 
 /* Mixer down projection: split-K W8 GEMV whose last workgroup per row tile
  * writes di = bf16(sum) [M, N] and bot = bf16(sc * sigmoid(sc)) [M, lr] with

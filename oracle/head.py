@@ -62,3 +62,27 @@ def full_mx8_logits(x_bits, w_codes, s_u8):
     """Exact-weight full-vocabulary logits (fp32, numpy order) for argmax
     agreement checks."""
     return bf16_to_f32(x_bits).astype(F32) @ quant.mx8_dequant(w_codes, s_u8).T
+
+
+# ----------------------------------------------------------------- draft head
+def nv4_rows(x_bits, P, S_codes, gs, rows, lpr):
+    """Exact NVFP4 logits [M, C] of the gathered rows rows [M, C], times gs:
+    the rescore kernel's order with IEEE fma steps (ordered model 2); the
+    operand e2m1 * e4m3 is exact in bf16.  [x/fp4x_kernels.py:391-415]"""
+    uniq, inv = np.unique(rows, return_inverse=True)
+    w_op = bf16_bits(quant.dequant_nv4_operand(P[uniq], S_codes[uniq]))
+    return ordered.ordered_gemv(x_bits, w_op, kpc=32, lpr=lpr, gs=gs, rows=inv.reshape(rows.shape),
+                                mode=ordered.FMA)
+
+
+def draft_head(x_bits, P2, S2, G, P, S_codes, gs, ids, vocab, dc, lpr_int2, lpr_nv4):
+    """The draft head over a token subset ids (x/fp4patch.py:312-320): INT2
+    coarse over the subset rows, the top dc by the total order, their exact
+    NVFP4 logits, scattered into a -inf bf16 row of the full vocabulary.
+    Returns (cand [M, dc] subset positions, vals fp32 [M, dc], full bf16 bits)."""
+    coarse = bf16_bits(int2_coarse(x_bits, P2, S2, G, lpr_int2))
+    cand = topk_total_order(coarse, dc)
+    vals = nv4_rows(x_bits, P, S_codes, gs, cand, lpr_nv4)
+    full = np.full((x_bits.shape[0], vocab), 0xFF80, np.uint16)          # bf16 -inf
+    np.put_along_axis(full, np.asarray(ids, np.int64)[cand], bf16_bits(vals), 1)
+    return cand, vals, full

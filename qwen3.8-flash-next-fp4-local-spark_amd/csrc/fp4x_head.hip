@@ -13,15 +13,36 @@ struct RefineArgs {
   void* out; int out_dtype; int64_t out_stride;
   const uint16_t* x;           // [M, K] contiguous
   const int64_t* idx;          // [M, C]
-  PlaneArgs pa;                // MXFP8 rows [V, K]
+  PlaneArgs pa;                // candidate rows [V, K] (MXFP8 or NVFP4)
+  float gs;                    // NVFP4 global scale
   int M, C, K, V, lpr, cpl;
 };
 
 // The candidate rows go through the chunk layout and lane butterfly of
 // mx8_linear, accumulated with IEEE fp32 fma (AccFma) so every rounding is
-// specified; e4m3 * 2^(e-127) is exact in bf16 and in fp32, and its product
-// with a bf16 activation is exact, as in the reference's fp32 dot.
-__global__ __launch_bounds__(kThreads) void refine_mx8_kernel(RefineArgs p) {
+// specified.  MXFP8: e4m3 * 2^(e-127) is exact in bf16 and in fp32, and its
+// product with a bf16 activation is exact, as in the reference's fp32 dot;
+// the sum goes in place to out[m, idx[m, c]] (x/fp4x_kernels.py:367-388).
+// NVFP4 (DENSE): e2m1 * e4m3 is exact in bf16; out[m, c] = sum * gs in fp32,
+// NaN for an index outside [0, V) (x/fp4x_kernels.py:391-417).
+// Every chunk load of the batch goes out unconditionally, at an in-bounds
+// address (row 0 for an invalid candidate, chunk 0 past the row's chunks):
+// loads under a branch would each be waited for at the branch's join, one
+// memory round trip per chunk.  compute_batch skips the dead chunks, and an
+// invalid candidate's sum is never stored.
+template <class F>
+__device__ __forceinline__ void load_batch_inbounds(ChunkBatch<F, 1>& b, const PlaneArgs& a, int64_t row, int cend,
+                                                    int lrow, int lpr, int jb, int cpl) {
+  const int64_t r = row >= 0 ? row : 0;
+#pragma unroll
+  for (int j = 0; j < kCplBatch; ++j) {
+    const int jj = jb + j, c = lrow + jj * lpr;
+    b.ch[0][j] = F::load(a, r, jj < cpl && c < cend ? c : 0);
+  }
+}
+
+template <class F, bool DENSE>
+__global__ __launch_bounds__(kThreads) void refine_kernel(RefineArgs p) {
   extern __shared__ __align__(16) uint16_t lds_x[];
   const int m = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -34,17 +55,22 @@ __global__ __launch_bounds__(kThreads) void refine_mx8_kernel(RefineArgs p) {
   }
   float acc[1][1] = {{0.0f}};
   for (int jb = 0; jb < p.cpl; jb += kCplBatch) {
-    ChunkBatch<FmtMX8, 1> cb;
-    load_batch<FmtMX8, 1>(cb, p.pa, rows, 0, p.K / 16, lrow, lpr, jb, p.cpl);
+    ChunkBatch<F, 1> cb;
+    load_batch_inbounds<F>(cb, p.pa, rows[0], p.K / F::KPC, lrow, lpr, jb, p.cpl);
     if (jb == 0) {
       stage_x<1>(lds_x, p.x + (int64_t)m * p.K, p.K, 1, 0, p.K);
       __syncthreads();
     }
-    compute_batch<FmtMX8, 1, 1, const uint16_t*, AccFma>(cb, (const uint16_t*)lds_x, p.K, 0, 1, 0, p.K / 16, lrow,
-                                                         lpr, jb, p.cpl, acc);
+    compute_batch<F, 1, 1, const uint16_t*, AccFma>(cb, (const uint16_t*)lds_x, p.K, 0, 1, 0, p.K / F::KPC, lrow,
+                                                    lpr, jb, p.cpl, acc);
   }
   const float v = group_allreduce(acc[0][0], lpr);
-  if (lrow == 0 && rows[0] >= 0) store_out(p.out, (int64_t)m * p.out_stride + rows[0], p.out_dtype, v);
+  if constexpr (DENSE) {
+    if (lrow == 0 && cand < p.C)
+      reinterpret_cast<float*>(p.out)[(int64_t)m * p.C + cand] = rows[0] >= 0 ? v * p.gs : __builtin_nanf("");
+  } else {
+    if (lrow == 0 && rows[0] >= 0) store_out(p.out, (int64_t)m * p.out_stride + rows[0], p.out_dtype, v);
+  }
 }
 
 // ------------------------------------------------------------------ top-k
@@ -687,8 +713,8 @@ int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int6
 
 int fp4x_refine_mx8(void* out, int out_dtype, int64_t out_stride, const void* x, const int64_t* idx, int M, int C,
                     const void* w, const void* s, int K, int V, void* stream) {
-  if (M < 0 || C < 0 || K <= 0 || K % 32 || V < 0 || out_stride < V) {
-    set_error("refine_mx8: bad shape (K % 32 == 0, out_stride >= V)");
+  if (M < 0 || C < 0 || K <= 0 || K % 32 || V < 0 || out_stride < V || (V == 0 && M > 0 && C > 0)) {
+    set_error("refine_mx8: bad shape (K % 32 == 0, out_stride >= V, V > 0)");
     return FP4X_ERR_ARG;
   }
   if (!al16(x) || !al16(w)) { set_error("refine_mx8: x and w must be 16-byte aligned"); return FP4X_ERR_ARG; }
@@ -706,8 +732,37 @@ int fp4x_refine_mx8(void* out, int out_dtype, int64_t out_stride, const void* x,
   p.cpl = (chunks + p.lpr - 1) / p.lpr;
   const int per_wg = kWaves * (64 / p.lpr);
   dim3 grid((C + per_wg - 1) / per_wg, M);
-  hipLaunchKernelGGL(refine_mx8_kernel, grid, dim3(kThreads), (size_t)K * 2, (hipStream_t)stream, p);
+  hipLaunchKernelGGL((refine_kernel<FmtMX8, false>), grid, dim3(kThreads), (size_t)K * 2, (hipStream_t)stream, p);
   return check_launch("refine_mx8");
+}
+
+int fp4x_refine_nv4(float* out, const void* x, const int64_t* idx, int M, int C, const void* wp, const void* s, float gs,
+                    int K, int V, void* stream) {
+  if (M < 0 || C < 0 || K <= 0 || K % 32 || V < 0 || (V == 0 && M > 0 && C > 0)) {
+    set_error("refine_nv4: bad shape (K % 32 == 0, V > 0)");
+    return FP4X_ERR_ARG;
+  }
+  if (!al16(x) || !al16(wp) || (reinterpret_cast<uintptr_t>(s) & 1)) {
+    set_error("refine_nv4: x and wp must be 16-byte aligned, s 2-byte aligned");
+    return FP4X_ERR_ARG;
+  }
+  if (M == 0 || C == 0) return FP4X_OK;
+  RefineArgs p{};
+  p.out = out; p.out_dtype = FP4X_DT_F32; p.out_stride = C;
+  p.x = static_cast<const uint16_t*>(x);
+  p.idx = idx;
+  p.pa.w0 = static_cast<const uint8_t*>(wp);
+  p.pa.s = static_cast<const uint8_t*>(s);
+  p.pa.K = K;
+  p.gs = gs;
+  p.M = M; p.C = C; p.K = K; p.V = V;
+  const int chunks = K / FmtNV4::KPC;
+  p.lpr = layout_lpr(chunks);
+  p.cpl = (chunks + p.lpr - 1) / p.lpr;
+  const int per_wg = kWaves * (64 / p.lpr);
+  dim3 grid((C + per_wg - 1) / per_wg, M);
+  hipLaunchKernelGGL((refine_kernel<FmtNV4, true>), grid, dim3(kThreads), (size_t)K * 2, (hipStream_t)stream, p);
+  return check_launch("refine_nv4");
 }
 
 }  // extern "C"

@@ -318,10 +318,90 @@ def _patch_fast_head():
     _log("fast target head patch installed")
 
 
-# Reference flags whose patches are outside this build (draft head, disk PLE
-# embeddings, drafter weight swap, MoE ablations, graph debugging).
+# ----------------------------------------------------------------- draft head
+# Device scalars 1 / FP4X_DRAFT_TSCALE per device (graph-safe sharpening of the draft logits).
+_DRAFT_INV_T = {}
+
+
+def _draft_prepare(F, w, s, gs, ids, dc, G=16):
+    """The MTP draft head's subset of an NVFP4 LM head: rows ids of w [V, K/2]
+    and s [V, K/16] (e4m3, row-major), and with dc > 0 their INT2 coarse copy
+    (quantized from the fp32 dequant in blocks of 8192 rows).  [x/fp4patch.py:290-307]"""
+    import torch
+    st = {"idx": ids, "w": w.index_select(0, ids).contiguous(), "s": s.index_select(0, ids).contiguous(),
+          "gs": float(gs)}
+    if dc:
+        parts = [F.quantize_int2(F.dequant_nv4(st["w"][a:a + 8192], st["s"][a:a + 8192], st["gs"]), group=G)
+                 for a in range(0, ids.numel(), 8192)]
+        st["c"] = (torch.cat([t[0] for t in parts]), torch.cat([t[1] for t in parts]))
+    return st
+
+
+def _draft_logits(F, h, st, vocab, dc, cfg=(32, 256, 4), inv_t=None):
+    """Draft logits [M, vocab] bf16: -inf outside the subset.  dc > 0 and M <= 16:
+    INT2 coarse over the subset, its top dc (one int2_topk call), their exact
+    NVFP4 logits; else the NVFP4 GEMV over the whole subset.  [x/fp4patch.py:309-330]"""
+    import torch
+    if dc and h.shape[0] <= 16:
+        _, cand = F.int2_topk(h, *st["c"], st["idx"].numel(), dc)
+        vals = F.refine_nv4(h, cand, st["w"], st["s"], st["gs"])
+        if inv_t is not None:
+            vals = vals * inv_t
+        full = torch.full((h.shape[0], vocab), float("-inf"), dtype=torch.bfloat16, device=h.device)
+        return full.scatter_(1, st["idx"][cand], vals.to(torch.bfloat16))
+    sub = F.nv4_linear(h, st["w"], st["s"], st["gs"], cfg)
+    full = torch.full((h.shape[0], vocab), float("-inf"), dtype=sub.dtype, device=sub.device)
+    full.index_copy_(1, st["idx"], sub)
+    return full
+
+
+def _patch_draft_vocab():
+    """MTP draft head over a reduced vocabulary (draft-only; verification stays exact)."""
+    import torch
+    from vllm.models.qwen4_exp.nvidia import mtp as MTP
+    import fp4x_kernels as F
+    path = os.environ["FP4X_DRAFT_VOCAB"]
+    cfg = tuple(int(v) for v in os.environ.get("FP4X_DRAFT_CFG", "32,256,4").split(","))
+    dc = int(os.environ.get("FP4X_DRAFT_INT2", "0"))         # > 0: INT2 coarse + exact rescore of the top dc
+    dts = float(os.environ.get("FP4X_DRAFT_TSCALE", "1.0"))  # draft logits / dts
+    G = int(os.environ.get("FP4X_DRAFT_INT2_G", "16"))
+    orig = MTP.Qwen4ExpMTP.compute_logits
+
+    def build(self, dev):
+        lm = self.lm_head
+        keep = {int(t) for t in open(path) if t.strip()} | set(range(lm.org_vocab_size - 320, lm.org_vocab_size))
+        ids = torch.tensor([i for i in sorted(keep) if i < lm.weight.shape[0]], device=dev, dtype=torch.long)
+        sc = lm.weight_scale.data
+        n, kb = sc.shape
+        # the NVFP4 scale tiles (128 rows x 4 scale columns, stored 32 x 4 x 4) back to row-major
+        rows = sc.view(torch.uint8).reshape(n // 128, kb // 4, 32, 4, 4).transpose(1, 3).reshape(n, kb)
+        self._fx = _draft_prepare(F, lm.weight.data, rows.view(torch.float8_e4m3fn), lm.weight_global_scale.item(),
+                                  ids, dc, G)
+        self._fx_vocab = lm.weight.shape[0]
+        _log(f"draft vocab head built: {ids.numel()} ids" + (f", INT2 coarse + exact NVFP4 rescore of the top {dc}"
+                                                             if dc else ""))
+
+    def compute_logits(self, hidden_states, spec_step_idx=0):
+        if getattr(self, "_fx", None) is None:
+            if torch.cuda.is_current_stream_capturing() or getattr(self.lm_head, "weight", None) is None:
+                return orig(self, hidden_states, spec_step_idx)
+            build(self, hidden_states.device)
+        h = hidden_states.reshape(-1, hidden_states.shape[-1]).contiguous()
+        inv_t = None
+        if dts != 1.0:
+            if _DRAFT_INV_T.get(h.device) is None:
+                _DRAFT_INV_T[h.device] = torch.full((1,), 1.0 / dts, dtype=torch.float32, device=h.device)
+            inv_t = _DRAFT_INV_T[h.device]
+        return _draft_logits(F, h, self._fx, self._fx_vocab, dc, cfg, inv_t)
+
+    MTP.Qwen4ExpMTP.compute_logits = compute_logits
+    _log(f"draft vocab head patch installed ({path})")
+
+
+# Reference flags whose patches are outside this build (disk PLE embeddings,
+# drafter weight swap, MoE ablations, graph debugging).
 _NOT_BUILT = ("FP4X_KEEP_GRAPH", "FP4X_MOE_ZERO", "FP4X_MOE_TAU", "FP4X_MTP_PATCH", "FP4X_PLE_SPIN",
-              "FP4X_PLE_EARLY", "FP4X_PLE_QD", "FP4X_DRAFT_VOCAB")
+              "FP4X_PLE_EARLY", "FP4X_PLE_QD")
 
 
 def register():
@@ -333,6 +413,11 @@ def register():
             _patch_fast_head()
         except Exception as e:
             _log(f"fast head patch failed: {type(e).__name__}: {e}")
+    if os.environ.get("FP4X_DRAFT_VOCAB"):
+        try:
+            _patch_draft_vocab()
+        except Exception as e:
+            _log(f"draft vocab patch failed: {type(e).__name__}: {e}")
     for flag, fn in (("FP4X_MX8", _patch_mx8), ("FP4X_HC", _patch_hc)):
         if os.environ.get(flag) == "1":
             try:

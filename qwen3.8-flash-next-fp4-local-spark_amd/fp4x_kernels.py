@@ -20,7 +20,7 @@ import torch
 import _fp4x as _L
 
 __all__ = [
-    "mx8_linear", "bf16_linear", "nv4_linear", "w8_linear", "w6_linear", "int2_logits", "refine_mx8_",
+    "mx8_linear", "bf16_linear", "nv4_linear", "w8_linear", "w6_linear", "int2_logits", "refine_mx8_", "refine_nv4",
     "topk_rows", "int2_topk", "w8_linear_layers", "HCFused", "hc_scaled_silu", "hc_gate_mean",
     "quantize_w8", "quantize_w6", "quantize_nv4", "quantize_int2", "quantize_mx8",
     "mx8_dequant", "dequant_int2", "dequant_nv4", "dequant_operand", "ORDER",
@@ -277,6 +277,19 @@ def refine_mx8_(out, x, idx, w8, s_u8, BC=16, BK=256, nw=4):
         raise ValueError("fp4x: refine_mx8_ needs out with unit column stride")
     _L.check(_L.lib().fp4x_refine_mx8(_ptr(out), _dt(out.dtype), out.stride(0), _ptr(x), _ptr(idx), m, C, _ptr(w8),
                                       _ptr(s_u8), K, out.shape[1], _L.stream_of(x)), "refine_mx8")
+    return out
+
+
+def refine_nv4(x, idx, wp, s, gs, BC=16, BK=256, nw=4):
+    """[M, C] exact NVFP4 logits for candidate rows idx[m, c] (fp32 accumulate, times gs)."""
+    _need_cuda(x, idx, wp, s)
+    x = x.to(torch.bfloat16).contiguous()
+    idx = idx.to(torch.int64).contiguous()
+    m, C = idx.shape
+    K = x.shape[1]
+    out = torch.empty((m, C), dtype=torch.float32, device=x.device)
+    _L.check(_L.lib().fp4x_refine_nv4(_ptr(out), _ptr(x), _ptr(idx), m, C, _ptr(wp), _ptr(s), float(gs), K,
+                                      wp.shape[0], _L.stream_of(x)), "refine_nv4")
     return out
 
 

@@ -259,3 +259,62 @@ def test_int2_topk_fused_equals_separate(gpu, F, V, M, rs):
     assert np.array_equal(bf16_bits(coarse), bf16_bits(coarse2))
     assert torch.equal(idx, idx2)
     assert np.array_equal(idx.cpu().numpy(), oh.topk_total_order(bf16_bits(coarse), C))
+
+
+# ------------------------------------------------------------------ draft head (NVFP4 rescore)
+def test_refine_nv4_exact(gpu, F):
+    """refine_nv4: the rescore kernel's fma order replayed by the oracle, bit for
+    bit, times gs; NaN for candidates outside [0, V); within tolerance of the
+    fp32 matmul of the dequantized rows."""
+    import _fp4x
+    rng = np.random.default_rng(31)
+    V, K, M, C = 20000, 2560, 3, 64
+    w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    P, S, gs = oq.quantize_nv4(w)
+    x, xb = act(rng, M, K)
+    idx = np.stack([rng.choice(V, C, replace=False) for _ in range(M)]).astype(np.int64)
+    out = F.refine_nv4(bf16_dev(x), dev(idx), dev(P), dev(S).view(torch.float8_e4m3fn), gs)
+    exact = oh.nv4_rows(xb, P, S, gs, idx, lpr_of(_fp4x.FMT_NV4, K))
+    assert out.shape == (M, C) and out.dtype == torch.float32
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), exact.view(np.uint32))
+    ref = og.matmul_f32(x[:1], oq.dequant_nv4_operand(P[idx[0]], S[idx[0]]))[0] * np.float32(gs)
+    assert_tol(out.cpu().numpy()[0], ref, what="refine_nv4 vs matmul")
+    bad = idx.copy()
+    bad[1, 5], bad[2, 0] = -1, V
+    out2 = F.refine_nv4(bf16_dev(x), dev(bad), dev(P), dev(S).view(torch.float8_e4m3fn), gs).cpu().numpy()
+    assert np.isnan(out2[1, 5]) and np.isnan(out2[2, 0])
+    keep = ~np.isnan(out2)
+    assert np.array_equal(out2[keep].view(np.uint32), exact[keep].view(np.uint32))
+
+
+@pytest.mark.parametrize("dc", [64, 0])
+def test_draft_head(gpu, F, dc):
+    """The plugin's draft head over a vocabulary subset (x/fp4patch.py:309-330):
+    -inf outside the subset; with dc > 0 the top dc of the GPU's own INT2
+    coarse logits (the oracle's total order) carry their exact NVFP4 logits;
+    with dc = 0 the subset carries the NVFP4 GEMV."""
+    import _fp4x
+    import fp4patch
+    rng = np.random.default_rng(32 + dc)
+    vocab, K, M, nsub = 30000, 2560, 3, 6000
+    w = (rng.standard_normal((vocab, K)) * 0.02).astype(np.float32)
+    P, S, gs = oq.quantize_nv4(w)
+    ids_np = np.sort(rng.choice(vocab, nsub, replace=False)).astype(np.int64)
+    x, xb = act(rng, M, K)
+    h = bf16_dev(x)
+    st = fp4patch._draft_prepare(F, dev(P), dev(S).view(torch.float8_e4m3fn), gs, dev(ids_np), dc)
+    full = fp4patch._draft_logits(F, h, st, vocab, dc)
+    got = bf16_bits(full)
+    outside = np.ones((M, vocab), bool)
+    if dc:
+        co = F.int2_logits(h, *st["c"], nsub, out_dtype=torch.bfloat16)
+        cand = oh.topk_total_order(bf16_bits(co), dc)
+        vals = oh.nv4_rows(xb, P[ids_np], S[ids_np], gs, cand, lpr_of(_fp4x.FMT_NV4, K))
+        pos = ids_np[cand]
+        assert np.array_equal(np.take_along_axis(got, pos, 1), fm.bf16_bits(vals))
+        np.put_along_axis(outside, pos, False, 1)
+    else:
+        sub = og.matmul_f32(x, oq.dequant_nv4_operand(P[ids_np], S[ids_np])) * np.float32(gs)
+        assert_tol(to_f32(full)[:, ids_np], sub, what="draft subset GEMV")
+        outside[:, ids_np] = False
+    assert np.all(got[outside] == 0xFF80)
