@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 4
+#define FP4X_ABI_VERSION 5
 
 enum {
   FP4X_OK = 0,
@@ -145,6 +145,16 @@ int fp4x_refine_mx8(void* out, int out_dtype, int64_t out_stride, const void* x,
  *  head, x/fp4patch.py:316] */
 int fp4x_refine_nv4(float* out, const void* x, const int64_t* idx, int M, int C, const void* wp, const void* s, float gs,
                     int K, int V, void* stream);
+
+/* Draft logits out [M, vocab] bf16 (row stride out_stride): -inf everywhere
+ * except out[m, ids[cand[m, c]]] = bf16(vals[m, c] * *inv_t) (bf16(vals[m, c])
+ * when inv_t is NULL).  vals fp32 [M, C], cand int64 [M, C] indexing ids,
+ * ids int64 [n_ids] column numbers; entries whose cand or ids value is out of
+ * range are not written.  Every element of out is written, so out need not be
+ * initialised.  inv_t is a device pointer (read on the device: graph-safe).
+ * [the draft head's full(-inf) + scatter_, x/fp4patch.py:316-320] */
+int fp4x_scatter_draft(void* out, int64_t out_stride, const float* vals, const int64_t* cand, const int64_t* ids,
+                       int64_t n_ids, const float* inv_t, int M, int C, int64_t vocab, void* stream);
 
 /* Mixer down projection: split-K W8 GEMV whose last workgroup per row tile
  * writes di = bf16(sum) [M, N] and bot = bf16(sc * sigmoid(sc)) [M, lr] with

@@ -659,6 +659,42 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t*
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// ---- Draft logits: -inf rows with the rescored candidates scattered in ----
+// (x/fp4patch.py:316-320: torch.full(-inf) + ids[cand] + (vals * inv_t).to(bf16)
+// + scatter_, one launch).  Workgroup (b, m) owns columns [b * 2048, b * 2048 +
+// 2048) of row m: it fills them with -inf, then, after the barrier, writes the
+// candidates that land in them, so every element is written by one workgroup
+// and the candidate store follows the fill in that workgroup's order.
+// Candidates whose cand or ids entry is out of range are not written.
+constexpr int kScatterCols = 2048;
+
+__global__ __launch_bounds__(256) void scatter_draft_kernel(uint16_t* out, int64_t out_stride, const float* vals,
+                                                            const int64_t* cand, const int64_t* ids, int64_t n_ids,
+                                                            const float* inv_t, int C, int64_t vocab) {
+  const int m = blockIdx.y;
+  const int64_t c0 = (int64_t)blockIdx.x * kScatterCols;
+  uint16_t* row = out + (int64_t)m * out_stride;
+  const int64_t e = c0 + (int64_t)threadIdx.x * 8;
+  const uint16_t ninf = 0xFF80;
+  if (e + 8 <= vocab && ((reinterpret_cast<uintptr_t>(row + e) & 15) == 0)) {
+    const uint32_t w = 0xFF80FF80u;
+    *reinterpret_cast<uint4*>(row + e) = make_uint4(w, w, w, w);
+  } else {
+    for (int i = 0; i < 8; ++i)
+      if (e + i < vocab) row[e + i] = ninf;
+  }
+  __syncthreads();
+  const float t = inv_t ? *inv_t : 1.0f;
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const int64_t j = cand[(int64_t)m * C + c];
+    if (j < 0 || j >= n_ids) continue;
+    const int64_t col = ids[j];
+    if (col < c0 || col >= c0 + kScatterCols || col >= vocab) continue;
+    const float v = vals[(int64_t)m * C + c];
+    row[col] = f32_to_bf16(inv_t ? v * t : v);
+  }
+}
+
 }  // namespace fp4x
 
 using namespace fp4x;
@@ -734,6 +770,19 @@ int fp4x_refine_mx8(void* out, int out_dtype, int64_t out_stride, const void* x,
   dim3 grid((C + per_wg - 1) / per_wg, M);
   hipLaunchKernelGGL((refine_kernel<FmtMX8, false>), grid, dim3(kThreads), (size_t)K * 2, (hipStream_t)stream, p);
   return check_launch("refine_mx8");
+}
+
+int fp4x_scatter_draft(void* out, int64_t out_stride, const float* vals, const int64_t* cand, const int64_t* ids,
+                       int64_t n_ids, const float* inv_t, int M, int C, int64_t vocab, void* stream) {
+  if (M < 0 || C < 0 || vocab < 1 || n_ids < 0 || out_stride < vocab) {
+    set_error("scatter_draft: bad shape (vocab >= 1, out_stride >= vocab)");
+    return FP4X_ERR_ARG;
+  }
+  if (M == 0) return FP4X_OK;
+  dim3 grid((unsigned)((vocab + kScatterCols - 1) / kScatterCols), M);
+  hipLaunchKernelGGL(scatter_draft_kernel, grid, dim3(256), 0, (hipStream_t)stream, static_cast<uint16_t*>(out),
+                     out_stride, vals, cand, ids, n_ids, inv_t, C, vocab);
+  return check_launch("scatter_draft");
 }
 
 int fp4x_refine_nv4(float* out, const void* x, const int64_t* idx, int M, int C, const void* wp, const void* s, float gs,

@@ -563,7 +563,8 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   const int64_t tiles = (p.N + 15) / 16;
   const int64_t nw = (int64_t)gridDim.x * W, gw = (int64_t)blockIdx.x * W + wave;
   const int64_t t0 = gw * tiles / nw, t1 = (gw + 1) * tiles / nw;
-  const int nt = (int)(t1 - t0);                     // >= 2 (host condition), so U >= D
+  const int nt = (int)(t1 - t0);                     // >= 1 (host condition); with U < D the units
+                                                     // past U reload the last tile and are never read
   const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
   char* ring = base + xbuf + wave * D * kInt2Unit;
   const int cb = K / 4, sbr = K / 8;                 // code and scale bytes per row
@@ -687,9 +688,11 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
 }
 
 // The INT2 head (fp16 scales, G = 16) through the streaming kernel when the
-// matrix has at least 2 tiles per wave of the grid; false otherwise (or when
-// FP4X_INT2_STREAM=0).  16 waves per CU (ring depth 3) when the staged
-// activations leave room, else 8 waves with the deepest ring that fits.
+// matrix has at least 2 tiles per wave of the grid, or at least 1 when one
+// tile's units fill the ring (the 65k-token draft subset: 4075 tiles over
+// 8 waves per CU); false otherwise (or when FP4X_INT2_STREAM=0).  16 waves per
+// CU (ring depth 3) when the staged activations leave room, else 8 waves with
+// the deepest ring that fits.
 template <int W, int D>
 bool launch_int2_stream_wd(GemvLaunch p, size_t lds, hipStream_t st) {
   auto kern = int2_stream_kernel<W, D>;
@@ -712,8 +715,11 @@ inline bool launch_int2_stream(GemvLaunch p, hipStream_t st) {
   if ((reinterpret_cast<uintptr_t>(p.pa.w0) & 15) || (reinterpret_cast<uintptr_t>(p.pa.s) & 15)) return false;
   const int64_t tiles = (p.N + 15) / 16;
   const size_t xb = (size_t)StreamGeom::xbuf_bytes(p.M, K);
-  auto fits = [&](int W, int D) { return xb + (size_t)W * D * kInt2Unit <= 160 * 1024 &&
-                                         tiles >= (int64_t)device_cus() * W * 2; };
+  const int64_t cus = device_cus();
+  auto fits = [&](int W, int D) {
+    return xb + (size_t)W * D * kInt2Unit <= 160 * 1024 &&
+           (tiles >= cus * W * 2 || (tiles >= cus * W && K / 512 >= D));
+  };
   if (fits(16, 3)) return launch_int2_stream_wd<16, 3>(p, xb + (size_t)16 * 3 * kInt2Unit, st);
   if (fits(8, 6)) return launch_int2_stream_wd<8, 6>(p, xb + (size_t)8 * 6 * kInt2Unit, st);
   if (fits(8, 4)) return launch_int2_stream_wd<8, 4>(p, xb + (size_t)8 * 4 * kInt2Unit, st);

@@ -345,10 +345,7 @@ def _draft_logits(F, h, st, vocab, dc, cfg=(32, 256, 4), inv_t=None):
     if dc and h.shape[0] <= 16:
         _, cand = F.int2_topk(h, *st["c"], st["idx"].numel(), dc)
         vals = F.refine_nv4(h, cand, st["w"], st["s"], st["gs"])
-        if inv_t is not None:
-            vals = vals * inv_t
-        full = torch.full((h.shape[0], vocab), float("-inf"), dtype=torch.bfloat16, device=h.device)
-        return full.scatter_(1, st["idx"][cand], vals.to(torch.bfloat16))
+        return F.scatter_draft(vals, cand, st["idx"], vocab, inv_t)
     sub = F.nv4_linear(h, st["w"], st["s"], st["gs"], cfg)
     full = torch.full((h.shape[0], vocab), float("-inf"), dtype=sub.dtype, device=sub.device)
     full.index_copy_(1, st["idx"], sub)

@@ -21,6 +21,7 @@ import _fp4x as _L
 
 __all__ = [
     "mx8_linear", "bf16_linear", "nv4_linear", "w8_linear", "w6_linear", "int2_logits", "refine_mx8_", "refine_nv4",
+    "scatter_draft",
     "topk_rows", "int2_topk", "w8_linear_layers", "HCFused", "hc_scaled_silu", "hc_gate_mean",
     "quantize_w8", "quantize_w6", "quantize_nv4", "quantize_int2", "quantize_mx8",
     "mx8_dequant", "dequant_int2", "dequant_nv4", "dequant_operand", "ORDER",
@@ -290,6 +291,30 @@ def refine_nv4(x, idx, wp, s, gs, BC=16, BK=256, nw=4):
     out = torch.empty((m, C), dtype=torch.float32, device=x.device)
     _L.check(_L.lib().fp4x_refine_nv4(_ptr(out), _ptr(x), _ptr(idx), m, C, _ptr(wp), _ptr(s), float(gs), K,
                                       wp.shape[0], _L.stream_of(x)), "refine_nv4")
+    return out
+
+
+def scatter_draft(vals, cand, ids, vocab, inv_t=None):
+    """Draft logits [M, vocab] bf16: -inf except column ids[cand[m, c]] of row m,
+    which holds bf16(vals[m, c] * inv_t) (inv_t: a one-element fp32 device
+    tensor, or None for no scaling).  One launch for the reference's
+    torch.full + ids[cand] + (vals * inv_t).to(bf16) + scatter_
+    (x/fp4patch.py:316-320)."""
+    _need_cuda(vals, cand, ids)
+    vals = vals.to(torch.float32).contiguous()
+    cand = cand.to(torch.int64).contiguous()
+    ids = ids.to(torch.int64).contiguous()
+    if inv_t is not None:
+        _need_cuda(inv_t)
+        if inv_t.dtype != torch.float32 or inv_t.numel() != 1:
+            raise ValueError("fp4x: scatter_draft needs inv_t as one fp32 element")
+    if vals.shape != cand.shape or vals.dim() != 2:
+        raise ValueError("fp4x: scatter_draft needs vals and cand of one [M, C] shape")
+    m, C = cand.shape
+    out = torch.empty((m, vocab), dtype=torch.bfloat16, device=vals.device)
+    _L.check(_L.lib().fp4x_scatter_draft(_ptr(out), out.stride(0), _ptr(vals), _ptr(cand), _ptr(ids), ids.numel(),
+                                         None if inv_t is None else _ptr(inv_t), m, C, vocab, _L.stream_of(vals)),
+             "scatter_draft")
     return out
 
 

@@ -28,7 +28,7 @@ def test_header_declares_entry_points():
     for must in ("fp4x_mx8_linear", "fp4x_w8_linear", "fp4x_w6_linear", "fp4x_nv4_linear", "fp4x_int2_logits",
                  "fp4x_topk_rows", "fp4x_refine_mx8", "fp4x_hc_down", "fp4x_hc_up", "fp4x_hc_scaled_silu",
                  "fp4x_hc_gate_mean", "fp4x_bf16_linear", "fp4x_w8_linear_layers", "fp4x_mx8_dequant",
-                 "fp4x_hc_mix", "fp4x_int2_topk"):
+                 "fp4x_hc_mix", "fp4x_int2_topk", "fp4x_refine_nv4", "fp4x_scatter_draft"):
         assert must in names
 
 
@@ -78,6 +78,12 @@ def test_argument_errors_without_gpu(lib):
     assert L.fp4x_hc_mix(None, 10240, None, None, 1, None, None, 3, 336, 10240, 320, 4, 8, None, None, 0, None,
                          None, None, 10240, None, 2560, 8, None) == _fp4x.ERR_ARG
     assert b"scratch" in L.fp4x_last_error()
+    # the draft head: the NVFP4 rescore needs K % 32 == 0 and rows to gather; the scatter a row stride >= vocab
+    assert L.fp4x_refine_nv4(None, None, None, 3, 64, None, None, 1.0, 2500, 100, None) == _fp4x.ERR_ARG
+    assert L.fp4x_refine_nv4(None, None, None, 3, 64, None, None, 1.0, 2560, 0, None) == _fp4x.ERR_ARG
+    assert b"refine_nv4" in L.fp4x_last_error()
+    assert L.fp4x_scatter_draft(None, 100, None, None, None, 10, None, 3, 64, 248320, None) == _fp4x.ERR_ARG
+    assert b"scatter_draft" in L.fp4x_last_error()
     # empty problems are no-ops
     assert L.fp4x_mx8_linear(None, 2560, None, None, None, 0, 0, 64, 2560, 1, None, None, None) == _fp4x.OK
 

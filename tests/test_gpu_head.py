@@ -200,13 +200,16 @@ def test_fast_head_full_size_exact(gpu, F):
 
 
 # ------------------------------------------------------------------ INT2 streaming kernel
-@pytest.mark.parametrize("M,rs", [(3, False), (16, False), (3, True)])
-def test_int2_stream(gpu, F, M, rs, monkeypatch):
-    """Heads of at least 4 tiles per wave of the grid take the streaming kernel
-    (one wave per tile, LDS ring of direct loads); N tail of 40 rows."""
-    rng = np.random.default_rng(77 + M + rs)
+@pytest.mark.parametrize("M,rs,one", [(3, False, False), (16, False, False), (3, True, False), (3, False, True)])
+def test_int2_stream(gpu, F, M, rs, one, monkeypatch):
+    """Heads of at least 2 tiles per wave of the grid take the streaming kernel
+    (one wave per tile, LDS ring of direct loads); N tail of 40 rows.  one:
+    between 1 and 2 tiles per wave at 8 waves per CU (the 65,197-row draft
+    subset on 256 CUs), 3 rows past the last full tile."""
+    rng = np.random.default_rng(77 + M + rs + 5 * one)
     K = 2560
-    V = 4 * 8 * 16 * torch.cuda.get_device_properties(0).multi_processor_count + 40
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    V = 16 * (16 * cus - 21) - 3 if one else 4 * 8 * 16 * cus + 40
     w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
     P, S = oq.quantize_int2(w, group=16)
     del w
@@ -238,12 +241,13 @@ def test_int2_stream(gpu, F, M, rs, monkeypatch):
 
 
 # ------------------------------------------------------------------ fused coarse + top-k
-@pytest.mark.parametrize("V,M,rs", [(248320, 3, False), (248320, 16, False), (200040, 3, True), (50000, 3, False)])
-def test_int2_topk_fused_equals_separate(gpu, F, V, M, rs):
+@pytest.mark.parametrize("V,M,rs,C", [(248320, 3, False, 512), (248320, 16, False, 512), (200040, 3, True, 512),
+                                      (50000, 3, False, 512), (65197, 3, False, 64), (20000, 3, False, 64)])
+def test_int2_topk_fused_equals_separate(gpu, F, V, M, rs, C):
     """int2_topk (slice maxima from the streaming coarse kernel's epilogue where
     it streams, else a slice-max launch) equals int2_logits + topk_rows bit for
     bit, and its selection is the oracle's total order on its own logits."""
-    K, C = 2560, 512
+    K = 2560
     g = torch.Generator(device=gpu).manual_seed(V + M)
     w = torch.randn((V, K), generator=g, device=gpu) * 0.02
     w[torch.randperm(V, generator=g, device=gpu)[:64]] *= 4
@@ -318,3 +322,32 @@ def test_draft_head(gpu, F, dc):
         assert_tol(to_f32(full)[:, ids_np], sub, what="draft subset GEMV")
         outside[:, ids_np] = False
     assert np.all(got[outside] == 0xFF80)
+
+
+@pytest.mark.parametrize("vocab", [248320, 30001, 300])
+def test_scatter_draft(gpu, F, vocab):
+    """The draft logits scatter equals torch.full(-inf) + scatter_ of
+    bf16(vals * inv_t) bit for bit (x/fp4patch.py:316-320), on 16-byte rows and
+    on odd row lengths (unaligned rows, ragged tails); out-of-range cand or ids
+    entries leave -inf."""
+    g = torch.Generator(device=gpu).manual_seed(vocab)
+    M, C = 3, 64
+    nsub = min(vocab, 6000)
+    ids = torch.sort(torch.randperm(vocab, generator=g, device=gpu)[:nsub]).values
+    cand = torch.stack([torch.randperm(nsub, generator=g, device=gpu)[:C] for _ in range(M)])
+    vals = torch.randn((M, C), generator=g, device=gpu) * 8
+    for inv_t in (None, torch.full((1,), 1.0 / 0.7, device=gpu)):
+        got = F.scatter_draft(vals, cand, ids, vocab, inv_t)
+        v = vals if inv_t is None else vals * inv_t
+        ref = torch.full((M, vocab), float("-inf"), dtype=torch.bfloat16, device=gpu)
+        ref.scatter_(1, ids[cand], v.to(torch.bfloat16))
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    bad = cand.clone()
+    bad[0, 0], bad[1, 1] = -1, nsub                  # out of range: not written
+    got = F.scatter_draft(vals, bad, ids, vocab)
+    ref = torch.full((M, vocab), float("-inf"), dtype=torch.bfloat16, device=gpu)
+    keep = torch.ones_like(cand, dtype=torch.bool)
+    keep[0, 0] = keep[1, 1] = False
+    for m in range(M):
+        ref[m, ids[cand[m][keep[m]]]] = vals[m][keep[m]].to(torch.bfloat16)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
