@@ -112,7 +112,9 @@ int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void*
 /* Top-C of each row of bf16 logits [M, V] under the total order (value
  * descending, then index ascending; -0 equals +0, NaN is largest); idx_out
  * int64 [M, C] lists the selected indices in that order.  C <= min(V, 2048);
- * logits 16-byte aligned with stride % 8 == 0.
+ * logits 16-byte aligned with stride % 8 == 0.  Rows are read in 16-byte
+ * units: each row must be readable up to round_up(V, 8) elements (the stride
+ * gives that to every row but the last; the elements past V are ignored).
  * [torch.topk(coarse, C) in the fast head, x/fp4patch.py:377] */
 int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int64_t* idx_out, void* workspace,
                    int64_t ws_bytes, void* stream);

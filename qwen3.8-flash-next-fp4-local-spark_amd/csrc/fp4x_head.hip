@@ -328,7 +328,7 @@ __device__ void tk_finish(uint64_t* cand, int n, int C, int64_t* out) {
 // ---- B: one workgroup of 16 waves per row, no cross-wave atomics ----------
 constexpr int kRsThreads = 1024;
 constexpr int kRsWaves = kRsThreads / 64;
-constexpr int kRsVpt = kTkMaxSlices / 8 / kRsThreads;   // 8-slice vectors per thread (registers)
+constexpr int kRsVptMax = kTkMaxSlices / 8 / kRsThreads;   // 8-slice vectors per thread (registers)
 constexpr int kRsIpt = 2;                                // candidate 8-element items per thread per round
 constexpr int kRsSortThreads = 256;                      // the sort runs on the first 4 waves
 
@@ -477,24 +477,53 @@ __device__ void tk_sort32(uint32_t* a, int n2) {
   }
 }
 
-// k-th largest (k >= 1) of the keys held N per thread (0 = none), two 8-bit
-// rounds over per-wave histograms (no atomics across waves).
+// k-th largest (k >= 1) of the keys held N per thread (0 = none; at least k
+// nonzero keys), a radix select over per-wave histograms (no atomics across
+// waves) whose bins are offsets from the smallest key: one 8-bit round when
+// the keys span fewer than 256 values (logit maxima of one row usually do),
+// else a round on the offset's high bits and one on its low sh bits.  Spread
+// bins also keep the LDS atomics of a wave off one address.
 template <int N>
-__device__ uint32_t rs_kth(const uint32_t (&key)[N], int k, uint32_t* wh, TkHist& h) {
+__device__ uint32_t rs_kth(const uint32_t (&key)[N], int k, uint32_t* wh, TkHist& h, uint32_t* ext) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t* mine = wh + wave * 256;
-  uint32_t prefix = 0;
-  int kk = k;
+  uint32_t hi = 0, lo = 0xffffu;
 #pragma unroll
-  for (int round = 0; round < 2; ++round) {
+  for (int j = 0; j < N; ++j)
+    if (key[j]) {
+      hi = max(hi, key[j]);
+      lo = min(lo, key[j]);
+    }
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    hi = max(hi, rs_xor_lane(hi, d));
+    lo = min(lo, rs_xor_lane(lo, d));
+  }
+  if (lane == 0) {
+    ext[wave] = hi;
+    ext[kRsWaves + wave] = lo;
+  }
+  __syncthreads();
+  hi = 0;
+  lo = 0xffffu;
+#pragma unroll
+  for (int w = 0; w < kRsWaves; ++w) {
+    hi = max(hi, ext[w]);
+    lo = min(lo, ext[kRsWaves + w]);
+  }
+  int sh = 0;
+  while (((hi - lo) >> sh) > 255u) ++sh;           // 0 .. 8
+  uint32_t* mine = wh + wave * 256;
+  uint32_t sel = 0;
+  int kk = k;
+  for (int round = 0; round < (sh ? 2 : 1); ++round) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) mine[lane * 4 + j] = 0;
     // (LDS operations of one wave complete in order: the zeros land before the adds)
 #pragma unroll
     for (int j = 0; j < N; ++j) {
-      const uint32_t kj = key[j];
-      const bool in = kj != 0 && (round == 0 || (kj >> 8) == prefix);
-      if (in) atomicAdd(&mine[round == 0 ? kj >> 8 : kj & 255u], 1u);
+      const uint32_t off = key[j] - lo;
+      const bool in = key[j] != 0 && (round == 0 || (off >> sh) == sel);
+      if (in) atomicAdd(&mine[round == 0 ? off >> sh : off & ((1u << sh) - 1u)], 1u);
     }
     __syncthreads();
     if (threadIdx.x < 256) {
@@ -509,21 +538,48 @@ __device__ uint32_t rs_kth(const uint32_t (&key)[N], int k, uint32_t* wh, TkHist
     const uint32_t bin = h.sel_bin;
     kk -= h.sel_above;
     __syncthreads();
-    prefix = round == 0 ? bin : (prefix << 8) | bin;
+    sel = round == 0 ? bin : (sel << sh) | bin;
   }
-  return prefix;
+  return lo + sel;
 }
 
+// Descending ranks of n <= 256 distinct keys a[0, n) in LDS: thread (t, q)
+// counts the keys above a[t] among a quarter (n2 = 256), an eighth (128) or a
+// sixteenth (<= 64) of them; the partial counts meet in part[1024].  Returns
+// the rank on threads t < n of the first part (threadIdx.x < n), else -1.
+__device__ int rs_rank256(const uint32_t* a, int n, int* part) {
+  int n2 = 64;
+  while (n2 < n) n2 <<= 1;
+  const int parts = kRsThreads / n2, span = n2 / parts;
+  const int t = threadIdx.x % n2, q = threadIdx.x / n2;
+  const uint32_t mine = t < n ? a[t] : 0xffffffffu;
+  int r = 0;
+  const int j0 = q * span, j1 = min(j0 + span, n);
+  for (int j = j0; j < j1; ++j) r += a[j] > mine ? 1 : 0;
+  part[threadIdx.x] = r;
+  __syncthreads();
+  if (threadIdx.x >= n) return -1;
+  int rank = 0;
+  for (int p = 0; p < parts; ++p) rank += part[p * n2 + threadIdx.x];
+  return rank;
+}
+
+// VPT: 8-slice vectors of the row's slice maxima per thread (1, 2 or 4, the
+// fewest that cover the row), so short rows run fewer register slots.
+template <int VPT>
 __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t* logits, int64_t stride, int V, int C,
                                                                  const uint16_t* smax, int64_t sstride,
                                                                  int64_t* idx_out) {
   __shared__ uint64_t cand[kTkCap];   // exact and short-row paths
-  __shared__ uint32_t ck[kTkCap];     // candidate sort keys: key << 16 | (0xffff - position)
-  __shared__ int cidx[kTkCap];        // candidate element indices, increasing
-  __shared__ int slist[kTkCap];       // candidate slices, increasing
+  // (the 64 entries past kTkCap of ck, cidx and slist take the writes of
+  // lanes with nothing to write, so the compactions run without branches)
+  __shared__ uint32_t ck[kTkCap + 64];    // candidate sort keys: key << 16 | (0xffff - position)
+  __shared__ int cidx[kTkCap + 64];       // candidate element indices, increasing
+  __shared__ int slist[kTkCap + 64];      // candidate slices, increasing
   __shared__ uint32_t wh[kRsWaves * 256];
   __shared__ TkHist h;
   __shared__ int slots[kRsWaves];
+  __shared__ uint32_t ext[2 * kRsWaves];
   __shared__ int n_x;
   const int m = blockIdx.x;
   const uint16_t* row = logits + (int64_t)m * stride;
@@ -538,88 +594,105 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t*
   int n_c = 0;
   bool exact = ns < C;
   if (!exact) {
-    // thread t holds the 8-slice vectors [t * vpt, t * vpt + vpt) of the row's
+    // thread t holds the 8-slice vectors [t * VPT, t * VPT + VPT) of the row's
     // slice maxima (the padding past ns is never written: masked)
-    const int nv = (ns + 7) / 8, vpt = (nv + kRsThreads - 1) / kRsThreads;
+    const int nv = (ns + 7) / 8;
     const uint4* src = reinterpret_cast<const uint4*>(smax + (int64_t)m * sstride);
-    uint32_t sk[kRsVpt * 8];
+    uint32_t sk[VPT * 8];
 #pragma unroll
-    for (int j = 0; j < kRsVpt; ++j) {
-      const int vi = threadIdx.x * vpt + j;
+    for (int j = 0; j < VPT; ++j) {
+      const int vi = threadIdx.x * VPT + j;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (j < vpt && vi < nv) v = src[vi];
+      if (vi < nv) v = src[vi];
       const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         const uint32_t kq = q & 1 ? d[q >> 1] >> 16 : d[q >> 1] & 0xffffu;
-        sk[j * 8 + q] = j < vpt && vi * 8 + q < ns ? kq : 0u;
+        sk[j * 8 + q] = vi * 8 + q < ns ? kq : 0u;
       }
     }
     // T0: the C-th largest maximum of 4-slice groups (a lower bound of the
     // C-th largest element: C groups each hold an element >= T0)
-    uint32_t key[kRsVpt * 2];
+    uint32_t key[VPT * 2];
 #pragma unroll
-    for (int j = 0; j < kRsVpt * 2; ++j)
+    for (int j = 0; j < VPT * 2; ++j)
       key[j] = max(max(sk[4 * j], sk[4 * j + 1]), max(sk[4 * j + 2], sk[4 * j + 3]));
     const int ng = (ns + 3) / 4;
-    const uint32_t T0 = ng >= C ? rs_kth(key, C, wh, h) : 1u;
-    // candidate slices (maximum >= T0), in increasing order: one scan
+    const uint32_t T0 = ng >= C ? rs_kth(key, C, wh, h, ext) : 1u;
+    // candidate slices (maximum >= T0), in increasing order: one scan.  Waves
+    // past the row's vectors (short rows) hold no slices and skip the work.
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool live = wv * 64 * VPT < nv;
     int cc = 0;
+    if (live) {
 #pragma unroll
-    for (int j = 0; j < kRsVpt * 8; ++j) cc += sk[j] >= T0 ? 1 : 0;
+      for (int j = 0; j < VPT * 8; ++j) cc += sk[j] >= T0 ? 1 : 0;
+    }
     int nsl;
     int pos = rs_scan(cc, slots, &nsl);
+    nsl = __builtin_amdgcn_readfirstlane(nsl);
+    if (live) {
+      const int dummy = kTkCap + (threadIdx.x & 63);
 #pragma unroll
-    for (int j = 0; j < kRsVpt * 8; ++j)
-      if (sk[j] >= T0) {
-        if (pos < kTkCap) slist[pos] = (threadIdx.x * vpt + (j >> 3)) * 8 + (j & 7);
-        ++pos;
+      for (int j = 0; j < VPT * 8; ++j) {
+        const bool in = sk[j] >= T0;
+        slist[in && pos < kTkCap ? pos : dummy] = (threadIdx.x * VPT + (j >> 3)) * 8 + (j & 7);
+        pos += in ? 1 : 0;
       }
+    }
     __syncthreads();
     exact = nsl > kTkCap;
     if (!exact) {
       // their elements >= T0 in increasing index order: thread t takes
-      // contiguous items (8 elements each) of a round, one scan per round
+      // contiguous items (8 elements each) of a round, one scan per round;
+      // waves holding no item of the round skip to the scan, and the second
+      // item slot is skipped when the round has at most one item per thread
       const int per = S / 8, tot = nsl * per;
       for (int r0 = 0; r0 < tot; r0 += kRsThreads * kRsIpt) {
         const int nr = min(tot - r0, kRsThreads * kRsIpt);
         const int ipt = (nr + kRsThreads - 1) / kRsThreads;
-        uint4 v[kRsIpt];
-        int e[kRsIpt];
-#pragma unroll
-        for (int j = 0; j < kRsIpt; ++j) {
-          const int it = r0 + threadIdx.x * ipt + j;
-          const bool ok = j < ipt && it < r0 + nr;
-          e[j] = ok ? slist[it / per] * S + (it % per) * 8 : -1;
-          v[j] = make_uint4(0, 0, 0, 0);
-          if (ok && e[j] + 8 <= V) v[j] = *reinterpret_cast<const uint4*>(row + e[j]);
-        }
+        const bool wlive = wv * 64 * ipt < nr;
         uint32_t k8[kRsIpt * 8];
+        int e[kRsIpt];
         int cnt = 0;
+        if (wlive) {
+          uint4 v[kRsIpt];
 #pragma unroll
-        for (int j = 0; j < kRsIpt; ++j) {
-          const uint32_t d[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+          for (int j = 0; j < kRsIpt; ++j) {
+            // every slot loads (a dead one reads the row's first 8 elements),
+            // so no load waits at a branch's join; the row's last item is
+            // read whole (rows are readable to round_up(V, 8)), its elements
+            // past V masked below
+            const int it = r0 + threadIdx.x * ipt + j;
+            const bool ok = j < ipt && it < r0 + nr;
+            e[j] = ok ? slist[it / per] * S + (it % per) * 8 : -1;
+            v[j] = *reinterpret_cast<const uint4*>(row + (ok ? e[j] : 0));
+          }
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            uint32_t kq = 0;
-            if (e[j] >= 0 && e[j] + q < V)
-              kq = e[j] + 8 <= V ? tk_key(q & 1 ? d[q >> 1] >> 16 : d[q >> 1] & 0xffffu) : tk_key(row[e[j] + q]);
-            k8[j * 8 + q] = kq;
-            cnt += kq >= T0 ? 1 : 0;
+          for (int j = 0; j < kRsIpt; ++j) {
+            const uint32_t d[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const uint32_t kq = tk_key(q & 1 ? d[q >> 1] >> 16 : d[q >> 1] & 0xffffu);
+              k8[j * 8 + q] = e[j] >= 0 && e[j] + q < V ? kq : 0u;
+              cnt += k8[j * 8 + q] >= T0 ? 1 : 0;
+            }
           }
         }
         int step;
         int p2 = n_c + rs_scan(cnt, slots, &step);
+        if (wlive) {
+          const int dummy = kTkCap + (threadIdx.x & 63);
 #pragma unroll
-        for (int j = 0; j < kRsIpt * 8; ++j)
-          if (k8[j] >= T0) {
-            if (p2 < kTkCap) {
-              ck[p2] = (k8[j] << 16) | (uint32_t)(0xffff - p2);
-              cidx[p2] = e[j >> 3] + (j & 7);
-            }
-            ++p2;
+          for (int j = 0; j < kRsIpt * 8; ++j) {
+            const bool in = k8[j] >= T0;
+            const int at = in && p2 < kTkCap ? p2 : dummy;
+            ck[at] = (k8[j] << 16) | (uint32_t)(0xffff - p2);
+            cidx[at] = e[j >> 3] + (j & 7);
+            p2 += in ? 1 : 0;
           }
-        n_c += step;
+        }
+        n_c += __builtin_amdgcn_readfirstlane(step);
       }
       __syncthreads();
       exact = n_c > kTkCap;
@@ -631,7 +704,10 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t*
     return;
   }
   // sort the candidates (positions follow the index order, so ties sort by index)
-  if (n_c <= 1024) {
+  if (n_c <= 256) {
+    const int r = rs_rank256(ck, n_c, reinterpret_cast<int*>(wh));
+    if (r >= 0 && r < C) out[r] = (int64_t)cidx[threadIdx.x];
+  } else if (n_c <= 1024) {
     uint32_t a[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -732,7 +808,10 @@ int topk_launch(const uint16_t* lg, int64_t stride, int M, int V, int C, int64_t
   const int64_t ss = tk_smax_stride(V);
   if (V > kTkCap && ns >= C && !have_smax)
     hipLaunchKernelGGL(topk_slicemax_kernel, dim3((ns + 255) / 256, M), dim3(256), 0, st, lg, stride, V, smax, ss);
-  hipLaunchKernelGGL(topk_rowsel_kernel, dim3(M), dim3(kRsThreads), 0, st, lg, stride, V, C, smax, ss, idx_out);
+  const int nv = (ns + 7) / 8;
+  auto kern = nv <= kRsThreads ? topk_rowsel_kernel<1> : nv <= 2 * kRsThreads ? topk_rowsel_kernel<2>
+                                                                            : topk_rowsel_kernel<kRsVptMax>;
+  hipLaunchKernelGGL(kern, dim3(M), dim3(kRsThreads), 0, st, lg, stride, V, C, smax, ss, idx_out);
   return check_launch("topk");
 }
 }  // namespace fp4x

@@ -241,8 +241,11 @@ def topk_rows(logits, C):
     if logits.dtype != torch.bfloat16:
         raise TypeError("fp4x: topk_rows takes bf16 logits")
     m, v = logits.shape
-    if logits.stride(1) != 1 or logits.stride(0) % 8 or logits.data_ptr() % 16:
-        padded = torch.empty((m, -(-v // 8) * 8), dtype=logits.dtype, device=logits.device)
+    v8 = -(-v // 8) * 8                            # rows are read in 8-element units
+    end = (logits.storage_offset() + (m - 1) * logits.stride(0) + v8) * 2
+    if (logits.stride(1) != 1 or logits.stride(0) % 8 or logits.data_ptr() % 16
+            or (m and end > logits.untyped_storage().nbytes())):
+        padded = torch.empty((m, v8), dtype=logits.dtype, device=logits.device)
         padded[:, :v] = logits
         logits = padded
     idx = torch.empty((m, C), dtype=torch.int64, device=logits.device)

@@ -35,8 +35,12 @@ def lpr_of(fmt, k):
 
 
 # ------------------------------------------------------------------ top-k
-@pytest.mark.parametrize("V,C", [(248320, 512), (1000, 512), (4096, 2048), (50000, 2048), (100, 1), (5000, 2048)])
+@pytest.mark.parametrize("V,C", [(248320, 512), (1000, 512), (4096, 2048), (50000, 2048), (100, 1), (5000, 2048),
+                                 (65197, 64), (130000, 200), (262000, 100), (300000, 512), (600000, 64)])
 def test_topk_rows_total_order(gpu, F, V, C):
+    """Rows of 1, 2 and 4 slice vectors per thread, candidate counts for the
+    rank sort (C <= about 200) and the bitonic sorts; row 2's specials widen its
+    key range past 256 values (two radix rounds), rows 0-1 stay within it."""
     rng = np.random.default_rng(V + C)
     vals = fm.round_bf16((rng.standard_normal((3, V)) * 2).astype(np.float32))
     vals[1] = fm.round_bf16(np.round(vals[1] * 4) / 4)          # heavy ties
@@ -46,6 +50,28 @@ def test_topk_rows_total_order(gpu, F, V, C):
     got = F.topk_rows(t, C).cpu().numpy()
     want = oh.topk_total_order(bits, C)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("view", [False, True])
+def test_topk_tail_item(gpu, F, view):
+    """Rows of 50,003 elements whose largest values sit in the last, partial
+    8-element item (read whole, the elements past V masked), from a padded copy
+    and from a view whose stride already covers round_up(V, 8)."""
+    rng = np.random.default_rng(50003)
+    V, C = 50003, 64
+    vals = fm.round_bf16(rng.standard_normal((3, V)).astype(np.float32))
+    vals[0, -3:] = [9.0, 8.5, 9.0]                   # ties at the very end
+    vals[1, -1] = 7.0
+    bits = fm.bf16_bits(vals)
+    if view:
+        big = np.full((3, V + 5), 0x7F80, np.uint16)   # +inf past V: must not be selected
+        big[:, :V] = bits
+        t = dev(big.view(np.int16)).view(torch.bfloat16)[:, :V]
+    else:
+        t = dev(bits.view(np.int16)).view(torch.bfloat16)
+    got = F.topk_rows(t, C).cpu().numpy()
+    assert np.array_equal(got, oh.topk_total_order(bits, C))
+    assert got[0, :3].tolist() == [V - 3, V - 1, V - 2] and got[1, 0] == V - 1
 
 
 def test_topk_all_equal_exact_path(gpu, F):
