@@ -359,21 +359,30 @@ def main():
     kernels = {}
     kernels["B_w8_gates_48_layers_M3"] = entry(ms_step * 1e3, step_bytes)
     sel = set("ABCDEF") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
+    def done(what):
+        print(f"[bench] {what} done", file=sys.stderr, flush=True)
+
+    done("headline")
     if "B" in sel:
         bench_gates_single(F, torch, dev, kernels, q, s)
+        done("B")
     del qs, out3, g_full, g_rem
     torch.cuda.empty_cache()
     if sel & {"A", "C"}:
         bench_dense(F, torch, dev, kernels)
+        done("A, C")
     if "D" in sel:
         bench_hc(F, torch, dev, kernels)
         torch.cuda.empty_cache()
+        done("D")
     if "E" in sel:
         bench_head(F, torch, dev, kernels)
         torch.cuda.empty_cache()
+        done("E")
     if "F" in sel:
         bench_draft(F, torch, dev, kernels)
         torch.cuda.empty_cache()
+        done("F")
 
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic_gates48_M3.json")

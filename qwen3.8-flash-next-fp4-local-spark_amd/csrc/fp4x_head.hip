@@ -750,24 +750,35 @@ __global__ __launch_bounds__(256) void scatter_draft_kernel(uint16_t* out, int64
   const int m = blockIdx.y;
   const int64_t c0 = (int64_t)blockIdx.x * kScatterCols;
   uint16_t* row = out + (int64_t)m * out_stride;
+  // the first 256 candidates' columns and values load before the fill, so
+  // their two dependent round trips overlap its stores
+  auto fetch = [&](int c, int64_t& col, float& v) {
+    col = -1;
+    v = 0.0f;
+    if (c >= C) return;
+    const int64_t j = cand[(int64_t)m * C + c];
+    if (j < 0 || j >= n_ids) return;
+    col = ids[j];
+    v = vals[(int64_t)m * C + c];
+  };
+  int64_t col;
+  float v;
+  fetch(threadIdx.x, col, v);
+  const float t = inv_t ? *inv_t : 1.0f;
   const int64_t e = c0 + (int64_t)threadIdx.x * 8;
-  const uint16_t ninf = 0xFF80;
   if (e + 8 <= vocab && ((reinterpret_cast<uintptr_t>(row + e) & 15) == 0)) {
     const uint32_t w = 0xFF80FF80u;
     *reinterpret_cast<uint4*>(row + e) = make_uint4(w, w, w, w);
   } else {
     for (int i = 0; i < 8; ++i)
-      if (e + i < vocab) row[e + i] = ninf;
+      if (e + i < vocab) row[e + i] = 0xFF80;
   }
   __syncthreads();
-  const float t = inv_t ? *inv_t : 1.0f;
-  for (int c = threadIdx.x; c < C; c += blockDim.x) {
-    const int64_t j = cand[(int64_t)m * C + c];
-    if (j < 0 || j >= n_ids) continue;
-    const int64_t col = ids[j];
-    if (col < c0 || col >= c0 + kScatterCols || col >= vocab) continue;
-    const float v = vals[(int64_t)m * C + c];
-    row[col] = f32_to_bf16(inv_t ? v * t : v);
+  for (int c = threadIdx.x;;) {
+    if (col >= c0 && col < c0 + kScatterCols && col < vocab) row[col] = f32_to_bf16(inv_t ? v * t : v);
+    c += blockDim.x;
+    if (c >= C) break;
+    fetch(c, col, v);
   }
 }
 
