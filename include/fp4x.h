@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 5
+#define FP4X_ABI_VERSION 6
 
 enum {
   FP4X_OK = 0,
@@ -56,6 +56,10 @@ enum {
   FP4X_FMT_INT2_E4M3 = 6,
   FP4X_FMT_BF16 = 7,
 };
+
+/* weight-preparation sources and targets (fp4x_quantize, fp4x_absmax) */
+enum { FP4X_SRC_F32 = 0, FP4X_SRC_BF16 = 1, FP4X_SRC_MX8 = 2, FP4X_SRC_NV4 = 3 };
+enum { FP4X_Q_W8 = 0, FP4X_Q_W6 = 1, FP4X_Q_NV4 = 2, FP4X_Q_INT2 = 3 };
 
 const char* fp4x_last_error(void);
 int fp4x_abi_version(void);
@@ -157,6 +161,27 @@ int fp4x_refine_nv4(float* out, const void* x, const int64_t* idx, int M, int C,
  * [the draft head's full(-inf) + scatter_, x/fp4patch.py:316-320] */
 int fp4x_scatter_draft(void* out, int64_t out_stride, const float* vals, const int64_t* cand, const int64_t* ids,
                        int64_t n_ids, const float* inv_t, int M, int C, int64_t vocab, void* stream);
+
+/* Weight preparation: quantize an [N, K] matrix (K % 64 == 0) group by group.
+ * Source src: FP4X_SRC_F32 / _BF16 (src_a rows, contiguous), _MX8 (src_a
+ * e4m3fn [N, K], src_b e8m0 [N, K/32]) or _NV4 (src_a e2m1 pairs [N, K/2],
+ * src_b e4m3fn [N, K/16], src_gs), packed rows decoded exactly as by
+ * mx8_dequant and dequant_nv4.  Target dst:
+ *   FP4X_Q_W8   out0 int8 q [N, K], out1 fp32 s [N, K/64]
+ *   FP4X_Q_W6   out0 L [N, K/2], out1 H [N, K/4], out2 fp16 S [N, K/32]; qmax 1..31
+ *   FP4X_Q_NV4  out0 P [N, K/2], out1 e4m3fn S [N, K/16]; dst_gs the global scale
+ *   FP4X_Q_INT2 out0 P [N, K/4], out1 fp16 S [N, K/G]; G = 16, 32 or 64
+ * Results equal the reference's torch quantizers evaluated in fp32 with IEEE
+ * division.  16-byte aligned sources and out0.
+ * [quantize_w8 :138-144, quantize_w6 :179-202 (clip_search = 0), quantize_nv4
+ *  :277-300, quantize_int2 :330-351 (fp16 scales); the weight preparation of
+ *  x/fp4patch.py:61-83, :179-182, :211-214, :357-359] */
+int fp4x_quantize(int src, const void* src_a, const void* src_b, float src_gs, int64_t N, int K, int dst, int G,
+                  int qmax, float dst_gs, void* out0, void* out1, void* out2, void* stream);
+/* max |w| of a source matrix (as fp4x_quantize reads it) into *out, a device
+ * float the caller zeroes first.  [quantize_nv4's global amax, x/fp4x_kernels.py:284-287] */
+int fp4x_absmax(int src, const void* src_a, const void* src_b, float src_gs, int64_t N, int K, float* out,
+                void* stream);
 
 /* Mixer down projection: split-K W8 GEMV whose last workgroup per row tile
  * writes di = bf16(sum) [M, N] and bot = bf16(sc * sigmoid(sc)) [M, lr] with

@@ -108,8 +108,8 @@ def quantize_nv4(w, rows=2048):
     f = _groups(w, 16)
     sc = np.clip(np.abs(f).max(-1, keepdims=True) / F32(6.0) / gs32, F32(2.0 ** -9), F32(448.0))
     sc_code = e4m3_encode(sc)
-    sf = e4m3_decode(sc_code) * gs32
-    v = np.clip(f / sf, F32(-6), F32(6))
+    sf = (e4m3_decode(sc_code) * gs32).astype(F32)     # fp32 product (the reference's sc.float() * gs)
+    v = np.clip(f / sf, F32(-6), F32(6))               # fp32 division
     mag = np.searchsorted(_MIDS, np.abs(v), side="left").astype(np.int64)
     q = (mag | ((v < 0).astype(np.int64) << 3)).reshape(n, k)
     P = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
@@ -134,8 +134,9 @@ def dequant_nv4_operand(P, S_codes):
 
 
 def dequant_nv4(P, S_codes, gs):
-    """fp32 (v * S) * gs.  [x/fp4x_kernels.py:420-426]"""
-    return dequant_nv4_operand(P, S_codes) * F32(gs)
+    """fp32 (v * S) * gs: the exact product v * S, one fp32 rounding by gs.
+    [x/fp4x_kernels.py:420-426]"""
+    return (dequant_nv4_operand(P, S_codes) * F32(gs)).astype(F32)
 
 
 # ----------------------------------------------------------------- INT2
@@ -153,7 +154,7 @@ def quantize_int2(w, scale_fmt="fp16", group=16):
     else:
         rs = s.max(1, keepdims=True) / F32(448.0)
         S = e4m3_encode(s / rs)
-        sf = e4m3_decode(S) * rs
+        sf = (e4m3_decode(S) * rs).astype(F32)         # fp32 product (s.float() * rs)
         rows = rs.reshape(n).astype(F32)
     with np.errstate(divide="ignore", invalid="ignore"):
         idx = np.clip(np.floor(f / sf) + 2, 0, 3).astype(np.uint8).reshape(n, k // 4, 4)
@@ -184,7 +185,7 @@ def mx8_dequant(w_codes, s_u8):
     """fp32 e4m3(w) * 2^(s - 127).  [x/fp4x_kernels.py:261-267]"""
     w = e4m3_decode(w_codes)
     n, k = w.shape
-    return (w.reshape(n, k // 32, 32) * e8m0_to_f32(s_u8)[..., None]).reshape(n, k)
+    return (w.reshape(n, k // 32, 32) * e8m0_to_f32(s_u8)[..., None]).reshape(n, k).astype(F32)   # exact in fp32
 
 
 def quantize_mx8(w):

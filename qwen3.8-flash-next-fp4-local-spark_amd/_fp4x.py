@@ -36,6 +36,8 @@ _SIGS = {
     "fp4x_refine_mx8": ([_P, _I, _I64, _P, _P, _I, _I, _P, _P, _I, _I, _P], _I),
     "fp4x_refine_nv4": ([_P, _P, _P, _I, _I, _P, _P, ctypes.c_float, _I, _I, _P], _I),
     "fp4x_scatter_draft": ([_P, _I64, _P, _P, _P, _I64, _P, _I, _I, _I64, _P], _I),
+    "fp4x_quantize": ([_I, _P, _P, ctypes.c_float, _I64, _I, _I, _I, _I, ctypes.c_float, _P, _P, _P, _P], _I),
+    "fp4x_absmax": ([_I, _P, _P, ctypes.c_float, _I64, _I, _P, _P], _I),
     "fp4x_hc_down": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "fp4x_hc_up": ([_P, _I64, _P, _P, _I, _P, _I64, _P, _I, _I, _I, _I, _I, _P], _I),
     "fp4x_hc_mix": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P, _I64, _P, _I, _I,
@@ -46,7 +48,7 @@ _SIGS = {
     "fp4x_mx8_dequant": ([_P, _P, _I, _I, _P, _P], _I),
     "fp4x_dot2_bf16": ([_P, _P, _P, _P, _I, _P], _I),
 }
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _LIB = None
 

@@ -73,10 +73,13 @@ def _patch_mx8():
         key = id(self)
         q = cache.get(key)
         if q is None and not torch.cuda.is_current_stream_capturing():
-            wf = F.mx8_dequant(w, s)
-            q = F.quantize_nv4(wf) if mode_for(*w.shape) != "w6" else F.quantize_w6(wf, qmax, clip)
+            if mode_for(*w.shape) != "w6":
+                q = F.requantize_mx8(w, s, "nv4")          # from the packed rows, no fp32 copy
+            elif not clip:
+                q = F.requantize_mx8(w, s, "w6", qmax=qmax)
+            else:                                          # the clip search runs on the torch formulas
+                q = F.quantize_w6(F.mx8_dequant(w, s), qmax, clip)
             cache[key] = q
-            del wf
             if len(cache) in (1, 200):
                 _log(f"dense {dense_mode}: quantized {len(cache)} layers")
         return q
@@ -276,10 +279,9 @@ def _patch_fast_head():
         w = pk.weight.values
         sc = pk.weight.scale_rows.view(torch.uint8).view(w.shape[0], -1)
         st["w"], st["s"] = w, sc
-        wf = F.mx8_dequant(w, sc)
         st["int2"] = os.environ.get("FP4X_HEAD_COARSE", "int2") == "int2"
-        st["coarse"] = F.quantize_int2(wf, group=G) if st["int2"] else F.quantize_nv4(wf)
-        del wf
+        # the coarse copy straight from the packed MXFP8 rows (no fp32 copy of the head)
+        st["coarse"] = F.requantize_mx8(w, sc, "int2", group=G) if st["int2"] else F.requantize_mx8(w, sc, "nv4")
         ref = orig(self, h)
         st["V"], st["dtype"] = ref.shape[-1], ref.dtype
         out = fast(self, h)
@@ -326,14 +328,13 @@ _DRAFT_INV_T = {}
 def _draft_prepare(F, w, s, gs, ids, dc, G=16):
     """The MTP draft head's subset of an NVFP4 LM head: rows ids of w [V, K/2]
     and s [V, K/16] (e4m3, row-major), and with dc > 0 their INT2 coarse copy
-    (quantized from the fp32 dequant in blocks of 8192 rows).  [x/fp4patch.py:290-307]"""
-    import torch
+    (the reference quantizes the fp32 dequant in blocks of 8192 rows; groups are
+    row-local, so one pass over the packed rows gives the same codes).
+    [x/fp4patch.py:290-307]"""
     st = {"idx": ids, "w": w.index_select(0, ids).contiguous(), "s": s.index_select(0, ids).contiguous(),
           "gs": float(gs)}
     if dc:
-        parts = [F.quantize_int2(F.dequant_nv4(st["w"][a:a + 8192], st["s"][a:a + 8192], st["gs"]), group=G)
-                 for a in range(0, ids.numel(), 8192)]
-        st["c"] = (torch.cat([t[0] for t in parts]), torch.cat([t[1] for t in parts]))
+        st["c"] = F.requantize_nv4(st["w"], st["s"], st["gs"], "int2", group=G)
     return st
 
 

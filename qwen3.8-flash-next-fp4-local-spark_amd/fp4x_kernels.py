@@ -24,7 +24,7 @@ __all__ = [
     "scatter_draft",
     "topk_rows", "int2_topk", "w8_linear_layers", "HCFused", "hc_scaled_silu", "hc_gate_mean",
     "quantize_w8", "quantize_w6", "quantize_nv4", "quantize_int2", "quantize_mx8",
-    "mx8_dequant", "dequant_int2", "dequant_nv4", "dequant_operand", "ORDER",
+    "mx8_dequant", "dequant_int2", "dequant_nv4", "dequant_operand", "requantize_mx8", "requantize_nv4", "ORDER",
 ]
 
 MAX_M = 16  # rows per launch; larger M runs as consecutive 16-row launches
@@ -463,9 +463,94 @@ ORDER = (0, 2, 1, 3)  # INT2: element j of each 4-group lives in bit pair ORDER[
 _E2M1 = {}
 
 
+# HIP weight preparation
+_SRC_F32, _SRC_BF16, _SRC_MX8, _SRC_NV4 = 0, 1, 2, 3
+_Q_W8, _Q_W6, _Q_NV4, _Q_INT2 = 0, 1, 2, 3
+
+
+def _hip_src(w):
+    """A dense fp32/bf16 device matrix as a HIP quantizer source, or None (CPU
+    tensors and other dtypes take the torch formulas)."""
+    if not isinstance(w, torch.Tensor) or not w.is_cuda or w.dim() != 2 or w.shape[1] % 64 \
+            or w.dtype not in (torch.float32, torch.bfloat16):
+        return None
+    w = w.contiguous()
+    return (_SRC_F32 if w.dtype == torch.float32 else _SRC_BF16, w, None, 0.0)
+
+
+def _hip_quantize(src, n, k, dst, G=16, qmax=31, gs=0.0):
+    """One fp4x_quantize call; returns the output planes of the target."""
+    kind, a, b, sgs = src
+    dev = a.device
+    shapes = {_Q_W8: [(k, torch.int8), (k // 64, torch.float32)],
+              _Q_W6: [(k // 2, torch.uint8), (k // 4, torch.uint8), (k // 32, torch.float16)],
+              _Q_NV4: [(k // 2, torch.uint8), (k // 16, torch.float8_e4m3fn)],
+              _Q_INT2: [(k // 4, torch.uint8), (k // G, torch.float16)]}[dst]
+    outs = [torch.empty((n, c), dtype=dt, device=dev) for c, dt in shapes]
+    o = [_ptr(t) for t in outs] + [None] * (3 - len(outs))
+    _L.check(_L.lib().fp4x_quantize(kind, _ptr(a), None if b is None else _ptr(b), float(sgs), n, k, dst, G, qmax,
+                                    float(gs), o[0], o[1], o[2], _L.stream_of(a)), "quantize")
+    return outs
+
+
+def _hip_nv4(src, n, k):
+    """NVFP4 of a source: the global amax on the device (one host read, as the
+    reference's .item()), gs = max(amax / 6 / 448, 1e-30), then the groups."""
+    kind, a, b, sgs = src
+    amax = torch.zeros(1, dtype=torch.float32, device=a.device)
+    _L.check(_L.lib().fp4x_absmax(kind, _ptr(a), None if b is None else _ptr(b), float(sgs), n, k, _ptr(amax),
+                                  _L.stream_of(a)), "absmax")
+    gs = max(float(amax.item()) / 6.0 / 448.0, 1e-30)
+    P, S = _hip_quantize(src, n, k, _Q_NV4, gs=gs)
+    return P, S, gs
+
+
+def requantize_mx8(w8, s_u8, fmt, group=16, qmax=31):
+    """quantize_<fmt>(mx8_dequant(w8, s_u8)) for fmt in w8, w6, nv4, int2, read
+    from the packed MXFP8 rows without their fp32 copy (the plugin's layer and
+    LM-head preparation, x/fp4patch.py:61-83, :357-359)."""
+    _need_cuda(w8, s_u8)
+    n, k = w8.shape
+    if k % 64 or (fmt == "int2" and group not in (16, 32, 64)):
+        wf = mx8_dequant(w8, s_u8)
+        return {"w8": quantize_w8, "w6": lambda t: quantize_w6(t, qmax), "nv4": quantize_nv4,
+                "int2": lambda t: quantize_int2(t, group=group)}[fmt](wf)
+    src = (_SRC_MX8, w8.contiguous(), s_u8.contiguous().view(torch.uint8), 0.0)
+    return _requantize(src, n, k, fmt, group, qmax)
+
+
+def requantize_nv4(P, S, gs, fmt, group=16, qmax=31):
+    """quantize_<fmt>(dequant_nv4(P, S, gs)) read from the packed NVFP4 rows
+    without their fp32 copy (the draft head's INT2 copy, x/fp4patch.py:303-306)."""
+    _need_cuda(P, S)
+    n, k = P.shape[0], P.shape[1] * 2
+    if k % 64 or (fmt == "int2" and group not in (16, 32, 64)):
+        wf = dequant_nv4(P, S, gs)
+        return {"w8": quantize_w8, "w6": lambda t: quantize_w6(t, qmax), "nv4": quantize_nv4,
+                "int2": lambda t: quantize_int2(t, group=group)}[fmt](wf)
+    src = (_SRC_NV4, P.contiguous(), S.contiguous().view(torch.uint8), float(gs))
+    return _requantize(src, n, k, fmt, group, qmax)
+
+
+def _requantize(src, n, k, fmt, group, qmax):
+    if fmt == "w8":
+        return tuple(_hip_quantize(src, n, k, _Q_W8))
+    if fmt == "w6":
+        return tuple(_hip_quantize(src, n, k, _Q_W6, qmax=qmax))
+    if fmt == "nv4":
+        return _hip_nv4(src, n, k)
+    if fmt == "int2":
+        return tuple(_hip_quantize(src, n, k, _Q_INT2, G=group))
+    raise ValueError(f"fp4x: unknown format {fmt!r}")
+
+
 @torch.no_grad()
 def quantize_w8(w):
-    """Symmetric int8 with fp32 scales per 64: (q [N, K], s [N, K/64])."""
+    """Symmetric int8 with fp32 scales per 64: (q [N, K], s [N, K/64]).
+    HIP kernel for device fp32/bf16 matrices, torch formulas otherwise."""
+    src = _hip_src(w)
+    if src is not None:
+        return tuple(_hip_quantize(src, w.shape[0], w.shape[1], _Q_W8))
     n, k = w.shape
     g = w.float().reshape(n, k // 64, 64)
     s = g.abs().amax(-1).clamp_min(1e-12) / 127.0
@@ -483,7 +568,11 @@ def _w6_pack(codes):
 @torch.no_grad()
 def quantize_w6(w, qmax=31, clip_search=0):
     """W6 g32 two-plane layout: (L [N, K/2], H [N, K/4], S fp16 [N, K/32]).
-    qmax < 31 quantizes to fewer levels in the same layout."""
+    qmax < 31 quantizes to fewer levels in the same layout.  HIP kernel for
+    device fp32/bf16 matrices without a clip search."""
+    src = _hip_src(w)
+    if src is not None and not clip_search:
+        return tuple(_hip_quantize(src, w.shape[0], w.shape[1], _Q_W6, qmax=qmax))
     n, k = w.shape
     L = torch.empty((n, k // 2), dtype=torch.uint8, device=w.device)
     H = torch.empty((n, k // 4), dtype=torch.uint8, device=w.device)
@@ -510,7 +599,11 @@ def quantize_w6(w, qmax=31, clip_search=0):
 
 @torch.no_grad()
 def quantize_nv4(w, rows=2048):
-    """RTN NVFP4: (P [N, K/2] e2m1 pairs, S [N, K/16] e4m3, gs python float)."""
+    """RTN NVFP4: (P [N, K/2] e2m1 pairs, S [N, K/16] e4m3, gs python float).
+    HIP kernels for device fp32/bf16 matrices."""
+    src = _hip_src(w)
+    if src is not None:
+        return _hip_nv4(src, w.shape[0], w.shape[1])
     n, k = w.shape
     lut = _E2M1.get(w.device)
     if lut is None:
@@ -534,7 +627,11 @@ def quantize_nv4(w, rows=2048):
 
 @torch.no_grad()
 def quantize_int2(weight, scale_fmt="fp16", group=16):
-    """INT2 per group (levels -1.5..1.5 x s): fp16 -> (P, S); e4m3 -> (P, S_e4m3, row_scale fp32)."""
+    """INT2 per group (levels -1.5..1.5 x s): fp16 -> (P, S); e4m3 -> (P, S_e4m3, row_scale fp32).
+    HIP kernel for device fp32/bf16 matrices with fp16 scales and G = 16, 32, 64."""
+    src = _hip_src(weight)
+    if src is not None and scale_fmt == "fp16" and group in (16, 32, 64):
+        return tuple(_hip_quantize(src, weight.shape[0], weight.shape[1], _Q_INT2, G=group))
     n, k = weight.shape
     P = torch.empty((n, k // 4), dtype=torch.uint8, device=weight.device)
     S = torch.empty((n, k // group), dtype=torch.float16 if scale_fmt == "fp16" else torch.float8_e4m3fn,

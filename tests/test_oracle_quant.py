@@ -172,3 +172,48 @@ def test_hc_oracle_closed_forms():
     nrm = np.full((1, 8), 2.0, np.float32)
     g = np.zeros((1, 8), np.float32)
     assert ohc.gate_mean(nrm, g, 4).tolist() == [[1.0, 1.0]]
+
+
+def nv4_midpoint_case(seed=0):
+    """A [2, 16] matrix whose row 0 holds, besides its scale-setting maximum,
+    elements w with fp32(w / sf) exactly on an e2m1 midpoint while the exact
+    quotient lies above it: fp32 and fp64 evaluation of the reference's
+    v = w / (sc.float() * gs) disagree on those elements' magnitude."""
+    rng = np.random.default_rng(seed)
+    mids = [0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0]
+    while True:
+        big = np.float32(rng.uniform(1.0, 2.0))
+        amax = np.float32(big * np.float32(rng.uniform(0.05, 0.9)))
+        w = np.zeros((2, 16), np.float32)
+        w[1, 0] = big                                             # the global maximum (sets gs)
+        w[0, 0] = amax
+        gs = max(float(big) / 6.0 / 448.0, 1e-30)
+        sc = np.clip(amax / np.float32(6.0) / np.float32(gs), np.float32(2.0 ** -9), np.float32(448.0))
+        sf = np.float32(fm.e4m3_decode(fm.e4m3_encode(np.array([sc])))[0] * np.float32(gs))
+        hits = []
+        for m in mids:
+            f = np.float32(np.float64(m) * np.float64(sf))
+            if f < amax and np.float32(f / sf) == np.float32(m) and np.float64(f) / np.float64(sf) > m:
+                hits.append(f)
+        if len(hits) >= 2:
+            w[0, 1:1 + len(hits)] = hits
+            return w, len(hits)
+
+
+def test_nv4_quotient_is_fp32():
+    """The oracle follows the reference's fp32 ops: sf = fp32(sc * gs) and v =
+    fp32(w / sf); ties at a midpoint round down.  Pinned against torch on CPU
+    evaluating the reference's expression (x/fp4x_kernels.py:293-296)."""
+    w, n = nv4_midpoint_case()
+    P, S, gs = oq.quantize_nv4(w)
+    nib = oq.nv4_values(P)[0, 1:1 + n]
+    g = torch.from_numpy(w).reshape(2, 1, 16)
+    sc = (g.abs().amax(-1, keepdim=True) / 6.0 / gs).clamp(min=2 ** -9, max=448.0).to(torch.float8_e4m3fn)
+    lut = torch.tensor([0, .5, 1, 1.5, 2, 3, 4, 6])
+    v = (g / (sc.float() * gs)).clamp(-6, 6)
+    want = lut[torch.bucketize(v.abs(), (lut[1:] + lut[:-1]) / 2)].reshape(2, 16)[0, 1:1 + n].numpy()
+    assert np.array_equal(nib, want)
+    # the same elements evaluated in fp64 land one level higher
+    sf64 = fm.e4m3_decode(S[0, 0]) * np.float64(np.float32(gs))
+    up = np.searchsorted(oq._MIDS, np.abs(w[0, 1:1 + n].astype(np.float64) / sf64), side="left")
+    assert np.all(fm.E2M1[up] > nib)
