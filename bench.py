@@ -12,7 +12,8 @@ HBM rather than the 256 MB MALL.
 
 `kernels` adds per-kernel µs and GB/s for every configuration (MXFP8 4096 x
 2560, W6 8192 x 2560, NVFP4 16384 x 2560 at M = 1/3/16, the 97-layer fused
-mixer, and the 248,320-row fast LM head), timed as HIP-graph replays.
+mixer, the 248,320-row fast LM head, the 65k-token draft head), timed as
+HIP-graph replays, and the load-time weight preparation (group G, eager).
 `cpu_baseline` times the oracle (numpy) on the host cores for a bounded
 sample of the headline workload.
 """
@@ -35,7 +36,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E,F")
+    ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E,F,G")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -256,6 +257,44 @@ def bench_draft(F, torch, dev, out):
     del copies, wc, st
 
 
+def bench_prep(F, torch, dev, out):
+    """Weight preparation (x/fp4patch.py:61-83, :179-182, :357-359), eager as the
+    plugin runs it at load: the LM head's INT2 copy and a dense layer's NVFP4
+    and W6 copies straight from packed MXFP8 rows, and the mixer's W8 copy of a
+    bf16 weight.  Bytes: packed source read + packed output written."""
+    g = torch.Generator(device=dev).manual_seed(9)
+
+    def timed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    V, K = 248320, 2560
+    q, s = F.quantize_mx8(torch.randn((V, K), generator=g, device=dev) * 0.02)
+    torch.cuda.empty_cache()
+    us = timed(lambda: F.requantize_mx8(q, s, "int2", group=16))
+    out["G_prep_int2_from_mx8_248320x2560"] = dict(entry(us, V * K + V * K // 32 + V * K // 4 + V * K // 16 * 2),
+                                                   fp32_copy_avoided_MB=round(V * K * 4 / 1e6))
+    del q, s
+    N = 16384
+    q, s = F.quantize_mx8(torch.randn((N, K), generator=g, device=dev) * 0.02)
+    src = N * K + N * K // 32
+    us = timed(lambda: F.requantize_mx8(q, s, "nv4"))
+    out["G_prep_nv4_from_mx8_16384x2560"] = entry(us, src + N * K // 2 + N * K // 16)
+    us = timed(lambda: F.requantize_mx8(q, s, "w6"))
+    out["G_prep_w6_from_mx8_16384x2560"] = entry(us, src + N * K // 2 + N * K // 4 + N * K // 32 * 2)
+    w = (torch.randn((336, 10240), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    us = timed(lambda: F.quantize_w8(w))
+    out["G_prep_w8_from_bf16_336x10240"] = entry(us, 336 * 10240 * 2 + 336 * 10240 + 336 * 160 * 4)
+    del q, s, w
+
+
 def cpu_baseline(seconds):
     """The oracle's dequantize-then-matmul router gates (numpy, all host
     cores) on a bounded sample: whole 48-layer passes at M = 3."""
@@ -358,7 +397,7 @@ def main():
 
     kernels = {}
     kernels["B_w8_gates_48_layers_M3"] = entry(ms_step * 1e3, step_bytes)
-    sel = set("ABCDEF") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
+    sel = set("ABCDEFG") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
     def done(what):
         print(f"[bench] {what} done", file=sys.stderr, flush=True)
 
@@ -383,6 +422,10 @@ def main():
         bench_draft(F, torch, dev, kernels)
         torch.cuda.empty_cache()
         done("F")
+    if "G" in sel:
+        bench_prep(F, torch, dev, kernels)
+        torch.cuda.empty_cache()
+        done("G")
 
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic_gates48_M3.json")
