@@ -28,7 +28,8 @@ def test_header_declares_entry_points():
     for must in ("fp4x_mx8_linear", "fp4x_w8_linear", "fp4x_w6_linear", "fp4x_nv4_linear", "fp4x_int2_logits",
                  "fp4x_topk_rows", "fp4x_refine_mx8", "fp4x_hc_down", "fp4x_hc_up", "fp4x_hc_scaled_silu",
                  "fp4x_hc_gate_mean", "fp4x_bf16_linear", "fp4x_w8_linear_layers", "fp4x_mx8_dequant",
-                 "fp4x_hc_mix", "fp4x_int2_topk", "fp4x_refine_nv4", "fp4x_scatter_draft"):
+                 "fp4x_hc_mix", "fp4x_int2_topk", "fp4x_refine_nv4", "fp4x_scatter_draft", "fp4x_quantize",
+                 "fp4x_absmax"):
         assert must in names
 
 
@@ -84,6 +85,16 @@ def test_argument_errors_without_gpu(lib):
     assert b"refine_nv4" in L.fp4x_last_error()
     assert L.fp4x_scatter_draft(None, 100, None, None, None, 10, None, 3, 64, 248320, None) == _fp4x.ERR_ARG
     assert b"scatter_draft" in L.fp4x_last_error()
+    # weight preparation: K % 64, the INT2 group, W6 qmax, NVFP4 gs, packed sources without scales
+    Q = L.fp4x_quantize
+    assert Q(0, None, None, 0.0, 8, 96, 0, 16, 31, 0.0, None, None, None, None) == _fp4x.ERR_ARG
+    assert b"K % 64" in L.fp4x_last_error()
+    assert Q(0, None, None, 0.0, 8, 128, 3, 128, 31, 0.0, None, None, None, None) == _fp4x.ERR_ARG
+    assert Q(0, None, None, 0.0, 8, 128, 1, 16, 40, 0.0, None, None, None, None) == _fp4x.ERR_ARG
+    assert Q(0, None, None, 0.0, 8, 128, 2, 16, 31, 0.0, None, None, None, None) == _fp4x.ERR_ARG
+    assert b"bad target" in L.fp4x_last_error()
+    assert Q(2, None, None, 0.0, 8, 128, 0, 16, 31, 0.0, None, None, None, None) == _fp4x.ERR_ARG
+    assert L.fp4x_absmax(1, None, None, 0.0, 8, 100, None, None) == _fp4x.ERR_ARG
     # empty problems are no-ops
     assert L.fp4x_mx8_linear(None, 2560, None, None, None, 0, 0, 64, 2560, 1, None, None, None) == _fp4x.OK
 
