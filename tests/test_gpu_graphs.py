@@ -108,3 +108,24 @@ def test_graph_int2_topk(gpu, F):
     expected = [e.clone() for e in run()]
     torch.cuda.synchronize()
     replay_and_check(run, expected, lambda: F.topk_rows(expected[0], C))
+
+
+def test_graph_draft_head(gpu, F):
+    """The draft head's INT2 coarse + top-64 + NVFP4 rescore + scatter
+    (fp4patch._draft_logits), with a device temperature scalar, replayed."""
+    import fp4patch
+    V, K, NS, DC = 60000, 2560, 20000, 64
+    gen = torch.Generator(device=gpu).manual_seed(8)
+    P, S, gs = F.quantize_nv4(torch.randn((V, K), generator=gen, device=gpu) * 0.02)
+    ids = torch.sort(torch.randperm(V, generator=gen, device=gpu)[:NS]).values
+    st = fp4patch._draft_prepare(F, P, S, gs, ids, DC)
+    x = torch.randn((3, K), generator=gen, device=gpu).to(torch.bfloat16)
+    inv_t = torch.full((1,), 1.25, device=gpu)
+
+    def run():
+        return [fp4patch._draft_logits(F, x, st, V, DC, inv_t=inv_t)]
+
+    expected = [e.clone() for e in run()]
+    torch.cuda.synchronize()
+    replay_and_check(run, expected, lambda: F.refine_nv4(x, torch.zeros((3, DC), dtype=torch.int64, device=gpu),
+                                                         st["w"], st["s"], st["gs"]))
