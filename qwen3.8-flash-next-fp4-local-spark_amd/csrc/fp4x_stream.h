@@ -545,6 +545,52 @@ __device__ __forceinline__ void int2_read_x(uint32_t xa, uint4 (&x)[8]) {
       : "v"(xa)
       : "memory");
 }
+// One unit's weights and scales plus both halves' activations in one go:
+// waits only for the first 12 reads (LDS operations of a wave complete in
+// order), so the second half's 8 activation reads stay in flight while the
+// first half computes; int2_wait_x then releases them.
+typedef uint32_t i2x_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void int2_read_unit_x(uint32_t wa, uint32_t wb, uint32_t sa, uint32_t sb, uint32_t xa,
+                                                 uint4& q0, uint4& q1, uint2& s0, uint2& s1, i2x_u32x4 (&x)[8],
+                                                 i2x_u32x4 (&y)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %20\n\t"
+      "ds_read_b128 %1, %21\n\t"
+      "ds_read_b64 %2, %22\n\t"
+      "ds_read_b64 %3, %23\n\t"
+      "ds_read_b128 %4, %24\n\t"
+      "ds_read_b128 %5, %24 offset:16\n\t"
+      "ds_read_b128 %6, %24 offset:32\n\t"
+      "ds_read_b128 %7, %24 offset:48\n\t"
+      "ds_read_b128 %8, %24 offset:64\n\t"
+      "ds_read_b128 %9, %24 offset:80\n\t"
+      "ds_read_b128 %10, %24 offset:96\n\t"
+      "ds_read_b128 %11, %24 offset:112\n\t"
+      "ds_read_b128 %12, %24 offset:512\n\t"
+      "ds_read_b128 %13, %24 offset:528\n\t"
+      "ds_read_b128 %14, %24 offset:544\n\t"
+      "ds_read_b128 %15, %24 offset:560\n\t"
+      "ds_read_b128 %16, %24 offset:576\n\t"
+      "ds_read_b128 %17, %24 offset:592\n\t"
+      "ds_read_b128 %18, %24 offset:608\n\t"
+      "ds_read_b128 %19, %24 offset:624\n\t"
+      "s_waitcnt lgkmcnt(8)"
+      : "=&v"(q0), "=&v"(q1), "=&v"(s0), "=&v"(s1), "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]),
+        "=&v"(x[4]), "=&v"(x[5]), "=&v"(x[6]), "=&v"(x[7]), "=&v"(y[0]), "=&v"(y[1]), "=&v"(y[2]), "=&v"(y[3]),
+        "=&v"(y[4]), "=&v"(y[5]), "=&v"(y[6]), "=&v"(y[7])
+      : "v"(wa), "v"(wb), "v"(sa), "v"(sb), "v"(xa)
+      : "memory");
+}
+// The second half's activations are in registers after this (tied to them so
+// that no use moves above the wait, and to the accumulator so that the first
+// half's MFMAs stay above it).
+__device__ __forceinline__ void int2_wait_x(i2x_u32x4 (&y)[8], f32x4_t& acc) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]), "+v"(y[6]), "+v"(y[7]),
+                 "+v"(acc)
+               :
+               : "memory");
+}
 __device__ __forceinline__ void lds_put_u128(uint32_t a, uint4 v) {
   typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
   const u32x4_t w = {v.x, v.y, v.z, v.w};
@@ -645,17 +691,19 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
       else wait_vmcnt<0>();
       const uint32_t so = cs * kInt2Unit;
       typename F::Chunk ch[2];
-      int2_read_unit(wlA + so, wlB + so, slA + so, slB + so, ch[0].q, ch[1].q, ch[0].s, ch[1].s);
+      i2x_u32x4 xh[2][8];
+      int2_read_unit_x(wlA + so, wlB + so, slA + so, slB + so, xl + j * 1024, ch[0].q, ch[1].q, ch[0].s, ch[1].s,
+                       xh[0], xh[1]);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        uint4 x[8];
-        int2_read_x(xl + j * 1024 + h * 512, x);
+        if (h == 1) int2_wait_x(xh[1], acc);
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
           uint32_t w[8];
           F::deq16t(ch[h], sub, w);
-          acc = mfma16(x[2 * sub], make_uint4(w[0], w[1], w[2], w[3]), acc);
-          acc = mfma16(x[2 * sub + 1], make_uint4(w[4], w[5], w[6], w[7]), acc);
+          const i2x_u32x4 a0 = xh[h][2 * sub], a1 = xh[h][2 * sub + 1];
+          acc = mfma16(make_uint4(a0.x, a0.y, a0.z, a0.w), make_uint4(w[0], w[1], w[2], w[3]), acc);
+          acc = mfma16(make_uint4(a1.x, a1.y, a1.z, a1.w), make_uint4(w[4], w[5], w[6], w[7]), acc);
         }
       }
       if (++cs == D) cs = 0;
