@@ -16,6 +16,8 @@ template <bool F16S> bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t 
 extern template bool launch_w8_stream<false>(GemvLaunch, int, hipStream_t);
 extern template bool launch_w8_stream<true>(GemvLaunch, int, hipStream_t);
 bool launch_int2_stream_f16(GemvLaunch p, hipStream_t st);
+bool launch_nv4_stream_entry(GemvLaunch p, hipStream_t st);
+bool launch_w6_stream_entry(GemvLaunch p, hipStream_t st);
 int topk_check(const void* logits, int64_t stride, int M, int V, int C, void* workspace, int64_t ws_bytes);
 int topk_launch(const uint16_t* lg, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
                 bool have_smax, hipStream_t st);
@@ -233,6 +235,7 @@ int fp4x_w6_linear(const void* x, int64_t x_stride, const void* L, const void* H
   p.pa.w0 = static_cast<const uint8_t*>(L);
   p.pa.w1 = static_cast<const uint8_t*>(H);
   p.pa.s = static_cast<const uint8_t*>(S);
+  if (launch_w6_stream_entry(p, (hipStream_t)stream)) return check_launch("w6_stream");     // many tiles
   return launch_gemv_mfma<FmtW6, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
@@ -246,6 +249,7 @@ int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* 
   p.pa.w0 = static_cast<const uint8_t*>(P);
   p.pa.s = static_cast<const uint8_t*>(S);
   p.gs = gs;
+  if (launch_nv4_stream_entry(p, (hipStream_t)stream)) return check_launch("nv4_stream");   // many tiles
   return launch_gemv_mfma<FmtNV4, EpiStore>(p, 1, (hipStream_t)stream);
 }
 

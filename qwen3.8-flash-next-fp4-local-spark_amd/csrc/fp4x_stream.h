@@ -776,3 +776,254 @@ inline bool launch_int2_stream(GemvLaunch p, hipStream_t st) {
 }
 
 }  // namespace fp4x
+
+namespace fp4x {
+
+// ---------------------------------------------------------------------------
+// Streaming dense GEMVs for a single matrix of many 16-row tiles (NVFP4 N =
+// 16384 x K = 2560, W6 N = 8192): the W8 streaming design, with a per-format
+// unit policy U.
+//   * A unit is 128 K values of the tile's 16 rows.  Lane (n, g) consumes
+//     piece g of row n, i.e. K values [32 g, 32 g + 32) of the unit: one chunk
+//     of the format's core dequant (FmtNV4, FmtW6), two 16-weight sub-blocks,
+//     four MFMAs with 64 bytes of activations.
+//   * U::issue puts a unit into LDS with U::NDMA direct loads per lane; the
+//     16-byte code pieces are swizzled (row r's piece p at position p ^ ((r >>
+//     2) & 3)) so that the 16 lanes of a quarter-wave reading piece g of rows
+//     0..15 spread over the LDS banks.  Lanes 32..63 of a 4-byte scale load
+//     repeat lanes 0..31 into an unread second half.
+//   * T tile slots x KW waves per workgroup, each wave with a ring of D
+//     units; the KW parts of a tile are summed in part order through LDS; gs
+//     multiplies the sum, as in the core kernel.
+
+// NVFP4 unit: 16 rows x 64 bytes of e2m1 codes, then 16 rows x 8 e4m3 scales.
+struct StreamNV4 {
+  static constexpr int BYTES = 1024 + 256, NDMA = 2;
+  const uint8_t* w;
+  const uint8_t* s;
+  uint32_t ow, os;
+  __device__ void set(const GemvLaunch& p, int64_t it, int k128, int lane, int lim) {
+    const int K = p.pa.K, dr = lane >> 2, pg = (lane & 3) ^ ((dr >> 2) & 3);
+    const int sr = (lane & 31) >> 1;
+    w = p.pa.w0 + it * 16 * (K / 2) + k128 * 64;
+    s = p.pa.s + it * 16 * (K / 16) + k128 * 8;
+    ow = (uint32_t)((dr < lim ? dr : lim) * (K / 2) + pg * 16);
+    os = (uint32_t)((sr < lim ? sr : lim) * (K / 16) + (lane & 1) * 4);
+  }
+  __device__ void issue(char* l, int ij) const {
+    dma_b128(w + ij * 64 + ow, l);
+    dma_b32(s + ij * 8 + os, l + 1024);
+  }
+  __device__ static void consume(uint32_t u, uint32_t xa, int n, int g, f32x4_t& acc) {
+    FmtNV4::Chunk ch;
+    uint4 x0, x1, x2, x3;
+    asm volatile(
+        "ds_read_b128 %0, %6\n\t"
+        "ds_read_u16 %1, %7\n\t"
+        "ds_read_b128 %2, %8\n\t"
+        "ds_read_b128 %3, %8 offset:16\n\t"
+        "ds_read_b128 %4, %8 offset:32\n\t"
+        "ds_read_b128 %5, %8 offset:48\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(ch.q), "=&v"(ch.s), "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
+        : "v"(u + n * 64 + ((g ^ ((n >> 2) & 3)) * 16)), "v"(u + 1024 + n * 8 + g * 2), "v"(xa)
+        : "memory");
+    uint32_t w[8];
+    FmtNV4::deq16(ch, 0, w);
+    acc = mfma16(x0, make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x1, make_uint4(w[4], w[5], w[6], w[7]), acc);
+    FmtNV4::deq16(ch, 1, w);
+    acc = mfma16(x2, make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x3, make_uint4(w[4], w[5], w[6], w[7]), acc);
+  }
+};
+
+// W6 unit: 16 rows x 64 bytes of low nibbles (L), 16 rows x 32 bytes of high
+// bit pairs (H, two 4-byte loads of 8 rows each), 16 rows x 4 fp16 scales.
+struct StreamW6 {
+  static constexpr int BYTES = 1024 + 512 + 256, NDMA = 4;
+  const uint8_t* l;
+  const uint8_t* h;
+  const uint8_t* s;
+  uint32_t ol, oha, ohb, os;
+  __device__ void set(const GemvLaunch& p, int64_t it, int k128, int lane, int lim) {
+    const int K = p.pa.K, dr = lane >> 2, pg = (lane & 3) ^ ((dr >> 2) & 3);
+    const int hr = lane >> 3, sr = (lane & 31) >> 1;
+    l = p.pa.w0 + it * 16 * (K / 2) + k128 * 64;
+    h = p.pa.w1 + it * 16 * (K / 4) + k128 * 32;
+    s = p.pa.s + it * 16 * (K / 16) + k128 * 8;
+    ol = (uint32_t)((dr < lim ? dr : lim) * (K / 2) + pg * 16);
+    oha = (uint32_t)((hr < lim ? hr : lim) * (K / 4) + (lane & 7) * 4);
+    ohb = (uint32_t)((hr + 8 < lim ? hr + 8 : lim) * (K / 4) + (lane & 7) * 4);
+    os = (uint32_t)((sr < lim ? sr : lim) * (K / 16) + (lane & 1) * 4);
+  }
+  __device__ void issue(char* d, int ij) const {
+    dma_b128(l + ij * 64 + ol, d);
+    dma_b32(h + ij * 32 + oha, d + 1024);
+    dma_b32(h + ij * 32 + ohb, d + 1280);
+    dma_b32(s + ij * 8 + os, d + 1536);
+  }
+  __device__ static void consume(uint32_t u, uint32_t xa, int n, int g, f32x4_t& acc) {
+    FmtW6::Chunk ch;
+    uint4 x0, x1, x2, x3;
+    asm volatile(
+        "ds_read_b128 %0, %7\n\t"
+        "ds_read_b64 %1, %8\n\t"
+        "ds_read_u16 %2, %9\n\t"
+        "ds_read_b128 %3, %10\n\t"
+        "ds_read_b128 %4, %10 offset:16\n\t"
+        "ds_read_b128 %5, %10 offset:32\n\t"
+        "ds_read_b128 %6, %10 offset:48\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(ch.lo), "=&v"(ch.hi), "=&v"(ch.s), "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
+        : "v"(u + n * 64 + ((g ^ ((n >> 2) & 3)) * 16)), "v"(u + 1024 + n * 32 + g * 8),
+          "v"(u + 1536 + n * 8 + g * 2), "v"(xa)
+        : "memory");
+    uint32_t w[8];
+    FmtW6::deq16(ch, 0, w);
+    acc = mfma16(x0, make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x1, make_uint4(w[4], w[5], w[6], w[7]), acc);
+    FmtW6::deq16(ch, 1, w);
+    acc = mfma16(x2, make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x3, make_uint4(w[4], w[5], w[6], w[7]), acc);
+  }
+};
+
+template <class U, int T, int KW, int D>
+__global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p) {
+  constexpr int NW = T * KW;
+  extern __shared__ __align__(16) uint16_t lds[];
+  char* base = reinterpret_cast<char*>(lds);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slot = wave / KW, part = wave - slot * KW;
+  const int n = lane & 15, g = lane >> 4;
+  const int tiles = (p.N + 15) / 16;
+  const int K = p.pa.K, JW = K / 128 / KW;           // units per wave per tile
+  const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
+  const int wg0 = blockIdx.x * p.per_wg;
+  const int wgend = wg0 + p.per_wg < tiles ? wg0 + p.per_wg : tiles;
+  if (wg0 >= wgend) return;
+  const int R = (wgend - wg0 + T - 1) / T;           // rounds of T tiles
+  char* part_base = base + xbuf;
+  char* ring = part_base + T * (KW - 1) * 1024 + wave * D * U::BYTES;
+
+  // activations: 1 KB pieces of each row
+  const int bpr = K * 2 / 1024, nblk = p.M * bpr;
+  for (int i = wave; i < nblk; i += NW) {
+    const int m = i / bpr, blk = i - m * bpr;
+    dma_b128(p.x + (int64_t)m * p.x_stride + blk * 512 + lane * 8, base + m * xrow + blk * 1024);
+  }
+
+  const int U_ = R * JW;
+  int ir = 0, ij = 0, is = 0, issued = 0;
+  U unit;
+  auto set_tile = [&](int rr) {
+    int it = wg0 + rr * T + slot;
+    if (it >= wgend) it = wgend - 1;                 // idle slot of the last round: reload a valid tile
+    unit.set(p, it, part * JW, lane, p.N - 1 - it * 16);   // rows past N read row N - 1
+  };
+  set_tile(0);
+  auto issue_next = [&]() {
+    unit.issue(ring + is * U::BYTES, ij);
+    if (++is == D) is = 0;
+    ++issued;
+    if (++ij == JW) {
+      ij = 0;
+      if (++ir < R) set_tile(ir);
+    }
+  };
+  const int pro = U_ < D ? U_ : D;
+  for (int u = 0; u < pro; ++u) issue_next();
+  // the activation loads went out first: wait for them only
+  if (pro == D) wait_vmcnt<U::NDMA * D>();
+  else wait_vmcnt<0>();
+  wg_barrier_raw();
+
+  const int xr = n < p.M ? n : 0;                    // rows m >= M: never stored
+  const uint32_t rl = lds_addr(ring);
+  const uint32_t pl = lds_addr(part_base) + slot * (KW - 1) * 1024 + lane * 16;
+  const uint32_t xl = lds_addr(base) + xr * xrow + part * JW * 256 + g * 64;
+  int cs = 0, u = 0;
+  for (int r = 0; r < R; ++r) {
+    const int it = wg0 + r * T + slot;
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < JW; ++j, ++u) {
+      if (issued - 1 - u >= D - 1) wait_vmcnt<U::NDMA * (D - 1)>();
+      else wait_vmcnt<0>();
+      U::consume(rl + cs * U::BYTES, xl + j * 256, n, g, acc);
+      if (++cs == D) cs = 0;
+      if (issued < U_) issue_next();
+    }
+    if constexpr (KW > 1) {
+      if (part > 0) lds_put_f32x4(pl + (part - 1) * 1024, acc);
+      wg_barrier_raw();
+      if (part == 0) {
+#pragma unroll
+        for (int h = 1; h < KW; ++h) {
+          const f32x4_t o = lds_get_f32x4(pl + (h - 1) * 1024);
+          acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
+        }
+      }
+      wg_barrier_raw();
+    }
+    if (part == 0 && it < wgend) {
+      const int64_t row = (int64_t)it * 16 + n;      // lane (n, g) holds D[m = 4g + i][n]
+      if (row < p.N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (g * 4 + i < p.M) EpiStore::apply(p, 0, g * 4 + i, row, acc[i] * p.gs);
+      }
+    }
+  }
+  wait_vmcnt<0>();                                   // no load of the prologue outlives the wave
+}
+
+// Launch U's streaming kernel when the call fits it (no split-K, M <= 16, K a
+// multiple of 512, 16-byte aligned code planes and 4-byte aligned scale /
+// high-bit planes, at least T tiles per CU, the LDS plan within 160 KB);
+// false (and nothing launched) otherwise, or when `env` is set to 0.
+template <class U, int T, int KW, int D>
+bool launch_dense_stream(GemvLaunch p, const char* env, hipStream_t st) {
+  const char* e = getenv(env);                        // "0": always use the MFMA core (read per call)
+  if (e && e[0] == '0') return false;
+  const int K = p.pa.K, tiles = (p.N + 15) / 16;
+  if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / 128) % KW != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(p.pa.w0) & 15) || (reinterpret_cast<uintptr_t>(p.pa.s) & 3) ||
+      (reinterpret_cast<uintptr_t>(p.pa.w1) & 3))
+    return false;
+  const int64_t cus = device_cus();
+  if (tiles < cus * T) return false;
+  const int64_t per = (tiles + cus * T - 1) / (cus * T) * T;
+  const size_t lds = (size_t)StreamGeom::xbuf_bytes(p.M, K) + (size_t)T * (KW - 1) * 1024 +
+                     (size_t)T * KW * D * U::BYTES;
+  if (lds > 160 * 1024) return false;
+  auto kern = dense_stream_kernel<U, T, KW, D>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess) {
+      (void)hipGetLastError();
+      return false;
+    }
+    attr_set = true;
+  }
+  p.batch = 1;
+  p.per_wg = (int)per;
+  p.xbufs = 1;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((tiles + per - 1) / per)), dim3(64 * T * KW), lds, st, p);
+  return true;
+}
+
+// NVFP4, measured on 16384 x 2560 (T, KW, D): (4, 2, 3) 8.8 / 8.9 / 9.9 us at
+// M = 1 / 3 / 16; (4, 4, 3) 9.5 / 9.4 / 10.6; (4, 2, 4) 9.1 / 9.1 / 10.0;
+// (2, 4, 3) 9.0 / 9.2 / 10.1; (4, 2, 2) 9.2 / 9.2 / 10.0; (2, 2, 3) 9.9 /
+// 10.2 / 11.6 (the core: 10.5 / 11.1 / 14.7).
+inline bool launch_nv4_stream(GemvLaunch p, hipStream_t st) {
+  return launch_dense_stream<StreamNV4, 4, 2, 3>(p, "FP4X_NV4_STREAM", st);
+}
+// W6 at 8192 x 2560: 512 tiles, two per CU.
+inline bool launch_w6_stream(GemvLaunch p, hipStream_t st) {
+  return launch_dense_stream<StreamW6, 2, 4, 3>(p, "FP4X_W6_STREAM", st);
+}
+
+}  // namespace fp4x

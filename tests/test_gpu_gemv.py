@@ -171,6 +171,34 @@ def test_gemv_tile_groups(gpu, F, fmt, M):
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
 
 
+@pytest.mark.parametrize("M", [1, 3, 16])
+@pytest.mark.parametrize("tail", [0, 40])
+@pytest.mark.parametrize("fmt,slots,parts,env", [("nv4", 4, 2, "FP4X_NV4_STREAM"), ("w6", 2, 4, "FP4X_W6_STREAM")])
+def test_dense_stream(gpu, F, fmt, slots, parts, env, M, tail, monkeypatch):
+    """NVFP4 matrices of at least 4 tiles per CU (4 tile slots x 2 waves per
+    workgroup) and W6 matrices of at least 2 (2 slots x 4 waves) take the
+    streaming kernel, a ring of 3 units per wave: fp32 sums within the MFMA
+    bound of the exact sum, as the core's are; a 40-row tail gives workgroups
+    of two rounds whose last round has idle slots."""
+    rng = np.random.default_rng(500 + M + tail + slots)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n, k = 16 * slots * cus + tail, 2560
+    planes, w_op, gs = prep(fmt, rng, n, k)
+    x, _ = act(rng, M, k)
+    y = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
+    monkeypatch.setenv(env, "0")
+    y_core = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
+    monkeypatch.delenv(env)
+    assert not np.array_equal(y.view(np.uint32), y_core.view(np.uint32)), "streaming kernel not taken"
+    exact = ordered.exact_sum(x, w_op) * gs
+    bound = ordered.mfma_bound(x, w_op, parts) * abs(gs)              # parts: K slices of a tile
+    for got in (y, y_core):
+        assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
+    assert_tol(y, og.matmul_f32(x, w_op) * np.float32(gs), what=f"{fmt} stream M={M}")
+    yb = run(F, fmt, bf16_dev(x), planes, 1)                        # bf16 output: the same sums rounded
+    assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
+
+
 @pytest.mark.parametrize("case", [
     # N, K, M, ksplit, scale dtype, split over workgroups
     (640, 10240, 3, 4, np.float16, True),    # the mixer's down projection: 5 workgroups per tile
