@@ -18,6 +18,7 @@ extern template bool launch_w8_stream<true>(GemvLaunch, int, hipStream_t);
 bool launch_int2_stream_f16(GemvLaunch p, hipStream_t st);
 bool launch_nv4_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_w6_stream_entry(GemvLaunch p, hipStream_t st);
+bool launch_mx8_stream_entry(GemvLaunch p, hipStream_t st);
 int topk_check(const void* logits, int64_t stride, int M, int V, int C, void* workspace, int64_t ws_bytes);
 int topk_launch(const uint16_t* lg, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
                 bool have_smax, hipStream_t st);
@@ -171,6 +172,7 @@ int fp4x_mx8_linear(const void* x, int64_t x_stride, const void* w, const void* 
   GemvLaunch p = base_launch(FP4X_FMT_MX8, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
   p.pa.w0 = static_cast<const uint8_t*>(w);
   p.pa.s = static_cast<const uint8_t*>(s);
+  if (launch_mx8_stream_entry(p, (hipStream_t)stream)) return check_launch("mx8_stream");   // many tiles
   return launch_gemv_mfma<FmtMX8, EpiStore>(p, 1, (hipStream_t)stream);
 }
 

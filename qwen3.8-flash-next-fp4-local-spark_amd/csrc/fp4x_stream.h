@@ -889,6 +889,55 @@ struct StreamW6 {
   }
 };
 
+// MXFP8 unit: 16 rows x 128 bytes of e4m3 codes (two 16-byte loads of 8 rows
+// each; row r's piece p at position p ^ ((r >> 1) & 7)), then 16 rows x 4
+// e8m0 scales (lanes 0..15 of a 4-byte load).
+struct StreamMX8 {
+  static constexpr int BYTES = 2048 + 256, NDMA = 3;
+  const uint8_t* w;
+  const uint8_t* s;
+  uint32_t oa, ob, os;
+  __device__ void set(const GemvLaunch& p, int64_t it, int k128, int lane, int lim) {
+    const int K = p.pa.K, ra = lane >> 3, rb = ra + 8, pp = lane & 7, sr = lane & 15;
+    w = p.pa.w0 + it * 16 * K + k128 * 128;
+    s = p.pa.s + it * 16 * (K / 32) + k128 * 4;
+    oa = (uint32_t)((ra < lim ? ra : lim) * K + (pp ^ ((ra >> 1) & 7)) * 16);
+    ob = (uint32_t)((rb < lim ? rb : lim) * K + (pp ^ ((rb >> 1) & 7)) * 16);
+    os = (uint32_t)((sr < lim ? sr : lim) * (K / 32));
+  }
+  __device__ void issue(char* d, int ij) const {
+    dma_b128(w + ij * 128 + oa, d);
+    dma_b128(w + ij * 128 + ob, d + 1024);
+    dma_b32(s + ij * 4 + os, d + 2048);
+  }
+  __device__ static void consume(uint32_t u, uint32_t xa, int n, int g, f32x4_t& acc) {
+    FmtMX8::Chunk a, b;
+    uint4 x0, x1, x2, x3;
+    const int f = (n >> 1) & 7;
+    asm volatile(
+        "ds_read_b128 %0, %7\n\t"
+        "ds_read_b128 %1, %8\n\t"
+        "ds_read_u8 %2, %9\n\t"
+        "ds_read_b128 %3, %10\n\t"
+        "ds_read_b128 %4, %10 offset:16\n\t"
+        "ds_read_b128 %5, %10 offset:32\n\t"
+        "ds_read_b128 %6, %10 offset:48\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(a.q), "=&v"(b.q), "=&v"(a.e), "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
+        : "v"(u + n * 128 + (((2 * g) ^ f) * 16)), "v"(u + n * 128 + (((2 * g + 1) ^ f) * 16)),
+          "v"(u + 2048 + n * 4 + g), "v"(xa)
+        : "memory");
+    b.e = a.e;
+    uint32_t w[8];
+    FmtMX8::deq16(a, 0, w);
+    acc = mfma16(x0, make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x1, make_uint4(w[4], w[5], w[6], w[7]), acc);
+    FmtMX8::deq16(b, 0, w);
+    acc = mfma16(x2, make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x3, make_uint4(w[4], w[5], w[6], w[7]), acc);
+  }
+};
+
 template <class U, int T, int KW, int D>
 __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p) {
   constexpr int NW = T * KW;
@@ -1014,14 +1063,25 @@ bool launch_dense_stream(GemvLaunch p, const char* env, hipStream_t st) {
   return true;
 }
 
-// NVFP4, measured on 16384 x 2560 (T, KW, D): (4, 2, 3) 8.8 / 8.9 / 9.9 us at
-// M = 1 / 3 / 16; (4, 4, 3) 9.5 / 9.4 / 10.6; (4, 2, 4) 9.1 / 9.1 / 10.0;
-// (2, 4, 3) 9.0 / 9.2 / 10.1; (4, 2, 2) 9.2 / 9.2 / 10.0; (2, 2, 3) 9.9 /
-// 10.2 / 11.6 (the core: 10.5 / 11.1 / 14.7).
+// Shapes measured as graph replays (T slots, KW waves per tile, D units per
+// ring -> us at M = 1 / 3 / 16).  NVFP4 16384 x 2560: (4, 2, 3) 8.8 / 8.9 /
+// 9.9; (4, 4, 3) 9.5 / 9.4 / 10.6; (4, 2, 4) 9.1 / 9.1 / 10.0; (2, 4, 3) 9.0 /
+// 9.2 / 10.1; (4, 2, 2) 9.2 / 9.2 / 10.0; (2, 2, 3) 9.9 / 10.2 / 11.6; (2, 5,
+// 2) 9.1 / 9.5 / 10.5; (1, 10, 2) 10.2 / 10.8 / 11.9; (1, 5, 4) 10.8 / 11.0 /
+// 12.3 (the core: 10.5 / 11.1 / 14.7).
 inline bool launch_nv4_stream(GemvLaunch p, hipStream_t st) {
   return launch_dense_stream<StreamNV4, 4, 2, 3>(p, "FP4X_NV4_STREAM", st);
 }
-// W6 at 8192 x 2560: 512 tiles, two per CU.
+// MXFP8 4096 x 2560 (256 tiles, one per CU; 10 waves of 2 units put a tile's
+// 46 KB in flight at once): (1, 10, 2) 5.1 / 5.8 / 6.6; (1, 5, 3) 5.2 / 6.0 /
+// 7.0; (1, 5, 4) 5.2 / 5.6 / 6.9; (1, 4, 5) 5.3 / 5.6 / 7.0 (the core: 6.5 /
+// 6.8 / 8.7).
+inline bool launch_mx8_stream(GemvLaunch p, hipStream_t st) {
+  return launch_dense_stream<StreamMX8, 1, 10, 2>(p, "FP4X_MX8_STREAM", st);
+}
+// W6 8192 x 2560 (512 tiles, two per CU): (2, 4, 3) 8.6 / 8.8 / 9.9; (2, 5, 2)
+// 8.4 / 9.0 / 9.8; (1, 10, 2) 9.0 / 9.3 / 10.2; (1, 4, 5) 9.4 / 9.8 / 11.2;
+// (1, 5, 4) 10.3 / 10.5 / 12.3 (the core: 9.8 / 10.2 / 12.4).
 inline bool launch_w6_stream(GemvLaunch p, hipStream_t st) {
   return launch_dense_stream<StreamW6, 2, 4, 3>(p, "FP4X_W6_STREAM", st);
 }
