@@ -12,7 +12,8 @@ HBM rather than the 256 MB MALL.
 
 `kernels` adds per-kernel µs and GB/s for every configuration (MXFP8 4096 x
 2560, W6 8192 x 2560, NVFP4 16384 x 2560 at M = 1/3/16, the 97-layer fused
-mixer, the 248,320-row fast LM head, the 65k-token draft head), timed as
+mixer, the 248,320-row fast LM head and the exact MXFP8 head it replaces, the
+65k-token draft head), timed as
 HIP-graph replays, and the load-time weight preparation (group G, eager).
 `cpu_baseline` times the oracle (numpy) on the host cores for a bounded
 sample of the headline workload.
@@ -211,6 +212,10 @@ def bench_head(F, torch, dev, out, vectors=1000):
         F.refine_mx8_(co, xx, ix, q, s)
     us = graph_time([lambda c=c: head(x, c) for c in copies], 10)
     out["E_fast_head_total_M3"] = {"us": round(us, 3)}
+    # the exact head the fast path replaces: the MXFP8 GEMV over all 248,320 rows
+    # (655 MB, above the 256 MB MALL, so one copy streams from HBM)
+    us = graph_time([lambda: F.mx8_linear(x, q, s, (32, 512, 1, 4))] * 2, 10)
+    out["E_exact_head_mx8_248320x2560_M3"] = entry(us, V * K + V * K // 32 + M * K * 2 + M * V * 2)
     # argmax agreement against the exact-weight MXFP8 GEMV over seeded vectors
     agree, n = 0, 0
     for b0 in range(1000, 1000 + vectors, M):
