@@ -781,119 +781,26 @@ namespace fp4x {
 
 // ---------------------------------------------------------------------------
 // Streaming dense GEMVs for a single matrix of many 16-row tiles (NVFP4 N =
-// 16384 x K = 2560, W6 N = 8192): the W8 streaming design, with a per-format
-// unit policy U.
-//   * A unit is 128 K values of the tile's 16 rows.  Lane (n, g) consumes
-//     piece g of row n, i.e. K values [32 g, 32 g + 32) of the unit: one chunk
-//     of the format's core dequant (FmtNV4, FmtW6), two 16-weight sub-blocks,
-//     four MFMAs with 64 bytes of activations.
+// 16384, W6 N = 8192, MXFP8 N = 4096 and the 248,320-row MXFP8 head, K =
+// 2560): the W8 streaming design, with a per-format unit policy U.
+//   * A unit is U::UK K values (128 or 256) of the tile's 16 rows; lane (n, g)
+//     consumes K values [g UK / 4, (g + 1) UK / 4) of row n as chunks of the
+//     format's core dequant (FmtMX8, FmtNV4, FmtW6), four MFMAs per 32 K
+//     values, reading UK / 2 bytes of activations.
 //   * U::issue puts a unit into LDS with U::NDMA direct loads per lane; the
-//     16-byte code pieces are swizzled (row r's piece p at position p ^ ((r >>
-//     2) & 3)) so that the 16 lanes of a quarter-wave reading piece g of rows
-//     0..15 spread over the LDS banks.  Lanes 32..63 of a 4-byte scale load
-//     repeat lanes 0..31 into an unread second half.
+//     16-byte pieces of each row are XOR-swizzled so that the 16 lanes of a
+//     quarter-wave, one per row, read distinct LDS bank groups.  Lanes of a
+//     4-byte scale load past the unit's scales repeat them into an unread
+//     tail.
 //   * T tile slots x KW waves per workgroup, each wave with a ring of D
 //     units; the KW parts of a tile are summed in part order through LDS; gs
 //     multiplies the sum, as in the core kernel.
-
-// NVFP4 unit: 16 rows x 64 bytes of e2m1 codes, then 16 rows x 8 e4m3 scales.
-struct StreamNV4 {
-  static constexpr int BYTES = 1024 + 256, NDMA = 2;
-  const uint8_t* w;
-  const uint8_t* s;
-  uint32_t ow, os;
-  __device__ void set(const GemvLaunch& p, int64_t it, int k128, int lane, int lim) {
-    const int K = p.pa.K, dr = lane >> 2, pg = (lane & 3) ^ ((dr >> 2) & 3);
-    const int sr = (lane & 31) >> 1;
-    w = p.pa.w0 + it * 16 * (K / 2) + k128 * 64;
-    s = p.pa.s + it * 16 * (K / 16) + k128 * 8;
-    ow = (uint32_t)((dr < lim ? dr : lim) * (K / 2) + pg * 16);
-    os = (uint32_t)((sr < lim ? sr : lim) * (K / 16) + (lane & 1) * 4);
-  }
-  __device__ void issue(char* l, int ij) const {
-    dma_b128(w + ij * 64 + ow, l);
-    dma_b32(s + ij * 8 + os, l + 1024);
-  }
-  __device__ static void consume(uint32_t u, uint32_t xa, int n, int g, f32x4_t& acc) {
-    FmtNV4::Chunk ch;
-    uint4 x0, x1, x2, x3;
-    asm volatile(
-        "ds_read_b128 %0, %6\n\t"
-        "ds_read_u16 %1, %7\n\t"
-        "ds_read_b128 %2, %8\n\t"
-        "ds_read_b128 %3, %8 offset:16\n\t"
-        "ds_read_b128 %4, %8 offset:32\n\t"
-        "ds_read_b128 %5, %8 offset:48\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(ch.q), "=&v"(ch.s), "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
-        : "v"(u + n * 64 + ((g ^ ((n >> 2) & 3)) * 16)), "v"(u + 1024 + n * 8 + g * 2), "v"(xa)
-        : "memory");
-    uint32_t w[8];
-    FmtNV4::deq16(ch, 0, w);
-    acc = mfma16(x0, make_uint4(w[0], w[1], w[2], w[3]), acc);
-    acc = mfma16(x1, make_uint4(w[4], w[5], w[6], w[7]), acc);
-    FmtNV4::deq16(ch, 1, w);
-    acc = mfma16(x2, make_uint4(w[0], w[1], w[2], w[3]), acc);
-    acc = mfma16(x3, make_uint4(w[4], w[5], w[6], w[7]), acc);
-  }
-};
-
-// W6 unit: 16 rows x 64 bytes of low nibbles (L), 16 rows x 32 bytes of high
-// bit pairs (H, two 4-byte loads of 8 rows each), 16 rows x 4 fp16 scales.
-struct StreamW6 {
-  static constexpr int BYTES = 1024 + 512 + 256, NDMA = 4;
-  const uint8_t* l;
-  const uint8_t* h;
-  const uint8_t* s;
-  uint32_t ol, oha, ohb, os;
-  __device__ void set(const GemvLaunch& p, int64_t it, int k128, int lane, int lim) {
-    const int K = p.pa.K, dr = lane >> 2, pg = (lane & 3) ^ ((dr >> 2) & 3);
-    const int hr = lane >> 3, sr = (lane & 31) >> 1;
-    l = p.pa.w0 + it * 16 * (K / 2) + k128 * 64;
-    h = p.pa.w1 + it * 16 * (K / 4) + k128 * 32;
-    s = p.pa.s + it * 16 * (K / 16) + k128 * 8;
-    ol = (uint32_t)((dr < lim ? dr : lim) * (K / 2) + pg * 16);
-    oha = (uint32_t)((hr < lim ? hr : lim) * (K / 4) + (lane & 7) * 4);
-    ohb = (uint32_t)((hr + 8 < lim ? hr + 8 : lim) * (K / 4) + (lane & 7) * 4);
-    os = (uint32_t)((sr < lim ? sr : lim) * (K / 16) + (lane & 1) * 4);
-  }
-  __device__ void issue(char* d, int ij) const {
-    dma_b128(l + ij * 64 + ol, d);
-    dma_b32(h + ij * 32 + oha, d + 1024);
-    dma_b32(h + ij * 32 + ohb, d + 1280);
-    dma_b32(s + ij * 8 + os, d + 1536);
-  }
-  __device__ static void consume(uint32_t u, uint32_t xa, int n, int g, f32x4_t& acc) {
-    FmtW6::Chunk ch;
-    uint4 x0, x1, x2, x3;
-    asm volatile(
-        "ds_read_b128 %0, %7\n\t"
-        "ds_read_b64 %1, %8\n\t"
-        "ds_read_u16 %2, %9\n\t"
-        "ds_read_b128 %3, %10\n\t"
-        "ds_read_b128 %4, %10 offset:16\n\t"
-        "ds_read_b128 %5, %10 offset:32\n\t"
-        "ds_read_b128 %6, %10 offset:48\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(ch.lo), "=&v"(ch.hi), "=&v"(ch.s), "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
-        : "v"(u + n * 64 + ((g ^ ((n >> 2) & 3)) * 16)), "v"(u + 1024 + n * 32 + g * 8),
-          "v"(u + 1536 + n * 8 + g * 2), "v"(xa)
-        : "memory");
-    uint32_t w[8];
-    FmtW6::deq16(ch, 0, w);
-    acc = mfma16(x0, make_uint4(w[0], w[1], w[2], w[3]), acc);
-    acc = mfma16(x1, make_uint4(w[4], w[5], w[6], w[7]), acc);
-    FmtW6::deq16(ch, 1, w);
-    acc = mfma16(x2, make_uint4(w[0], w[1], w[2], w[3]), acc);
-    acc = mfma16(x3, make_uint4(w[4], w[5], w[6], w[7]), acc);
-  }
-};
 
 // MXFP8 unit: 16 rows x 128 bytes of e4m3 codes (two 16-byte loads of 8 rows
 // each; row r's piece p at position p ^ ((r >> 1) & 7)), then 16 rows x 4
 // e8m0 scales (lanes 0..15 of a 4-byte load).
 struct StreamMX8 {
-  static constexpr int BYTES = 2048 + 256, NDMA = 3;
+  static constexpr int UK = 128, BYTES = 2048 + 256, NDMA = 3;
   const uint8_t* w;
   const uint8_t* s;
   uint32_t oa, ob, os;
@@ -938,6 +845,138 @@ struct StreamMX8 {
   }
 };
 
+// W6 unit of 256 K values: 16 rows x 128 bytes of L (two 16-byte loads of 8
+// rows, pieces swizzled by (row >> 1) & 7), 16 rows x 64 bytes of H (one
+// 16-byte load, pieces swizzled by (row >> 2) & 3), 16 rows x 8 fp16 scales
+// (one 4-byte load): four loads per 256 K values instead of eight.  Lane (n,
+// g) takes chunks 2g and 2g + 1 of row n, K values [64 g, 64 g + 64).
+struct StreamW6 {
+  static constexpr int UK = 256, BYTES = 2048 + 1024 + 256, NDMA = 4;
+  const uint8_t* l;
+  const uint8_t* h;
+  const uint8_t* s;
+  uint32_t ola, olb, oh, os;
+  __device__ void set(const GemvLaunch& p, int64_t it, int ku, int lane, int lim) {
+    const int K = p.pa.K, ra = lane >> 3, rb = ra + 8, pp = lane & 7;
+    const int hr = lane >> 2, hp = (lane & 3) ^ ((hr >> 2) & 3);
+    l = p.pa.w0 + it * 16 * (K / 2) + ku * 128;
+    h = p.pa.w1 + it * 16 * (K / 4) + ku * 64;
+    s = p.pa.s + it * 16 * (K / 16) + ku * 16;
+    ola = (uint32_t)((ra < lim ? ra : lim) * (K / 2) + (pp ^ ((ra >> 1) & 7)) * 16);
+    olb = (uint32_t)((rb < lim ? rb : lim) * (K / 2) + (pp ^ ((rb >> 1) & 7)) * 16);
+    oh = (uint32_t)((hr < lim ? hr : lim) * (K / 4) + hp * 16);
+    os = (uint32_t)((hr < lim ? hr : lim) * (K / 16) + (lane & 3) * 4);
+  }
+  __device__ void issue(char* d, int ij) const {
+    dma_b128(l + ij * 128 + ola, d);
+    dma_b128(l + ij * 128 + olb, d + 1024);
+    dma_b128(h + ij * 64 + oh, d + 2048);
+    dma_b32(s + ij * 16 + os, d + 3072);
+  }
+  __device__ static void consume(uint32_t u, uint32_t xa, int n, int g, f32x4_t& acc) {
+    uint4 la, lb, hh, x[8];
+    uint32_t sc;
+    const int f = (n >> 1) & 7;
+    asm volatile(
+        "ds_read_b128 %0, %12\n\t"
+        "ds_read_b128 %1, %13\n\t"
+        "ds_read_b128 %2, %14\n\t"
+        "ds_read_b32 %3, %15\n\t"
+        "ds_read_b128 %4, %16\n\t"
+        "ds_read_b128 %5, %16 offset:16\n\t"
+        "ds_read_b128 %6, %16 offset:32\n\t"
+        "ds_read_b128 %7, %16 offset:48\n\t"
+        "ds_read_b128 %8, %16 offset:64\n\t"
+        "ds_read_b128 %9, %16 offset:80\n\t"
+        "ds_read_b128 %10, %16 offset:96\n\t"
+        "ds_read_b128 %11, %16 offset:112\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(la), "=&v"(lb), "=&v"(hh), "=&v"(sc), "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]),
+          "=&v"(x[4]), "=&v"(x[5]), "=&v"(x[6]), "=&v"(x[7])
+        : "v"(u + n * 128 + (((2 * g) ^ f) * 16)), "v"(u + n * 128 + (((2 * g + 1) ^ f) * 16)),
+          "v"(u + 2048 + n * 64 + ((g ^ ((n >> 2) & 3)) * 16)), "v"(u + 3072 + n * 16 + g * 4), "v"(xa)
+        : "memory");
+    FmtW6::Chunk c0, c1;
+    c0.lo = la; c0.hi = make_uint2(hh.x, hh.y); c0.s = sc & 0xffffu;
+    c1.lo = lb; c1.hi = make_uint2(hh.z, hh.w); c1.s = sc >> 16;
+    uint32_t w[8];
+    FmtW6::deq16(c0, 0, w);
+    acc = mfma16(x[0], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[1], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    FmtW6::deq16(c0, 1, w);
+    acc = mfma16(x[2], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[3], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    FmtW6::deq16(c1, 0, w);
+    acc = mfma16(x[4], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[5], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    FmtW6::deq16(c1, 1, w);
+    acc = mfma16(x[6], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[7], make_uint4(w[4], w[5], w[6], w[7]), acc);
+  }
+};
+
+// NVFP4 unit of 256 K values: 16 rows x 128 bytes of codes (two 16-byte
+// loads of 8 rows, pieces swizzled by (row >> 1) & 7), 16 rows x 16 e4m3
+// scales (one 4-byte load).  Lane (n, g) takes chunks 2g and 2g + 1 of row n.
+struct StreamNV4 {
+  static constexpr int UK = 256, BYTES = 2048 + 256, NDMA = 3;
+  const uint8_t* w;
+  const uint8_t* s;
+  uint32_t oa, ob, os;
+  __device__ void set(const GemvLaunch& p, int64_t it, int ku, int lane, int lim) {
+    const int K = p.pa.K, ra = lane >> 3, rb = ra + 8, pp = lane & 7, sr = lane >> 2;
+    w = p.pa.w0 + it * 16 * (K / 2) + ku * 128;
+    s = p.pa.s + it * 16 * (K / 16) + ku * 16;
+    oa = (uint32_t)((ra < lim ? ra : lim) * (K / 2) + (pp ^ ((ra >> 1) & 7)) * 16);
+    ob = (uint32_t)((rb < lim ? rb : lim) * (K / 2) + (pp ^ ((rb >> 1) & 7)) * 16);
+    os = (uint32_t)((sr < lim ? sr : lim) * (K / 16) + (lane & 3) * 4);
+  }
+  __device__ void issue(char* d, int ij) const {
+    dma_b128(w + ij * 128 + oa, d);
+    dma_b128(w + ij * 128 + ob, d + 1024);
+    dma_b32(s + ij * 16 + os, d + 2048);
+  }
+  __device__ static void consume(uint32_t u, uint32_t xa, int n, int g, f32x4_t& acc) {
+    uint4 qa, qb, x[8];
+    uint32_t sc;
+    const int f = (n >> 1) & 7;
+    asm volatile(
+        "ds_read_b128 %0, %11\n\t"
+        "ds_read_b128 %1, %12\n\t"
+        "ds_read_b32 %2, %13\n\t"
+        "ds_read_b128 %3, %14\n\t"
+        "ds_read_b128 %4, %14 offset:16\n\t"
+        "ds_read_b128 %5, %14 offset:32\n\t"
+        "ds_read_b128 %6, %14 offset:48\n\t"
+        "ds_read_b128 %7, %14 offset:64\n\t"
+        "ds_read_b128 %8, %14 offset:80\n\t"
+        "ds_read_b128 %9, %14 offset:96\n\t"
+        "ds_read_b128 %10, %14 offset:112\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(qa), "=&v"(qb), "=&v"(sc), "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]),
+          "=&v"(x[5]), "=&v"(x[6]), "=&v"(x[7])
+        : "v"(u + n * 128 + (((2 * g) ^ f) * 16)), "v"(u + n * 128 + (((2 * g + 1) ^ f) * 16)),
+          "v"(u + 2048 + n * 16 + g * 4), "v"(xa)
+        : "memory");
+    FmtNV4::Chunk c0, c1;
+    c0.q = qa; c0.s = sc & 0xffffu;
+    c1.q = qb; c1.s = sc >> 16;
+    uint32_t w[8];
+    FmtNV4::deq16(c0, 0, w);
+    acc = mfma16(x[0], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[1], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    FmtNV4::deq16(c0, 1, w);
+    acc = mfma16(x[2], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[3], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    FmtNV4::deq16(c1, 0, w);
+    acc = mfma16(x[4], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[5], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    FmtNV4::deq16(c1, 1, w);
+    acc = mfma16(x[6], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[7], make_uint4(w[4], w[5], w[6], w[7]), acc);
+  }
+};
+
 template <class U, int T, int KW, int D>
 __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p) {
   constexpr int NW = T * KW;
@@ -947,7 +986,7 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
   const int slot = wave / KW, part = wave - slot * KW;
   const int n = lane & 15, g = lane >> 4;
   const int tiles = (p.N + 15) / 16;
-  const int K = p.pa.K, JW = K / 128 / KW;           // units per wave per tile
+  const int K = p.pa.K, JW = K / U::UK / KW;         // units per wave per tile
   const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
   const int wg0 = blockIdx.x * p.per_wg;
   const int wgend = wg0 + p.per_wg < tiles ? wg0 + p.per_wg : tiles;
@@ -991,7 +1030,7 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
   const int xr = n < p.M ? n : 0;                    // rows m >= M: never stored
   const uint32_t rl = lds_addr(ring);
   const uint32_t pl = lds_addr(part_base) + slot * (KW - 1) * 1024 + lane * 16;
-  const uint32_t xl = lds_addr(base) + xr * xrow + part * JW * 256 + g * 64;
+  const uint32_t xl = lds_addr(base) + xr * xrow + part * JW * U::UK * 2 + g * (U::UK / 2);
   int cs = 0, u = 0;
   for (int r = 0; r < R; ++r) {
     const int it = wg0 + r * T + slot;
@@ -999,7 +1038,7 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
     for (int j = 0; j < JW; ++j, ++u) {
       if (issued - 1 - u >= D - 1) wait_vmcnt<U::NDMA * (D - 1)>();
       else wait_vmcnt<0>();
-      U::consume(rl + cs * U::BYTES, xl + j * 256, n, g, acc);
+      U::consume(rl + cs * U::BYTES, xl + j * U::UK * 2, n, g, acc);
       if (++cs == D) cs = 0;
       if (issued < U_) issue_next();
     }
@@ -1030,15 +1069,16 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
 // Launch U's streaming kernel when the call fits it (no split-K, M <= 16, K a
 // multiple of 512, 16-byte aligned code planes and 4-byte aligned scale /
 // high-bit planes, at least T tiles per CU, the LDS plan within 160 KB);
-// false (and nothing launched) otherwise, or when `env` is set to 0.
+// false (and nothing launched) otherwise, or when `env` is set to 0.  (The
+// second weight plane, W6's H, must be 16-byte aligned.)
 template <class U, int T, int KW, int D>
 bool launch_dense_stream(GemvLaunch p, const char* env, hipStream_t st) {
   const char* e = getenv(env);                        // "0": always use the MFMA core (read per call)
   if (e && e[0] == '0') return false;
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
-  if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / 128) % KW != 0) return false;
+  if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / U::UK) % KW != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.pa.w0) & 15) || (reinterpret_cast<uintptr_t>(p.pa.s) & 3) ||
-      (reinterpret_cast<uintptr_t>(p.pa.w1) & 3))
+      (reinterpret_cast<uintptr_t>(p.pa.w1) & 15))
     return false;
   const int64_t cus = device_cus();
   if (tiles < cus * T) return false;
@@ -1064,13 +1104,14 @@ bool launch_dense_stream(GemvLaunch p, const char* env, hipStream_t st) {
 }
 
 // Shapes measured as graph replays (T slots, KW waves per tile, D units per
-// ring -> us at M = 1 / 3 / 16).  NVFP4 16384 x 2560: (4, 2, 3) 8.8 / 8.9 /
-// 9.9; (4, 4, 3) 9.5 / 9.4 / 10.6; (4, 2, 4) 9.1 / 9.1 / 10.0; (2, 4, 3) 9.0 /
-// 9.2 / 10.1; (4, 2, 2) 9.2 / 9.2 / 10.0; (2, 2, 3) 9.9 / 10.2 / 11.6; (2, 5,
-// 2) 9.1 / 9.5 / 10.5; (1, 10, 2) 10.2 / 10.8 / 11.9; (1, 5, 4) 10.8 / 11.0 /
-// 12.3 (the core: 10.5 / 11.1 / 14.7).
+// ring -> us at M = 1 / 3 / 16).
+// NVFP4 16384 x 2560, 256-K units: (4, 2, 2) 8.2 / 8.5 / 9.2; (4, 2, 3) 8.5 /
+// 8.6 / 9.8; (4, 1, 3) 8.8 / 8.7 / 10.1; (2, 5, 2) 8.7 / 9.4 / 10.3.  With
+// 128-K units (two loads each): (4, 2, 3) 8.8 / 8.9 / 9.9; (4, 4, 3) 9.5 / 9.4
+// / 10.6; (2, 4, 3) 9.0 / 9.2 / 10.1; (2, 5, 2) 9.1 / 9.5 / 10.5; (1, 10, 2)
+// 10.2 / 10.8 / 11.9.  The core: 10.5 / 11.1 / 14.7.
 inline bool launch_nv4_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamNV4, 4, 2, 3>(p, "FP4X_NV4_STREAM", st);
+  return launch_dense_stream<StreamNV4, 4, 2, 2>(p, "FP4X_NV4_STREAM", st);
 }
 // MXFP8 4096 x 2560 (256 tiles, one per CU; 10 waves of 2 units put a tile's
 // 46 KB in flight at once): (1, 10, 2) 5.1 / 5.8 / 6.6; (1, 5, 3) 5.2 / 6.0 /
@@ -1079,11 +1120,14 @@ inline bool launch_nv4_stream(GemvLaunch p, hipStream_t st) {
 inline bool launch_mx8_stream(GemvLaunch p, hipStream_t st) {
   return launch_dense_stream<StreamMX8, 1, 10, 2>(p, "FP4X_MX8_STREAM", st);
 }
-// W6 8192 x 2560 (512 tiles, two per CU): (2, 4, 3) 8.6 / 8.8 / 9.9; (2, 5, 2)
-// 8.4 / 9.0 / 9.8; (1, 10, 2) 9.0 / 9.3 / 10.2; (1, 4, 5) 9.4 / 9.8 / 11.2;
-// (1, 5, 4) 10.3 / 10.5 / 12.3 (the core: 9.8 / 10.2 / 12.4).
+// W6 8192 x 2560 (512 tiles, two per CU), 256-K units: (2, 2, 2) 7.9 / 8.2 /
+// 9.5; (2, 2, 3) 8.1 / 8.3 / 9.6; (2, 2, 4) 8.5 / 8.8 / 10.0; (2, 5, 2) 8.9 /
+// 9.5 / 10.6; (2, 2, 5) 8.9 / 9.2 / 10.5; (2, 1, 3) 11.0 / 11.4 / 14.3.  With
+// 128-K units (four loads each, three of them 4-byte): (2, 4, 3) 8.6 / 8.8 /
+// 9.9; (2, 5, 2) 8.4 / 9.0 / 9.8; (1, 10, 2) 9.0 / 9.3 / 10.2.  The core: 9.8
+// / 10.2 / 12.4.
 inline bool launch_w6_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamW6, 2, 4, 3>(p, "FP4X_W6_STREAM", st);
+  return launch_dense_stream<StreamW6, 2, 2, 2>(p, "FP4X_W6_STREAM", st);
 }
 
 }  // namespace fp4x

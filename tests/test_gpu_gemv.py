@@ -173,13 +173,13 @@ def test_gemv_tile_groups(gpu, F, fmt, M):
 
 @pytest.mark.parametrize("M", [1, 3, 16])
 @pytest.mark.parametrize("tail", [0, 40])
-@pytest.mark.parametrize("fmt,slots,parts,env", [("nv4", 4, 2, "FP4X_NV4_STREAM"), ("w6", 2, 4, "FP4X_W6_STREAM"),
+@pytest.mark.parametrize("fmt,slots,parts,env", [("nv4", 4, 2, "FP4X_NV4_STREAM"), ("w6", 2, 2, "FP4X_W6_STREAM"),
                                                    ("mx8", 1, 10, "FP4X_MX8_STREAM")])
 def test_dense_stream(gpu, F, fmt, slots, parts, env, M, tail, monkeypatch):
     """NVFP4 matrices of at least 4 tiles per CU (4 tile slots x 2 waves per
-    workgroup, a ring of 3 units per wave), W6 matrices of at least 2 (2 slots
-    x 4 waves, 3 units) and MXFP8 matrices of at least 1 (1 slot x 10 waves, 2
-    units) take the streaming kernel: fp32 sums within the MFMA
+    workgroup, a ring of 2 units of 256 K per wave), W6 matrices of at least 2
+    (2 slots x 2 waves, 2 units of 256 K) and MXFP8 matrices of at least 1 (1
+    slot x 10 waves, 2 units of 128 K) take the streaming kernel: fp32 sums within the MFMA
     bound of the exact sum, as the core's are; a 40-row tail gives workgroups
     of two rounds whose last round has idle slots."""
     rng = np.random.default_rng(500 + M + tail + slots)
