@@ -414,11 +414,23 @@ bool launch_w8_stream_cfg(GemvLaunch p, size_t lds, int gx, hipStream_t st) {
 // (whole 1 KB activation pieces and whole units per part), scales and their
 // batch stride 4-byte aligned, enough tiles for a full round on every CU, and
 // the LDS plan within the CU's 160 KB.
+struct StreamW8H;
+template <class U, int T, int KW, int D>
+bool launch_dense_stream(GemvLaunch p, int batch, const char* env, hipStream_t st);
+
 template <bool F16S>
 bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
   constexpr int T = 6, KW = 2, D = 3;
   const char* env = getenv("FP4X_W8_STREAM");          // "0": always use the MFMA core (read per call)
   if (env && env[0] == '0') return false;
+  // fp16 scales: 256-K units (five loads per 256 K values instead of six).
+  // The 48 layer-batched gates [512 x 2560] at M = 3, measured back to back
+  // on one GPU: (T, KW, D) = (6, 2, 2) 15.2 us against 15.5 for this kernel's
+  // 128-K units; (6, 1, 3) 16.2, (3, 2, 3) 16.6, (2, 5, 2) 16.8.  Calls whose
+  // LDS plan does not fit (M >= 5 with two batch entries per workgroup) take
+  // the 128-K kernel below.
+  if constexpr (F16S)
+    if (launch_dense_stream<StreamW8H, 6, 2, 2>(p, batch, "FP4X_W8_STREAM", st)) return true;
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
   if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / 128) % KW != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.pa.s) & 3) || (batch > 1 && (p.s_bstride & 3))) return false;
@@ -804,10 +816,12 @@ struct StreamMX8 {
   const uint8_t* w;
   const uint8_t* s;
   uint32_t oa, ob, os;
-  __device__ void set(const GemvLaunch& p, int64_t it, int k128, int lane, int lim) {
+  static constexpr int XG = 64;                       // activation bytes between lane groups g
+  static constexpr bool BATCHED = false;              // single matrices only
+  __device__ void set(const GemvLaunch& p, int b, int64_t t, int k128, int lane, int lim) {
     const int K = p.pa.K, ra = lane >> 3, rb = ra + 8, pp = lane & 7, sr = lane & 15;
-    w = p.pa.w0 + it * 16 * K + k128 * 128;
-    s = p.pa.s + it * 16 * (K / 32) + k128 * 4;
+    w = p.pa.w0 + b * p.w0_bstride + t * 16 * K + k128 * 128;
+    s = p.pa.s + b * p.s_bstride + t * 16 * (K / 32) + k128 * 4;
     oa = (uint32_t)((ra < lim ? ra : lim) * K + (pp ^ ((ra >> 1) & 7)) * 16);
     ob = (uint32_t)((rb < lim ? rb : lim) * K + (pp ^ ((rb >> 1) & 7)) * 16);
     os = (uint32_t)((sr < lim ? sr : lim) * (K / 32));
@@ -856,12 +870,14 @@ struct StreamW6 {
   const uint8_t* h;
   const uint8_t* s;
   uint32_t ola, olb, oh, os;
-  __device__ void set(const GemvLaunch& p, int64_t it, int ku, int lane, int lim) {
+  static constexpr int XG = 128;
+  static constexpr bool BATCHED = false;
+  __device__ void set(const GemvLaunch& p, int b, int64_t t, int ku, int lane, int lim) {
     const int K = p.pa.K, ra = lane >> 3, rb = ra + 8, pp = lane & 7;
     const int hr = lane >> 2, hp = (lane & 3) ^ ((hr >> 2) & 3);
-    l = p.pa.w0 + it * 16 * (K / 2) + ku * 128;
-    h = p.pa.w1 + it * 16 * (K / 4) + ku * 64;
-    s = p.pa.s + it * 16 * (K / 16) + ku * 16;
+    l = p.pa.w0 + b * p.w0_bstride + t * 16 * (K / 2) + ku * 128;
+    h = p.pa.w1 + b * p.w1_bstride + t * 16 * (K / 4) + ku * 64;
+    s = p.pa.s + b * p.s_bstride + t * 16 * (K / 16) + ku * 16;
     ola = (uint32_t)((ra < lim ? ra : lim) * (K / 2) + (pp ^ ((ra >> 1) & 7)) * 16);
     olb = (uint32_t)((rb < lim ? rb : lim) * (K / 2) + (pp ^ ((rb >> 1) & 7)) * 16);
     oh = (uint32_t)((hr < lim ? hr : lim) * (K / 4) + hp * 16);
@@ -923,10 +939,12 @@ struct StreamNV4 {
   const uint8_t* w;
   const uint8_t* s;
   uint32_t oa, ob, os;
-  __device__ void set(const GemvLaunch& p, int64_t it, int ku, int lane, int lim) {
+  static constexpr int XG = 128;
+  static constexpr bool BATCHED = false;
+  __device__ void set(const GemvLaunch& p, int b, int64_t t, int ku, int lane, int lim) {
     const int K = p.pa.K, ra = lane >> 3, rb = ra + 8, pp = lane & 7, sr = lane >> 2;
-    w = p.pa.w0 + it * 16 * (K / 2) + ku * 128;
-    s = p.pa.s + it * 16 * (K / 16) + ku * 16;
+    w = p.pa.w0 + b * p.w0_bstride + t * 16 * (K / 2) + ku * 128;
+    s = p.pa.s + b * p.s_bstride + t * 16 * (K / 16) + ku * 16;
     oa = (uint32_t)((ra < lim ? ra : lim) * (K / 2) + (pp ^ ((ra >> 1) & 7)) * 16);
     ob = (uint32_t)((rb < lim ? rb : lim) * (K / 2) + (pp ^ ((rb >> 1) & 7)) * 16);
     os = (uint32_t)((sr < lim ? sr : lim) * (K / 16) + (lane & 3) * 4);
@@ -977,6 +995,75 @@ struct StreamNV4 {
   }
 };
 
+// W8 g64 unit of 256 K values with fp16 scales: 16 rows x 256 bytes of int8
+// (four 16-byte loads of 4 rows; row r's piece p at position p ^ (r & 15)),
+// then 16 rows x 4 fp16 scales (lanes 0..31 of a 4-byte load).  Lane (n, g)
+// takes the 16-value chunks g, g + 4, g + 8, g + 12 of row n, chunk g + 4i in
+// g64 group i, with the activations of K values [16 c, 16 c + 16).
+struct StreamW8H {
+  static constexpr int UK = 256, BYTES = 4096 + 256, NDMA = 5, XG = 32;
+  static constexpr bool BATCHED = true;               // layer-batched calls (the 48 gates)
+  const uint8_t* w;
+  const uint8_t* s;
+  uint32_t o[4], os;
+  __device__ void set(const GemvLaunch& p, int b, int64_t t, int ku, int lane, int lim) {
+    const int K = p.pa.K, sr = (lane & 31) >> 1;
+    w = p.pa.w0 + b * p.w0_bstride + t * 16 * K + ku * 256;
+    s = p.pa.s + b * p.s_bstride + (t * 16 * (K / 64) + ku * 4) * 2;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int r = 4 * h + (lane >> 4);
+      o[h] = (uint32_t)((r < lim ? r : lim) * K + ((lane & 15) ^ r) * 16);
+    }
+    os = (uint32_t)((sr < lim ? sr : lim) * (K / 64) * 2 + (lane & 1) * 4);
+  }
+  __device__ void issue(char* d, int ij) const {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) dma_b128(w + ij * 256 + o[h], d + h * 1024);
+    dma_b32(s + ij * 8 + os, d + 4096);
+  }
+  __device__ static void consume(uint32_t u, uint32_t xa, int n, int g, f32x4_t& acc) {
+    uint4 q[4], x[8];
+    uint2 sc;
+    asm volatile(
+        "ds_read_b128 %0, %13\n\t"
+        "ds_read_b128 %1, %14\n\t"
+        "ds_read_b128 %2, %15\n\t"
+        "ds_read_b128 %3, %16\n\t"
+        "ds_read_b64 %4, %17\n\t"
+        "ds_read_b128 %5, %18\n\t"
+        "ds_read_b128 %6, %18 offset:16\n\t"
+        "ds_read_b128 %7, %18 offset:128\n\t"
+        "ds_read_b128 %8, %18 offset:144\n\t"
+        "ds_read_b128 %9, %18 offset:256\n\t"
+        "ds_read_b128 %10, %18 offset:272\n\t"
+        "ds_read_b128 %11, %18 offset:384\n\t"
+        "ds_read_b128 %12, %18 offset:400\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(sc), "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]),
+          "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]), "=&v"(x[6]), "=&v"(x[7])
+        : "v"(u + n * 256 + ((g ^ n) * 16)), "v"(u + n * 256 + (((g + 4) ^ n) * 16)),
+          "v"(u + n * 256 + (((g + 8) ^ n) * 16)), "v"(u + n * 256 + (((g + 12) ^ n) * 16)),
+          "v"(u + 4096 + n * 8), "v"(xa)
+        : "memory");
+    const float s0 = f16_to_f32((uint16_t)sc.x), s1 = f16_to_f32((uint16_t)(sc.x >> 16));
+    const float s2 = f16_to_f32((uint16_t)sc.y), s3 = f16_to_f32((uint16_t)(sc.y >> 16));
+    uint32_t w[8];
+    w8_chunk_bf16(q[0], s0, w);
+    acc = mfma16(x[0], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[1], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    w8_chunk_bf16(q[1], s1, w);
+    acc = mfma16(x[2], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[3], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    w8_chunk_bf16(q[2], s2, w);
+    acc = mfma16(x[4], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[5], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    w8_chunk_bf16(q[3], s3, w);
+    acc = mfma16(x[6], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[7], make_uint4(w[4], w[5], w[6], w[7]), acc);
+  }
+};
+
 template <class U, int T, int KW, int D>
 __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p) {
   constexpr int NW = T * KW;
@@ -985,21 +1072,34 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slot = wave / KW, part = wave - slot * KW;
   const int n = lane & 15, g = lane >> 4;
-  const int tiles = (p.N + 15) / 16;
+  // items: (batch entry, tile); single-matrix policies compile the batch terms away
+  const int tiles = (p.N + 15) / 16, items = (U::BATCHED ? p.batch : 1) * tiles;
   const int K = p.pa.K, JW = K / U::UK / KW;         // units per wave per tile
   const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
   const int wg0 = blockIdx.x * p.per_wg;
-  const int wgend = wg0 + p.per_wg < tiles ? wg0 + p.per_wg : tiles;
+  const int wgend = wg0 + p.per_wg < items ? wg0 + p.per_wg : items;
   if (wg0 >= wgend) return;
   const int R = (wgend - wg0 + T - 1) / T;           // rounds of T tiles
-  char* part_base = base + xbuf;
+  const int b0 = U::BATCHED ? wg0 / tiles : 0;
+  const int nbuf = U::BATCHED ? (wgend - 1) / tiles - b0 + 1 : 1;   // nbuf <= p.xbufs
+  char* part_base = base + (U::BATCHED ? p.xbufs : 1) * xbuf;
   char* ring = part_base + T * (KW - 1) * 1024 + wave * D * U::BYTES;
 
-  // activations: 1 KB pieces of each row
-  const int bpr = K * 2 / 1024, nblk = p.M * bpr;
-  for (int i = wave; i < nblk; i += NW) {
-    const int m = i / bpr, blk = i - m * bpr;
-    dma_b128(p.x + (int64_t)m * p.x_stride + blk * 512 + lane * 8, base + m * xrow + blk * 1024);
+  // activations of the workgroup's batch entries: 1 KB pieces of each row
+  const int bpr = K * 2 / 1024;
+  if constexpr (U::BATCHED) {
+    const int nblk = nbuf * p.M * bpr;
+    for (int i = wave; i < nblk; i += NW) {
+      const int bi = i / (p.M * bpr), r = i - bi * (p.M * bpr), m = r / bpr, blk = r - m * bpr;
+      dma_b128(p.x + (int64_t)(b0 + bi) * p.x_bstride + (int64_t)m * p.x_stride + blk * 512 + lane * 8,
+               base + bi * xbuf + m * xrow + blk * 1024);
+    }
+  } else {
+    const int nblk = p.M * bpr;
+    for (int i = wave; i < nblk; i += NW) {
+      const int m = i / bpr, blk = i - m * bpr;
+      dma_b128(p.x + (int64_t)m * p.x_stride + blk * 512 + lane * 8, base + m * xrow + blk * 1024);
+    }
   }
 
   const int U_ = R * JW;
@@ -1008,7 +1108,8 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
   auto set_tile = [&](int rr) {
     int it = wg0 + rr * T + slot;
     if (it >= wgend) it = wgend - 1;                 // idle slot of the last round: reload a valid tile
-    unit.set(p, it, part * JW, lane, p.N - 1 - it * 16);   // rows past N read row N - 1
+    const int b = U::BATCHED ? it / tiles : 0, t = it - b * tiles;
+    unit.set(p, b, t, part * JW, lane, p.N - 1 - t * 16);   // rows past N read row N - 1
   };
   set_tile(0);
   auto issue_next = [&]() {
@@ -1030,10 +1131,13 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
   const int xr = n < p.M ? n : 0;                    // rows m >= M: never stored
   const uint32_t rl = lds_addr(ring);
   const uint32_t pl = lds_addr(part_base) + slot * (KW - 1) * 1024 + lane * 16;
-  const uint32_t xl = lds_addr(base) + xr * xrow + part * JW * U::UK * 2 + g * (U::UK / 2);
+  const uint32_t xl0 = lds_addr(base) + xr * xrow + part * JW * U::UK * 2 + g * U::XG;
   int cs = 0, u = 0;
   for (int r = 0; r < R; ++r) {
     const int it = wg0 + r * T + slot;
+    const int itc = it < wgend ? it : wgend - 1;
+    const int b = U::BATCHED ? itc / tiles : 0, t = itc - b * tiles;
+    const uint32_t xl = U::BATCHED ? xl0 + (b - b0) * xbuf : xl0;
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int j = 0; j < JW; ++j, ++u) {
       if (issued - 1 - u >= D - 1) wait_vmcnt<U::NDMA * (D - 1)>();
@@ -1055,11 +1159,11 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
       wg_barrier_raw();
     }
     if (part == 0 && it < wgend) {
-      const int64_t row = (int64_t)it * 16 + n;      // lane (n, g) holds D[m = 4g + i][n]
+      const int64_t row = (int64_t)t * 16 + n;       // lane (n, g) holds D[m = 4g + i][n]
       if (row < p.N) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (g * 4 + i < p.M) EpiStore::apply(p, 0, g * 4 + i, row, acc[i] * p.gs);
+          if (g * 4 + i < p.M) EpiStore::apply(p, b, g * 4 + i, row, acc[i] * p.gs);
       }
     }
   }
@@ -1072,18 +1176,23 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
 // false (and nothing launched) otherwise, or when `env` is set to 0.  (The
 // second weight plane, W6's H, must be 16-byte aligned.)
 template <class U, int T, int KW, int D>
-bool launch_dense_stream(GemvLaunch p, const char* env, hipStream_t st) {
+bool launch_dense_stream(GemvLaunch p, int batch, const char* env, hipStream_t st) {
   const char* e = getenv(env);                        // "0": always use the MFMA core (read per call)
   if (e && e[0] == '0') return false;
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
-  if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / U::UK) % KW != 0) return false;
+  if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / U::UK) % KW != 0 || batch < 1) return false;
+  if (!U::BATCHED && batch != 1) return false;
   if ((reinterpret_cast<uintptr_t>(p.pa.w0) & 15) || (reinterpret_cast<uintptr_t>(p.pa.s) & 3) ||
       (reinterpret_cast<uintptr_t>(p.pa.w1) & 15))
     return false;
-  const int64_t cus = device_cus();
-  if (tiles < cus * T) return false;
-  const int64_t per = (tiles + cus * T - 1) / (cus * T) * T;
-  const size_t lds = (size_t)StreamGeom::xbuf_bytes(p.M, K) + (size_t)T * (KW - 1) * 1024 +
+  if (batch > 1 && ((p.w0_bstride & 15) || (p.w1_bstride & 15) || (p.s_bstride & 3))) return false;
+  const int64_t cus = device_cus(), items = (int64_t)batch * tiles;
+  if (items < cus * T) return false;
+  const int64_t per = (items + cus * T - 1) / (cus * T) * T;
+  // batch entries one workgroup can span (its first and last item), each with its activations
+  const int64_t span = batch > 1 ? (per + tiles - 1) / tiles + 1 : 1;
+  if (span > 2) return false;
+  const size_t lds = (size_t)span * StreamGeom::xbuf_bytes(p.M, K) + (size_t)T * (KW - 1) * 1024 +
                      (size_t)T * KW * D * U::BYTES;
   if (lds > 160 * 1024) return false;
   auto kern = dense_stream_kernel<U, T, KW, D>;
@@ -1096,10 +1205,10 @@ bool launch_dense_stream(GemvLaunch p, const char* env, hipStream_t st) {
     }
     attr_set = true;
   }
-  p.batch = 1;
+  p.batch = batch;
   p.per_wg = (int)per;
-  p.xbufs = 1;
-  hipLaunchKernelGGL(kern, dim3((unsigned)((tiles + per - 1) / per)), dim3(64 * T * KW), lds, st, p);
+  p.xbufs = (int)span;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((items + per - 1) / per)), dim3(64 * T * KW), lds, st, p);
   return true;
 }
 
@@ -1111,14 +1220,14 @@ bool launch_dense_stream(GemvLaunch p, const char* env, hipStream_t st) {
 // / 10.6; (2, 4, 3) 9.0 / 9.2 / 10.1; (2, 5, 2) 9.1 / 9.5 / 10.5; (1, 10, 2)
 // 10.2 / 10.8 / 11.9.  The core: 10.5 / 11.1 / 14.7.
 inline bool launch_nv4_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamNV4, 4, 2, 2>(p, "FP4X_NV4_STREAM", st);
+  return launch_dense_stream<StreamNV4, 4, 2, 2>(p, 1, "FP4X_NV4_STREAM", st);
 }
 // MXFP8 4096 x 2560 (256 tiles, one per CU; 10 waves of 2 units put a tile's
 // 46 KB in flight at once): (1, 10, 2) 5.1 / 5.8 / 6.6; (1, 5, 3) 5.2 / 6.0 /
 // 7.0; (1, 5, 4) 5.2 / 5.6 / 6.9; (1, 4, 5) 5.3 / 5.6 / 7.0 (the core: 6.5 /
 // 6.8 / 8.7).
 inline bool launch_mx8_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamMX8, 1, 10, 2>(p, "FP4X_MX8_STREAM", st);
+  return launch_dense_stream<StreamMX8, 1, 10, 2>(p, 1, "FP4X_MX8_STREAM", st);
 }
 // W6 8192 x 2560 (512 tiles, two per CU), 256-K units: (2, 2, 2) 7.9 / 8.2 /
 // 9.5; (2, 2, 3) 8.1 / 8.3 / 9.6; (2, 2, 4) 8.5 / 8.8 / 10.0; (2, 5, 2) 8.9 /
@@ -1127,7 +1236,7 @@ inline bool launch_mx8_stream(GemvLaunch p, hipStream_t st) {
 // 9.9; (2, 5, 2) 8.4 / 9.0 / 9.8; (1, 10, 2) 9.0 / 9.3 / 10.2.  The core: 9.8
 // / 10.2 / 12.4.
 inline bool launch_w6_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamW6, 2, 2, 2>(p, "FP4X_W6_STREAM", st);
+  return launch_dense_stream<StreamW6, 2, 2, 2>(p, 1, "FP4X_W6_STREAM", st);
 }
 
 }  // namespace fp4x
