@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 6
+#define FP4X_ABI_VERSION 7
 
 enum {
   FP4X_OK = 0,
@@ -113,29 +113,34 @@ int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* 
 int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
                      void* out, int out_dtype, int M, int N, int K, int G, void* stream);
 
-/* Top-C of each row of bf16 logits [M, V] under the total order (value
- * descending, then index ascending; -0 equals +0, NaN is largest); idx_out
- * int64 [M, C] lists the selected indices in that order.  C <= min(V, 2048);
- * logits 16-byte aligned with stride % 8 == 0.  Rows are read in 16-byte
- * units: each row must be readable up to round_up(V, 8) elements (the stride
- * gives that to every row but the last; the elements past V are ignored).
- * [torch.topk(coarse, C) in the fast head, x/fp4patch.py:377] */
-int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int64_t* idx_out, void* workspace,
-                   int64_t ws_bytes, void* stream);
+/* Top-C of each row of logits [M, V] (dtype FP4X_DT_BF16 or FP4X_DT_F32)
+ * under the total order (value descending, then index ascending; -0 equals
+ * +0, NaN is largest); idx_out int64 [M, C] lists the selected indices in
+ * that order.  C <= min(V, 2048); logits 16-byte aligned with 16-byte aligned
+ * rows (stride a multiple of 8 bf16 or 4 fp32 elements).  Rows are read in
+ * 16-byte units: each row must be readable up to the next 16-byte boundary
+ * past its V elements (the stride gives that to every row but the last; the
+ * elements past V are ignored).
+ * [torch.topk(coarse, C) in the fast head, x/fp4patch.py:377 (bf16), and
+ *  torch.topk(co, dc) in the draft head, x/fp4patch.py:314 (fp32)] */
+int fp4x_topk_rows(const void* logits, int dtype, int64_t stride, int M, int V, int C, int64_t* idx_out,
+                   void* workspace, int64_t ws_bytes, void* stream);
 /* Bytes of device workspace fp4x_topk_rows and fp4x_int2_topk need for M
  * rows of V elements (16-byte aligned, no initial contents required).  Calls
  * that share a workspace must be stream-ordered. */
 int64_t fp4x_topk_workspace_size(int M, int V);
 
-/* The fast head's coarse stage in one call: fp4x_int2_logits into bf16
- * coarse [M, N] (row stride coarse_stride, a multiple of 8), then
- * fp4x_topk_rows of it into idx_out [M, C], with the top-k's slice maxima
- * written by the coarse kernel's epilogue where it streams.  Results equal
- * the two calls made separately.
- * [int2_logits then torch.topk(coarse, C) in the fast head, x/fp4patch.py:371-377] */
+/* The coarse stage of the fast head and of the draft head in one call:
+ * fp4x_int2_logits into coarse [M, N] (coarse_dtype FP4X_DT_BF16 for the
+ * target head, FP4X_DT_F32 for the draft head; 16-byte aligned rows of
+ * coarse_stride elements), then fp4x_topk_rows of it into idx_out [M, C],
+ * with the top-k's slice maxima written by the coarse kernel's epilogue where
+ * it streams.  Results equal the two calls made separately.
+ * [int2_logits then torch.topk(coarse, C), x/fp4patch.py:371-377 (bf16);
+ *  x/fp4patch.py:313-314 (fp32, the draft head)] */
 int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
-                   void* coarse, int64_t coarse_stride, int M, int N, int K, int G, int C, int64_t* idx_out,
-                   void* workspace, int64_t ws_bytes, void* stream);
+                   void* coarse, int coarse_dtype, int64_t coarse_stride, int M, int N, int K, int G, int C,
+                   int64_t* idx_out, void* workspace, int64_t ws_bytes, void* stream);
 
 /* In place: out[m, idx[m, c]] = cast(sum_k float(e4m3(w)*2^(s-127)) * float(x[m, k])).
  * out is [M, V] in out_dtype, x bf16 [M, K] contiguous, idx int64 [M, C].
@@ -202,10 +207,15 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
  * bit-identical to those two calls.  When both halves take their planned
  * decompositions it runs as one launch (the up weights stream while the down
  * projection runs); otherwise it makes the two calls.  tickets: n_tickets
- * int32, zero before the first call and re-armed by every call; the single
- * launch needs at least round_up(ceil(N / 16), 64) + 32 * (CUs + 1) (a count
- * and one 128-byte flag line per workgroup, after the tile tickets) and makes
- * the two calls with fewer.  FP4X_HC_MIX=0 forces the two calls.
+ * int32, zero before the first call and never touched by the caller
+ * afterwards; the single launch needs at least
+ * round_up(ceil(N / 16), 64) + 32 * (CUs + 1): the tile tickets, then at
+ * offset S = round_up(ceil(N / 16), 64) the down-tile count (S), a status
+ * word (S + 1) and one 128-byte generation-flag line per workgroup.  With
+ * fewer it makes the two calls.  A workgroup whose flag wait gives up (only
+ * possible when other work holds the GPU's CUs for about a second) writes NaN
+ * to its outputs and sets bit 0 of the status word; the next call is not
+ * affected.  FP4X_HC_MIX=0 forces the two calls.
  * [HCFused.down then HCFused.up as the plugin's fused mixer calls them,
  *  x/fp4patch.py:217-218 (_mix_fused); x/fp4x_kernels.py:503-526] */
 int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* di, void* bot,
@@ -232,11 +242,13 @@ int fp4x_dequant_bf16(int fmt, const void* w0, const void* w1, const void* s, in
 /* fp32 MXFP8 dequant, out [N, K].  [mx8_dequant, x/fp4x_kernels.py:261-267] */
 int fp4x_mx8_dequant(const void* w, const void* s, int N, int K, float* out, void* stream);
 
-/* out[i] = a[i].lo*b[i].lo + a[i].hi*b[i].hi + c[i] with v_dot2_f32_bf16.
- * No counterpart in the reference: exposed so tests can measure the
- * instruction's rounding (it is not IEEE; the GEMVs accumulate with MFMA and
- * the rescore with IEEE fp32 fma instead). */
-int fp4x_dot2_bf16(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n, void* stream);
+/* Re-read the path switches from the environment (they are read once, when
+ * first needed, never per launch): FP4X_W8_STREAM, FP4X_INT2_STREAM,
+ * FP4X_NV4_STREAM, FP4X_W6_STREAM, FP4X_MX8_STREAM and FP4X_HC_MIX ("0"
+ * selects the MFMA core or the two-call mixer), FP4X_WAVES_PER_CU.  Not
+ * thread-safe against concurrent launches.  No counterpart in the reference
+ * (its Triton launches take no such switches). */
+int fp4x_reload_env(void);
 
 #ifdef __cplusplus
 }

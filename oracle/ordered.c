@@ -1,85 +1,36 @@
-/* Order-exact replica of the fp4x GEMV sums (oracle; test infrastructure only).
+/* Order-exact replica of the rescore sums (oracle; test infrastructure only).
  *
- * The HIP kernels fix every fp32 rounding of a dot product: a row slice is cut
- * into chunks of `kpc` weights; lane l of `lpr` lanes owns chunks
- * l, l + lpr, ... of the slice; each lane runs a chain of v_dot2_f32_bf16
- * steps over its chunks in increasing k, starting from 0; the lpr partials
- * meet in a butterfly (step s = 1, 2, 4, ...: v[l] += v[l ^ s]); split-K
- * slices are summed in slice order.  The reference leaves this order open
- * (fp32 accumulation in tl.dot, x/fp4x_kernels.py:24, :322, :380), so this
- * file restates the reference sums in the order the kernels use; with the same
- * order the sums agree bit for bit, which is what makes the INT2 coarse
- * top-C set and the refined logits comparable exactly.
- *
- * dot2 models (pinned against the hardware by tests/test_gpu_dot2.py):
- *   0  RN(a0*b0 + a1*b1 + c)          single rounding of the exact sum
- *   1  RN(RN(a0*b0 + a1*b1) + c)
- *   2  RN(RN(c + a0*b0) + a1*b1)      two chained fma
- *   3  RN(RN(c + a1*b1) + a0*b0)
- * bf16 x bf16 products are exact in fp32 and in double.
+ * The reference's refine kernels (x/fp4x_kernels.py:367-381, :391-409) sum
+ * exact fp32 products of a bf16 activation and an exactly representable
+ * weight (MXFP8 e4m3 * 2^k, NVFP4 e2m1 * e4m3) with fp32 accumulation whose
+ * order Triton leaves open.  The HIP rescore kernels fix that order, and this
+ * file restates the same sums in it, so the refined logits can be compared
+ * bit for bit:
+ *   - a candidate row is cut into chunks of `kpc` weights;
+ *   - lane l of `lpr` lanes owns chunks l, l + lpr, l + 2 lpr, ... ;
+ *   - each lane starts from 0 and folds its chunks in increasing k, one
+ *     IEEE fp32 fma per element: acc = fma(w_k, x_k, acc);
+ *   - the lpr partials meet in a butterfly: for s = 1, 2, 4, ...,
+ *     v[l] = v[l] + v[l ^ s];
+ *   - ksplit equal K slices (1 for the rescore) are scaled by gs and added in
+ *     slice order.
+ * The GEMV kernels accumulate on MFMA, whose internal rounding is not IEEE;
+ * their sums are compared against float64 exact sums within an error bound
+ * instead (oracle/ordered.py mfma_bound), not replayed here.
  */
 #include <math.h>
 #include <stdint.h>
 #include <string.h>
 
-static inline float bf16f(uint32_t b) {
-  uint32_t u = (b & 0xffffu) << 16;
+static inline float bf16f(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
   float f;
   memcpy(&f, &u, 4);
   return f;
 }
 
-/* RN to float of the exact value t + e, where t = RN_double(exact) and e is
- * the exact double error of that rounding (|e| <= ulp(t)/2). */
-static float rn_f32_of(double t, double e) {
-  float f = (float)t;
-  if (e == 0.0) return f;
-  double df = (double)f;
-  if (df == t) return f;            /* t on the float grid; e far below half a float ulp */
-  double d = t - df;                /* exact */
-  float g = nextafterf(f, d > 0 ? INFINITY : -INFINITY);
-  double half = fabs((double)g - df) * 0.5;
-  if (fabs(d) != half) return f;    /* not a tie: RN(t) is RN(t + e) */
-  /* tie at t: the exact value t + e lies on the side of e */
-  if ((d > 0) == (e > 0)) return g;
-  return f;
-}
-
-static inline void two_sum(double a, double b, double* s, double* e) {
-  double ss = a + b;
-  double bb = ss - a;
-  *e = (a - (ss - bb)) + (b - bb);
-  *s = ss;
-}
-
-static float rn3_exact(double p0, double p1, double c) {
-  double s, e1, t, e2;
-  two_sum(p0, p1, &s, &e1);
-  if (e1 == 0.0) {
-    two_sum(s, c, &t, &e2);
-    return rn_f32_of(t, e2);
-  }
-  __float128 q = (__float128)p0 + (__float128)p1;
-  q += (__float128)c;
-  return (float)q;
-}
-
-static inline float dot2_model(uint32_t a, uint32_t b, float c, int mode) {
-  const float a0 = bf16f(a), a1 = bf16f(a >> 16), b0 = bf16f(b), b1 = bf16f(b >> 16);
-  switch (mode) {
-    case 0: return rn3_exact((double)a0 * b0, (double)a1 * b1, (double)c);
-    case 1: { float p1 = a1 * b1; float s = fmaf(a0, b0, p1); return s + c; }
-    case 2: return fmaf(a1, b1, fmaf(a0, b0, c));
-    default: return fmaf(a0, b0, fmaf(a1, b1, c));
-  }
-}
-
-void oracle_dot2_batch(const uint32_t* a, const uint32_t* b, const float* c, float* out, int64_t n, int mode) {
-  for (int64_t i = 0; i < n; ++i) out[i] = dot2_model(a[i], b[i], c[i], mode);
-}
-
 /* One row slice: x and w point at the slice start, `chunks` chunks of kpc. */
-static float slice_sum(const uint16_t* x, const uint16_t* w, int chunks, int kpc, int lpr, int mode) {
+static float slice_sum(const uint16_t* x, const uint16_t* w, int chunks, int kpc, int lpr) {
   float v[64];
   const int cpl = (chunks + lpr - 1) / lpr;
   for (int l = 0; l < lpr; ++l) {
@@ -89,11 +40,7 @@ static float slice_sum(const uint16_t* x, const uint16_t* w, int chunks, int kpc
       if (c >= chunks) continue;
       const uint16_t* xc = x + (int64_t)c * kpc;
       const uint16_t* wc = w + (int64_t)c * kpc;
-      for (int k = 0; k < kpc; k += 2) {
-        const uint32_t wp = (uint32_t)wc[k] | ((uint32_t)wc[k + 1] << 16);
-        const uint32_t xp = (uint32_t)xc[k] | ((uint32_t)xc[k + 1] << 16);
-        acc = dot2_model(wp, xp, acc, mode);
-      }
+      for (int k = 0; k < kpc; ++k) acc = fmaf(bf16f(wc[k]), bf16f(xc[k]), acc);
     }
     v[l] = acc;
   }
@@ -109,7 +56,7 @@ static float slice_sum(const uint16_t* x, const uint16_t* w, int chunks, int kpc
  * (bf16 x [M, K], bf16 operand w [*, K]), slices multiplied by gs and summed
  * in slice order.  Rows < 0 give 0. */
 void oracle_ordered_gemv(const uint16_t* x, const uint16_t* w, const int64_t* rows, int M, int N, int K, int kpc,
-                         int ksplit, int lpr, float gs, int mode, float* out) {
+                         int ksplit, int lpr, float gs, float* out) {
   const int ks = K / ksplit, chunks = ks / kpc;
 #pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m) {
@@ -119,7 +66,7 @@ void oracle_ordered_gemv(const uint16_t* x, const uint16_t* w, const int64_t* ro
       float tot = 0.0f;
       for (int s = 0; s < ksplit; ++s) {
         const float p = slice_sum(x + (int64_t)m * K + (int64_t)s * ks, w + r * (int64_t)K + (int64_t)s * ks,
-                                  chunks, kpc, lpr, mode) * gs;
+                                  chunks, kpc, lpr) * gs;
         tot = s == 0 ? p : tot + p;
       }
       out[(int64_t)m * N + i] = tot;

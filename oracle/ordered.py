@@ -1,5 +1,6 @@
-"""ctypes front end of ordered.c: the HIP kernels' exact summation order
-(oracle; test infrastructure only)."""
+"""ctypes front end of ordered.c, the rescore kernels' exact fma order, plus
+the float64 sums and error bounds the MFMA-accumulated GEMVs are checked
+against (oracle; test infrastructure only)."""
 import ctypes
 import os
 
@@ -7,28 +8,19 @@ import numpy as np
 
 from . import build as _build
 
-# Step models (ordered.c).  FMA (two IEEE fma, low element first) is the
-# rescore kernel's step and is exact.  DOT2_MODE models v_dot2_f32_bf16 by a
-# single rounding of the exact three-term sum; the hardware's rounding of
-# that instruction differs in the last bit for about 12% of random operands
-# (tests/test_gpu_dot2.py measures it), so sums built from it are compared to
-# this model within a per-step one-ulp bound (step_bound).
-FMA = 2
-DOT2_MODE = 0
-
 _LIB = None
 
 
 def lib():
     global _LIB
     if _LIB is None:
-        if not os.path.exists(_build.SO):
+        src = os.path.join(os.path.dirname(_build.SO), "..", "ordered.c")
+        if not os.path.exists(_build.SO) or os.path.getmtime(_build.SO) < os.path.getmtime(src):
             _build.build()
         L = ctypes.CDLL(_build.SO)
         P = ctypes.c_void_p
-        L.oracle_dot2_batch.argtypes = [P, P, P, P, ctypes.c_int64, ctypes.c_int]
         L.oracle_ordered_gemv.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                          ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, P]
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_float, P]
         L.oracle_int2_operand.argtypes = [P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, P]
         _LIB = L
     return _LIB
@@ -38,20 +30,12 @@ def _p(a):
     return a.ctypes.data_as(ctypes.c_void_p)
 
 
-def dot2(a, b, c, mode=None):
-    """Elementwise dot2 model: a, b uint32 bf16 pairs, c float32."""
-    a = np.ascontiguousarray(a, np.uint32)
-    b = np.ascontiguousarray(b, np.uint32)
-    c = np.ascontiguousarray(c, np.float32)
-    out = np.empty(a.shape, np.float32)
-    lib().oracle_dot2_batch(_p(a), _p(b), _p(c), _p(out), a.size, DOT2_MODE if mode is None else mode)
-    return out
-
-
-def ordered_gemv(x_bits, w_bits, kpc, lpr, ksplit=1, gs=1.0, rows=None, mode=None):
-    """fp32 sums in kernel order.  x_bits uint16 bf16 [M, K]; w_bits uint16
-    bf16 operand [R, K]; rows (int64 [M, N]) gathers weight rows per output,
-    else N = R.  Returns float32 [M, N]."""
+def ordered_gemv(x_bits, w_bits, kpc, lpr, ksplit=1, gs=1.0, rows=None):
+    """fp32 sums in the rescore kernels' order (ordered.c): per lane a chain of
+    IEEE fma over its chunks, a butterfly over the lpr lanes, slices times gs
+    added in order.  x_bits uint16 bf16 [M, K]; w_bits uint16 bf16 operand
+    [R, K]; rows (int64 [M, N]) gathers weight rows per output, else N = R.
+    Returns float32 [M, N]."""
     x_bits = np.ascontiguousarray(x_bits, np.uint16)
     w_bits = np.ascontiguousarray(w_bits, np.uint16)
     M, K = x_bits.shape
@@ -62,18 +46,20 @@ def ordered_gemv(x_bits, w_bits, kpc, lpr, ksplit=1, gs=1.0, rows=None, mode=Non
         N = w_bits.shape[0]
     out = np.empty((M, N), np.float32)
     lib().oracle_ordered_gemv(_p(x_bits), _p(w_bits), None if rows is None else _p(rows), M, N, K, kpc, ksplit, lpr,
-                              float(gs), DOT2_MODE if mode is None else mode, _p(out))
+                              float(gs), _p(out))
     return out
 
 
 def step_bound(x, w, kpc, lpr, ksplit=1):
-    """|error| bound of a sum built from steps that may each differ by one
-    fp32 ulp of the running partial: n_steps * 2^-23 * sum_k |x_k w_k|.
+    """|error| bound of an fma-ordered sum against the exact one: every fma and
+    butterfly addition rounds once (at most half an ulp of a partial that is
+    itself at most sum_k |x_k w_k|), so the error is at most
+    n_steps * 2^-24 * sum_k |x_k w_k|; taken here with 2^-23 per step.
     x, w: fp32 values [M, K], [N, K]."""
     K = x.shape[1]
     chunks = K // ksplit // kpc
     cpl = -(-chunks // lpr)
-    n_steps = cpl * kpc // 2 + max(lpr.bit_length() - 1, 0) + ksplit + 1
+    n_steps = cpl * kpc + max(lpr.bit_length() - 1, 0) + ksplit + 1
     l1 = np.abs(np.asarray(x, np.float64)) @ np.abs(np.asarray(w, np.float64)).T
     return n_steps * 2.0 ** -23 * l1
 
@@ -91,8 +77,9 @@ def mfma_bound(x, w, ksplit=1):
 
 
 def exact_sum(x, w):
-    """float64 x @ w.T (exact for bf16-valued operands at these sizes up to
-    float64 rounding, far below the fp32 bounds it is compared with)."""
+    """float64 x @ w.T: for bf16-valued operands every product is exact in
+    float64, and the float64 summation error at these sizes lies far below
+    the fp32 bounds it is compared with."""
     return np.asarray(x, np.float64) @ np.asarray(w, np.float64).T
 
 

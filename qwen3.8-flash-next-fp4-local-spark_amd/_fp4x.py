@@ -30,9 +30,9 @@ _SIGS = {
     "fp4x_w6_linear": ([_P, _I64, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "fp4x_nv4_linear": ([_P, _I64, _P, _P, _F, _P, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "fp4x_int2_logits": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P], _I),
-    "fp4x_topk_rows": ([_P, _I64, _I, _I, _I, _P, _P, _I64, _P], _I),
+    "fp4x_topk_rows": ([_P, _I, _I64, _I, _I, _I, _P, _P, _I64, _P], _I),
     "fp4x_topk_workspace_size": ([_I, _I], _I64),
-    "fp4x_int2_topk": ([_P, _I64, _P, _P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _I64, _P], _I),
+    "fp4x_int2_topk": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I64, _I, _I, _I, _I, _I, _P, _P, _I64, _P], _I),
     "fp4x_refine_mx8": ([_P, _I, _I64, _P, _P, _I, _I, _P, _P, _I, _I, _P], _I),
     "fp4x_refine_nv4": ([_P, _P, _P, _I, _I, _P, _P, ctypes.c_float, _I, _I, _P], _I),
     "fp4x_scatter_draft": ([_P, _I64, _P, _P, _P, _I64, _P, _I, _I, _I64, _P], _I),
@@ -46,9 +46,9 @@ _SIGS = {
     "fp4x_hc_gate_mean": ([_P, _I64, _P, _I64, _P, _I, _I, _I, _P], _I),
     "fp4x_dequant_bf16": ([_I, _P, _P, _P, _I, _I, _I, _P, _P], _I),
     "fp4x_mx8_dequant": ([_P, _P, _I, _I, _P, _P], _I),
-    "fp4x_dot2_bf16": ([_P, _P, _P, _P, _I, _P], _I),
+    "fp4x_reload_env": ([], _I),
 }
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _LIB = None
 
@@ -96,6 +96,11 @@ def splitk_sizes(fmt, M, N, K, ksplit, batch=1):
     pf, nt = ctypes.c_int64(), ctypes.c_int64()
     check(lib().fp4x_splitk_sizes(fmt, M, N, K, ksplit, batch, ctypes.byref(pf), ctypes.byref(nt)), "splitk_sizes")
     return pf.value, nt.value
+
+
+def reload_env():
+    """Re-read the library's FP4X_* path switches (read once otherwise)."""
+    check(lib().fp4x_reload_env(), "reload_env")
 
 
 DTYPE_CODE = {torch.bfloat16: DT_BF16, torch.float32: DT_F32, torch.float16: DT_F16}

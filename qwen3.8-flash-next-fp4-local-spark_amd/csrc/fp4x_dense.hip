@@ -19,8 +19,9 @@ bool launch_int2_stream_f16(GemvLaunch p, hipStream_t st);
 bool launch_nv4_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_w6_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_mx8_stream_entry(GemvLaunch p, hipStream_t st);
-int topk_check(const void* logits, int64_t stride, int M, int V, int C, void* workspace, int64_t ws_bytes);
-int topk_launch(const uint16_t* lg, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
+int topk_check(const void* logits, int dtype, int64_t stride, int M, int V, int C, void* workspace,
+               int64_t ws_bytes);
+int topk_launch(const void* lg, int dtype, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
                 bool have_smax, hipStream_t st);
 int topk_slice_len(int V);
 int64_t topk_smax_stride(int V);
@@ -50,15 +51,37 @@ int device_cus() {
   return cus;
 }
 
-int waves_per_cu_cap() {
-  static int cap = -1;
-  if (cap < 0) {
-    const char* e = getenv("FP4X_WAVES_PER_CU");
-    const int v = e ? atoi(e) : 0;
-    cap = v >= 1 && v <= 64 ? v : 0;
-  }
-  return cap;
+static Switches g_switches;
+static bool g_switches_read = false;
+
+void reload_switches() {
+  auto on = [](const char* name) {
+    const char* e = getenv(name);
+    return !(e && e[0] == '0');
+  };
+  Switches w;
+  w.w8_stream = on("FP4X_W8_STREAM");
+  w.int2_stream = on("FP4X_INT2_STREAM");
+  w.nv4_stream = on("FP4X_NV4_STREAM");
+  w.w6_stream = on("FP4X_W6_STREAM");
+  w.mx8_stream = on("FP4X_MX8_STREAM");
+  w.hc_mix = on("FP4X_HC_MIX");
+  const char* e = getenv("FP4X_WAVES_PER_CU");
+  const int v = e ? atoi(e) : 0;
+  w.waves_per_cu = v >= 1 && v <= 64 ? v : 0;
+  const char* sp = getenv("FP4X_HC_SPIN_LIMIT");
+  const long spin = sp ? atol(sp) : -1;
+  w.hc_spin_limit = spin >= 0 && spin <= (1 << 22) ? (int)spin : 1 << 22;
+  g_switches = w;
+  g_switches_read = true;
 }
+
+const Switches& switches() {
+  if (!g_switches_read) reload_switches();
+  return g_switches;
+}
+
+int waves_per_cu_cap() { return switches().waves_per_cu; }
 void set_error(const std::string& msg) { g_err = msg; }
 
 int check_launch(const char* what) {
@@ -313,22 +336,20 @@ int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void*
 }
 
 int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
-                   void* coarse, int64_t coarse_stride, int M, int N, int K, int G, int C, int64_t* idx_out,
-                   void* workspace, int64_t ws_bytes, void* stream) {
-  if (coarse_stride < N || coarse_stride % 8 || !aligned(coarse, 16))
-    return fail(FP4X_ERR_ARG, "int2_topk: coarse logits need 16-byte aligned rows with a stride (%lld) that is a "
-                "multiple of 8 and >= N (%lld)", coarse_stride, N);
-  int rc = topk_check(coarse, coarse_stride, M, N, C, workspace, ws_bytes);
+                   void* coarse, int coarse_dtype, int64_t coarse_stride, int M, int N, int K, int G, int C,
+                   int64_t* idx_out, void* workspace, int64_t ws_bytes, void* stream) {
+  int rc = topk_check(coarse, coarse_dtype, coarse_stride, M, N, C, workspace, ws_bytes);
   if (rc) return rc;
   if (M == 0) return FP4X_OK;
   hipStream_t st = (hipStream_t)stream;
   uint16_t* smax = static_cast<uint16_t*>(workspace);
-  // the streaming kernel's per-tile maxima are the top-k's slices when they are 16 elements
+  // the streaming kernel's per-tile maxima (of the bf16-rounded logits, also
+  // for fp32 coarse logits) are the top-k's slices when they are 16 elements
   const bool fuse = topk_slice_len(N) == 16;
-  rc = int2_coarse(x, x_stride, P, S, s_fmt, rs, coarse, FP4X_DT_BF16, coarse_stride, M, N, K, G,
+  rc = int2_coarse(x, x_stride, P, S, s_fmt, rs, coarse, coarse_dtype, coarse_stride, M, N, K, G,
                    fuse ? smax : nullptr, topk_smax_stride(N), st);
   if (rc < 0) return rc;
-  return topk_launch(static_cast<const uint16_t*>(coarse), coarse_stride, M, N, C, idx_out, smax, rc == 1, st);
+  return topk_launch(coarse, coarse_dtype, coarse_stride, M, N, C, idx_out, smax, rc == 1, st);
 }
 
 }  // extern "C"
@@ -367,28 +388,29 @@ __global__ __launch_bounds__(256) void mx8_dequant_f32_kernel(const uint8_t* w, 
   const float sc = e8m0_to_f32(ld_u8(s + row * (K / 32) + (c >> 1)));
   const uint32_t d[4] = {q.x, q.y, q.z, q.w};
   float4* o = reinterpret_cast<float4*>(out + row * K + c * 16);
+  const bool inf_scale = ld_u8(s + row * (K / 32) + (c >> 1)) == 255u;   // exp2(128) = +inf (see FmtMX8)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const f32x2_t a = fp8x2_to_f32x2<false>(d[i], sc), b = fp8x2_to_f32x2<true>(d[i], sc);
+    f32x2_t a = fp8x2_to_f32x2<false>(d[i], sc), b = fp8x2_to_f32x2<true>(d[i], sc);
+    if (inf_scale) {
+      const float v[4] = {__uint_as_float(FmtMX8::inf_bf16(d[i] & 0xffu) << 16),
+                          __uint_as_float(FmtMX8::inf_bf16((d[i] >> 8) & 0xffu) << 16),
+                          __uint_as_float(FmtMX8::inf_bf16((d[i] >> 16) & 0xffu) << 16),
+                          __uint_as_float(FmtMX8::inf_bf16(d[i] >> 24) << 16)};
+      a = f32x2_t{v[0], v[1]};
+      b = f32x2_t{v[2], v[3]};
+    }
     o[i] = make_float4(a.x, a.y, b.x, b.y);
   }
-}
-
-__global__ __launch_bounds__(256) void dot2_kernel(const uint32_t* a, const uint32_t* b, const float* c, float* out,
-                                                   int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = dot2_bf16(a[i], b[i], c[i]);
 }
 
 }  // namespace fp4x
 
 extern "C" {
 
-int fp4x_dot2_bf16(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n, void* stream) {
-  if (n < 0) return fail(FP4X_ERR_ARG, "dot2: n=%lld", n);
-  if (n == 0) return FP4X_OK;
-  hipLaunchKernelGGL(dot2_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, a, b, c, out, n);
-  return check_launch("dot2");
+int fp4x_reload_env(void) {
+  reload_switches();
+  return FP4X_OK;
 }
 
 int fp4x_dequant_bf16(int fmt, const void* w0, const void* w1, const void* s, int N, int K, int G, void* out,

@@ -40,12 +40,6 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 
-// D = a.lo*b.lo + a.hi*b.hi + c  (v_dot2_f32_bf16), bf16 pairs in dwords.
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
 // ---------------------------------------------------------------- order keys
 // bf16 bits -> 16-bit key increasing with the value; -0 counts as +0 and
 // every NaN as the largest value.  Key 0 lies below every value (the key of
@@ -55,6 +49,14 @@ __device__ __forceinline__ uint32_t tk_key(uint32_t b) {
   if ((b & 0x7fffu) == 0) b = 0;
   else if ((b & 0x7f80u) == 0x7f80u && (b & 0x7fu)) b = 0x7fc0u;
   return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+// fp32 bits -> 32-bit key with the same order rules (-0 as +0, every NaN
+// as the largest value).  No value maps to key 0 (-inf has 0x007fffff), so
+// it marks "no element" here too.
+__device__ __forceinline__ uint32_t tk_key32(uint32_t b) {
+  if ((b & 0x7fffffffu) == 0) b = 0;
+  else if ((b & 0x7fffffffu) > 0x7f800000u) b = 0x7fc00000u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
 // ---------------------------------------------------------------- fp8 / fp4
@@ -102,13 +104,16 @@ __device__ __forceinline__ float group_allreduce(float v, int n) {
   return v;
 }
 
-// Logistic sigmoid from its definition 1 / (1 + e^-x), with e^-x evaluated
-// as 2^(-x * log2 e) on the hardware exp2 (v_exp_f32) and an IEEE divide.
-// One implementation serves the fused and unfused mixer epilogues.
+// Logistic sigmoid 1 / (1 + e^-x) rounded to fp32: evaluated in fp64 (the
+// fp64 exp and an IEEE fp64 divide, within two fp64 ulps of the exact value)
+// and rounded once to fp32, so the result is the correctly rounded fp32
+// sigmoid unless the exact value lies within 2^-51 relative of an fp32
+// rounding boundary.  One implementation serves the fused and unfused mixer
+// epilogues; they evaluate a few hundred sigmoids per workgroup, where fp64
+// costs nothing measurable.
 __device__ __forceinline__ float sigmoid_f32(float x) {
-  const float log2e = 1.4426950408889634f;
-  float t = __builtin_amdgcn_exp2f(-x * log2e);
-  return 1.0f / (1.0f + t);
+  const double t = exp(-(double)x);
+  return (float)(1.0 / (1.0 + t));
 }
 
 // ---------------------------------------------------------------- memory

@@ -1,25 +1,23 @@
-// Decode-shaped (M <= 16) quantized GEMV engine for gfx950.
+// Format decoders and the chunk layout shared by the fp4x kernels (gfx950).
 //
 // y[m, n] = sum_k x[m, k] * w[n, k] with x bf16 and w dequantized to the
 // bf16 operand the plugin's kernels feed to their dot (x/fp4x_kernels.py:23,
 // :92, :129, :170, :322), fp32 accumulation.
 //
-// Work decomposition (one definition, used by every kernel so that results
-// of different entry points are bitwise comparable):
-//   * A weight row is cut into 16-byte "chunks" of the main packed plane
-//     (16 fp8/int8 weights, 32 W6/NVFP4 weights, 64 INT2 weights).
-//   * `lpr` lanes (a power of two) share one row; lane `l` of the group owns
-//     chunks l, l + lpr, l + 2*lpr, ... of the row (or of the row's K slice
-//     under split-K), so a group reads lpr*16 contiguous bytes per load.
-//   * Each lane accumulates its chunks in increasing k with v_dot2_f32_bf16
-//     on (weight pair, activation pair), starting from 0.0f.
-//   * The lpr partials are combined by the butterfly in group_allreduce.
-//   * Split-K: slice s of ksplit equal K slices writes its fp32 partial to
-//     slot s; the last-arriving workgroup of a row tile sums slots 0..ks-1
-//     in order (((p0 + p1) + p2) + ...), runs the epilogue and re-arms the
-//     tile's ticket to 0.  No fp32 atomics: results are deterministic.
-//   * Activations are staged once per workgroup in LDS (or read from global
-//     memory when the K slice does not fit).
+// This header holds what the GEMV engines have in common:
+//   * the per-format decoders Fmt* (one 16-byte "chunk" of the main packed
+//     plane: 16 fp8/int8 weights, 32 W6/NVFP4 weights, 64 INT2 weights, and
+//     its scales, decoded in registers to bf16 operand pairs);
+//   * the chunk layout of the rescore kernels: `lpr` lanes (a power of two)
+//     share one row, lane l owns chunks l, l + lpr, ... and folds them in
+//     increasing k with IEEE fma (AccFma), the partials meeting in the
+//     butterfly of group_allreduce;
+//   * the split-K slot protocol (splitk_arrive): slice s of ksplit equal K
+//     slices writes its fp32 partial to slot s; the last-arriving workgroup of
+//     a row tile sums slots 0..ks-1 in order (((p0 + p1) + p2) + ...), runs the
+//     epilogue and re-arms the tile's ticket.  No fp32 atomics: results are
+//     deterministic.
+// The GEMVs themselves accumulate on MFMA (fp4x_mfma.h, fp4x_stream.h).
 #pragma once
 #include "fp4x_device.h"
 
@@ -88,6 +86,23 @@ struct FmtMX8 {
     w[2] = fp8x2_to_bf16x2<false>(ch.q.y, sc); w[3] = fp8x2_to_bf16x2<true>(ch.q.y, sc);
     w[4] = fp8x2_to_bf16x2<false>(ch.q.z, sc); w[5] = fp8x2_to_bf16x2<true>(ch.q.z, sc);
     w[6] = fp8x2_to_bf16x2<false>(ch.q.w, sc); w[7] = fp8x2_to_bf16x2<true>(ch.q.w, sc);
+    if (__builtin_expect(ch.e == 255u, 0)) inf_scale(ch.q, w);
+  }
+  // Exponent 255: the reference's scale exp2(255 - 127) is +inf in fp32, so
+  // each weight is +-inf, or NaN for a zero or NaN code; the scaled convert
+  // treats that exponent as a NaN scale instead (OCP MX's e8m0 NaN) and gives
+  // NaN for every code.
+  __device__ static uint32_t inf_bf16(uint32_t c) {
+    const uint32_t mag = c & 0x7fu;
+    return mag == 0u || mag == 0x7fu ? 0x7fc0u : 0x7f80u | ((c & 0x80u) << 8);
+  }
+  __device__ static void inf_scale(const uint4& q, uint32_t (&w)[8]) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[2 * i] = inf_bf16(d[i] & 0xffu) | (inf_bf16((d[i] >> 8) & 0xffu) << 16);
+      w[2 * i + 1] = inf_bf16((d[i] >> 16) & 0xffu) | (inf_bf16(d[i] >> 24) << 16);
+    }
   }
 };
 
@@ -485,14 +500,9 @@ struct FmtBF16 {
 };
 
 // ------------------------------------------------------------------ core
-// Accumulation step of one (weight pair, activation pair).
-//   AccDot2: v_dot2_f32_bf16 (one instruction per pair; its internal rounding
-//            is the hardware's).
-//   AccFma:  two IEEE fp32 fma, low element first: every rounding is
-//            specified, so the sum can be replayed bit for bit on a CPU.
-struct AccDot2 {
-  __device__ static float step(uint32_t w, uint32_t x, float acc) { return dot2_bf16(w, x, acc); }
-};
+// Accumulation step of one (weight pair, activation pair) in the rescore
+// kernels: two IEEE fp32 fma, low element first.  Every rounding is
+// specified, so the sum can be replayed bit for bit on a CPU.
 struct AccFma {
   __device__ static float step(uint32_t w, uint32_t x, float acc) {
     acc = __builtin_fmaf(bf16_lo(w), bf16_lo(x), acc);
@@ -525,7 +535,7 @@ __device__ __forceinline__ void load_batch(ChunkBatch<F, RPL>& b, const PlaneArg
 
 // x[m][k] lives at xs[m * xstride + k - kx0] (LDS or global, bf16).
 // Rows m >= M of x are not read (their accumulators stay 0).
-template <class F, int MT, int RPL, class XPtr, class Acc = AccDot2>
+template <class F, int MT, int RPL, class XPtr, class Acc = AccFma>
 __device__ __forceinline__ void compute_batch(const ChunkBatch<F, RPL>& b, XPtr xs, int xstride, int kx0, int M,
                                               int c0, int cend, int lrow, int lpr, int jb, int cpl,
                                               float (&acc)[RPL][MT]) {

@@ -166,24 +166,30 @@ static bool al(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & 
 //     (Issued first, they would share each CU's bandwidth with the down
 //     loads and lengthen the critical path.)
 //   * The workgroup whose count completes the down tiles re-arms the count
-//     and raises one flag per workgroup, each on a 128-byte line of its own.
-//     One lane per workgroup waits for its flag (s_sleep between reads, at
-//     most spin_limit reads) and lowers it; the workgroup then stages the
+//     and advances every workgroup's flag by one (a fetch-add per 128-byte
+//     flag line).  Each workgroup read its own flag when it started, and one
+//     lane waits until the flag differs from that value (s_sleep between
+//     reads, at most spin_limit reads); the workgroup then stages the
 //     bottleneck with device-coherent loads and runs its up tiles.  (200
 //     workgroups polling one shared counter instead made a hot spot that cost
 //     about 13 us per mixer.)
+//   * The flags are generation counters, never lowered: a call waits for the
+//     advance that follows its own start, so an advance that comes late (after
+//     its waiter gave up) can never satisfy the next call, whose waiters read
+//     the flag afresh.
 //   * The down items sit in the lowest workgroup indices, which the hardware
 //     dispatches first, so the wait never depends on a workgroup that could
 //     not get a CU; the grid is at most one workgroup per CU.
 //   * A wait that reaches spin_limit (which would need another kernel
 //     holding the CUs for about a second) writes NaN to that workgroup's
-//     outputs.
+//     outputs and sets bit 0 of the status word sync[1].
 constexpr int kMixFlagStride = 32;               // int32 between flags: one 128-byte line each
 
 struct HcMixArgs {
   GemvLaunch d;          // down: x, q, s, di (out), bot (out2), lr, hc, split-K slots and tickets
   HcUpArgs u;            // up: bot [M, lr] contiguous, interleaved q/s, normalized, out
-  int* sync;             // [0] down tiles done, [kMixFlagStride * (w + 1)] flag of workgroup w; zero between calls
+  int* sync;             // [0] down tiles done (zero between calls), [1] status (bit 0: a wait gave up),
+                         // [kMixFlagStride * (w + 1)] generation flag of workgroup w
   int C, D, tiles_d, R, spin_limit;
 };
 
@@ -206,6 +212,9 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   const int nch = u.K / F::KPC, cw = wv * 4 + g;
   const int J = ((nch + CPS - 1) / CPS + DP - 1) / DP;
   const int64_t urow = (int64_t)tuc * T + grp * 16 + n;
+  int* flag = a.sync + kMixFlagStride * (blockIdx.x + 1);
+  int gen0 = 0;                                     // this workgroup's flag before the call's advance
+  if (threadIdx.x == 0) gen0 = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // 1. one down item in each of the first D workgroups (the critical path:
   //    its loads go out first)
@@ -216,10 +225,10 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
       int old = 0;
       if (lane == 0) old = __hip_atomic_fetch_add(a.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       old = __builtin_amdgcn_readfirstlane(old);
-      if (old == a.tiles_d - 1) {                   // the last down tile: re-arm the count, raise every flag
+      if (old == a.tiles_d - 1) {                   // the last down tile: re-arm the count, advance every flag
         if (lane == 0) __hip_atomic_store(a.sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (int w = lane; w < (int)gridDim.x; w += 64)
-          __hip_atomic_store(a.sync + kMixFlagStride * (w + 1), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(a.sync + kMixFlagStride * (w + 1), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
@@ -230,16 +239,15 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   mfma_load_full<F, DP, CPS>(cb, F::lane(u.pa, urow, CPS * cw));
   __syncthreads();
 
-  // 3. wait for this workgroup's flag, then lower it for the next call
+  // 3. wait for this workgroup's flag to advance past its value at the start
   if (threadIdx.x == 0) {
-    int* flag = a.sync + kMixFlagStride * (blockIdx.x + 1);
     int f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int it = 0; f == 0 && it < a.spin_limit; ++it) {
+    for (int it = 0; f == gen0 && it < a.spin_limit; ++it) {
       __builtin_amdgcn_s_sleep(4);
       f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    s_ok = f != 0;
-    __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_ok = f != gen0;
+    if (!s_ok) __hip_atomic_fetch_or(a.sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   const bool ok = s_ok != 0;
@@ -406,8 +414,7 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
     if (rc != FP4X_OK) return rc;
     return fp4x_hc_up(bot, lr, qi, si, s_dtype, nrm, nrm_stride, out, M, lr, H, hc, bj, stream);
   };
-  const char* env = getenv("FP4X_HC_MIX");
-  if ((env && env[0] == '0') || M < 1 || M > 16 || N <= 0 || K <= 0 || K % 64 || lr <= 0 || lr > N || lr % 64 ||
+  if (!switches().hc_mix || M < 1 || M > 16 || N <= 0 || K <= 0 || K % 64 || lr <= 0 || lr > N || lr % 64 ||
       hc <= 0 || bj <= 0 || H <= 0 || H % bj || ksplit < 2 || ksplit > 64 || K % ksplit || (K / ksplit) % 16 ||
       !part || !tickets || (s_dtype != FP4X_DT_F32 && s_dtype != FP4X_DT_F16))
     return two();
@@ -480,7 +487,7 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   a.D = D;
   a.tiles_d = tiles_d;
   a.R = R;
-  a.spin_limit = 1 << 22;
+  a.spin_limit = switches().hc_spin_limit;
   hipStream_t st = (hipStream_t)stream;
   bool launched;
   if (s_dtype == FP4X_DT_F16)

@@ -166,34 +166,38 @@ __device__ __forceinline__ void tk_hist_add(uint32_t* hist, uint32_t bin, bool v
   }
 }
 
-// Exact k-th largest key among n keys get(i) (two 8-bit rounds); *n_above
-// receives the number of keys strictly above it.
-template <class Get>
+// Exact k-th largest key among n keys get(i) of BITS bits (16 or 32; one
+// 8-bit radix round per byte); *n_above receives the number of keys strictly
+// above it.  The first round's bins are the keys' high bytes, skewed for
+// logits, so its adds are wave-aggregated; later rounds' bins are spread out.
+template <int BITS, class Get>
 __device__ uint32_t tk_kth(TkHist& h, Get get, int n, int k, int* n_above) {
-  for (int i = threadIdx.x; i < 256; i += blockDim.x) h.hist[i] = 0;
-  __syncthreads();
-  for (int i0 = 0; i0 < n; i0 += blockDim.x) {
-    const int i = i0 + threadIdx.x;
-    tk_hist_add(h.hist, i < n ? get(i) >> 8 : 0u, i < n);
+  uint32_t prefix = 0;
+  int above = 0;
+#pragma unroll
+  for (int r = 0; r < BITS / 8; ++r) {
+    const int sh = BITS - 8 * (r + 1);
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) h.hist[i] = 0;
+    __syncthreads();
+    if (r == 0) {
+      for (int i0 = 0; i0 < n; i0 += blockDim.x) {
+        const int i = i0 + threadIdx.x;
+        tk_hist_add(h.hist, i < n ? get(i) >> sh : 0u, i < n);
+      }
+    } else {
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint32_t kk = get(i);
+        if ((kk >> (sh + 8)) == prefix) atomicAdd(&h.hist[(kk >> sh) & 255u], 1u);
+      }
+    }
+    __syncthreads();
+    tk_walk(h, k - above);
+    prefix = (prefix << 8) | (uint32_t)h.sel_bin;
+    above += h.sel_above;
+    __syncthreads();
   }
-  __syncthreads();
-  tk_walk(h, k);
-  const uint32_t b1 = h.sel_bin;
-  const int above1 = h.sel_above;
-  __syncthreads();
-  for (int i = threadIdx.x; i < 256; i += blockDim.x) h.hist[i] = 0;
-  __syncthreads();
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    // low bytes within one high-byte bin are spread out: plain atomics
-    const uint32_t kk = get(i);
-    if ((kk >> 8) == b1) atomicAdd(&h.hist[kk & 255u], 1u);
-  }
-  __syncthreads();
-  tk_walk(h, k - above1);
-  const uint32_t t = (b1 << 8) | (uint32_t)h.sel_bin;
-  *n_above = above1 + h.sel_above;
-  __syncthreads();
-  return t;
+  *n_above = above;
+  return prefix;
 }
 
 // Wave-aggregated append of v (when flag) to list[*count]; positions past
@@ -213,24 +217,47 @@ __device__ __forceinline__ void tk_append(T* list, int* count, int cap, bool fla
   }
 }
 
-// A: slice maxima of rows whose slices are S elements (S a multiple of 16).
-__global__ __launch_bounds__(256) void topk_slicemax_kernel(const uint16_t* logits, int64_t stride, int V,
+// Row elements as order keys: Elem16 (bf16 rows) and Elem32 (fp32 rows).
+// key() is the full order key, key16() the key of the element rounded to
+// bf16 (round to nearest even, a monotone map), which the slice maxima and
+// the candidate threshold use for both: every element whose full key is among
+// the row's C largest has a key16 at least the threshold derived from them.
+struct Elem16 {
+  using T = uint16_t;
+  static constexpr int BITS = 16, PER16 = 8;      // key bits, elements per 16 bytes
+  __device__ static uint32_t key(T v) { return tk_key(v); }
+  __device__ static uint32_t key16(T v) { return tk_key(v); }
+  __device__ static uint32_t at(const uint4& q, int i) {   // element i of a 16-byte item
+    const uint32_t d = i < 4 ? (i < 2 ? q.x : q.y) : (i < 6 ? q.z : q.w);
+    return i & 1 ? d >> 16 : d & 0xffffu;
+  }
+};
+struct Elem32 {
+  using T = uint32_t;
+  static constexpr int BITS = 32, PER16 = 4;
+  __device__ static uint32_t key(T v) { return tk_key32(v); }
+  __device__ static uint32_t key16(T v) { return tk_key(f32_to_bf16(__uint_as_float(v))); }
+  __device__ static uint32_t at(const uint4& q, int i) { return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w; }
+};
+
+// A: slice maxima (key16) of rows whose slices are S elements (S a multiple of 16).
+template <class E>
+__global__ __launch_bounds__(256) void topk_slicemax_kernel(const typename E::T* logits, int64_t stride, int V,
                                                             uint16_t* smax, int64_t sstride) {
   const int m = blockIdx.y;
-  const uint16_t* row = logits + (int64_t)m * stride;
+  const typename E::T* row = logits + (int64_t)m * stride;
   const int S = tk_slice(V), ns = (V + S - 1) / S;
   const int sl = blockIdx.x * blockDim.x + threadIdx.x;
   if (sl >= ns) return;
   uint32_t mx = 0;
   const int e0 = sl * S;
-  for (int e = e0; e < e0 + S; e += 8) {
-    if (e + 8 <= V) {
+  for (int e = e0; e < e0 + S; e += E::PER16) {
+    if (e + E::PER16 <= V) {
       const uint4 v = *reinterpret_cast<const uint4*>(row + e);
-      const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) mx = max(mx, max(tk_key(d[q] & 0xffffu), tk_key(d[q] >> 16)));
+      for (int q = 0; q < E::PER16; ++q) mx = max(mx, E::key16((typename E::T)E::at(v, q)));
     } else {
-      for (int i = e; i < V; ++i) mx = max(mx, tk_key(row[i]));
+      for (int i = e; i < V; ++i) mx = max(mx, E::key16(row[i]));
     }
   }
   smax[(int64_t)m * sstride + sl] = (uint16_t)mx;
@@ -254,14 +281,15 @@ __device__ void tk_sort(uint64_t* a, int n2) {
 
 // The exact path: T = the C-th largest key of the row, the elements above
 // it, then ties at T in index order; n = C on return in cand[0, C).
-__device__ void tk_exact(const uint16_t* row, int V, int C, uint64_t* cand, TkHist& h, int* n_sh) {
+template <class E>
+__device__ void tk_exact(const typename E::T* row, int V, int C, uint64_t* cand, TkHist& h, int* n_sh) {
   if (threadIdx.x == 0) *n_sh = 0;
   __syncthreads();
   int above;
-  const uint32_t T = tk_kth(h, [&](int i) { return tk_key(row[i]); }, V, C, &above);
+  const uint32_t T = tk_kth<E::BITS>(h, [&](int i) { return E::key(row[i]); }, V, C, &above);
   for (int i0 = 0; i0 < V; i0 += blockDim.x) {
     const int i = i0 + threadIdx.x;
-    const uint32_t key = i < V ? tk_key(row[i]) : 0u;
+    const uint32_t key = i < V ? E::key(row[i]) : 0u;
     tk_append<uint64_t>(cand, n_sh, kTkCap, i < V && key > T, tk_comp(key, i));
   }
   __syncthreads();
@@ -270,7 +298,7 @@ __device__ void tk_exact(const uint16_t* row, int V, int C, uint64_t* cand, TkHi
     int taken = 0;
     for (int i0 = 0; i0 < V && taken < need; i0 += 64) {
       const int i = i0 + threadIdx.x;
-      const bool eq = i < V && tk_key(row[i]) == T;
+      const bool eq = i < V && E::key(row[i]) == T;
       const uint64_t mask = __ballot(eq);
       const int pos = taken + __popcll(mask & ((1ull << threadIdx.x) - 1ull));
       if (eq && pos < need) cand[above + pos] = tk_comp(T, i);
@@ -565,16 +593,21 @@ __device__ int rs_rank256(const uint32_t* a, int n, int* part) {
 }
 
 // VPT: 8-slice vectors of the row's slice maxima per thread (1, 2 or 4, the
-// fewest that cover the row), so short rows run fewer register slots.
-template <int VPT>
-__global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t* logits, int64_t stride, int V, int C,
-                                                                 const uint16_t* smax, int64_t sstride,
+// fewest that cover the row), so short rows run fewer register slots.  E:
+// the row's element type (Elem16 for bf16 logits, Elem32 for fp32).  The
+// slice maxima and the threshold T0 are keys of the bf16-rounded elements
+// for both; fp32 candidates are then ordered by their full 32-bit keys.
+template <int VPT, class E>
+__global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename E::T* logits, int64_t stride, int V,
+                                                                 int C, const uint16_t* smax, int64_t sstride,
                                                                  int64_t* idx_out) {
-  __shared__ uint64_t cand[kTkCap];   // exact and short-row paths
-  // (the 64 entries past kTkCap of ck, cidx and slist take the writes of
-  // lanes with nothing to write, so the compactions run without branches)
-  __shared__ uint32_t ck[kTkCap + 64];    // candidate sort keys: key << 16 | (0xffff - position)
-  __shared__ int cidx[kTkCap + 64];       // candidate element indices, increasing
+  constexpr bool F32 = E::BITS == 32;
+  constexpr int EPI = E::PER16;         // elements per 16-byte item
+  // (the 64 entries past kTkCap of cand, ck, cidx and slist take the writes
+  // of lanes with nothing to write, so the compactions run without branches)
+  __shared__ uint64_t cand[kTkCap + 64];  // exact and short-row paths; fp32 candidates: key << 32 | ~index
+  __shared__ uint32_t ck[kTkCap + 64];    // bf16 candidate sort keys: key << 16 | (0xffff - position)
+  __shared__ int cidx[kTkCap + 64];       // bf16 candidate element indices, increasing
   __shared__ int slist[kTkCap + 64];      // candidate slices, increasing
   __shared__ uint32_t wh[kRsWaves * 256];
   __shared__ TkHist h;
@@ -582,10 +615,10 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t*
   __shared__ uint32_t ext[2 * kRsWaves];
   __shared__ int n_x;
   const int m = blockIdx.x;
-  const uint16_t* row = logits + (int64_t)m * stride;
+  const typename E::T* row = logits + (int64_t)m * stride;
   int64_t* out = idx_out + (int64_t)m * C;
   if (V <= kTkCap) {
-    for (int i = threadIdx.x; i < V; i += blockDim.x) cand[i] = tk_comp(tk_key(row[i]), i);
+    for (int i = threadIdx.x; i < V; i += blockDim.x) cand[i] = tk_comp(E::key(row[i]), i);
     __syncthreads();
     tk_finish(cand, V, C, out);
     return;
@@ -643,39 +676,41 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t*
     __syncthreads();
     exact = nsl > kTkCap;
     if (!exact) {
-      // their elements >= T0 in increasing index order: thread t takes
-      // contiguous items (8 elements each) of a round, one scan per round;
-      // waves holding no item of the round skip to the scan, and the second
-      // item slot is skipped when the round has at most one item per thread
-      const int per = S / 8, tot = nsl * per;
+      // their elements whose key16 >= T0, in increasing index order: thread t
+      // takes contiguous 16-byte items (8 bf16 or 4 fp32 elements) of a round,
+      // one scan per round; waves holding no item of the round skip to the
+      // scan, and the second item slot is skipped when the round has at most
+      // one item per thread
+      const int per = S / EPI, tot = nsl * per;
       for (int r0 = 0; r0 < tot; r0 += kRsThreads * kRsIpt) {
         const int nr = min(tot - r0, kRsThreads * kRsIpt);
         const int ipt = (nr + kRsThreads - 1) / kRsThreads;
         const bool wlive = wv * 64 * ipt < nr;
-        uint32_t k8[kRsIpt * 8];
+        uint32_t k8[kRsIpt * EPI];        // key16 (0: no element)
+        uint32_t raw[kRsIpt * EPI];       // the elements (fp32 rows: for the full key)
         int e[kRsIpt];
         int cnt = 0;
         if (wlive) {
           uint4 v[kRsIpt];
 #pragma unroll
           for (int j = 0; j < kRsIpt; ++j) {
-            // every slot loads (a dead one reads the row's first 8 elements),
-            // so no load waits at a branch's join; the row's last item is
-            // read whole (rows are readable to round_up(V, 8)), its elements
-            // past V masked below
+            // every slot loads (a dead one reads the row's first item), so no
+            // load waits at a branch's join; the row's last item is read whole
+            // (rows are readable to a whole item past V), its elements past V
+            // masked below
             const int it = r0 + threadIdx.x * ipt + j;
             const bool ok = j < ipt && it < r0 + nr;
-            e[j] = ok ? slist[it / per] * S + (it % per) * 8 : -1;
+            e[j] = ok ? slist[it / per] * S + (it % per) * EPI : -1;
             v[j] = *reinterpret_cast<const uint4*>(row + (ok ? e[j] : 0));
           }
 #pragma unroll
           for (int j = 0; j < kRsIpt; ++j) {
-            const uint32_t d[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-              const uint32_t kq = tk_key(q & 1 ? d[q >> 1] >> 16 : d[q >> 1] & 0xffffu);
-              k8[j * 8 + q] = e[j] >= 0 && e[j] + q < V ? kq : 0u;
-              cnt += k8[j * 8 + q] >= T0 ? 1 : 0;
+            for (int q = 0; q < EPI; ++q) {
+              raw[j * EPI + q] = E::at(v[j], q);
+              const uint32_t kq = E::key16((typename E::T)raw[j * EPI + q]);
+              k8[j * EPI + q] = e[j] >= 0 && e[j] + q < V ? kq : 0u;
+              cnt += k8[j * EPI + q] >= T0 ? 1 : 0;
             }
           }
         }
@@ -684,11 +719,16 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t*
         if (wlive) {
           const int dummy = kTkCap + (threadIdx.x & 63);
 #pragma unroll
-          for (int j = 0; j < kRsIpt * 8; ++j) {
+          for (int j = 0; j < kRsIpt * EPI; ++j) {
             const bool in = k8[j] >= T0;
             const int at = in && p2 < kTkCap ? p2 : dummy;
-            ck[at] = (k8[j] << 16) | (uint32_t)(0xffff - p2);
-            cidx[at] = e[j >> 3] + (j & 7);
+            const int ei = e[j / EPI] + (j % EPI);
+            if constexpr (F32) {
+              cand[at] = tk_comp(E::key((typename E::T)raw[j]), (uint32_t)ei);
+            } else {
+              ck[at] = (k8[j] << 16) | (uint32_t)(0xffff - p2);
+              cidx[at] = ei;
+            }
             p2 += in ? 1 : 0;
           }
         }
@@ -699,8 +739,12 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const uint16_t*
     }
   }
   if (exact) {
-    tk_exact(row, V, C, cand, h, &n_x);
+    tk_exact<E>(row, V, C, cand, h, &n_x);
     tk_finish(cand, C, C, out);
+    return;
+  }
+  if constexpr (F32) {
+    tk_finish(cand, n_c, C, out);       // (full key, index) composites
     return;
   }
   // sort the candidates (positions follow the index order, so ties sort by index)
@@ -799,10 +843,13 @@ namespace fp4x {
 int topk_slice_len(int V) { return tk_slice(V); }
 int64_t topk_smax_stride(int V) { return tk_smax_stride(V); }
 
-int topk_check(const void* logits, int64_t stride, int M, int V, int C, void* workspace, int64_t ws_bytes) {
+int topk_check(const void* logits, int dtype, int64_t stride, int M, int V, int C, void* workspace,
+               int64_t ws_bytes) {
+  if (dtype != FP4X_DT_BF16 && dtype != FP4X_DT_F32) { set_error("topk: logits must be bf16 or fp32"); return FP4X_ERR_ARG; }
   if (M < 0 || V < 1 || C < 1 || C > V || C > 2048) { set_error("topk: need 1 <= C <= min(V, 2048)"); return FP4X_ERR_ARG; }
-  if (stride < V || stride % 8 || !al16(logits)) {
-    set_error("topk: logits must be 16-byte aligned with a row stride that is a multiple of 8");
+  const int per16 = dtype == FP4X_DT_F32 ? 4 : 8;
+  if (stride < V || stride % per16 || !al16(logits)) {
+    set_error("topk: logits must be 16-byte aligned with 16-byte aligned rows (stride >= V)");
     return FP4X_ERR_ARG;
   }
   if (ws_bytes < fp4x_topk_workspace_size(M, V) || (M > 0 && !al16(workspace))) {
@@ -813,28 +860,36 @@ int topk_check(const void* logits, int64_t stride, int M, int V, int C, void* wo
 }
 
 // B (and A unless the slice maxima are already in the workspace).
-int topk_launch(const uint16_t* lg, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
-                       bool have_smax, hipStream_t st) {
+template <class E>
+static int topk_launch_t(const typename E::T* lg, int64_t stride, int M, int V, int C, int64_t* idx_out,
+                         uint16_t* smax, bool have_smax, hipStream_t st) {
   const int S = tk_slice(V), ns = (V + S - 1) / S;
   const int64_t ss = tk_smax_stride(V);
   if (V > kTkCap && ns >= C && !have_smax)
-    hipLaunchKernelGGL(topk_slicemax_kernel, dim3((ns + 255) / 256, M), dim3(256), 0, st, lg, stride, V, smax, ss);
+    hipLaunchKernelGGL(topk_slicemax_kernel<E>, dim3((ns + 255) / 256, M), dim3(256), 0, st, lg, stride, V, smax, ss);
   const int nv = (ns + 7) / 8;
-  auto kern = nv <= kRsThreads ? topk_rowsel_kernel<1> : nv <= 2 * kRsThreads ? topk_rowsel_kernel<2>
-                                                                            : topk_rowsel_kernel<kRsVptMax>;
+  auto kern = nv <= kRsThreads ? topk_rowsel_kernel<1, E> : nv <= 2 * kRsThreads ? topk_rowsel_kernel<2, E>
+                                                                               : topk_rowsel_kernel<kRsVptMax, E>;
   hipLaunchKernelGGL(kern, dim3(M), dim3(kRsThreads), 0, st, lg, stride, V, C, smax, ss, idx_out);
   return check_launch("topk");
+}
+
+int topk_launch(const void* lg, int dtype, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
+                bool have_smax, hipStream_t st) {
+  if (dtype == FP4X_DT_F32)
+    return topk_launch_t<Elem32>(static_cast<const uint32_t*>(lg), stride, M, V, C, idx_out, smax, have_smax, st);
+  return topk_launch_t<Elem16>(static_cast<const uint16_t*>(lg), stride, M, V, C, idx_out, smax, have_smax, st);
 }
 }  // namespace fp4x
 
 extern "C" {
 
-int fp4x_topk_rows(const void* logits, int64_t stride, int M, int V, int C, int64_t* idx_out, void* workspace,
-                   int64_t ws_bytes, void* stream) {
-  int rc = topk_check(logits, stride, M, V, C, workspace, ws_bytes);
+int fp4x_topk_rows(const void* logits, int dtype, int64_t stride, int M, int V, int C, int64_t* idx_out,
+                   void* workspace, int64_t ws_bytes, void* stream) {
+  int rc = topk_check(logits, dtype, stride, M, V, C, workspace, ws_bytes);
   if (rc || M == 0) return rc;
-  return topk_launch(static_cast<const uint16_t*>(logits), stride, M, V, C, idx_out, static_cast<uint16_t*>(workspace),
-                     false, (hipStream_t)stream);
+  return topk_launch(logits, dtype, stride, M, V, C, idx_out, static_cast<uint16_t*>(workspace), false,
+                     (hipStream_t)stream);
 }
 
 int fp4x_refine_mx8(void* out, int out_dtype, int64_t out_stride, const void* x, const int64_t* idx, int M, int C,

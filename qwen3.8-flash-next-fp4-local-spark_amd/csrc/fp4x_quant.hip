@@ -64,13 +64,19 @@ struct SrcMX8 {
     for (int c = 0; c < G / 16; ++c) {
       const int k = k0 + 16 * c;
       const uint4 q = *reinterpret_cast<const uint4*>(w + row * K + k);
-      const float sc = e8m0_to_f32(s[row * (K / 32) + k / 32]);
+      const uint32_t e = s[row * (K / 32) + k / 32];
+      const float sc = e8m0_to_f32(e);
       const uint32_t d[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x2_t a = fp8x2_to_f32x2<false>(d[i], sc), b = fp8x2_to_f32x2<true>(d[i], sc);
         f[16 * c + 4 * i] = a.x; f[16 * c + 4 * i + 1] = a.y;
         f[16 * c + 4 * i + 2] = b.x; f[16 * c + 4 * i + 3] = b.y;
+      }
+      if (e == 255u) {                                    // exp2(128) = +inf, as mx8_dequant (FmtMX8)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          f[16 * c + j] = __uint_as_float(FmtMX8::inf_bf16((d[j / 4] >> (8 * (j % 4))) & 0xffu) << 16);
       }
     }
   }

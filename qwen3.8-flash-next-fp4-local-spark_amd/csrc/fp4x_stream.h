@@ -416,13 +416,12 @@ bool launch_w8_stream_cfg(GemvLaunch p, size_t lds, int gx, hipStream_t st) {
 // the LDS plan within the CU's 160 KB.
 struct StreamW8H;
 template <class U, int T, int KW, int D>
-bool launch_dense_stream(GemvLaunch p, int batch, const char* env, hipStream_t st);
+bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st);
 
 template <bool F16S>
 bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
   constexpr int T = 6, KW = 2, D = 3;
-  const char* env = getenv("FP4X_W8_STREAM");          // "0": always use the MFMA core (read per call)
-  if (env && env[0] == '0') return false;
+  if (!switches().w8_stream) return false;            // FP4X_W8_STREAM=0: always the MFMA core
   // fp16 scales: 256-K units (five loads per 256 K values instead of six).
   // The 48 layer-batched gates [512 x 2560] at M = 3, measured back to back
   // on one GPU: (T, KW, D) = (6, 2, 2) 15.2 us against 15.5 for this kernel's
@@ -430,7 +429,7 @@ bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
   // LDS plan does not fit (M >= 5 with two batch entries per workgroup) take
   // the 128-K kernel below.
   if constexpr (F16S)
-    if (launch_dense_stream<StreamW8H, 6, 2, 2>(p, batch, "FP4X_W8_STREAM", st)) return true;
+    if (launch_dense_stream<StreamW8H, 6, 2, 2>(p, batch, true, st)) return true;
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
   if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / 128) % KW != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.pa.s) & 3) || (batch > 1 && (p.s_bstride & 3))) return false;
@@ -472,8 +471,7 @@ constexpr int kSplitWaves = 8, kSplitUnits = 2;     // w8_splitk_kernel: waves p
 // per tile) and the LDS bytes when w8_splitk_kernel takes it.
 inline bool w8_splitk_plan(const GemvLaunch& p, int& C, size_t& lds) {
   constexpr int SU = kSplitWaves * kSplitUnits;
-  const char* env = getenv("FP4X_W8_STREAM");
-  if (env && env[0] == '0') return false;
+  if (!switches().w8_stream) return false;
   const int K = p.pa.K, tiles = (p.N + 15) / 16, units = K / 128;
   if (p.ksplit < 2 || K % 512 != 0 || p.M > 16) return false;
   if (reinterpret_cast<uintptr_t>(p.pa.s) & 3) return false;
@@ -487,8 +485,7 @@ inline bool w8_splitk_plan(const GemvLaunch& p, int& C, size_t& lds) {
 template <bool F16S, class Epi>
 bool launch_w8_ktile(GemvLaunch p, hipStream_t st) {
   constexpr int KW = 16, D = 2;
-  const char* env = getenv("FP4X_W8_STREAM");
-  if (env && env[0] == '0') return false;
+  if (!switches().w8_stream) return false;
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
   if (p.ksplit < 2 || K % 512 != 0 || p.M > 16) return false;
   if (reinterpret_cast<uintptr_t>(p.pa.s) & 3) return false;
@@ -768,8 +765,7 @@ bool launch_int2_stream_wd(GemvLaunch p, size_t lds, hipStream_t st) {
 }
 
 inline bool launch_int2_stream(GemvLaunch p, hipStream_t st) {
-  const char* env = getenv("FP4X_INT2_STREAM");
-  if (env && env[0] == '0') return false;
+  if (!switches().int2_stream) return false;
   const int K = p.pa.K;
   if (p.pa.G != 16 || K % 512 != 0 || p.M > 16 || p.ksplit != 1) return false;
   if ((reinterpret_cast<uintptr_t>(p.pa.w0) & 15) || (reinterpret_cast<uintptr_t>(p.pa.s) & 15)) return false;
@@ -1176,9 +1172,8 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
 // false (and nothing launched) otherwise, or when `env` is set to 0.  (The
 // second weight plane, W6's H, must be 16-byte aligned.)
 template <class U, int T, int KW, int D>
-bool launch_dense_stream(GemvLaunch p, int batch, const char* env, hipStream_t st) {
-  const char* e = getenv(env);                        // "0": always use the MFMA core (read per call)
-  if (e && e[0] == '0') return false;
+bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st) {
+  if (!on) return false;                              // the format's switch is off: the MFMA core runs
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
   if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / U::UK) % KW != 0 || batch < 1) return false;
   if (!U::BATCHED && batch != 1) return false;
@@ -1220,14 +1215,14 @@ bool launch_dense_stream(GemvLaunch p, int batch, const char* env, hipStream_t s
 // / 10.6; (2, 4, 3) 9.0 / 9.2 / 10.1; (2, 5, 2) 9.1 / 9.5 / 10.5; (1, 10, 2)
 // 10.2 / 10.8 / 11.9.  The core: 10.5 / 11.1 / 14.7.
 inline bool launch_nv4_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamNV4, 4, 2, 2>(p, 1, "FP4X_NV4_STREAM", st);
+  return launch_dense_stream<StreamNV4, 4, 2, 2>(p, 1, switches().nv4_stream, st);
 }
 // MXFP8 4096 x 2560 (256 tiles, one per CU; 10 waves of 2 units put a tile's
 // 46 KB in flight at once): (1, 10, 2) 5.1 / 5.8 / 6.6; (1, 5, 3) 5.2 / 6.0 /
 // 7.0; (1, 5, 4) 5.2 / 5.6 / 6.9; (1, 4, 5) 5.3 / 5.6 / 7.0 (the core: 6.5 /
 // 6.8 / 8.7).
 inline bool launch_mx8_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamMX8, 1, 10, 2>(p, 1, "FP4X_MX8_STREAM", st);
+  return launch_dense_stream<StreamMX8, 1, 10, 2>(p, 1, switches().mx8_stream, st);
 }
 // W6 8192 x 2560 (512 tiles, two per CU), 256-K units: (2, 2, 2) 7.9 / 8.2 /
 // 9.5; (2, 2, 3) 8.1 / 8.3 / 9.6; (2, 2, 4) 8.5 / 8.8 / 10.0; (2, 5, 2) 8.9 /
@@ -1236,7 +1231,7 @@ inline bool launch_mx8_stream(GemvLaunch p, hipStream_t st) {
 // 9.9; (2, 5, 2) 8.4 / 9.0 / 9.8; (1, 10, 2) 9.0 / 9.3 / 10.2.  The core: 9.8
 // / 10.2 / 12.4.
 inline bool launch_w6_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamW6, 2, 2, 2>(p, 1, "FP4X_W6_STREAM", st);
+  return launch_dense_stream<StreamW6, 2, 2, 2>(p, 1, switches().w6_stream, st);
 }
 
 }  // namespace fp4x

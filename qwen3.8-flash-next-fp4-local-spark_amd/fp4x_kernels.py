@@ -210,17 +210,21 @@ def int2_logits(x, P, S, N, BN=64, BK=512, nw=4, RS=None, out_dtype=torch.float3
     return out
 
 
-def int2_topk(x, P, S, N, C, RS=None):
-    """The fast head's coarse stage: (coarse bf16 [M, N], idx int64 [M, C]) =
-    (int2_logits(x, P, S, N, RS=RS, out_dtype=bfloat16), topk_rows(coarse, C)),
-    in one call that lets the coarse kernel produce the top-k's slice maxima."""
+def int2_topk(x, P, S, N, C, RS=None, out_dtype=torch.bfloat16):
+    """The coarse stage of the fast head (bf16) or of the draft head (fp32):
+    (coarse [M, N], idx int64 [M, C]) = (int2_logits(x, P, S, N, RS=RS,
+    out_dtype=out_dtype), topk_rows(coarse, C)), in one call that lets the
+    coarse kernel produce the top-k's slice maxima."""
     _need_cuda(x, P, S)
     x = x.to(torch.bfloat16).contiguous()
     m, k = x.shape
     G = k // S.shape[1]
     sfmt = _L.DT_E4M3 if S.dtype == torch.float8_e4m3fn else _L.DT_F16
-    ld = -(-N // 8) * 8
-    coarse = torch.empty((m, ld), dtype=torch.bfloat16, device=x.device)[:, :N]
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("fp4x: int2_topk gives bf16 or fp32 coarse logits")
+    per16 = 16 // torch.empty((), dtype=out_dtype).element_size()
+    ld = -(-N // per16) * per16
+    coarse = torch.empty((m, ld), dtype=out_dtype, device=x.device)[:, :N]
     idx = torch.empty((m, C), dtype=torch.int64, device=x.device)
     st = _L.stream_of(x)
     for m0 in _rows_blocks(m):
@@ -228,44 +232,54 @@ def int2_topk(x, P, S, N, C, RS=None):
         nbytes = _L.lib().fp4x_topk_workspace_size(mb, N)
         ws = _topk_workspace(x.device, nbytes)
         _L.check(_L.lib().fp4x_int2_topk(_ptr(x[m0:]), k, _ptr(P), _ptr(S), sfmt,
-                                         _ptr(RS) if RS is not None else None, _ptr(coarse[m0:]), ld, mb, N, k, G,
-                                         C, _ptr(idx[m0:]), _ptr(ws), nbytes, st), "int2_topk")
+                                         _ptr(RS) if RS is not None else None, _ptr(coarse[m0:]), _dt(out_dtype), ld,
+                                         mb, N, k, G, C, _ptr(idx[m0:]), _ptr(ws), nbytes, st), "int2_topk")
     return coarse, idx
 
 
 def topk_rows(logits, C):
-    """Indices [M, C] (int64) of the C largest bf16 logits of each row, in
-    the order (value desc, index asc) — the selection the fast head takes
-    with torch.topk, with a defined tie order."""
+    """Indices [M, C] (int64) of the C largest logits (bf16 or fp32) of each
+    row, in the order (value desc, index asc) — the selection the fast head
+    and the draft head take with torch.topk, with a defined tie order."""
     _need_cuda(logits)
-    if logits.dtype != torch.bfloat16:
-        raise TypeError("fp4x: topk_rows takes bf16 logits")
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("fp4x: topk_rows takes bf16 or fp32 logits")
     m, v = logits.shape
-    v8 = -(-v // 8) * 8                            # rows are read in 8-element units
-    end = (logits.storage_offset() + (m - 1) * logits.stride(0) + v8) * 2
-    if (logits.stride(1) != 1 or logits.stride(0) % 8 or logits.data_ptr() % 16
+    per16 = 16 // logits.element_size()
+    vr = -(-v // per16) * per16                    # rows are read in 16-byte items
+    end = (logits.storage_offset() + (m - 1) * logits.stride(0) + vr) * logits.element_size()
+    if (logits.stride(1) != 1 or logits.stride(0) % per16 or logits.data_ptr() % 16
             or (m and end > logits.untyped_storage().nbytes())):
-        padded = torch.empty((m, v8), dtype=logits.dtype, device=logits.device)
+        padded = torch.empty((m, vr), dtype=logits.dtype, device=logits.device)
         padded[:, :v] = logits
         logits = padded
     idx = torch.empty((m, C), dtype=torch.int64, device=logits.device)
     nbytes = _L.lib().fp4x_topk_workspace_size(m, v)
     ws = _topk_workspace(logits.device, nbytes)
-    _L.check(_L.lib().fp4x_topk_rows(_ptr(logits), logits.stride(0), m, v, C, _ptr(idx), _ptr(ws), nbytes,
-                                     _L.stream_of(logits)), "topk_rows")
+    _L.check(_L.lib().fp4x_topk_rows(_ptr(logits), _dt(logits.dtype), logits.stride(0), m, v, C, _ptr(idx), _ptr(ws),
+                                     nbytes, _L.stream_of(logits)), "topk_rows")
     return idx
 
 
 _TOPK_WS = {}
+_TOPK_WS_OLD = []
 
 
 def _topk_workspace(device, nbytes):
     """Top-k workspace per device, grown on demand and reused (calls on one
-    device must be stream-ordered)."""
+    device must be stream-ordered).  A replaced buffer is kept alive, since
+    a graph captured earlier may still address it; growing it during a
+    capture raises (the capture would address memory sized for this call
+    only), so run the largest shape eagerly once before capturing."""
     key = device.index if device.index is not None else torch.cuda.current_device()
     ws = _TOPK_WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=device)
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("fp4x: top-k workspace too small during graph capture; run the largest shape "
+                               "once eagerly first")
+        if ws is not None:
+            _TOPK_WS_OLD.append(ws)
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
         _TOPK_WS[key] = ws
     return ws
 
@@ -377,7 +391,20 @@ class HCFused:
                                       hc, KS, _ptr(self.part), _ptr(self.tickets), self.tickets.numel(), _ptr(qi),
                                       _ptr(si), _ptr(normalized), normalized.stride(0), _ptr(out), h, BJ,
                                       _L.stream_of(x)), "hc_mix")
+        self._status_at = -(-(-(-n // 16)) // 64) * 64 + 1
         return di, bot, out
+
+    def wait_timeouts(self, clear=True):
+        """True if a single-launch mixer call since the last check gave up
+        waiting for its bottleneck (its outputs then hold NaN).  Reads the
+        device status word: synchronizes the stream."""
+        at = getattr(self, "_status_at", None)
+        if at is None:
+            return False
+        hit = bool(int(self.tickets[at].item()) & 1)
+        if clear and hit:
+            self.tickets[at].zero_()
+        return hit
 
     @staticmethod
     def interleave_up(q, s, hc, bj):

@@ -1,4 +1,6 @@
 """Shared helpers of the GPU parity tests (numpy <-> device tensors)."""
+import contextlib
+
 import numpy as np
 import torch
 
@@ -36,3 +38,17 @@ def assert_tol(got, ref, rel=2e-3, abs_=1e-2, what=""):
     bad = np.abs(got - ref) > abs_ + rel * np.abs(ref)
     assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} outside |d| <= {abs_} + {rel}|ref|; "
                            f"max |d| {np.abs(got - ref).max():.3g}")
+
+
+@contextlib.contextmanager
+def path_switch(monkeypatch, name, value="0"):
+    """Set one of the library's FP4X_* path switches for the block (the
+    library reads them once, so each change is followed by a reload)."""
+    import _fp4x
+    monkeypatch.setenv(name, value)
+    _fp4x.reload_env()
+    try:
+        yield
+    finally:
+        monkeypatch.delenv(name, raising=False)
+        _fp4x.reload_env()

@@ -64,13 +64,16 @@ def test_argument_errors_without_gpu(lib):
     assert L.fp4x_w8_linear(None, 100, None, None, 1, None, 0, 1, 8, 100, 1, None, None, None) == _fp4x.ERR_ARG
     assert L.fp4x_w6_linear(None, 2560, None, None, None, None, 0, 1, 8, 2560, 4, None, None, None) == _fp4x.ERR_ARG
     assert L.fp4x_int2_logits(None, 2560, None, None, 2, None, None, 0, 1, 8, 2560, 48, None) == _fp4x.ERR_ARG
-    assert L.fp4x_topk_rows(None, 64, 1, 64, 65, None, None, 0, None) == _fp4x.ERR_ARG
+    assert L.fp4x_topk_rows(None, 0, 64, 1, 64, 65, None, None, 0, None) == _fp4x.ERR_ARG      # C > V
+    assert L.fp4x_topk_rows(None, 2, 64, 1, 64, 8, None, None, 0, None) == _fp4x.ERR_ARG       # fp16 logits
+    assert b"bf16 or fp32" in L.fp4x_last_error()
+    assert L.fp4x_topk_rows(None, 1, 66, 1, 64, 8, None, None, 0, None) == _fp4x.ERR_ARG       # fp32 rows not 16-byte
     # one u16 maximum per 16-element slice, rows padded to 8 slices
     assert L.fp4x_topk_workspace_size(3, 248320) == 3 * 15520 * 2
     assert L.fp4x_topk_workspace_size(1, 1 << 20) == (1 << 20) // 32 * 2     # 32-element slices past 2^19
-    assert L.fp4x_int2_topk(None, 2560, None, None, 2, None, None, 100, 1, 248320, 2560, 16, 512, None, None, 0,
+    assert L.fp4x_int2_topk(None, 2560, None, None, 2, None, None, 0, 100, 1, 248320, 2560, 16, 512, None, None, 0,
                             None) == _fp4x.ERR_ARG                             # coarse stride < N
-    assert b"int2_topk" in L.fp4x_last_error()
+    assert b"topk" in L.fp4x_last_error()
     assert L.fp4x_hc_up(None, 640, None, None, 1, None, 10240, None, 1, 640, 2560, 4, 3, None) == _fp4x.ERR_ARG
     # the whole mixer: shapes it cannot take reach the down projection's checks (M = 17; split-K without scratch)
     assert L.fp4x_hc_mix(None, 10240, None, None, 1, None, None, 17, 336, 10240, 320, 4, 8, None, None, 0, None,
@@ -97,6 +100,16 @@ def test_argument_errors_without_gpu(lib):
     assert L.fp4x_absmax(1, None, None, 0.0, 8, 100, None, None) == _fp4x.ERR_ARG
     # empty problems are no-ops
     assert L.fp4x_mx8_linear(None, 2560, None, None, None, 0, 0, 64, 2560, 1, None, None, None) == _fp4x.OK
+
+
+def test_reload_env(lib, monkeypatch):
+    """The path switches are read once; fp4x_reload_env re-reads them
+    (no GPU needed: nothing launches)."""
+    import _fp4x
+    monkeypatch.setenv("FP4X_HC_SPIN_LIMIT", "0")
+    _fp4x.reload_env()
+    monkeypatch.delenv("FP4X_HC_SPIN_LIMIT")
+    _fp4x.reload_env()
 
 
 def test_splitk_sizes():

@@ -16,7 +16,7 @@ from oracle import gemv as og
 from oracle import ordered
 from oracle import quant as oq
 
-from gpu_helpers import act, assert_tol, bf16_bits, bf16_dev, dev, to_f32
+from gpu_helpers import act, assert_tol, bf16_bits, bf16_dev, dev, to_f32, path_switch
 
 pytestmark = pytest.mark.gpu
 
@@ -33,17 +33,33 @@ def weights(rng, n, k, scale=0.02):
 
 # ------------------------------------------------------------------ dequant
 def test_dequant_mx8_all_codes(gpu, F):
-    codes = np.tile(np.arange(256, dtype=np.uint8), 64).reshape(64, 256)
-    codes[codes == 0x7F] = 0x7E
+    """Every fp8 code under every e8m0 exponent 0..255 (row r uses exponent
+    r): the bf16 operand of the GEMVs and the fp32 mx8_dequant are bit-exact
+    with the oracle, including results that are bf16 or fp32 subnormals,
+    zeros from underflow, and overflow to inf (exponent 255, 2^128 in fp32,
+    as exp2 gives it); 0 x 2^128 is NaN, as in the reference's fp32 product."""
+    codes = np.tile(np.arange(256, dtype=np.uint8), (256, 1))
+    codes[codes == 0x7F] = 0x7E                      # the two NaN codes are checked below
     codes[codes == 0xFF] = 0xFE
-    exps = np.random.default_rng(0).integers(100, 140, (64, 8)).astype(np.uint8)
-    exps[0] = 127
+    exps = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 8, 1)
     w, s = dev(codes), dev(exps)
-    got = bf16_bits(F.dequant_operand("mx8", w, None, s, K=256))
-    want = fm.bf16_bits(oq.mx8_dequant(codes, exps))
-    assert np.array_equal(got, want)
+    want32 = oq.mx8_dequant(codes, exps)
     got32 = F.mx8_dequant(w, s).cpu().numpy()
-    assert np.array_equal(got32.view(np.uint32), oq.mx8_dequant(codes, exps).view(np.uint32))
+    nan = np.isnan(want32)
+    assert np.array_equal(np.isnan(got32), nan)
+    assert np.array_equal(got32[~nan].view(np.uint32), want32[~nan].view(np.uint32))
+    got = bf16_bits(F.dequant_operand("mx8", w, None, s, K=256))
+    want = fm.bf16_bits(want32)
+    gnan = (got & 0x7FFF) > 0x7F80
+    assert np.array_equal(gnan, nan)
+    bad = (got != want) & ~nan
+    assert not bad.any(), (f"{int(bad.sum())} operands differ, e.g. code {int(np.argwhere(bad)[0][1])} exponent "
+                           f"{int(np.argwhere(bad)[0][0])}: {got[bad][0]:#06x} vs {want[bad][0]:#06x}")
+    # NaN codes stay NaN under every finite scale
+    nc = np.tile(np.array([0x7F, 0xFF] * 16, np.uint8), (255, 1))
+    ne = np.arange(255, dtype=np.uint8)[:, None]
+    gn = bf16_bits(F.dequant_operand("mx8", dev(nc), None, dev(ne), K=32))
+    assert np.all((gn & 0x7FFF) > 0x7F80)
 
 
 @pytest.mark.parametrize("fmt", ["w8", "w8_f16", "w6", "nv4", "int2", "int2_g32", "int2_g128", "int2_e4m3"])
@@ -188,9 +204,8 @@ def test_dense_stream(gpu, F, fmt, slots, parts, env, M, tail, monkeypatch):
     planes, w_op, gs = prep(fmt, rng, n, k)
     x, _ = act(rng, M, k)
     y = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
-    monkeypatch.setenv(env, "0")
-    y_core = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
-    monkeypatch.delenv(env)
+    with path_switch(monkeypatch, env):
+        y_core = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
     assert not np.array_equal(y.view(np.uint32), y_core.view(np.uint32)), "streaming kernel not taken"
     exact = ordered.exact_sum(x, w_op) * gs
     bound = ordered.mfma_bound(x, w_op, parts) * abs(gs)              # parts: K slices of a tile
@@ -226,9 +241,8 @@ def test_w8_splitk_workgroups(gpu, F, case, monkeypatch):
     assert_tol(to_f32(y), og.matmul_f32(x, w_op), what=str(case))
     for _ in range(3):                        # re-armed tickets, arrival order does not matter
         assert torch.equal(y, F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32))
-    monkeypatch.setenv("FP4X_W8_STREAM", "0")
-    y_core = F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32)
-    monkeypatch.delenv("FP4X_W8_STREAM")
+    with path_switch(monkeypatch, "FP4X_W8_STREAM"):
+        y_core = F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32)
     assert np.all(np.abs(to_f32(y_core) - exact) <= bound)
     # another K decomposition than the core's: its fp32 sums differ in the last bits
     assert (not torch.equal(y, y_core)) == split
@@ -300,9 +314,8 @@ def test_w8_stream_layers(gpu, F, case, monkeypatch):
     x3n = np.stack([act(rng, M, k)[0] for _ in range(Ly)])
     q3, s3, x3 = dev(q3n), dev(s3n), bf16_dev(x3n)
     y = to_f32(F.w8_linear_layers(x3, q3, s3, torch.float32))
-    monkeypatch.setenv("FP4X_W8_STREAM", "0")
-    y_core = to_f32(F.w8_linear_layers(x3, q3, s3, torch.float32))
-    monkeypatch.delenv("FP4X_W8_STREAM")
+    with path_switch(monkeypatch, "FP4X_W8_STREAM"):
+        y_core = to_f32(F.w8_linear_layers(x3, q3, s3, torch.float32))
     worst = 0.0
     for i in range(Ly):
         w_op = og.operand("w8", q3n[i], s3n[i].astype(np.float32))

@@ -54,9 +54,36 @@ def test_draft_head_scatter():
     P2, S2 = oq.quantize_int2(oq.dequant_nv4(P, S, gs), group=16)
     ids = np.sort(rng.choice(vocab, V, replace=False))
     x = fm.round_bf16(rng.standard_normal((M, K)).astype(np.float32))
-    cand, vals, full = oh.draft_head(fm.bf16_bits(x), P2, S2, 16, P, S, gs, ids, vocab, dc, 4, 2)
+    cand, vals, full = oh.draft_head(fm.bf16_bits(x), P2, S2, 16, P, S, gs, ids, vocab, dc, 2)
     assert cand.shape == (M, dc) and len(set(cand[0].tolist())) == dc
+    # candidates: the top dc of the fp32 coarse logits (int2_logits' default
+    # dtype, x/fp4patch.py:313-314), not of their bf16 rounding
+    co = oh.int2_coarse(fm.bf16_bits(x), P2, S2, 16)
+    assert co.dtype == np.float32
+    assert np.array_equal(cand, oh.topk_total_order(co, dc))
+    # the temperature scales the fp32 values before the bf16 cast
+    _, vals_t, full_t = oh.draft_head(fm.bf16_bits(x), P2, S2, 16, P, S, gs, ids, vocab, dc, 2, inv_t=0.625)
+    assert np.array_equal(vals_t, (vals * np.float32(0.625)).astype(np.float32))
+    assert np.array_equal(np.take_along_axis(full_t, ids[cand], 1), fm.bf16_bits(vals_t))
     keep = np.zeros((M, vocab), bool)
     np.put_along_axis(keep, ids[cand], True, 1)
     assert np.all(full[~keep] == 0xFF80)                 # -inf outside the candidates
     assert np.array_equal(np.take_along_axis(full, ids[cand], 1), fm.bf16_bits(vals))
+
+
+def test_int2_coarse_is_rounded_exact_sum():
+    """Coarse logits are the exact (float64) sum rounded once to fp32: equal
+    to the fp32 rounding of a brute-force exact sum on a tiny head."""
+    rng = np.random.default_rng(14)
+    V, K = 24, 128
+    w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    P, S = oq.quantize_int2(w, group=16)
+    x = fm.round_bf16(rng.standard_normal((2, K)).astype(np.float32))
+    got = oh.int2_coarse(fm.bf16_bits(x), P, S, 16, rows_per_chunk=7)
+    op = fm.round_bf16(oq.dequant_int2(P, S))        # the bf16 operand bf16((code - 1.5) * s)
+    from fractions import Fraction
+    import exact_round as er
+    for m in range(2):
+        for v in range(V):
+            ex = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(x[m], op[v]))
+            assert Fraction(float(got[m, v])) == er.f32(ex), (m, v)

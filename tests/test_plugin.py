@@ -53,9 +53,9 @@ def test_every_switch_installs_its_hook(plugin, monkeypatch, tmp_path, capfd):
     after = originals(cls)
     assert all(after[k] is not before[k] for k in before), after
     err = capfd.readouterr().err
-    for line in ("MXFP8 decode GEMV installed", "HC decode GEMV installed", "UnquantizedLinear decode hook",
-                 "fast target head patch installed", "draft vocab head patch installed",
-                 "FP4X_MOE_ZERO is not part of the MI355X build; ignored"):
+    for line in ("b12x MXFP8 linears of up to 16 rows", "hyper-connection mixers of up to 16 rows",
+                 "unquantized linears hooked", "target LM head of up to 16 rows", "MTP draft head restricted",
+                 "FP4X_MOE_ZERO: that reference patch is not part of this build; ignored"):
         assert line in err, line
     import torch
     assert hasattr(torch.ops.vllm, "fp4x_bf16_linear")            # the plugin's custom op
@@ -79,4 +79,4 @@ def test_failing_patch_only_logs(plugin, monkeypatch, capfd):
     monkeypatch.setenv("FP4X_MX8", "1")
     fp4patch.register()                                            # must not raise
     err = capfd.readouterr().err
-    assert "FP4X_HC patch failed" in err and "MXFP8 decode GEMV installed" in err
+    assert "FP4X_HC: could not install" in err and "b12x MXFP8 linears" in err
