@@ -142,6 +142,19 @@ int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S
                    void* coarse, int coarse_dtype, int64_t coarse_stride, int M, int N, int K, int G, int C,
                    int64_t* idx_out, void* workspace, int64_t ws_bytes, void* stream);
 
+/* fp4x_int2_topk with its workspace (the top-k's slice maxima) in a static
+ * device array of the library, fp4x_int2_topk_noalloc_limit() = 1 MiB per
+ * device (enough for every M <= 16 and N), instead of a caller's buffer: it
+ * allocates nothing.  No counterpart in the reference; it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops).  Requests above the limit return FP4X_ERR_ARG.  Each device's array
+ * is found on the first call on that device and kept until the process ends;
+ * calls on one device share it, so calls that overlap in time race. */
+int fp4x_int2_topk_noalloc(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
+                           void* coarse, int coarse_dtype, int64_t coarse_stride, int M, int N, int K, int G, int C,
+                           int64_t* idx_out, void* stream);
+int64_t fp4x_int2_topk_noalloc_limit(void);
+
 /* In place: out[m, idx[m, c]] = cast(sum_k float(e4m3(w)*2^(s-127)) * float(x[m, k])).
  * out is [M, V] in out_dtype, x bf16 [M, K] contiguous, idx int64 [M, C].
  * [refine_mx8_ -> _refine_mx8, x/fp4x_kernels.py:384-388, :367-381] */
