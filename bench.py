@@ -11,12 +11,18 @@ Weights rotate through copies totalling > 512 MB so every launch streams from
 HBM rather than the 256 MB MALL.
 
 `kernels` adds per-kernel µs and GB/s for every configuration (MXFP8 4096 x
-2560, W6 8192 x 2560, NVFP4 16384 x 2560 at M = 1/3/16, the 97-layer fused
-mixer, the 248,320-row fast LM head and the exact MXFP8 head it replaces, the
-65k-token draft head), timed as
-HIP-graph replays, and the load-time weight preparation (group G, eager).
-`cpu_baseline` times the oracle (numpy) on the host cores for a bounded
-sample of the headline workload.
+2560, W6 8192 x 2560, NVFP4 16384 x 2560 at M = 1/3/16, single router gates
+and the 48-gate launch with fp16 and with the reference's fp32 scales, the
+97-layer mixer at the synthetic and the served shape, the 248,320-row fast
+LM head and the exact MXFP8 head it replaces, the 65k-token draft head),
+timed as HIP-graph replays, and the load-time weight preparation (group G,
+eager).  `read_ceiling` times a plain coalesced read of each kernel's bytes
+under the same protocol (the fastest of a sweep of load depths and grids);
+each kernel row carries `frac_of_ceiling`, that read's time over the
+kernel's.  `cpu_baseline` times the reference math as PyTorch CPU ops
+(oracle/torch_cpu.py) on the host cores for every configuration, with and
+without the dequantization, and the fast head's selection and argmax against
+the oracle on a sample of full-size rows.
 """
 import argparse
 import json
@@ -38,8 +44,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E,F,G")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-ceiling", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (--steps times): the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -142,26 +148,58 @@ def bench_dense(F, torch, dev, out):
 
 
 def bench_gates_single(F, torch, dev, out, q, s):
+    """One router gate per launch, as the plugin calls them (x/fp4patch.py:264-272):
+    the 48 gates back to back, fp16 scales and the reference's fp32 scales;
+    and the 48-gate layer-batched launch with fp32 scales."""
     M, n, k = 3, 512, 2560
     x = torch.randn((M, k), device=dev).to(torch.bfloat16)
     calls = [lambda i=i: F.w8_linear(x, q[i], s[i], (16, 512, 1, 4), torch.float32) for i in range(q.shape[0])]
-    us = graph_time(calls)
-    out["B_w8_gate_single_layer_M3"] = entry(us, gate_bytes(1, M, n, k))
+    out["B_w8_gate_single_layer_M3"] = entry(graph_time(calls), gate_bytes(1, M, n, k))
+    s32 = s.float()
+    calls = [lambda i=i: F.w8_linear(x, q[i], s32[i], (16, 512, 1, 4), torch.float32) for i in range(q.shape[0])]
+    out["B_w8_gate_single_layer_M3_f32s"] = entry(graph_time(calls), gate_bytes(1, M, n, k, s_bytes=4))
+    L = q.shape[0]
+    b32 = gate_bytes(L, M, n, k, s_bytes=4)
+    ncp = copies_for(L * (n * k + n * (k // 64) * 4))
+    qs = [(q.clone(), s32.clone()) for _ in range(ncp - 1)] + [(q, s32)]
+    x3 = torch.randn((L, M, k), device=dev).to(torch.bfloat16)
+    us = graph_time([lambda c=c: F.w8_linear_layers(x3, c[0], c[1], torch.float32) for c in qs] * 2)
+    out["B_w8_gates_48_layers_M3_f32s"] = entry(us, b32)
+    del qs
+
+
+def mixer_bytes(M, nd, lr, hc, H, s_bytes):
+    down = nd * hc * H + nd * (hc * H // 64) * s_bytes + M * hc * H * 2 + M * nd * 2 + M * lr * 2
+    up = hc * H * lr + hc * H * (lr // 64) * s_bytes + M * lr * 2 + M * hc * H * 2 + M * H * 2
+    return down, up
 
 
 def bench_hc(F, torch, dev, out, layers=97):
-    HC, H, LR, ND, KS, M = 4, 2560, 640, 640, 16, 3
+    """97 mixers back to back: the synthetic shape (down [640 x 10240], up
+    [10240 x 640], 16 K slices) with fp16 scales (as two launches and as one)
+    and with the reference's fp32 scales; the served shape (down [336 x
+    10240], up [10240 x 320], 8 K slices, fp32 scales: the plugin's fused
+    mixer, x/fp4patch.py:201-220)."""
+    HC, H, M = 4, 2560, 3
     g = torch.Generator(device=dev).manual_seed(1)
-    fx = F.HCFused(dev, n_down=ND, max_ksplit=KS)
-    mix = []
-    for _ in range(layers):
-        qd, sd = w8_f16(torch, torch.randn((ND, HC * H), generator=g, device=dev) * 0.02)
-        qu, su = w8_f16(torch, torch.randn((HC * H, LR), generator=g, device=dev) * 0.02)
-        qi, si = F.HCFused.interleave_up(qu, su, HC, 8)
-        mix.append((qd, sd, qi, si))
     x = torch.randn((M, HC * H), generator=g, device=dev).to(torch.bfloat16)
-    down_b = ND * HC * H + ND * (HC * H // 64) * 2 + M * HC * H * 2 + M * ND * 2 + M * LR * 2
-    up_b = HC * H * LR + HC * H * (LR // 64) * 2 + M * LR * 2 + M * HC * H * 2 + M * H * 2
+
+    def layers_of(nd, lr, f16):
+        mix = []
+        for _ in range(layers):
+            wd = torch.randn((nd, HC * H), generator=g, device=dev) * 0.02
+            wu = torch.randn((HC * H, lr), generator=g, device=dev) * 0.02
+            qd, sd = w8_f16(torch, wd) if f16 else F.quantize_w8(wd)
+            qu, su = w8_f16(torch, wu) if f16 else F.quantize_w8(wu)
+            qi, si = F.HCFused.interleave_up(qu, su, HC, 8)
+            mix.append((qd, sd, qi, si))
+        return mix
+
+    # synthetic shape, fp16 scales: down, up, the pair as two launches, one launch
+    ND, LR, KS = 640, 640, 16
+    fx = F.HCFused(dev, n_down=ND, max_ksplit=KS)
+    mix = layers_of(ND, LR, True)
+    down_b, up_b = mixer_bytes(M, ND, LR, HC, H, 2)
     bots = [fx.down(x, qd, sd, LR, HC, (32, 256, KS, 4))[1] for qd, sd, _, _ in mix]
     us_down = graph_time([lambda m=m: fx.down(x, m[0], m[1], LR, HC, (32, 256, KS, 4)) for m in mix], replays=5)
     us_up = graph_time([lambda m=m, b=b: F.HCFused.up(b, m[2], m[3], x, HC, (8, 64, 4)) for m, b in zip(mix, bots)],
@@ -171,18 +209,41 @@ def bench_hc(F, torch, dev, out, layers=97):
         _, bot = fx.down(x, m[0], m[1], LR, HC, (32, 256, KS, 4))
         F.HCFused.up(bot, m[2], m[3], x, HC, (8, 64, 4))
     us_pair = graph_time([lambda m=m: both(m) for m in mix], replays=5)
-    # the whole mixer as one call (one launch per mixer at this shape)
     us_mix = graph_time([lambda m=m: fx.mix(x, m[0], m[1], LR, HC, m[2], m[3], x, (32, 256, KS, 4)) for m in mix],
                         replays=5)
     out["D_hc_down_640x10240_M3"] = entry(us_down, down_b)
     out["D_hc_up_10240x640_M3"] = entry(us_up, up_b)
-    out["D_hc_mixer_97_layers_M3"] = entry(us_pair * layers, (down_b + up_b) * layers)
-    out["D_hc_mixer_97_layers_M3"]["us_per_mixer"] = round(us_pair, 3)
-    out["D_hc_mix_one_call_97_layers_M3"] = entry(us_mix * layers, (down_b + up_b) * layers)
-    out["D_hc_mix_one_call_97_layers_M3"]["us_per_mixer"] = round(us_mix, 3)
+    out["D_hc_mixer_97_layers_M3"] = dict(entry(us_pair * layers, (down_b + up_b) * layers),
+                                          us_per_mixer=round(us_pair, 3))
+    out["D_hc_mix_one_call_97_layers_M3"] = dict(entry(us_mix * layers, (down_b + up_b) * layers),
+                                                 us_per_mixer=round(us_mix, 3))
+    del mix, bots
+    # synthetic shape, fp32 scales (the reference's quantize_w8 layout)
+    mix = layers_of(ND, LR, False)
+    down_b, up_b = mixer_bytes(M, ND, LR, HC, H, 4)
+    us_mix = graph_time([lambda m=m: fx.mix(x, m[0], m[1], LR, HC, m[2], m[3], x, (32, 256, KS, 4)) for m in mix],
+                        replays=5)
+    out["D_hc_mix_one_call_97_layers_M3_f32s"] = dict(entry(us_mix * layers, (down_b + up_b) * layers),
+                                                      us_per_mixer=round(us_mix, 3))
+    del mix
+    # the served shape, fp32 scales, 8 K slices
+    ND, LR, KS = 336, 320, 8
+    fx = F.HCFused(dev)
+    mix = layers_of(ND, LR, False)
+    down_b, up_b = mixer_bytes(M, ND, LR, HC, H, 4)
+    us_mix = graph_time([lambda m=m: fx.mix(x, m[0], m[1], LR, HC, m[2], m[3], x, (32, 256, KS, 4)) for m in mix],
+                        replays=5)
+    out["D_hc_mix_served_336x10240_10240x320_97_layers_M3_f32s"] = dict(
+        entry(us_mix * layers, (down_b + up_b) * layers), us_per_mixer=round(us_mix, 3))
+    del mix
 
 
-def bench_head(F, torch, dev, out, vectors=1000):
+def bench_head(F, torch, dev, out, vectors=1000, n_x=128):
+    """The fast target head at V = 248,320, K = 2560, M = 3, G = 16, C = 512.
+    The coarse pass rotates three INT2 copies (720 MB); the refine and the
+    whole head rotate n_x activation sets, so the 3 x 512 MXFP8 rows each call
+    gathers (4 MB) differ from call to call and come from HBM, not the MALL.
+    Returns the head's tensors for the CPU leg's parity check."""
     V, K, C, M = 248320, 2560, 512, 3
     g = torch.Generator(device=dev).manual_seed(2)
     w = torch.randn((V, K), generator=g, device=dev) * 0.02
@@ -203,15 +264,19 @@ def bench_head(F, torch, dev, out, vectors=1000):
     # the coarse pass and the top-C in one call (slice maxima from the coarse kernel)
     us = graph_time([lambda c=c: F.int2_topk(x, c[0], c[1], V, C) for c in copies], 10)
     out["E_int2_coarse_plus_topk512_M3"] = entry(us, int2_b + M * C * 8)
-    idx = F.topk_rows(coarse, C)
-    us = graph_time([lambda: F.refine_mx8_(coarse, x, idx, q, s)] * 4, 10)
-    out["E_refine_mx8_3x512_M3"] = entry(us, M * C * (K + K // 32 + 8) + M * K * 2 + M * C * 2)
+    # the exact rescore of 3 x 512 candidate rows, over n_x activation sets and their candidates
+    xs = [torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_x)]
+    pairs = [F.int2_topk(xx, P, S, V, C) for xx in xs]
+    ref_b = M * C * (K + K // 32 + 8) + M * K * 2 + M * C * 2
+    us = graph_time([lambda i=i: F.refine_mx8_(pairs[i][0], xs[i], pairs[i][1], q, s) for i in range(n_x)], 5)
+    out["E_refine_mx8_3x512_M3"] = dict(entry(us, ref_b), activation_sets=n_x)
 
     def head(xx, c):
         co, ix = F.int2_topk(xx, c[0], c[1], V, C)
         F.refine_mx8_(co, xx, ix, q, s)
-    us = graph_time([lambda c=c: head(x, c) for c in copies], 10)
-    out["E_fast_head_total_M3"] = {"us": round(us, 3)}
+    us = graph_time([lambda i=i: head(xs[i], copies[i % 3]) for i in range(n_x)], 3)
+    out["E_fast_head_total_M3"] = {"us": round(us, 3), "activation_sets": n_x}
+    del pairs
     # the exact head the fast path replaces: the MXFP8 GEMV over all 248,320 rows
     # (655 MB, above the 256 MB MALL, so one copy streams from HBM)
     us = graph_time([lambda: F.mx8_linear(x, q, s, (32, 512, 1, 4))] * 2, 10)
@@ -220,15 +285,17 @@ def bench_head(F, torch, dev, out, vectors=1000):
     agree, n = 0, 0
     for b0 in range(1000, 1000 + vectors, M):
         rng = torch.Generator(device=dev).manual_seed(b0)
-        xs = torch.randn((M, K), generator=rng, device=dev).to(torch.bfloat16)
-        co, ix = F.int2_topk(xs, P, S, V, C)
-        fast = F.refine_mx8_(co, xs, ix, q, s)
-        full = F.mx8_linear(xs, q, s, (32, 512, 1, 4))
+        xs_ = torch.randn((M, K), generator=rng, device=dev).to(torch.bfloat16)
+        co, ix = F.int2_topk(xs_, P, S, V, C)
+        fast = F.refine_mx8_(co, xs_, ix, q, s)
+        full = F.mx8_linear(xs_, q, s, (32, 512, 1, 4))
         m = min(M, 1000 + vectors - b0)
         agree += int((fast[:m].argmax(-1) == full[:m].argmax(-1)).sum())
         n += m
     out["E_fast_head_total_M3"]["argmax_agreement"] = round(agree / n, 4)
     out["E_fast_head_total_M3"]["vectors"] = n
+    del copies, xs
+    return q, s, P, S
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -300,29 +367,192 @@ def bench_prep(F, torch, dev, out):
     del q, s, w
 
 
-def cpu_baseline(seconds):
-    """The oracle's dequantize-then-matmul router gates (numpy, all host
-    cores) on a bounded sample: whole 48-layer passes at M = 3."""
+# ------------------------------------------------------------------ read ceiling
+def bench_read_ceiling(F, torch, dev, sizes, replays=10):
+    """{bytes: (µs, shape)}: the fastest plain coalesced read (fp4x_read_ceiling)
+    of each size, timed as the kernels are: graph replays back to back, the
+    source rotating over > 512 MB so every read streams from HBM; swept over
+    4/8/16 loads in flight and 2/4/8 workgroups per CU."""
+    import ctypes
+    lib = F._L.lib()
+    total = 640 << 20
+    buf = torch.ones(total, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    base = buf.data_ptr()
+    res = {}
+    for nbytes in sorted(set(sizes)):
+        b16 = -(-nbytes // 16) * 16
+        if b16 > total // 2:
+            continue
+        span = -(-b16 // 4096) * 4096
+        ncp = max(2, min(total // span, -(-MALL_COLD_BYTES // span)))
+        best = None
+        for unroll in (4, 8, 16):
+            for wpc in (2, 4, 8):
+                def call(off, unroll=unroll, wpc=wpc):
+                    F._L.check(lib.fp4x_read_ceiling(ctypes.c_void_p(base + off), b16, unroll, wpc, F._ptr(sink),
+                                                     F._L.stream_of(buf)), "read_ceiling")
+                us = graph_time([lambda o=i * span: call(o) for i in range(ncp)], replays)
+                if best is None or us < best[0]:
+                    best = (us, f"{unroll} loads in flight x {wpc} WG/CU")
+        res[nbytes] = best
+    del buf
+    torch.cuda.empty_cache()
+    return res
+
+
+def attach_ceilings(kernels, ceil):
+    """frac_of_ceiling = plain-read µs / kernel µs for each kernel row (per
+    mixer for the 97-layer rows)."""
+    for row in kernels.values():
+        if "bytes" not in row:
+            continue
+        nb, us = row["bytes"], row["us"]
+        if "us_per_mixer" in row:
+            nb, us = nb // 97, row["us_per_mixer"]
+        c = ceil.get(nb)
+        if c:
+            row["read_ceiling_us"] = round(c[0], 3)
+            row["frac_of_ceiling"] = round(c[0] / us, 4)
+
+
+def ceiling_sizes(kernels):
+    out = []
+    for row in kernels.values():
+        if "bytes" in row:
+            out.append(row["bytes"] // 97 if "us_per_mixer" in row else row["bytes"])
+    return out
+
+
+# ------------------------------------------------------------------ CPU baseline
+def _median_us(fn, reps, warm=3):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter_ns()
+        fn()
+        ts.append(time.perf_counter_ns() - t0)
+    ts.sort()
+    return ts[len(ts) // 2] / 1e3
+
+
+def cpu_baseline(F, torch, dev, head=None, reps=20, parity_batches=8):
+    """The reference math as PyTorch CPU ops (oracle/torch_cpu.py) on the host
+    cores, for every configuration, in the same run and on the same kind of
+    seeded inputs as the GPU rows: per call with the dequantization (the
+    reference's full semantics) and with pre-dequantized bf16-valued fp32
+    weights (matmul only, a lower bound); the median of `reps` calls after 3
+    warm-ups, GB/s over the GPU rows' algorithmic bytes.  The mixer is timed
+    per layer, the LM head's coarse pass on an 8,192-row slice, both scaled
+    to the full workload.  Also, with `head`: the fast head's top-512 set and
+    argmax against the oracle (numpy, exact coarse sums) on parity_batches
+    full-size M = 3 batches."""
+    from oracle import torch_cpu as tc
+    threads = tc.host_threads()
+    torch.set_num_threads(threads)
+    g = torch.Generator(device=dev).manual_seed(11)
+    cg = torch.Generator().manual_seed(11)
+    M, K = 3, 2560
+    x = torch.randn((M, K), generator=cg).to(torch.bfloat16)
+    rows = {}
+
+    def row(name, nbytes, full, mm, scale=1.0, note=None):
+        us_f, us_m = _median_us(full, reps) * scale, _median_us(mm, reps) * scale
+        rows[name] = {"us_with_dequant": round(us_f, 1), "us_matmul_only": round(us_m, 1),
+                      "GBps_with_dequant": round(nbytes / us_f / 1e3, 3),
+                      "GBps_matmul_only": round(nbytes / us_m / 1e3, 3)}
+        if note:
+            rows[name]["sample"] = note
+
+    def dev_w(n, k):
+        return torch.randn((n, k), generator=g, device=dev) * 0.02
+
+    # A: MXFP8 [4096 x 2560]
+    q, s = (t.cpu() for t in F.quantize_mx8(dev_w(4096, K)))
+    wop = tc.bf16_operand(tc.deq_mx8(q, s))
+    row("A_mx8_4096x2560_M3", 4096 * K + 4096 * K // 32 + M * K * 2 + M * 4096 * 2,
+        lambda: tc.mx8_linear(x, q, s), lambda: tc.gemv(x, wop))
+    # B: 48 router gates [512 x 2560], fp16 scales, fp32 logits
+    gates = [tuple(t.cpu() for t in w8_f16(torch, dev_w(512, K))) for _ in range(48)]
+    gops = [tc.bf16_operand(tc.deq_w8(qq, ss)) for qq, ss in gates]
+    row("B_w8_gates_48_layers_M3", gate_bytes(48, M, 512, K),
+        lambda: [tc.w8_linear(x, qq, ss, torch.float32) for qq, ss in gates],
+        lambda: [tc.gemv(x, w, torch.float32) for w in gops])
+    del gops
+    # C: W6 [8192 x 2560] and NVFP4 [16384 x 2560]
+    L6, H6, S6 = (t.cpu() for t in F.quantize_w6(dev_w(8192, K)))
+    wop = tc.bf16_operand(tc.deq_w6(L6, H6, S6))
+    row("C_w6_8192x2560_M3", 8192 * K // 2 + 8192 * K // 4 + 8192 * (K // 32) * 2 + M * K * 2 + M * 8192 * 2,
+        lambda: tc.w6_linear(x, L6, H6, S6), lambda: tc.gemv(x, wop))
+    P4, S4, gs = F.quantize_nv4(dev_w(16384, K))
+    P4, S4 = P4.cpu(), S4.view(torch.uint8).cpu()
+    wop = tc.bf16_operand(tc.deq_nv4(P4, S4))
+    row("C_nv4_16384x2560_M3", 16384 * K // 2 + 16384 * (K // 16) + 4 + M * K * 2 + M * 16384 * 2,
+        lambda: tc.nv4_linear(x, P4, S4, gs), lambda: tc.gemv(x, wop, gs=gs))
+    del wop
+    # D: one mixer at the synthetic shape (fp32 scales), scaled to 97 layers
+    HC, H, ND, LR = 4, 2560, 640, 640
+    xd = torch.randn((M, HC * H), generator=cg).to(torch.bfloat16)
+    qd, sd = (t.cpu() for t in F.quantize_w8(dev_w(ND, HC * H)))
+    qu, su = (t.cpu() for t in F.quantize_w8(dev_w(HC * H, LR)))
+    wd, wu = tc.bf16_operand(tc.deq_w8(qd, sd)), tc.bf16_operand(tc.deq_w8(qu, su))
+
+    def mix_mm():
+        di = tc.gemv(xd, wd)
+        gl = tc.gemv(tc.scaled_silu(di, LR, HC), wu)
+        return tc.gate_mean(xd, gl, HC)
+    down_b, up_b = mixer_bytes(M, ND, LR, HC, H, 4)
+    row("D_hc_mix_one_call_97_layers_M3_f32s", (down_b + up_b) * 97, lambda: tc.mixer(xd, qd, sd, qu, su, LR, HC),
+        mix_mm, scale=97.0, note="one mixer timed, times 97")
+    # E: the INT2 coarse pass on an 8,192-row slice of the head, scaled to 248,320 rows
+    V, NS = 248320, 8192
+    P2, S2 = (t.cpu() for t in F.quantize_int2(dev_w(NS, K), group=16))
+    wop = tc.bf16_operand(tc.deq_int2(P2, S2))
+    row("E_int2_coarse_248320x2560_M3", V * K // 4 + V * (K // 16) * 2 + M * K * 2 + M * V * 2,
+        lambda: tc.int2_logits(x, P2, S2, torch.bfloat16), lambda: tc.gemv(x, wop), scale=V / NS,
+        note=f"{NS} of {V} rows timed, times {V / NS:.2f}")
+    del wop
+    res = {"value": rows["B_w8_gates_48_layers_M3"]["GBps_with_dequant"], "unit": "GB/s", "cores": threads,
+           "kind": "port",
+           "sample": f"48 router gates [512x2560] int8 g64 (fp16 scales) at M=3 as PyTorch CPU ops: dequant, bf16 "
+                     f"operand rounding, fp32 matmul, fp32 logits; median of {reps} passes after 3 warm-ups on "
+                     f"{threads} host threads",
+           "cpu_model": tc.cpu_model(), "torch_version": torch.__version__, "per_config": rows}
+    if head is not None:
+        res["fast_head_parity"] = head_parity(F, torch, dev, head, parity_batches)
+    return res
+
+
+def head_parity(F, torch, dev, head, batches):
+    """The fast head (int2_topk + refine_mx8_, the production calls) on
+    `batches` seeded M = 3 batches at full size, against the oracle's fast head
+    (exact coarse sums rounded to fp32 then bf16, the total-order top-512, the
+    rescore's fma order): the share of rows whose top-512 set is identical,
+    and of rows whose argmax is."""
     import numpy as np
-    from oracle import gemv as og, quant as oq, formats as fm
-    cores = len(os.sched_getaffinity(0))
-    rng = np.random.default_rng(0)
-    layers = [oq.quantize_w8((rng.standard_normal((512, 2560)) * 0.02).astype(np.float32)) for _ in range(48)]
-    layers = [(q, s.astype(np.float16).astype(np.float32)) for q, s in layers]     # fp16 scale values
-    x = fm.round_bf16(rng.standard_normal((3, 2560)).astype(np.float32))
-    passes, t0 = 0, time.perf_counter()
-    while True:
-        for q, s in layers:
-            og.w8_linear(x, q, s, "f32")
-        passes += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = (time.perf_counter() - t0) / passes
-    nbytes = gate_bytes(48, 3, 512, 2560)
-    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "ms_per_step": round(dt * 1e3, 2),
-            "sample": f"{passes} passes of 48 router gates [512x2560] int8 g64 at M=3 (numpy dequant, bf16 "
-                      f"operand rounding, fp32 matmul; {cores} host threads)"}
+    from oracle import formats as fm
+    from oracle import head as oh
+    q, s, P, S = head
+    V, K, C, M = P.shape[0], P.shape[1] * 4, 512, 3
+    xs, sel, outs = [], [], []
+    for b in range(batches):
+        gx = torch.Generator(device=dev).manual_seed(5000 + b)
+        x = torch.randn((M, K), generator=gx, device=dev).to(torch.bfloat16)
+        co, ix = F.int2_topk(x, P, S, V, C)
+        out = F.refine_mx8_(co, x, ix, q, s)
+        xs.append(x.view(torch.int16).cpu().numpy().view(np.uint16))
+        sel.append(ix.cpu().numpy())
+        outs.append(out.view(torch.int16).cpu().numpy().view(np.uint16))
+    xb, sel, outs = np.concatenate(xs), np.concatenate(sel), np.concatenate(outs)
+    Pn, Sn, qn, sn = P.cpu().numpy(), S.cpu().numpy(), q.view(torch.uint8).cpu().numpy(), s.cpu().numpy()
+    import _fp4x
+    o_coarse, o_idx, o_out = oh.fast_head(xb, Pn, Sn, 16, qn, sn, C, _fp4x.layout(_fp4x.FMT_MX8, K)[0])
+    same_set = float(np.mean([set(a) == set(b) for a, b in zip(sel.tolist(), o_idx.tolist())]))
+    am = np.argmax(fm.bf16_to_f32(outs), -1)
+    am_o = np.argmax(fm.bf16_to_f32(o_out), -1)
+    return {"rows": int(xb.shape[0]), "top512_set_identity_vs_oracle": round(same_set, 4),
+            "argmax_agreement_vs_oracle": round(float(np.mean(am == am_o)), 4)}
 
 
 # ------------------------------------------------------------------ main
@@ -419,8 +649,9 @@ def main():
         bench_hc(F, torch, dev, kernels)
         torch.cuda.empty_cache()
         done("D")
+    head = None
     if "E" in sel:
-        bench_head(F, torch, dev, kernels)
+        head = bench_head(F, torch, dev, kernels)
         torch.cuda.empty_cache()
         done("E")
     if "F" in sel:
@@ -432,6 +663,11 @@ def main():
         torch.cuda.empty_cache()
         done("G")
 
+    ceil = {}
+    if not args.no_ceiling:
+        ceil = bench_read_ceiling(F, torch, dev, ceiling_sizes(kernels))
+        attach_ceilings(kernels, ceil)
+        done("read ceilings")
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic_gates48_M3.json")
     if os.path.exists(tf):
@@ -456,9 +692,12 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / PEAK_GBS, 4), "traffic": traffic},
         "kernels": kernels,
+        "read_ceiling": {f"{nb / 1e6:.2f}MB": {"us": round(c[0], 3), "GBps": round(nb / c[0] / 1e3, 1),
+                                                "shape": c[1]} for nb, c in sorted(ceil.items())},
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(F, torch, dev, head)
+        done("cpu baseline")
     print(json.dumps(line), flush=True)
 
 

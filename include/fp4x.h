@@ -255,6 +255,13 @@ int fp4x_dequant_bf16(int fmt, const void* w0, const void* w1, const void* s, in
 /* fp32 MXFP8 dequant, out [N, K].  [mx8_dequant, x/fp4x_kernels.py:261-267] */
 int fp4x_mx8_dequant(const void* w, const void* s, int N, int K, float* out, void* stream);
 
+/* A plain coalesced read of `bytes` (a multiple of 16, src 16-byte aligned)
+ * with `unroll` (2, 4, 8 or 16) 16-byte loads in flight per thread over
+ * wgs_per_cu (1..32) workgroups of 256 threads per CU; *sink is written only
+ * if the data fold to one particular word.  No counterpart in the reference:
+ * the benchmark's measured ceiling of a one-shot read of a GEMV's bytes. */
+int fp4x_read_ceiling(const void* src, int64_t bytes, int unroll, int wgs_per_cu, uint32_t* sink, void* stream);
+
 /* Re-read the path switches from the environment (they are read once, when
  * first needed, never per launch): FP4X_W8_STREAM, FP4X_INT2_STREAM,
  * FP4X_NV4_STREAM, FP4X_W6_STREAM, FP4X_MX8_STREAM and FP4X_HC_MIX ("0"
