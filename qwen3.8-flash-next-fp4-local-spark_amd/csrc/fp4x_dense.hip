@@ -1,6 +1,7 @@
 // Dense decode GEMVs (MXFP8, W8 g64, W6 g32, NVFP4, INT2 coarse head), the
 // layer-batched W8 launch, and the dequant kernels, behind a C ABI.
 #include "fp4x_mfma.h"
+#include "fp4x_rows.h"
 #include "../../include/fp4x.h"
 #include <cstdio>
 #include <cstdlib>
@@ -66,6 +67,7 @@ void reload_switches() {
   w.w6_stream = on("FP4X_W6_STREAM");
   w.mx8_stream = on("FP4X_MX8_STREAM");
   w.hc_mix = on("FP4X_HC_MIX");
+  w.rows = on("FP4X_ROWS");
   const char* e = getenv("FP4X_WAVES_PER_CU");
   const int v = e ? atoi(e) : 0;
   w.waves_per_cu = v >= 1 && v <= 64 ? v : 0;
@@ -196,6 +198,7 @@ int fp4x_mx8_linear(const void* x, int64_t x_stride, const void* w, const void* 
   p.pa.w0 = static_cast<const uint8_t*>(w);
   p.pa.s = static_cast<const uint8_t*>(s);
   if (launch_mx8_stream_entry(p, (hipStream_t)stream)) return check_launch("mx8_stream");   // many tiles
+  if (launch_rows_gemv<FmtMX8>(p, 1, (hipStream_t)stream)) return check_launch("mx8_rows");  // few rows
   return launch_gemv_mfma<FmtMX8, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
@@ -207,6 +210,7 @@ int fp4x_bf16_linear(const void* x, int64_t x_stride, const void* w, void* out, 
   if (M == 0 || N == 0) return FP4X_OK;
   GemvLaunch p = base_launch(FP4X_FMT_BF16, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
   p.pa.w0 = static_cast<const uint8_t*>(w);
+  if (launch_rows_gemv<FmtBF16>(p, 1, (hipStream_t)stream)) return check_launch("bf16_rows");
   return launch_gemv_mfma<FmtBF16, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
@@ -237,10 +241,12 @@ int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, co
   if (fmt == FP4X_FMT_W8_F16) {
     if (launch_w8_stream<true>(p, layers, st)) return check_launch("w8_stream");
     if (layers == 1 && launch_w8_ktile<true, EpiStore>(p, st)) return check_launch("w8_ktile");
+    if (launch_rows_gemv<FmtW8<true>>(p, layers, st)) return check_launch("w8_rows");   // few rows (a router gate)
     return launch_gemv_mfma<FmtW8<true>, EpiStore>(p, layers, st);
   }
   if (launch_w8_stream<false>(p, layers, st)) return check_launch("w8_stream");
   if (layers == 1 && launch_w8_ktile<false, EpiStore>(p, st)) return check_launch("w8_ktile");
+  if (launch_rows_gemv<FmtW8<false>>(p, layers, st)) return check_launch("w8_rows");
   return launch_gemv_mfma<FmtW8<false>, EpiStore>(p, layers, st);
 }
 
@@ -261,6 +267,7 @@ int fp4x_w6_linear(const void* x, int64_t x_stride, const void* L, const void* H
   p.pa.w1 = static_cast<const uint8_t*>(H);
   p.pa.s = static_cast<const uint8_t*>(S);
   if (launch_w6_stream_entry(p, (hipStream_t)stream)) return check_launch("w6_stream");     // many tiles
+  if (launch_rows_gemv<FmtW6>(p, 1, (hipStream_t)stream)) return check_launch("w6_rows");    // few rows
   return launch_gemv_mfma<FmtW6, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
@@ -275,6 +282,7 @@ int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* 
   p.pa.s = static_cast<const uint8_t*>(S);
   p.gs = gs;
   if (launch_nv4_stream_entry(p, (hipStream_t)stream)) return check_launch("nv4_stream");   // many tiles
+  if (launch_rows_gemv<FmtNV4>(p, 1, (hipStream_t)stream)) return check_launch("nv4_rows");  // few rows
   return launch_gemv_mfma<FmtNV4, EpiStore>(p, 1, (hipStream_t)stream);
 }
 

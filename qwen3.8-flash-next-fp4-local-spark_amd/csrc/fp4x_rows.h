@@ -1,0 +1,320 @@
+// Few-rows GEMV: matrices of so few rows that 16-row tiles would leave most
+// CUs idle (a router gate's 512 x 2560 is 32 tiles on 256 CUs).  A
+// workgroup owns whole weight rows, so no row's sum spans two workgroups: no
+// cross-workgroup reduction, no scratch, no tickets.  Each kernel takes a
+// compact argument block read in one round of scalar loads at its start, and
+// issues every memory load before using any, so a lane waits for one memory
+// round trip.  Two kernels:
+//
+//   * M <= 4 (rows_fma_kernel): one weight row per workgroup, thread c
+//     owning chunk c (the format's 16-byte unit of the main plane, with its
+//     scale), dequantized to the bf16 operand and multiplied with the M
+//     activation rows by fp32 fma (each product exact, one rounding per
+//     step).  Each wave sums its partials with DPP steps, lane 63 stores the
+//     wave's sums, and thread m adds the waves' sums in wave order.
+//   * 4 < M <= 16 (rows_mfma_kernel): R <= 4 weight rows per workgroup,
+//     products on v_mfma_f32_4x4x4bf16_1k: 16 independent blocks of
+//     D[4 x 4] += A[4 x 4] B[4 x 4].  Lane 4b + q of a wave holds, for block
+//     b, A row q (activation row m = 4g + q over 4 consecutive k) and B column
+//     q (weight row q over the same 4 k); D[m][q] lands in lane 4b + q,
+//     element m.  Each lane dequantizes CPL chunks of one weight row and feeds
+//     the bf16 pairs and the bf16 activations to the MFMA as they are; two DPP
+//     row rotations add the 4 blocks of each 16-lane row, and thread (q, m)
+//     adds the rows' sums of every wave in a fixed order.
+//
+// Both orders are fixed, so results repeat bit for bit.  At M <= 4 the fma
+// kernel's extra VALU work costs less than the MFMA kernel's 4-lane
+// replication of every chunk's loads (measured on the 512 x 2560 gate:
+// 3.0 against 3.4 us at M = 1); at M = 16 the MFMA kernel is faster
+// (5.6 against 6.8 us).
+#pragma once
+#include "fp4x_mfma.h"
+
+namespace fp4x {
+
+// The few-rows kernels' arguments: only what they read, 80 bytes.
+struct RowsLaunch {
+  PlaneArgs pa;
+  const uint16_t* x;     // bf16 activations [M][x_stride]
+  void* out;             // [M][out_stride]
+  int x_stride, out_stride;
+  int N, M, R, out_dtype;
+  float gs;              // applied to every sum (NVFP4 global scale; 1 otherwise)
+};
+
+// ------------------------------------------------------------------ M <= 4
+
+constexpr int kRowsFmaMaxThreads = 256;              // K up to 256 chunks (4096 int8, 8192 NVFP4 weights)
+
+// Sum over each row of 16 lanes, every lane of the row receiving it: DPP
+// xor-partner additions with partners 1, 2 (quad permutes), 4 (half-row
+// mirror, within the already uniform quads) and 8 (row mirror).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
+  return v;
+}
+
+// Wave sum, complete in lane 63: the four row sums s0..s3 of row16_sum added
+// as (s3 + s2) + (s1 + s0) by two DPP broadcasts (row_bcast:15 adds each
+// even row's sum into the next row, row_bcast:31 adds row 1 into rows 2
+// and 3; rows outside the row mask add the +0 of `old`).
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+  v = row16_sum(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));  // row_bcast:15
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));  // row_bcast:31
+  return v;
+}
+
+template <class F, int MT>
+__global__ __launch_bounds__(kRowsFmaMaxThreads) void rows_fma_kernel(RowsLaunch p) {
+  extern __shared__ float red[];                       // [waves][MT]
+  // every argument read up front (the empty asm needs each value in a
+  // register), so no scalar load waits between the main loads and the store
+  const PlaneArgs pa = p.pa;
+  const uint16_t* const xg = p.x;
+  void* const out = p.out;
+  const int xs = p.x_stride, os = p.out_stride, N = p.N, M = p.M, odt = p.out_dtype;
+  const float gs = p.gs;
+  asm volatile("" ::"s"(pa.w0), "s"(pa.w1), "s"(pa.s), "s"(pa.K), "s"(pa.G), "s"(xg), "s"(out), "s"(xs), "s"(os),
+               "s"(N), "s"(M), "s"(odt), "s"(gs));
+  const int nch = pa.K / F::KPC;
+  const int c = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  // Lanes past the row's chunks load the last chunk (their sums are zeroed
+  // below); loads under a branch would each be waited for at its join.
+  const int cc = c < nch ? c : nch - 1;
+  const typename F::Chunk ch = F::load(pa, row, cc);
+  uint4 xr[F::SUB][MT][2];
+#pragma unroll
+  for (int sub = 0; sub < F::SUB; ++sub)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const uint4* xp = reinterpret_cast<const uint4*>(xg + (int64_t)m * xs + cc * F::KPC + sub * 16);
+      xr[sub][m][0] = xp[0];
+      xr[sub][m][1] = xp[1];
+    }
+  __builtin_amdgcn_sched_barrier(0);                   // every load above issues before any use below
+  float acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+#pragma unroll
+  for (int sub = 0; sub < F::SUB; ++sub) {
+    uint32_t w[8];
+    F::deq16(ch, sub, w);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const uint4 xa = xr[sub][m][0], xb = xr[sub][m][1];
+      const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+      float t = acc[m];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        t = __builtin_fmaf(bf16_lo(w[i]), bf16_lo(xv[i]), t);
+        t = __builtin_fmaf(bf16_hi(w[i]), bf16_hi(xv[i]), t);
+      }
+      acc[m] = t;
+    }
+  }
+  if (c >= nch) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nwaves = (nch + 63) >> 6;
+  float sums[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) sums[m] = wave_sum_lane63(acc[m]);
+  if (lane == 63) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) red[wave * MT + m] = sums[m];
+  }
+  __syncthreads();
+  const int m = threadIdx.x;
+  if (m < MT) {
+    float v = red[m];
+    for (int j = 1; j < nwaves; ++j) v += red[j * MT + m];
+    store_out(out, (int64_t)m * os + row, odt, v * gs);
+  }
+}
+
+// ------------------------------------------------------------------ 4 < M <= 16
+
+typedef short rows_s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma4(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4_t c) {
+  const uint2 a = make_uint2(a0, a1), b = make_uint2(b0, b1);
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(rows_s16x4, a), __builtin_bit_cast(rows_s16x4, b),
+                                                c, 0, 0, 0);
+}
+
+// v + the same lane's value 4 and then 8 lanes round its row of 16 (DPP
+// row_ror): every lane ends with the sum over the 4 blocks of its row for
+// its column q = lane % 4.
+__device__ __forceinline__ float row_blocks_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+  return v;
+}
+
+// MG groups of 4 activation rows (M <= 4 MG); CPL chunks per lane.
+template <class F, int MG, int CPL>
+__global__ __launch_bounds__(512) void rows_mfma_kernel(RowsLaunch p) {
+  extern __shared__ float red[];                       // [waves * 4 rows][4 MG][4]
+  // every argument read up front (the empty asm needs each value in a
+  // register), so no scalar load waits between the main loads and the store
+  const PlaneArgs pa = p.pa;
+  const uint16_t* const xg = p.x;
+  void* const out = p.out;
+  const int xs = p.x_stride, os = p.out_stride, N = p.N, M = p.M, R = p.R, odt = p.out_dtype;
+  const float gs = p.gs;
+  asm volatile("" ::"s"(pa.w0), "s"(pa.w1), "s"(pa.s), "s"(pa.K), "s"(pa.G), "s"(xg), "s"(out), "s"(xs), "s"(os),
+               "s"(N), "s"(M), "s"(R), "s"(odt), "s"(gs));
+  const int nch = pa.K / F::KPC;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane & 3;
+  const int64_t row0 = (int64_t)blockIdx.x * R;
+  // Every load goes out unconditionally, before any is used, so a lane waits
+  // for one memory round trip: columns q >= R load row R - 1 (the same
+  // lines as column R - 1, so no extra traffic; never stored), rows past N
+  // load row N - 1, activation rows past M load row 0 (never stored), and
+  // chunks past the row's end load its last chunk (their B operand is zeroed
+  // below).  Lane chunk t of wave w is chunk (CPL w + t) 16 + block: each
+  // load instruction reads 16 consecutive chunks of every row.
+  int64_t wr = row0 + (q < R ? q : R - 1);
+  if (wr >= N) wr = N - 1;
+  typename F::Chunk ch[CPL];
+  uint4 xr[CPL][MG][F::SUB][2];
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const int c = (wave * CPL + t) * 16 + (lane >> 2);
+    const int cc = c < nch ? c : nch - 1;
+    ch[t] = F::load(pa, wr, cc);
+#pragma unroll
+    for (int g = 0; g < MG; ++g) {
+      const int m = 4 * g + q;
+      const uint4* xp = reinterpret_cast<const uint4*>(xg + (int64_t)(m < M ? m : 0) * xs + cc * F::KPC);
+#pragma unroll
+      for (int sub = 0; sub < F::SUB; ++sub) {
+        xr[t][g][sub][0] = xp[2 * sub];
+        xr[t][g][sub][1] = xp[2 * sub + 1];
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);                   // every load above issues before any use below
+  f32x4_t acc[MG];
+#pragma unroll
+  for (int g = 0; g < MG; ++g) acc[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const bool live = (wave * CPL + t) * 16 + (lane >> 2) < nch;
+#pragma unroll
+    for (int sub = 0; sub < F::SUB; ++sub) {
+      uint32_t w[8];
+      F::deq16(ch[t], sub, w);
+      if (!live) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = 0u;
+      }
+#pragma unroll
+      for (int g = 0; g < MG; ++g) {
+        const uint4 xa = xr[t][g][sub][0], xb = xr[t][g][sub][1];
+        acc[g] = mfma4(xa.x, xa.y, w[0], w[1], acc[g]);
+        acc[g] = mfma4(xa.z, xa.w, w[2], w[3], acc[g]);
+        acc[g] = mfma4(xb.x, xb.y, w[4], w[5], acc[g]);
+        acc[g] = mfma4(xb.z, xb.w, w[6], w[7], acc[g]);
+      }
+    }
+  }
+  // block sums per 16-lane row, stored by lanes 0-3 of the row as
+  // red[wave * 4 + row][m][q]
+  const int slot = wave * 4 + (lane >> 4);
+#pragma unroll
+  for (int g = 0; g < MG; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v = row_blocks_sum(acc[g][e]);
+      if ((lane & 12) == 0) red[(slot * (4 * MG) + 4 * g + e) * 4 + q] = v;
+    }
+  __syncthreads();
+  const int o = threadIdx.x;
+  if (o < R * M) {
+    const int j = o / M, m = o % M;
+    const int nslots = (blockDim.x >> 6) * 4;
+    float v = red[m * 4 + j];
+    for (int s2 = 1; s2 < nslots; ++s2) v += red[(s2 * (4 * MG) + m) * 4 + j];
+    const int64_t row = row0 + j;
+    if (row < N) store_out(out, (int64_t)m * os + row, odt, v * gs);
+  }
+}
+
+// Chunks per lane for a row of nch chunks and MG activation groups: about 5
+// waves a workgroup (fewer chunks per lane leave more fixed cost per chunk,
+// more leave longer waits on each wave's slowest load), within the registers
+// that hold every activation load of a lane (CPL MG SUB <= 8).
+template <class F>
+inline int rows_cpl(int nch, int MG) {
+  int cpl = (nch + 79) / 80;
+  while (cpl > 1 && cpl * MG * F::SUB > 8) --cpl;
+  return cpl;
+}
+
+// Launch a few-rows kernel when the call fits one: one matrix, no split-K,
+// no per-row scale, strides within int32, the 16-row tiles of the MFMA core
+// filling under half of the CUs, and (M <= 4) at most 256 chunks per row or
+// (M > 4) at most 8 waves of chunks; false (nothing launched) otherwise, or
+// when FP4X_ROWS=0.
+template <class F>
+bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
+  if (!switches().rows || batch != 1 || p.ksplit != 1 || p.M < 1 || p.M > 16 || p.rs) return false;
+  if (p.x_stride > INT32_MAX || p.out_stride > INT32_MAX) return false;
+  const int cus = device_cus();
+  const int tiles = (p.N + 15) / 16;
+  if (tiles * 2 >= cus || p.pa.K % F::KPC) return false;
+  const int nch = p.pa.K / F::KPC;
+  if (nch < 1) return false;
+  RowsLaunch a;
+  a.pa = p.pa;
+  a.x = p.x;
+  a.out = p.out;
+  a.x_stride = (int)p.x_stride;
+  a.out_stride = (int)p.out_stride;
+  a.N = p.N;
+  a.M = p.M;
+  a.out_dtype = p.out_dtype;
+  a.gs = p.gs;
+  if (p.M <= 4) {
+    const int threads = (nch + 63) / 64 * 64;
+    if (threads > kRowsFmaMaxThreads) return false;
+    a.R = 1;
+    const size_t lds = (size_t)(threads / 64) * p.M * sizeof(float);
+    const dim3 grid((unsigned)p.N), block((unsigned)threads);
+    switch (p.M) {
+      case 1: hipLaunchKernelGGL((rows_fma_kernel<F, 1>), grid, block, lds, st, a); return true;
+      case 2: hipLaunchKernelGGL((rows_fma_kernel<F, 2>), grid, block, lds, st, a); return true;
+      case 3: hipLaunchKernelGGL((rows_fma_kernel<F, 3>), grid, block, lds, st, a); return true;
+      case 4: hipLaunchKernelGGL((rows_fma_kernel<F, 4>), grid, block, lds, st, a); return true;
+    }
+    return false;
+  }
+  // rows per workgroup: the fewest that keep the grid within the CUs
+  a.R = p.N <= cus ? 1 : p.N <= 2 * cus ? 2 : p.N <= 3 * cus ? 3 : 4;
+  const int MG = p.M <= 8 ? 2 : 4;
+  const int cpl = rows_cpl<F>(nch, MG);
+  const int waves = (nch + 16 * cpl - 1) / (16 * cpl);
+  if (waves > 8) return false;
+  const size_t lds = (size_t)waves * 4 * (4 * MG) * 4 * sizeof(float);
+  const dim3 grid((unsigned)((p.N + a.R - 1) / a.R)), block((unsigned)(64 * waves));
+#define FP4X_ROWS_CASE(G, C)                                                                         \
+  if (MG == G && cpl == C) {                                                                         \
+    hipLaunchKernelGGL((rows_mfma_kernel<F, G, C>), grid, block, lds, st, a);                        \
+    return true;                                                                                     \
+  }
+  FP4X_ROWS_CASE(2, 1) FP4X_ROWS_CASE(2, 2) FP4X_ROWS_CASE(2, 3) FP4X_ROWS_CASE(2, 4)
+  FP4X_ROWS_CASE(4, 1) FP4X_ROWS_CASE(4, 2)
+#undef FP4X_ROWS_CASE
+  return false;
+}
+
+}  // namespace fp4x

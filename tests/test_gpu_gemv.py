@@ -150,6 +150,41 @@ def test_gemv_parity(gpu, F, fmt, M):
     print(f"{fmt} M={M}: max |y - exact| / bound = {(np.abs(y32 - exact) / bound).max():.3g}")
 
 
+@pytest.mark.parametrize("fmt", ["mx8", "w8", "w8_f16", "w6", "nv4", "bf16"])
+@pytest.mark.parametrize("N,M", [(512, 3), (512, 1), (512, 16), (96, 3), (1000, 4), (480, 8), (1024, 4), (200, 16)])
+def test_rows_gemv(gpu, F, fmt, N, M, monkeypatch):
+    """Matrices whose 16-row tiles fill under half of the CUs (a router gate's
+    512 x 2560) take the few-rows kernel (R rows per workgroup, one chunk per
+    thread): fp32 sums within the accumulation bound of the exact sums, equal
+    to the MFMA core's (FP4X_ROWS=0) within the two bounds, repeated calls bit
+    for bit, bf16 outputs the same sums rounded."""
+    rng = np.random.default_rng(4000 + N + M)
+    k = 2560
+    base = "w8" if fmt == "w8_f16" else fmt
+    planes, w_op, gs = prep(base, rng, N, k)
+    if fmt == "w8_f16":
+        q, s = planes
+        s16 = s.half()
+        planes = (q, s16)
+        w_op = og.operand("w8", q.cpu().numpy(), s16.float().cpu().numpy())
+    x, _ = act(rng, M, k)
+    xd = bf16_dev(x)
+    y = to_f32(run(F, base, xd, planes, 1, torch.float32))
+    with path_switch(monkeypatch, "FP4X_ROWS"):
+        y_core = to_f32(run(F, base, xd, planes, 1, torch.float32))
+    if N * M >= 500:
+        assert not np.array_equal(y.view(np.uint32), y_core.view(np.uint32)), "few-rows kernel not taken"
+    exact = ordered.exact_sum(x, w_op) * gs
+    bound = ordered.mfma_bound(x, w_op) * abs(gs)
+    for got in (y, y_core):
+        assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
+    assert_tol(y, og.matmul_f32(x, w_op) * np.float32(gs), what=f"{fmt} rows N={N} M={M}")
+    y2 = to_f32(run(F, base, xd, planes, 1, torch.float32))
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    yb = run(F, base, xd, planes, 1)
+    assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
+
+
 @pytest.mark.parametrize("fmt", ["mx8", "w8", "w6", "nv4"])
 @pytest.mark.parametrize("ks", [2, 4, 5])
 def test_gemv_split_k(gpu, F, fmt, ks):
