@@ -236,6 +236,7 @@ int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, co
   // long runs of tiles (layer-batched gates) stream through LDS; split-K calls of
   // few tiles spread each tile's K over several workgroups (or over the waves
   // of one workgroup), the mixer's down projection taking the same path; other
+  // matrices of few rows (a router gate) take the few-rows kernels; other
   // shapes use the MFMA core
   hipStream_t st = (hipStream_t)stream;
   if (fmt == FP4X_FMT_W8_F16) {

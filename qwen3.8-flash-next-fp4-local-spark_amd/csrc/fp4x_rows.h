@@ -158,10 +158,122 @@ __device__ __forceinline__ float row_blocks_sum(float v) {
   return v;
 }
 
-// MG groups of 4 activation rows (M <= 4 MG); CPL chunks per lane.
+// The MFMA few-rows decomposition of rows of nch chunks at M activation
+// rows: MG groups of 4 activation rows, CPL chunks per lane, `waves` waves.
+// CPL aims at about 5 waves (fewer chunks per lane leave more fixed cost per
+// chunk, more leave longer waits on each wave's slowest load), within the
+// registers that hold every activation load of a lane (CPL MG SUB <= 16).
+struct RowsPlan {
+  int MG, cpl, waves;
+};
+
+template <class F>
+inline bool rows_mfma_plan(int nch, int M, RowsPlan& pl) {
+  if (nch < 1 || M < 1 || M > 16) return false;
+  pl.MG = M <= 4 ? 1 : M <= 8 ? 2 : 4;
+  int cpl = (nch + 79) / 80;
+  while (cpl > 1 && cpl * pl.MG * F::SUB > 16) --cpl;
+  if (cpl > 8) cpl = 8;
+  pl.cpl = cpl;
+  pl.waves = (nch + 16 * cpl - 1) / (16 * cpl);
+  return pl.waves <= 8;
+}
+
+// One workgroup's R <= 4 rows [row0, row0 + R) of the MFMA few-rows GEMV
+// (MG groups of 4 activation rows, CPL chunks per lane) on its first `waves`
+// waves; the other waves only meet the barrier.  store(m, row, v) receives
+// every sum of a row below N.  red: LDS of waves * 4 * 4 MG * 4 floats.
+template <class F, int MG, int CPL, class Store>
+__device__ __forceinline__ void rows_mfma_item(const PlaneArgs& pa, const uint16_t* xg, int xs, int N, int M, int R,
+                                               int64_t row0, int waves, float* red, Store store) {
+  const int nch = pa.K / F::KPC;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane & 3;
+  if (wave < waves) {
+    // Every load goes out unconditionally, before any is used, so a lane
+    // waits for one memory round trip: columns q >= R load row R - 1 (the
+    // same lines as column R - 1, so no extra traffic; never stored), rows
+    // past N load row N - 1, activation rows past M load row 0 (never
+    // stored), and chunks past the row's end load its last chunk (their B
+    // operand is zeroed below).  Lane chunk t of wave w is chunk
+    // (CPL w + t) 16 + block: each load instruction reads 16 consecutive
+    // chunks of every row.
+    int64_t wr = row0 + (q < R ? q : R - 1);
+    if (wr >= N) wr = N - 1;
+    typename F::Chunk ch[CPL];
+    uint4 xr[CPL][MG][F::SUB][2];
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) {
+      const int c = (wave * CPL + t) * 16 + (lane >> 2);
+      const int cc = c < nch ? c : nch - 1;
+      ch[t] = F::load(pa, wr, cc);
+#pragma unroll
+      for (int g = 0; g < MG; ++g) {
+        const int m = 4 * g + q;
+        const uint4* xp = reinterpret_cast<const uint4*>(xg + (int64_t)(m < M ? m : 0) * xs + cc * F::KPC);
+#pragma unroll
+        for (int sub = 0; sub < F::SUB; ++sub) {
+          xr[t][g][sub][0] = xp[2 * sub];
+          xr[t][g][sub][1] = xp[2 * sub + 1];
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);                 // every load above issues before any use below
+    f32x4_t acc[MG];
+#pragma unroll
+    for (int g = 0; g < MG; ++g) acc[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) {
+      const bool live = (wave * CPL + t) * 16 + (lane >> 2) < nch;
+#pragma unroll
+      for (int sub = 0; sub < F::SUB; ++sub) {
+        uint32_t w[8];
+        F::deq16(ch[t], sub, w);
+        if (!live) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) w[i] = 0u;
+        }
+#pragma unroll
+        for (int g = 0; g < MG; ++g) {
+          const uint4 xa = xr[t][g][sub][0], xb = xr[t][g][sub][1];
+          acc[g] = mfma4(xa.x, xa.y, w[0], w[1], acc[g]);
+          acc[g] = mfma4(xa.z, xa.w, w[2], w[3], acc[g]);
+          acc[g] = mfma4(xb.x, xb.y, w[4], w[5], acc[g]);
+          acc[g] = mfma4(xb.z, xb.w, w[6], w[7], acc[g]);
+        }
+      }
+    }
+    // block sums per 16-lane row, stored by lanes 0-3 of the row as
+    // red[wave * 4 + row][m][q]
+    const int slot = wave * 4 + (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < MG; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = row_blocks_sum(acc[g][e]);
+        if ((lane & 12) == 0) red[(slot * (4 * MG) + 4 * g + e) * 4 + q] = v;
+      }
+  }
+  __syncthreads();
+  const int o = threadIdx.x;
+  if (o < R * M) {
+    const int j = o / M, m = o % M;
+    // every row sum read at once (slots past the workgroup's waves read slot
+    // 0 and add nothing), then added in slot order
+    float t[32];
+#pragma unroll
+    for (int s2 = 0; s2 < 32; ++s2) t[s2] = red[((s2 < waves * 4 ? s2 : 0) * (4 * MG) + m) * 4 + j];
+    float v = t[0];
+#pragma unroll
+    for (int s2 = 1; s2 < 32; ++s2) v += s2 < waves * 4 ? t[s2] : 0.0f;
+    const int64_t row = row0 + j;
+    if (row < N) store(m, row, v);
+  }
+}
+
 template <class F, int MG, int CPL>
 __global__ __launch_bounds__(512) void rows_mfma_kernel(RowsLaunch p) {
-  extern __shared__ float red[];                       // [waves * 4 rows][4 MG][4]
+  extern __shared__ float red[];
   // every argument read up front (the empty asm needs each value in a
   // register), so no scalar load waits between the main loads and the store
   const PlaneArgs pa = p.pa;
@@ -171,109 +283,75 @@ __global__ __launch_bounds__(512) void rows_mfma_kernel(RowsLaunch p) {
   const float gs = p.gs;
   asm volatile("" ::"s"(pa.w0), "s"(pa.w1), "s"(pa.s), "s"(pa.K), "s"(pa.G), "s"(xg), "s"(out), "s"(xs), "s"(os),
                "s"(N), "s"(M), "s"(R), "s"(odt), "s"(gs));
-  const int nch = pa.K / F::KPC;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int q = lane & 3;
-  const int64_t row0 = (int64_t)blockIdx.x * R;
-  // Every load goes out unconditionally, before any is used, so a lane waits
-  // for one memory round trip: columns q >= R load row R - 1 (the same
-  // lines as column R - 1, so no extra traffic; never stored), rows past N
-  // load row N - 1, activation rows past M load row 0 (never stored), and
-  // chunks past the row's end load its last chunk (their B operand is zeroed
-  // below).  Lane chunk t of wave w is chunk (CPL w + t) 16 + block: each
-  // load instruction reads 16 consecutive chunks of every row.
-  int64_t wr = row0 + (q < R ? q : R - 1);
-  if (wr >= N) wr = N - 1;
-  typename F::Chunk ch[CPL];
-  uint4 xr[CPL][MG][F::SUB][2];
-#pragma unroll
-  for (int t = 0; t < CPL; ++t) {
-    const int c = (wave * CPL + t) * 16 + (lane >> 2);
-    const int cc = c < nch ? c : nch - 1;
-    ch[t] = F::load(pa, wr, cc);
-#pragma unroll
-    for (int g = 0; g < MG; ++g) {
-      const int m = 4 * g + q;
-      const uint4* xp = reinterpret_cast<const uint4*>(xg + (int64_t)(m < M ? m : 0) * xs + cc * F::KPC);
-#pragma unroll
-      for (int sub = 0; sub < F::SUB; ++sub) {
-        xr[t][g][sub][0] = xp[2 * sub];
-        xr[t][g][sub][1] = xp[2 * sub + 1];
-      }
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);                   // every load above issues before any use below
-  f32x4_t acc[MG];
-#pragma unroll
-  for (int g = 0; g < MG; ++g) acc[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int t = 0; t < CPL; ++t) {
-    const bool live = (wave * CPL + t) * 16 + (lane >> 2) < nch;
-#pragma unroll
-    for (int sub = 0; sub < F::SUB; ++sub) {
-      uint32_t w[8];
-      F::deq16(ch[t], sub, w);
-      if (!live) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = 0u;
-      }
-#pragma unroll
-      for (int g = 0; g < MG; ++g) {
-        const uint4 xa = xr[t][g][sub][0], xb = xr[t][g][sub][1];
-        acc[g] = mfma4(xa.x, xa.y, w[0], w[1], acc[g]);
-        acc[g] = mfma4(xa.z, xa.w, w[2], w[3], acc[g]);
-        acc[g] = mfma4(xb.x, xb.y, w[4], w[5], acc[g]);
-        acc[g] = mfma4(xb.z, xb.w, w[6], w[7], acc[g]);
-      }
-    }
-  }
-  // block sums per 16-lane row, stored by lanes 0-3 of the row as
-  // red[wave * 4 + row][m][q]
-  const int slot = wave * 4 + (lane >> 4);
-#pragma unroll
-  for (int g = 0; g < MG; ++g)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float v = row_blocks_sum(acc[g][e]);
-      if ((lane & 12) == 0) red[(slot * (4 * MG) + 4 * g + e) * 4 + q] = v;
-    }
-  __syncthreads();
-  const int o = threadIdx.x;
-  if (o < R * M) {
-    const int j = o / M, m = o % M;
-    const int nslots = (blockDim.x >> 6) * 4;
-    float v = red[m * 4 + j];
-    for (int s2 = 1; s2 < nslots; ++s2) v += red[(s2 * (4 * MG) + m) * 4 + j];
-    const int64_t row = row0 + j;
-    if (row < N) store_out(out, (int64_t)m * os + row, odt, v * gs);
-  }
+  rows_mfma_item<F, MG, CPL>(pa, xg, xs, N, M, R, (int64_t)blockIdx.x * R, (int)(blockDim.x >> 6), red,
+                             [&](int m, int64_t row, float v) { store_out(out, (int64_t)m * os + row, odt, v * gs); });
 }
 
-// Chunks per lane for a row of nch chunks and MG activation groups: about 5
-// waves a workgroup (fewer chunks per lane leave more fixed cost per chunk,
-// more leave longer waits on each wave's slowest load), within the registers
-// that hold every activation load of a lane (CPL MG SUB <= 8).
+// Rows per workgroup of an MFMA few-rows launch: the fewest (<= 4) that keep
+// the grid within the CUs; 0 when N needs more.
+inline int rows_per_wg(int N, int cus) {
+  for (int r = 1; r <= 4; ++r)
+    if ((N + r - 1) / r <= cus) return r;
+  return 0;
+}
+
+// Launch rows_mfma_item's kernel for plan pl.
+template <class F, int MG, int CPL>
+inline void rows_mfma_launch1(const RowsLaunch& a, const RowsPlan& pl, hipStream_t st) {
+  const size_t lds = (size_t)pl.waves * 4 * (4 * MG) * 4 * sizeof(float);
+  hipLaunchKernelGGL((rows_mfma_kernel<F, MG, CPL>), dim3((unsigned)((a.N + a.R - 1) / a.R)),
+                     dim3((unsigned)(64 * pl.waves)), lds, st, a);
+}
+
+// Dispatch over the (MG, CPL) instances rows_mfma_plan can produce: MG 1
+// with CPL 1..8, MG 2 with 1..8, MG 4 with 1..4 (SUB 1) or 1..2 (SUB 2).
+template <class F, class Body>
+inline bool rows_dispatch(const RowsPlan& pl, Body body) {
+#define FP4X_ROWS_C(G, C)                                        \
+  if constexpr (C * G * F::SUB <= 16) {                          \
+    if (pl.MG == G && pl.cpl == C) {                             \
+      body.template run<G, C>();                                 \
+      return true;                                               \
+    }                                                            \
+  }
+  FP4X_ROWS_C(1, 1) FP4X_ROWS_C(1, 2) FP4X_ROWS_C(1, 3) FP4X_ROWS_C(1, 4)
+  FP4X_ROWS_C(1, 5) FP4X_ROWS_C(1, 6) FP4X_ROWS_C(1, 7) FP4X_ROWS_C(1, 8)
+  FP4X_ROWS_C(2, 1) FP4X_ROWS_C(2, 2) FP4X_ROWS_C(2, 3) FP4X_ROWS_C(2, 4)
+  FP4X_ROWS_C(2, 5) FP4X_ROWS_C(2, 6) FP4X_ROWS_C(2, 7) FP4X_ROWS_C(2, 8)
+  FP4X_ROWS_C(4, 1) FP4X_ROWS_C(4, 2) FP4X_ROWS_C(4, 3) FP4X_ROWS_C(4, 4)
+#undef FP4X_ROWS_C
+  return false;
+}
+
 template <class F>
-inline int rows_cpl(int nch, int MG) {
-  int cpl = (nch + 79) / 80;
-  while (cpl > 1 && cpl * MG * F::SUB > 8) --cpl;
-  return cpl;
+struct RowsGemvBody {
+  const RowsLaunch& a;
+  const RowsPlan& pl;
+  hipStream_t st;
+  template <int G, int C>
+  void run() const { rows_mfma_launch1<F, G, C>(a, pl, st); }
+};
+
+// The few-rows shapes: one matrix of so few rows that the MFMA core's 16-row
+// tiles fill under half of the CUs, at most 4 rows per workgroup.
+inline bool rows_shape_ok(int N, int M, int cus) {
+  const int tiles = (N + 15) / 16;
+  return M >= 1 && M <= 16 && N >= 1 && tiles * 2 < cus && rows_per_wg(N, cus) > 0;
 }
 
-// Launch a few-rows kernel when the call fits one: one matrix, no split-K,
-// no per-row scale, strides within int32, the 16-row tiles of the MFMA core
-// filling under half of the CUs, and (M <= 4) at most 256 chunks per row or
-// (M > 4) at most 8 waves of chunks; false (nothing launched) otherwise, or
-// when FP4X_ROWS=0.
+// Launch a few-rows kernel when the call fits one: one matrix, no per-row
+// scale, strides within int32, a few-rows shape, and (M <= 4, at most 256
+// chunks per row) the fma kernel or else an MFMA plan of at most 8 waves;
+// false (nothing launched) otherwise, or when FP4X_ROWS=0.  The split count
+// of the call is a shape precondition only: these kernels sum each row over
+// its whole K inside one workgroup, in a fixed order.
 template <class F>
 bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
-  if (!switches().rows || batch != 1 || p.ksplit != 1 || p.M < 1 || p.M > 16 || p.rs) return false;
+  if (!switches().rows || batch != 1 || p.rs) return false;
   if (p.x_stride > INT32_MAX || p.out_stride > INT32_MAX) return false;
   const int cus = device_cus();
-  const int tiles = (p.N + 15) / 16;
-  if (tiles * 2 >= cus || p.pa.K % F::KPC) return false;
+  if (!rows_shape_ok(p.N, p.M, cus) || p.pa.K % F::KPC) return false;
   const int nch = p.pa.K / F::KPC;
-  if (nch < 1) return false;
   RowsLaunch a;
   a.pa = p.pa;
   a.x = p.x;
@@ -284,9 +362,8 @@ bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
   a.M = p.M;
   a.out_dtype = p.out_dtype;
   a.gs = p.gs;
-  if (p.M <= 4) {
-    const int threads = (nch + 63) / 64 * 64;
-    if (threads > kRowsFmaMaxThreads) return false;
+  const int threads = (nch + 63) / 64 * 64;
+  if (p.M <= 4 && threads <= kRowsFmaMaxThreads) {
     a.R = 1;
     const size_t lds = (size_t)(threads / 64) * p.M * sizeof(float);
     const dim3 grid((unsigned)p.N), block((unsigned)threads);
@@ -298,23 +375,10 @@ bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
     }
     return false;
   }
-  // rows per workgroup: the fewest that keep the grid within the CUs
-  a.R = p.N <= cus ? 1 : p.N <= 2 * cus ? 2 : p.N <= 3 * cus ? 3 : 4;
-  const int MG = p.M <= 8 ? 2 : 4;
-  const int cpl = rows_cpl<F>(nch, MG);
-  const int waves = (nch + 16 * cpl - 1) / (16 * cpl);
-  if (waves > 8) return false;
-  const size_t lds = (size_t)waves * 4 * (4 * MG) * 4 * sizeof(float);
-  const dim3 grid((unsigned)((p.N + a.R - 1) / a.R)), block((unsigned)(64 * waves));
-#define FP4X_ROWS_CASE(G, C)                                                                         \
-  if (MG == G && cpl == C) {                                                                         \
-    hipLaunchKernelGGL((rows_mfma_kernel<F, G, C>), grid, block, lds, st, a);                        \
-    return true;                                                                                     \
-  }
-  FP4X_ROWS_CASE(2, 1) FP4X_ROWS_CASE(2, 2) FP4X_ROWS_CASE(2, 3) FP4X_ROWS_CASE(2, 4)
-  FP4X_ROWS_CASE(4, 1) FP4X_ROWS_CASE(4, 2)
-#undef FP4X_ROWS_CASE
-  return false;
+  RowsPlan pl;
+  if (!rows_mfma_plan<F>(nch, p.M, pl)) return false;
+  a.R = rows_per_wg(p.N, cus);
+  return rows_dispatch<F>(pl, RowsGemvBody<F>{a, pl, st});
 }
 
 }  // namespace fp4x

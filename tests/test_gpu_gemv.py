@@ -187,19 +187,26 @@ def test_rows_gemv(gpu, F, fmt, N, M, monkeypatch):
 
 @pytest.mark.parametrize("fmt", ["mx8", "w8", "w6", "nv4"])
 @pytest.mark.parametrize("ks", [2, 4, 5])
-def test_gemv_split_k(gpu, F, fmt, ks):
+def test_gemv_split_k(gpu, F, fmt, ks, monkeypatch):
+    """K split over ks slices summed in slice order (the MFMA core and the
+    split-K tile kernels; with FP4X_ROWS=0, since a 520-row matrix otherwise
+    takes the few-rows kernels, which sum each row whole): within the bound,
+    and repeated calls reuse the re-armed tickets bit for bit.  The default
+    path is checked against the same bound."""
     rng = np.random.default_rng(7 + ks)
     n, k = 520, 2560
     planes, w_op, gs = prep(fmt, rng, n, k)
     x, xb = act(rng, 3, k)
-    y = run(F, fmt, bf16_dev(x), planes, ks, torch.float32)
     exact = ordered.exact_sum(x, w_op) * gs
     bound = ordered.mfma_bound(x, w_op, ks) * abs(gs)
-    assert np.all(np.abs(to_f32(y) - exact) <= bound), (np.abs(to_f32(y) - exact) / bound).max()
-    # repeated calls reuse the re-armed tickets and give identical results
-    for _ in range(3):
-        y2 = run(F, fmt, bf16_dev(x), planes, ks, torch.float32)
-        assert torch.equal(y, y2)
+    with path_switch(monkeypatch, "FP4X_ROWS"):
+        y = run(F, fmt, bf16_dev(x), planes, ks, torch.float32)
+        assert np.all(np.abs(to_f32(y) - exact) <= bound), (np.abs(to_f32(y) - exact) / bound).max()
+        for _ in range(3):
+            y2 = run(F, fmt, bf16_dev(x), planes, ks, torch.float32)
+            assert torch.equal(y, y2)
+    y3 = to_f32(run(F, fmt, bf16_dev(x), planes, ks, torch.float32))
+    assert np.all(np.abs(y3 - exact) <= bound), (np.abs(y3 - exact) / bound).max()
 
 
 @pytest.mark.parametrize("fmt", ["mx8", "w8", "w6", "nv4"])
@@ -261,28 +268,33 @@ def test_dense_stream(gpu, F, fmt, slots, parts, env, M, tail, monkeypatch):
 ])
 def test_w8_splitk_workgroups(gpu, F, case, monkeypatch):
     """W8 split-K of few tiles with K a multiple of 2048: each tile's K spread over
-    several workgroups, partials summed in slot order by the last one to arrive."""
+    several workgroups, partials summed in slot order by the last one to arrive
+    (FP4X_ROWS=0: these shapes otherwise take the few-rows kernels)."""
     n, k, M, ks, s_dtype, split = case
     rng = np.random.default_rng(2000 + n + k + M + ks)
     q, s = oq.quantize_w8(weights(rng, n, k))
     s = s.astype(s_dtype)
     x, _ = act(rng, M, k)
     qd, sd, xd = dev(q), dev(s), bf16_dev(x)
-    y = F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32)
     w_op = og.operand("w8", q, s.astype(np.float32))
     exact = ordered.exact_sum(x, w_op)
     bound = ordered.mfma_bound(x, w_op, max(ks, k // 2048))
-    assert np.all(np.abs(to_f32(y) - exact) <= bound), (np.abs(to_f32(y) - exact) / bound).max()
-    assert_tol(to_f32(y), og.matmul_f32(x, w_op), what=str(case))
-    for _ in range(3):                        # re-armed tickets, arrival order does not matter
-        assert torch.equal(y, F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32))
-    with path_switch(monkeypatch, "FP4X_W8_STREAM"):
-        y_core = F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32)
+    with path_switch(monkeypatch, "FP4X_ROWS"):
+        y = F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32)
+        assert np.all(np.abs(to_f32(y) - exact) <= bound), (np.abs(to_f32(y) - exact) / bound).max()
+        assert_tol(to_f32(y), og.matmul_f32(x, w_op), what=str(case))
+        for _ in range(3):                        # re-armed tickets, arrival order does not matter
+            assert torch.equal(y, F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32))
+        with path_switch(monkeypatch, "FP4X_W8_STREAM"):
+            y_core = F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32)
     assert np.all(np.abs(to_f32(y_core) - exact) <= bound)
     # another K decomposition than the core's: its fp32 sums differ in the last bits
     assert (not torch.equal(y, y_core)) == split
     print(f"N={n} K={k} M={M} ksplit={ks}: split={split}, max |y - exact| / bound = "
           f"{(np.abs(to_f32(y) - exact) / bound).max():.3g}")
+    # the default path (few-rows kernels where they apply) within the same bound
+    y_def = to_f32(F.w8_linear(xd, qd, sd, (32, 64, ks, 4), torch.float32))
+    assert np.all(np.abs(y_def - exact) <= bound), (np.abs(y_def - exact) / bound).max()
 
 
 def test_gemv_out_dtypes_and_strided_x(gpu, F):
@@ -321,10 +333,17 @@ def test_w8_fp16_scales_and_layers(gpu, F):
         x3 = bf16_dev(np.stack(xs))
         y = F.w8_linear_layers(x3, q3, s3, torch.float32)
         for i in range(Ly):
-            ref = og.matmul_f32(xs[i], og.operand("w8", qs[i][0], qs[i][1].astype(s_dtype).astype(np.float32)))
+            w_op = og.operand("w8", qs[i][0], qs[i][1].astype(s_dtype).astype(np.float32))
+            ref = og.matmul_f32(xs[i], w_op)
             assert_tol(to_f32(y[i]), ref, what=f"layer {i}")
+            # the single-layer call (the few-rows kernel) sums in another fixed
+            # order: both within the accumulation bound of the exact sums, and
+            # the single call repeats bit for bit
             single = F.w8_linear(x3[i], q3[i], s3[i], (16, 512, 1, 4), torch.float32)
-            assert torch.equal(single, y[i])
+            exact, bound = ordered.exact_sum(xs[i], w_op), ordered.mfma_bound(xs[i], w_op)
+            for got in (to_f32(single), to_f32(y[i])):
+                assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
+            assert torch.equal(single, F.w8_linear(x3[i], q3[i], s3[i], (16, 512, 1, 4), torch.float32))
 
 
 # ------------------------------------------------------------------ streaming W8 (layer-batched gates)

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import act, bf16_dev
+from gpu_helpers import act, bf16_dev, path_switch
 
 pytestmark = pytest.mark.gpu
 
@@ -75,7 +75,11 @@ def test_graph_mixer_one_launch(gpu, F):
     assert int(fx.tickets[:65].abs().sum()) == 0
 
 
-def test_graph_splitk_and_gates(gpu, F):
+@pytest.mark.parametrize("rows", ["1", "0"])
+def test_graph_splitk_and_gates(gpu, F, rows, monkeypatch):
+    """The mixer-shaped W8 GEMV (640 x 10240, 4 K slices) and the 48-layer
+    gates under replay: with the few-rows kernels (default) and with the
+    split-K tile kernel and its tickets (FP4X_ROWS=0)."""
     gen = torch.Generator(device=gpu).manual_seed(6)
     q, s = F.quantize_w8(torch.randn((640, 10240), generator=gen, device=gpu) * 0.02)
     x = torch.randn((3, 10240), generator=gen, device=gpu).to(torch.bfloat16)
@@ -87,10 +91,11 @@ def test_graph_splitk_and_gates(gpu, F):
         return [F.w8_linear(x, q, s, (32, 256, 4, 4), torch.float32),
                 F.w8_linear_layers(xg, qg, sg, torch.float32)]
 
-    expected = run()
-    torch.cuda.synchronize()
-    replay_and_check(run, [e.clone() for e in expected],
-                     lambda: F.w8_linear(x[:1], q, s, (32, 256, 4, 4), torch.float32))
+    with path_switch(monkeypatch, "FP4X_ROWS", rows):
+        expected = run()
+        torch.cuda.synchronize()
+        replay_and_check(run, [e.clone() for e in expected],
+                         lambda: F.w8_linear(x[:1], q, s, (32, 256, 4, 4), torch.float32))
 
 
 def test_graph_int2_topk(gpu, F):
