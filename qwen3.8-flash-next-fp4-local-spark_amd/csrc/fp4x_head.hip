@@ -43,6 +43,8 @@ __device__ __forceinline__ void load_batch_inbounds(ChunkBatch<F, 1>& b, const P
 
 template <class F, bool DENSE>
 __global__ __launch_bounds__(kThreads) void refine_kernel(RefineArgs p) {
+  asm volatile("" ::"s"(p.out), "s"(p.out_dtype), "s"(p.out_stride), "s"(p.x), "s"(p.idx), "s"(p.pa.w0),
+               "s"(p.pa.s), "s"(p.pa.K), "s"(p.gs), "s"(p.M), "s"(p.C), "s"(p.K), "s"(p.V), "s"(p.lpr), "s"(p.cpl));
   extern __shared__ __align__(16) uint16_t lds_x[];
   const int m = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;

@@ -30,6 +30,17 @@ struct GemvLaunch {
   int lr, hc;
 };
 
+// Reads the launch fields the streaming kernels use in one round of scalar
+// loads at kernel entry.  Left to itself the compiler loads the arguments in
+// several rounds, each behind a branch or a first use, and every round waits
+// out the argument memory's latency before the first weight load can issue.
+__device__ __forceinline__ void load_launch_once(const GemvLaunch& p) {
+  asm volatile("" ::"s"(p.x), "s"(p.x_stride), "s"(p.x_bstride), "s"(p.pa.w0), "s"(p.pa.w1), "s"(p.pa.s),
+               "s"(p.pa.K), "s"(p.w0_bstride), "s"(p.w1_bstride), "s"(p.s_bstride), "s"(p.out), "s"(p.out_dtype),
+               "s"(p.out_stride), "s"(p.out_bstride), "s"(p.gs), "s"(p.rs), "s"(p.M), "s"(p.N), "s"(p.batch),
+               "s"(p.per_wg), "s"(p.xbufs));
+}
+
 // Plain store: out[b][m * out_stride + row] = cast(v)
 struct EpiStore {
   __device__ static void apply(const GemvLaunch& p, int b, int m, int64_t row, float v) {

@@ -60,10 +60,20 @@ __device__ __forceinline__ void wg_barrier_raw() { asm volatile("s_barrier" ::: 
 __device__ __forceinline__ void lds_put_f32x4(uint32_t a, f32x4_t v) {
   asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(a), "v"(v) : "memory");
 }
-__device__ __forceinline__ f32x4_t lds_get_f32x4(uint32_t a) {
-  f32x4_t v;
-  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a) : "memory");
-  return v;
+
+// acc += the N partial sums at LDS byte addresses a + 1024 h (h = 0 .. N - 1),
+// added in h order.  The reads are ordinary LDS loads, so every one issues
+// before the first add waits (one LDS round trip, not N).
+template <int N>
+__device__ __forceinline__ void lds_add_parts(uint32_t a, f32x4_t& acc) {
+  typedef const __attribute__((address_space(3))) f32x4_t* lds_f32x4_ptr;
+  f32x4_t o[N];
+#pragma unroll
+  for (int h = 0; h < N; ++h) o[h] = *reinterpret_cast<lds_f32x4_ptr>((uintptr_t)(a + h * 1024));
+#pragma unroll
+  for (int h = 0; h < N; ++h) {
+    acc[0] += o[h][0]; acc[1] += o[h][1]; acc[2] += o[h][2]; acc[3] += o[h][3];
+  }
 }
 
 // One unit's operands for lane (n, g): weight chunks g and g + 4 of row n (at
@@ -222,13 +232,7 @@ __global__ __launch_bounds__(64 * T * KW) void w8_stream_kernel(GemvLaunch p) {
     if constexpr (KW > 1) {
       if (part > 0) lds_put_f32x4(pl + (part - 1) * 1024, acc);
       wg_barrier_raw();
-      if (part == 0) {
-#pragma unroll
-        for (int h = 1; h < KW; ++h) {
-          const f32x4_t o = lds_get_f32x4(pl + (h - 1) * 1024);
-          acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
-        }
-      }
+      if (part == 0) lds_add_parts<KW - 1>(pl, acc);
       wg_barrier_raw();
     }
     if (part == 0 && it < wgend) {
@@ -345,11 +349,7 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
     if (wave > 0) lds_put_f32x4(pl + (wave - 1) * 1024, acc);
     wg_barrier_raw();
     if (wave > 0) return false;
-#pragma unroll
-    for (int h = 1; h < WPG; ++h) {
-      const f32x4_t o = lds_get_f32x4(pl + (h - 1) * 1024);
-      acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
-    }
+    lds_add_parts<WPG - 1>(pl, acc);
   }
   // wave 0: slot c of tile t holds [M][16] fp32 partials
   float* slots = p.part + (int64_t)t * C * p.M * 16;
@@ -1062,6 +1062,7 @@ struct StreamW8H {
 
 template <class U, int T, int KW, int D>
 __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p) {
+  load_launch_once(p);
   constexpr int NW = T * KW;
   extern __shared__ __align__(16) uint16_t lds[];
   char* base = reinterpret_cast<char*>(lds);
@@ -1145,13 +1146,7 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
     if constexpr (KW > 1) {
       if (part > 0) lds_put_f32x4(pl + (part - 1) * 1024, acc);
       wg_barrier_raw();
-      if (part == 0) {
-#pragma unroll
-        for (int h = 1; h < KW; ++h) {
-          const f32x4_t o = lds_get_f32x4(pl + (h - 1) * 1024);
-          acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
-        }
-      }
+      if (part == 0) lds_add_parts<KW - 1>(pl, acc);
       wg_barrier_raw();
     }
     if (part == 0 && it < wgend) {
