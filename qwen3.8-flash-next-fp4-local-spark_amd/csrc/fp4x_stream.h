@@ -814,8 +814,8 @@ struct StreamMX8 {
   uint32_t oa, ob, os;
   static constexpr int XG = 64;                       // activation bytes between lane groups g
   static constexpr bool BATCHED = false;              // single matrices only
-  __device__ void set(const GemvLaunch& p, int b, int64_t t, int k128, int lane, int lim) {
-    const int K = p.pa.K, ra = lane >> 3, rb = ra + 8, pp = lane & 7, sr = lane & 15;
+  __device__ void set(const GemvLaunch& p, int K, int b, int64_t t, int k128, int lane, int lim) {
+    const int ra = lane >> 3, rb = ra + 8, pp = lane & 7, sr = lane & 15;
     w = p.pa.w0 + b * p.w0_bstride + t * 16 * K + k128 * 128;
     s = p.pa.s + b * p.s_bstride + t * 16 * (K / 32) + k128 * 4;
     oa = (uint32_t)((ra < lim ? ra : lim) * K + (pp ^ ((ra >> 1) & 7)) * 16);
@@ -868,8 +868,8 @@ struct StreamW6 {
   uint32_t ola, olb, oh, os;
   static constexpr int XG = 128;
   static constexpr bool BATCHED = false;
-  __device__ void set(const GemvLaunch& p, int b, int64_t t, int ku, int lane, int lim) {
-    const int K = p.pa.K, ra = lane >> 3, rb = ra + 8, pp = lane & 7;
+  __device__ void set(const GemvLaunch& p, int K, int b, int64_t t, int ku, int lane, int lim) {
+    const int ra = lane >> 3, rb = ra + 8, pp = lane & 7;
     const int hr = lane >> 2, hp = (lane & 3) ^ ((hr >> 2) & 3);
     l = p.pa.w0 + b * p.w0_bstride + t * 16 * (K / 2) + ku * 128;
     h = p.pa.w1 + b * p.w1_bstride + t * 16 * (K / 4) + ku * 64;
@@ -937,8 +937,8 @@ struct StreamNV4 {
   uint32_t oa, ob, os;
   static constexpr int XG = 128;
   static constexpr bool BATCHED = false;
-  __device__ void set(const GemvLaunch& p, int b, int64_t t, int ku, int lane, int lim) {
-    const int K = p.pa.K, ra = lane >> 3, rb = ra + 8, pp = lane & 7, sr = lane >> 2;
+  __device__ void set(const GemvLaunch& p, int K, int b, int64_t t, int ku, int lane, int lim) {
+    const int ra = lane >> 3, rb = ra + 8, pp = lane & 7, sr = lane >> 2;
     w = p.pa.w0 + b * p.w0_bstride + t * 16 * (K / 2) + ku * 128;
     s = p.pa.s + b * p.s_bstride + t * 16 * (K / 16) + ku * 16;
     oa = (uint32_t)((ra < lim ? ra : lim) * (K / 2) + (pp ^ ((ra >> 1) & 7)) * 16);
@@ -1002,8 +1002,8 @@ struct StreamW8H {
   const uint8_t* w;
   const uint8_t* s;
   uint32_t o[4], os;
-  __device__ void set(const GemvLaunch& p, int b, int64_t t, int ku, int lane, int lim) {
-    const int K = p.pa.K, sr = (lane & 31) >> 1;
+  __device__ void set(const GemvLaunch& p, int K, int b, int64_t t, int ku, int lane, int lim) {
+    const int sr = (lane & 31) >> 1;
     w = p.pa.w0 + b * p.w0_bstride + t * 16 * K + ku * 256;
     s = p.pa.s + b * p.s_bstride + (t * 16 * (K / 64) + ku * 4) * 2;
 #pragma unroll
@@ -1060,7 +1060,7 @@ struct StreamW8H {
   }
 };
 
-template <class U, int T, int KW, int D>
+template <class U, int T, int KW, int D, int KC>
 __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p) {
   load_launch_once(p);
   constexpr int NW = T * KW;
@@ -1071,7 +1071,7 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
   const int n = lane & 15, g = lane >> 4;
   // items: (batch entry, tile); single-matrix policies compile the batch terms away
   const int tiles = (p.N + 15) / 16, items = (U::BATCHED ? p.batch : 1) * tiles;
-  const int K = p.pa.K, JW = K / U::UK / KW;         // units per wave per tile
+  const int K = KC ? KC : p.pa.K, JW = K / U::UK / KW;   // units per wave per tile
   const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
   const int wg0 = blockIdx.x * p.per_wg;
   const int wgend = wg0 + p.per_wg < items ? wg0 + p.per_wg : items;
@@ -1106,7 +1106,7 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
     int it = wg0 + rr * T + slot;
     if (it >= wgend) it = wgend - 1;                 // idle slot of the last round: reload a valid tile
     const int b = U::BATCHED ? it / tiles : 0, t = it - b * tiles;
-    unit.set(p, b, t, part * JW, lane, p.N - 1 - t * 16);   // rows past N read row N - 1
+    unit.set(p, K, b, t, part * JW, lane, p.N - 1 - t * 16);   // rows past N read row N - 1
   };
   set_tile(0);
   auto issue_next = [&]() {
@@ -1161,6 +1161,28 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
   wait_vmcnt<0>();                                   // no load of the prologue outlives the wave
 }
 
+// The model's hidden size, the K of every dense decode GEMV: the streaming
+// kernels compile it as a constant (their address and activation-staging
+// arithmetic then folds; measured 0.1-0.6 us per call), other K take the
+// instantiation that reads K at run time.
+constexpr int kStreamKc = 2560;
+
+template <class U, int T, int KW, int D, int KC>
+bool launch_dense_stream_k(const GemvLaunch& p, size_t lds, unsigned gx, hipStream_t st) {
+  auto kern = dense_stream_kernel<U, T, KW, D, KC>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess) {
+      (void)hipGetLastError();
+      return false;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(gx), dim3(64 * T * KW), lds, st, p);
+  return true;
+}
+
 // Launch U's streaming kernel when the call fits it (no split-K, M <= 16, K a
 // multiple of 512, 16-byte aligned code planes and 4-byte aligned scale /
 // high-bit planes, at least T tiles per CU, the LDS plan within 160 KB);
@@ -1185,21 +1207,12 @@ bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st) {
   const size_t lds = (size_t)span * StreamGeom::xbuf_bytes(p.M, K) + (size_t)T * (KW - 1) * 1024 +
                      (size_t)T * KW * D * U::BYTES;
   if (lds > 160 * 1024) return false;
-  auto kern = dense_stream_kernel<U, T, KW, D>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024) != hipSuccess) {
-      (void)hipGetLastError();
-      return false;
-    }
-    attr_set = true;
-  }
   p.batch = batch;
   p.per_wg = (int)per;
   p.xbufs = (int)span;
-  hipLaunchKernelGGL(kern, dim3((unsigned)((items + per - 1) / per)), dim3(64 * T * KW), lds, st, p);
-  return true;
+  const unsigned gx = (unsigned)((items + per - 1) / per);
+  return K == kStreamKc ? launch_dense_stream_k<U, T, KW, D, kStreamKc>(p, lds, gx, st)
+                        : launch_dense_stream_k<U, T, KW, D, 0>(p, lds, gx, st);
 }
 
 // Shapes measured as graph replays (T slots, KW waves per tile, D units per

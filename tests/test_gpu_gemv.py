@@ -239,10 +239,24 @@ def test_dense_stream(gpu, F, fmt, slots, parts, env, M, tail, monkeypatch):
     (2 slots x 2 waves, 2 units of 256 K) and MXFP8 matrices of at least 1 (1
     slot x 10 waves, 2 units of 128 K) take the streaming kernel: fp32 sums within the MFMA
     bound of the exact sum, as the core's are; a 40-row tail gives workgroups
-    of two rounds whose last round has idle slots."""
-    rng = np.random.default_rng(500 + M + tail + slots)
+    of two rounds whose last round has idle slots.  K = 2560 runs the
+    instantiation compiled for that row length."""
+    _dense_stream_case(F, fmt, slots, parts, env, M, tail, 2560, monkeypatch)
+
+
+@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("fmt,slots,parts,env", [("nv4", 4, 2, "FP4X_NV4_STREAM"), ("w6", 2, 2, "FP4X_W6_STREAM"),
+                                                   ("mx8", 1, 10, "FP4X_MX8_STREAM")])
+def test_dense_stream_other_k(gpu, F, fmt, slots, parts, env, M, monkeypatch):
+    """K = 5120: the streaming kernels' instantiation that reads the row
+    length at run time (twice the units per wave), against the same bound."""
+    _dense_stream_case(F, fmt, slots, parts, env, M, 40, 5120, monkeypatch)
+
+
+def _dense_stream_case(F, fmt, slots, parts, env, M, tail, k, monkeypatch):
+    rng = np.random.default_rng(500 + M + tail + slots + k)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    n, k = 16 * slots * cus + tail, 2560
+    n = 16 * slots * cus + tail
     planes, w_op, gs = prep(fmt, rng, n, k)
     x, _ = act(rng, M, k)
     y = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
