@@ -212,30 +212,24 @@ struct FmtW6 {
   __device__ static Chunk zero() {
     Chunk ch; ch.lo = make_uint4(0, 0, 0, 0); ch.hi = make_uint2(0, 0); ch.s = 0; return ch;
   }
-  // 8 weights: lo nibbles from dword L (nibble i = weight i), hi bits from
-  // the two H bytes hb0 (weights 0-3) and hb1 (weights 4-7) of `hd`.
-  __device__ static void codes8(uint32_t L, uint32_t g0, uint32_t g1, uint32_t g2, uint32_t g3,
-                                int hbyte, uint32_t& c03, uint32_t& c47) {
-    const uint32_t ev = L & 0x0F0F0F0Fu;          // nibbles 0,2,4,6
-    const uint32_t od = (L >> 4) & 0x0F0F0F0Fu;   // nibbles 1,3,5,7
-    const uint32_t lo03 = perm_b32(od, ev, 0x05010400u);  // [n0, n1, n2, n3]
-    const uint32_t lo47 = perm_b32(od, ev, 0x07030602u);  // [n4, n5, n6, n7]
-    // g_t holds (hi of weight 4j+t) << 4 in byte j.
-    const uint32_t j0 = hbyte, j1 = hbyte + 1;
-    const uint32_t a0 = perm_b32(g1, g0, 0x0c0c0400u | (j0 * 0x0101u));
-    const uint32_t b0 = perm_b32(g3, g2, 0x04000c0cu | (j0 * 0x01010000u));
-    const uint32_t a1 = perm_b32(g1, g0, 0x0c0c0400u | (j1 * 0x0101u));
-    const uint32_t b1 = perm_b32(g3, g2, 0x04000c0cu | (j1 * 0x01010000u));
-    c03 = lo03 | a0 | b0;
-    c47 = lo47 | a1 | b1;
+  // The 6-bit codes of 8 weights k = 0..7: low nibbles from dword L (nibble
+  // k = weight k), high bit pairs from H bytes 2 * half and 2 * half + 1 of hd
+  // (weights 0-3 and 4-7; an H byte holds k%4 = 0, 2 in its low nibble, bits
+  // 1:0 and 3:2, and k%4 = 1, 3 in its high nibble, bits 5:4 and 7:6).  Even k
+  // go to ce (byte j: weight 2j), odd k to co (byte j: weight 2j + 1), so the
+  // nibble split needs no byte shuffle: about 1.4 instructions per weight.
+  __device__ static void codes8(uint32_t L, uint32_t hd, int half, uint32_t& ce, uint32_t& co) {
+    const uint32_t ev = L & 0x0F0F0F0Fu;             // nibbles 0, 2, 4, 6
+    const uint32_t od = (L >> 4) & 0x0F0F0F0Fu;      // nibbles 1, 3, 5, 7
+    const uint32_t u = perm_b32(hd, hd, half ? 0x03030202u : 0x01010000u);   // [Hb, Hb, Hb+1, Hb+1]
+    ce = ev | ((u << 4) & 0x00300030u) | ((u << 2) & 0x30003000u);
+    co = od | (u & 0x00300030u) | ((u >> 2) & 0x30003000u);
   }
-  __device__ static void deq4(uint32_t c, float s, float ms, uint32_t& p01, uint32_t& p23) {
-    float f0 = __builtin_fmaf(ubyte_to_f32<0>(c), s, ms);
-    float f1 = __builtin_fmaf(ubyte_to_f32<1>(c), s, ms);
-    float f2 = __builtin_fmaf(ubyte_to_f32<2>(c), s, ms);
-    float f3 = __builtin_fmaf(ubyte_to_f32<3>(c), s, ms);
-    p01 = pack_bf16x2(f0, f1);
-    p23 = pack_bf16x2(f2, f3);
+  // bf16 pairs (weights 2j, 2j + 1) of the codes in ce / co: (code - 32) * s
+  // exactly in fp32, rounded to bf16.
+  template <int J>
+  __device__ static uint32_t deq2(uint32_t ce, uint32_t co, float s, float ms) {
+    return pack_bf16x2(__builtin_fmaf(ubyte_to_f32<J>(ce), s, ms), __builtin_fmaf(ubyte_to_f32<J>(co), s, ms));
   }
   __device__ static void deq16(const Chunk& ch, int sub, uint32_t (&w)[8]) {
     const float s = f16_to_f32((uint16_t)ch.s);
@@ -243,17 +237,13 @@ struct FmtW6 {
     const uint32_t L0 = sub ? ch.lo.z : ch.lo.x;
     const uint32_t L1 = sub ? ch.lo.w : ch.lo.y;
     const uint32_t hd = sub ? ch.hi.y : ch.hi.x;
-    const uint32_t g0 = (hd << 4) & 0x30303030u;  // k%4 == 0 (bits 1:0)
-    const uint32_t g1 = hd & 0x30303030u;         // k%4 == 1 (bits 5:4)
-    const uint32_t g2 = (hd << 2) & 0x30303030u;  // k%4 == 2 (bits 3:2)
-    const uint32_t g3 = (hd >> 2) & 0x30303030u;  // k%4 == 3 (bits 7:6)
-    uint32_t c0, c1, c2, c3;
-    codes8(L0, g0, g1, g2, g3, 0, c0, c1);
-    codes8(L1, g0, g1, g2, g3, 2, c2, c3);
-    deq4(c0, s, ms, w[0], w[1]);
-    deq4(c1, s, ms, w[2], w[3]);
-    deq4(c2, s, ms, w[4], w[5]);
-    deq4(c3, s, ms, w[6], w[7]);
+    uint32_t e0, o0, e1, o1;
+    codes8(L0, hd, 0, e0, o0);
+    codes8(L1, hd, 1, e1, o1);
+    w[0] = deq2<0>(e0, o0, s, ms); w[1] = deq2<1>(e0, o0, s, ms);
+    w[2] = deq2<2>(e0, o0, s, ms); w[3] = deq2<3>(e0, o0, s, ms);
+    w[4] = deq2<0>(e1, o1, s, ms); w[5] = deq2<1>(e1, o1, s, ms);
+    w[6] = deq2<2>(e1, o1, s, ms); w[7] = deq2<3>(e1, o1, s, ms);
   }
 };
 

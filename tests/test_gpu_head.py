@@ -288,14 +288,15 @@ def test_fast_head_full_size_32_batches(gpu, F):
 
 
 # ------------------------------------------------------------------ INT2 streaming kernel
-@pytest.mark.parametrize("M,rs,one", [(3, False, False), (16, False, False), (3, True, False), (3, False, True)])
-def test_int2_stream(gpu, F, M, rs, one, monkeypatch):
+@pytest.mark.parametrize("M,rs,one,K", [(3, False, False, 2560), (16, False, False, 2560), (3, True, False, 2560),
+                                        (3, False, True, 2560), (3, False, False, 1536)])
+def test_int2_stream(gpu, F, M, rs, one, K, monkeypatch):
     """Heads of at least 2 tiles per wave of the grid take the streaming kernel
     (one wave per tile, LDS ring of direct loads); N tail of 40 rows.  one:
     between 1 and 2 tiles per wave at 8 waves per CU (the 65,197-row draft
-    subset on 256 CUs), 3 rows past the last full tile."""
-    rng = np.random.default_rng(77 + M + rs + 5 * one)
-    K = 2560
+    subset on 256 CUs), 3 rows past the last full tile; K = 1536: three units
+    per tile instead of five."""
+    rng = np.random.default_rng(77 + M + rs + 5 * one + K)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     V = 16 * (16 * cus - 21) - 3 if one else 4 * 8 * 16 * cus + 40
     w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
