@@ -193,6 +193,9 @@ struct HcMixArgs {
   int C, D, tiles_d, R, spin_limit;
 };
 
+constexpr int kMixMaxHc = 4;                     // streams the single-launch mixer takes
+constexpr int kMixOutPer = 2;                    // epilogue outputs per thread
+
 template <bool F16S, int KW, int CPS>
 __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   using F = FmtW8<F16S>;
@@ -237,6 +240,21 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   //    once in a workgroup without a down item)
   MfmaBatch<F, CPS> cb;
   mfma_load_full<F, DP, CPS>(cb, F::lane(u.pa, urow, CPS * cw));
+  // ... and the normalized inputs of this thread's epilogue outputs (at most
+  // kMixOutPer), into registers, so that the epilogue waits for no load
+  // (outputs past the workgroup's read a valid element and are not stored)
+  const int per_slot = u.M * u.bj, nout = a.R * per_slot;
+  uint16_t nrv[kMixOutPer][kMixMaxHc];
+#pragma unroll
+  for (int q = 0; q < kMixOutPer; ++q) {
+    const int e = (int)threadIdx.x + q * (int)blockDim.x, ec = e < nout ? e : 0;
+    const int sl = ec / per_slot, r = ec - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
+    const int tsl = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + sl;
+    const int64_t j = (int64_t)(tsl < ntu ? tsl : ntu - 1) * u.bj + jj;
+    const uint16_t* nm = u.nrm + m * u.nrm_stride + j;
+#pragma unroll
+    for (int s = 0; s < kMixMaxHc; ++s) nrv[q][s] = nm[(int64_t)(s < u.hc ? s : u.hc - 1) * u.H];
+  }
   __syncthreads();
 
   // 3. wait for this workgroup's flag to advance past its value at the start
@@ -285,18 +303,23 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
       if (g * 4 + i < u.M) gls[(g * 4 + i) * T + grp * 16 + n] = round_bf16(acc[i]);
   }
   __syncthreads();
-  const int per_slot = u.M * u.bj;
-  for (int e = threadIdx.x; e < a.R * per_slot; e += blockDim.x) {
+#pragma unroll
+  for (int q = 0; q < kMixOutPer; ++q) {
+    const int e = (int)threadIdx.x + q * (int)blockDim.x;
     const int sl = e / per_slot, r = e - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
     const int tsl = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + sl;
-    if (tsl >= ntu) continue;
+    if (e >= nout || tsl >= ntu) continue;
     const int64_t j = (int64_t)tsl * u.bj + jj;
     const float* gm = gl + (size_t)sl * u.M * T + m * T + jj;
-    const uint16_t* nm = u.nrm + m * u.nrm_stride + j;
-    const int64_t H = u.H;
+    auto nrm_s = [&](int s) {
+      uint16_t v = nrv[q][0];
+#pragma unroll
+      for (int t = 1; t < kMixMaxHc; ++t)
+        if (s == t) v = nrv[q][t];
+      return bf16_to_f32(v);
+    };
     u.out[(int64_t)m * u.H + j] =
-        ok ? hc_gate_mean([&](int s) { return gm[s * u.bj]; }, [&](int s) { return bf16_to_f32(nm[s * H]); }, u.hc)
-           : (uint16_t)0x7fc0u;
+        ok ? hc_gate_mean([&](int s) { return gm[s * u.bj]; }, nrm_s, u.hc) : (uint16_t)0x7fc0u;
   }
 }
 
@@ -464,6 +487,7 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   // the up tiles sharing workgroups with down items (measured: spreading only
   // part of the up tiles to extra workgroups is slower than not at all)
   const int R = 8 / WT, ntu = H / bj, D = tiles_d * C, cus = device_cus();
+  if (hc > kMixMaxHc || R * M * bj > kMixOutPer * 512) return two();
   const int need_u = (ntu + R - 1) / R;
   const int P = D + need_u <= cus ? D + need_u : (D > need_u ? D : need_u);
   if (P > cus || (int64_t)n_tickets < (int64_t)sync_at + (int64_t)kMixFlagStride * (P + 1)) return two();
