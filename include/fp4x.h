@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 7
+#define FP4X_ABI_VERSION 8
 
 enum {
   FP4X_OK = 0,
@@ -221,11 +221,12 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
  * decompositions it runs as one launch (the up weights stream while the down
  * projection runs); otherwise it makes the two calls.  tickets: n_tickets
  * int32, zero before the first call and never touched by the caller
- * afterwards; the single launch needs at least
- * round_up(ceil(N / 16), 64) + 32 * (CUs + 1): the tile tickets, then at
- * offset S = round_up(ceil(N / 16), 64) the down-tile count (S), a status
- * word (S + 1) and one 128-byte generation-flag line per workgroup.  With
- * fewer it makes the two calls.  A workgroup whose flag wait gives up (only
+ * afterwards.  The single launch keeps one tile ticket per 128-byte line,
+ * ticket t at 32 t, and at S = (n_tickets - 32 * (CUs + 1)) rounded down to
+ * a multiple of 32 the down-tile count (S), a status word (S + 1) and one
+ * 128-byte generation-flag line per workgroup, so it needs S >= 32 *
+ * ceil(N / 16); with fewer it makes the two calls.  (S depends on the buffer
+ * alone: calls of any shape on one buffer agree on it.)  A workgroup whose flag wait gives up (only
  * possible when other work holds the GPU's CUs for about a second) writes NaN
  * to its outputs and sets bit 0 of the status word; the next call is not
  * affected.  FP4X_HC_MIX=0 forces the two calls.

@@ -468,7 +468,14 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   int C = 0;
   size_t lds_d = 0;
   const int tiles_d = (N + 15) / 16;
-  const int sync_at = (tiles_d + 63) & ~63;          // the count and the flags, away from the tile tickets
+  // tile tickets one 128-byte line apart from the start of the buffer (the
+  // 200 items' ticket atomics of a mixer would otherwise queue on two lines);
+  // the count, the status word and the flags in its last 32 * (cus + 1) ints,
+  // at the same place for every shape the buffer serves
+  d.tstride = kMixFlagStride;
+  const int64_t sync_at =
+      ((int64_t)n_tickets - (int64_t)kMixFlagStride * (device_cus() + 1)) & ~(int64_t)(kMixFlagStride - 1);
+  if (sync_at < (int64_t)tiles_d * kMixFlagStride) return two();
   if (!w8_splitk_plan(d, C, lds_d)) return two();
   // the up projection's shape, as fp4x_hc_up plans it
   const int chunks = lr / 16;
@@ -490,7 +497,7 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   if (hc > kMixMaxHc || R * M * bj > kMixOutPer * 512) return two();
   const int need_u = (ntu + R - 1) / R;
   const int P = D + need_u <= cus ? D + need_u : (D > need_u ? D : need_u);
-  if (P > cus || (int64_t)n_tickets < (int64_t)sync_at + (int64_t)kMixFlagStride * (P + 1)) return two();
+  if (P > cus) return two();
   const size_t lds_u = (((size_t)M * lr * 2 + 15) & ~(size_t)15) + (size_t)R * (T / 16) * (KW - 1) * 1024 +
                        (size_t)R * M * T * 4;
   const size_t lds = lds_d > lds_u ? lds_d : lds_u;

@@ -25,6 +25,7 @@ struct GemvLaunch {
   int64_t smax_stride;   //   elements between rows m of smax
   float* part;           // split-K slots [batch][ksplit][MT][N]
   int* tickets;          // split-K tickets [batch][tiles], zero between calls
+  int tstride = 1;       //   ints between consecutive tickets (the single-launch mixer: one 128-byte line each)
   // mixer-down epilogue
   void* out2;
   int lr, hc;

@@ -359,7 +359,8 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
       __hip_atomic_store(slots + (c * p.M + g * 4 + i) * 16 + n, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   wait_vmcnt<0>();                                   // the slot stores have completed
   int tk = 0;
-  if (lane == 0) tk = __hip_atomic_fetch_add(p.tickets + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int* const ticket = p.tickets + (int64_t)t * p.tstride;
+  if (lane == 0) tk = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   tk = __builtin_amdgcn_readfirstlane(tk);
   if (tk != C - 1) return false;
   for (int e = lane; e < p.M * 16; e += 64) {        // e = m * 16 + n
@@ -369,7 +370,7 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
     const int64_t orow = (int64_t)t * 16 + (e & 15);
     if (orow < p.N) Epi::apply(p, 0, e >> 4, orow, tot * p.gs);
   }
-  if (lane == 0) ticket_reset(p.tickets + t);
+  if (lane == 0) ticket_reset(ticket);
   return true;
 }
 

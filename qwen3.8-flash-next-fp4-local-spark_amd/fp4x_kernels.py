@@ -344,10 +344,13 @@ class HCFused:
     def __init__(self, device, n_down=336, max_m=16, bn=32, max_ksplit=16):
         self.n_down, self.max_m, self.max_ksplit = n_down, max_m, max_ksplit
         self.part = torch.empty(max_ksplit * MAX_M * n_down, dtype=torch.float32, device=device)
-        # one ticket per 16-row tile, then the single-launch mixer's count and one
-        # 128-byte flag line per workgroup (at most one workgroup per CU)
+        # one ticket per 16-row tile (the single-launch mixer: one per 128-byte
+        # line, 2 * n_down ints); its count, status word and one 128-byte flag
+        # line per workgroup (at most one workgroup per CU) in the last
+        # 32 * (cus + 1) ints, at the same place for every shape
         cus = torch.cuda.get_device_properties(device).multi_processor_count
-        self.tickets = torch.zeros(max(n_down, 1) + 64 + 32 * (cus + 1), dtype=torch.int32, device=device)
+        self.tickets = torch.zeros(2 * max(n_down, 16) + 64 + 32 * (cus + 1), dtype=torch.int32, device=device)
+        self._status_at = (self.tickets.numel() - 32 * (cus + 1)) // 32 * 32 + 1
 
     def down(self, x, q, s, lr, hc, cfg=(32, 512, 4, 4)):
         """(di bf16 [M, N], bot bf16 [M, lr]) = split-K W8 GEMV + cast + scaled SiLU."""
@@ -391,15 +394,15 @@ class HCFused:
                                       hc, KS, _ptr(self.part), _ptr(self.tickets), self.tickets.numel(), _ptr(qi),
                                       _ptr(si), _ptr(normalized), normalized.stride(0), _ptr(out), h, BJ,
                                       _L.stream_of(x)), "hc_mix")
-        self._status_at = -(-(-(-n // 16)) // 64) * 64 + 1
+        self._mixed = True
         return di, bot, out
 
     def wait_timeouts(self, clear=True):
         """True if a single-launch mixer call since the last check gave up
         waiting for its bottleneck (its outputs then hold NaN).  Reads the
         device status word: synchronizes the stream."""
-        at = getattr(self, "_status_at", None)
-        if at is None:
+        at = self._status_at
+        if not getattr(self, "_mixed", False):
             return False
         hit = bool(int(self.tickets[at].item()) & 1)
         if clear and hit:

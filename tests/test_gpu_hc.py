@@ -100,7 +100,7 @@ def test_fused_equals_unfused_97_layers(gpu, F):
         bi = F.HCFused.up(bot, qi, si, x_t, HC, (8, 64, 4))
         di2, bot2, bi2, g = unfused(F, x_t, qd_t, sd_t, qu_t, su_t, LR, KS)
         assert torch.equal(di, di2) and torch.equal(bot, bot2) and torch.equal(bi, bi2), f"layer {i}"
-        assert int(fx.tickets[:65].abs().sum()) == 0
+        assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
         di3, bot3, bi3 = fx.mix(x_t, qd_t, sd_t, LR, HC, qi, si, x_t, (32, 256, KS, 4))
         assert torch.equal(di, di3) and torch.equal(bot, bot3) and torch.equal(bi, bi3), f"layer {i} mix"
         qd, sd, qu, su = (t.cpu().numpy() for t in (qd_t, sd_t, qu_t, su_t))
@@ -126,7 +126,7 @@ def test_mixer_served_shape(gpu, F, M):
     for _ in range(3):                                # one launch, counters re-armed every call
         di3, bot3, bi3 = fx.mix(x_t, dev(qd), dev(sd), 320, HC, qi, si, x_t, (32, 256, 8, 4))
         assert torch.equal(di, di3) and torch.equal(bot, bot3) and torch.equal(bi, bi3)
-        assert int(fx.tickets[:65].abs().sum()) == 0
+        assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
     agree = check_against_oracle(x, qd, sd, qu, su, 320, di, bot, g, bi, 8, f"M={M}")
     print(f"served shape M={M}: block_input bit agreement with the oracle mixer {agree:.5f}")
 
@@ -189,7 +189,7 @@ def test_mix_fallback_and_fp16_scales(gpu, F, monkeypatch):
         for a, b, c in zip(one, two, (di, bot, bi)):
             assert torch.equal(a, b) and torch.equal(a, c), M
         assert not torch.isnan(one[2].float()).any()
-        assert int(fx.tickets[:65].abs().sum()) == 0
+        assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
     assert not fx.wait_timeouts()
 
 
@@ -225,5 +225,5 @@ def test_mix_wait_give_up_then_recovers(gpu, F, monkeypatch):
         again = fx.mix(x_t, qd, sd, 320, HC, qi, si, x_t, (32, 256, 8, 4))
         for a, b in zip(again, ref):
             assert torch.equal(a, b)
-        assert int(fx.tickets[:65].abs().sum()) == 0
+        assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
     assert not fx.wait_timeouts()
