@@ -387,8 +387,10 @@ bool launch_w8_splitk(GemvLaunch p, int C, size_t lds, int gx, hipStream_t st) {
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024) != hipSuccess)
+                            160 * 1024) != hipSuccess) {
+      (void)hipGetLastError();
       return false;
+    }
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, dim3(gx), dim3(64 * WPG), lds, st, p, C);
@@ -401,8 +403,10 @@ bool launch_w8_stream_cfg(GemvLaunch p, size_t lds, int gx, hipStream_t st) {
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024) != hipSuccess)
+                            160 * 1024) != hipSuccess) {
+      (void)hipGetLastError();
       return false;
+    }
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, dim3(gx), dim3(64 * T * KW), lds, st, p);
@@ -617,10 +621,15 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   const int n = lane & 15, g = lane >> 4;
   const int K = p.pa.K, J = K / 512;                 // units per tile
   const int64_t tiles = (p.N + 15) / 16;
-  const int64_t nw = (int64_t)gridDim.x * W, gw = (int64_t)blockIdx.x * W + wave;
-  const int64_t t0 = gw * tiles / nw, t1 = (gw + 1) * tiles / nw;
-  const int nt = (int)(t1 - t0);                     // >= 1 (host condition); with U < D the units
-                                                     // past U reload the last tile and are never read
+  // The workgroup's tiles [T0, T1) go to its waves as they free up: wave w
+  // starts on tile T0 + w and takes each further one from a counter in LDS.
+  // (Contiguous equal ranges per wave left the waves of one SIMD finishing
+  // one after another - the SIMD favours its oldest wave - so the last
+  // quarter of the kernel ran on a quarter of the waves.)
+  const int64_t nw = (int64_t)gridDim.x * W, g0 = (int64_t)blockIdx.x * W;
+  const int T0 = (int)(g0 * tiles / nw), T1 = (int)((g0 + W) * tiles / nw);   // T1 - T0 >= W (host condition)
+  __shared__ int s_next;
+  if (threadIdx.x == 0) s_next = T0 + W;              // (visible after the staging barrier below)
   const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
   char* ring = base + xbuf + wave * D * kInt2Unit;
   const int cb = K / 4, sbr = K / 8;                 // code and scale bytes per row
@@ -629,25 +638,40 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   const int dr = lane >> 3, dc = lane & 7;
   const int cA = dc ^ (dr >> 1), cB = dc ^ (4 + (dr >> 1));
   const int sr = lane >> 2, sp = (lane & 3) ^ ((sr >> 2) & 3);
-  const int U = nt * J;
-  int iq = 0, ij = 0, is = 0, issued = 0;
+  // issuer: the tile whose units go out (ij: next unit; a new tile is taken
+  // when its first unit is issued, never before the staging barrier since
+  // D <= J), the tiles taken so far (ngot), the last two of them (fifo)
+  int ij = 0, is = 0, issued = 0, ngot = 1;
+  bool need = false, idone = false;
+  int fifo[2] = {T0 + wave, 0};
   const uint8_t* iw = nullptr;
   const uint8_t* isb = nullptr;
   uint32_t o0 = 0, o1 = 0, os = 0;
-  auto set_tile = [&](int q) {
-    int64_t t = t0 + q;
-    if (t >= t1) t = t1 - 1 >= 0 ? t1 - 1 : 0;      // beyond the range: reload the last tile (not consumed)
-    const int64_t lim64 = (int64_t)p.N - 1 - t * 16;
+  auto set_tile = [&](int t) {
+    const int64_t lim64 = (int64_t)p.N - 1 - (int64_t)t * 16;
     const int lim = (int)(lim64 < 15 ? lim64 : 15);
-    iw = p.pa.w0 + t * 16 * cb;
-    isb = p.pa.s + t * 16 * sbr;
+    iw = p.pa.w0 + (int64_t)t * 16 * cb;
+    isb = p.pa.s + (int64_t)t * 16 * sbr;
     const int rA = dr < lim ? dr : lim, rB = dr + 8 < lim ? dr + 8 : lim, rS = sr < lim ? sr : lim;
     o0 = (uint32_t)(rA * cb + cA * 16);
     o1 = (uint32_t)(rB * cb + cB * 16);
     os = (uint32_t)(rS * sbr + sp * 16);
   };
-  set_tile(0);
+  set_tile(T0 + wave);
   auto issue_next = [&]() {
+    if (need) {
+      int t = 0;
+      if (lane == 0) t = atomicAdd(&s_next, 1);
+      t = __builtin_amdgcn_readfirstlane(t);
+      need = false;
+      if (t >= T1) {
+        idone = true;
+        return;
+      }
+      fifo[ngot & 1] = t;
+      ++ngot;
+      set_tile(t);
+    }
     char* l = ring + is * kInt2Unit;
     dma_b128(iw + ij * 128 + o0, l);
     dma_b128(iw + ij * 128 + o1, l + 1024);
@@ -656,11 +680,11 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
     ++issued;
     if (++ij == J) {
       ij = 0;
-      set_tile(++iq);
+      need = true;
     }
   };
-  // D units go out first (units past the wave's range reload its last tile
-  // and are never read), then the activations are staged while they fly.
+  // D units of the first tile go out first, then the activations are staged
+  // while they fly.
 #pragma unroll
   for (int u = 0; u < D; ++u) issue_next();
   {
@@ -694,7 +718,8 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   const uint32_t slB = rl + 2048 + n * 64 + (((2 + (g >> 1)) ^ sx) * 16) + (g & 1) * 8;
   const uint32_t xl = lds_addr(base) + xr * xrow + g * 128;   // chunk g of unit 0
   int cs = 0, u = 0;
-  for (int q = 0; q < nt; ++q) {
+  for (int q = 0; q < ngot; ++q) {                   // (ngot grows while tiles are taken)
+    const int64_t tq = fifo[q & 1];
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int j = 0; j < J; ++j, ++u) {
       if (issued - 1 - u >= D - 1) wait_vmcnt<3 * (D - 1)>();
@@ -717,9 +742,9 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
         }
       }
       if (++cs == D) cs = 0;
-      if (issued < U) issue_next();
+      if (!idone) issue_next();
     }
-    const int64_t row = (t0 + q) * 16 + n;           // lane (n, g) holds D[m = 4g + i][n]
+    const int64_t row = tq * 16 + n;                 // lane (n, g) holds D[m = 4g + i][n]
     if (row < p.N) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -738,7 +763,7 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
         key = max(key, (uint32_t)__builtin_amdgcn_mov_dpp((int)key, 0x4E, 0xF, 0xF, false));
         key = max(key, (uint32_t)__builtin_amdgcn_mov_dpp((int)key, 0x141, 0xF, 0xF, false));
         key = max(key, (uint32_t)__builtin_amdgcn_mov_dpp((int)key, 0x140, 0xF, 0xF, false));
-        if (n == 0 && g * 4 + i < p.M) p.smax[(int64_t)(g * 4 + i) * p.smax_stride + t0 + q] = (uint16_t)key;
+        if (n == 0 && g * 4 + i < p.M) p.smax[(int64_t)(g * 4 + i) * p.smax_stride + tq] = (uint16_t)key;
       }
     }
   }
@@ -746,19 +771,23 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
 }
 
 // The INT2 head (fp16 scales, G = 16) through the streaming kernel when the
-// matrix has at least 2 tiles per wave of the grid, or at least 1 when one
-// tile's units fill the ring (the 65k-token draft subset: 4075 tiles over
-// 8 waves per CU); false otherwise (or when FP4X_INT2_STREAM=0).  16 waves per
-// CU (ring depth 3) when the staged activations leave room, else 8 waves with
-// the deepest ring that fits.
+// matrix has at least one tile per wave of the grid and a tile's units fill
+// the ring (the 65k-token draft subset: 4075 tiles over 8 waves per CU);
+// false otherwise (or when FP4X_INT2_STREAM=0).  16 waves per CU (ring depth
+// 3) when the staged activations leave room, else 8 waves with the deepest
+// ring that fits.
+constexpr int kInt2DynLds = 160 * 1024 - 256;      // room for the kernel's static LDS (the tile counter)
+
 template <int W, int D>
 bool launch_int2_stream_wd(GemvLaunch p, size_t lds, hipStream_t st) {
   auto kern = int2_stream_kernel<W, D>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024) != hipSuccess)
+                            kInt2DynLds) != hipSuccess) {
+      (void)hipGetLastError();
       return false;
+    }
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, dim3(device_cus()), dim3(64 * W), lds, st, p);
@@ -774,8 +803,7 @@ inline bool launch_int2_stream(GemvLaunch p, hipStream_t st) {
   const size_t xb = (size_t)StreamGeom::xbuf_bytes(p.M, K);
   const int64_t cus = device_cus();
   auto fits = [&](int W, int D) {
-    return xb + (size_t)W * D * kInt2Unit <= 160 * 1024 &&
-           (tiles >= cus * W * 2 || (tiles >= cus * W && K / 512 >= D));
+    return xb + (size_t)W * D * kInt2Unit <= (size_t)kInt2DynLds && K / 512 >= D && tiles >= cus * W;
   };
   if (fits(16, 3)) return launch_int2_stream_wd<16, 3>(p, xb + (size_t)16 * 3 * kInt2Unit, st);
   if (fits(8, 6)) return launch_int2_stream_wd<8, 6>(p, xb + (size_t)8 * 6 * kInt2Unit, st);
