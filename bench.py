@@ -270,18 +270,21 @@ def bench_head(F, torch, dev, out, vectors=1000, n_x=128):
     coarse = F.int2_logits(x, P, S, V, out_dtype=torch.bfloat16)
     us = graph_time([lambda: F.topk_rows(coarse, C)] * 4, 10)
     out["E_topk512_M3"] = entry(us, M * V * 2 + M * C * 8)
-    # the coarse pass and the top-C in one call (slice maxima from the coarse kernel)
+    # the coarse pass and the top-C in one call (slice maxima from the coarse kernel);
+    # the fast head asks for the set only (it scatters exact logits at the indices)
     us = graph_time([lambda c=c: F.int2_topk(x, c[0], c[1], V, C) for c in copies], 10)
     out["E_int2_coarse_plus_topk512_M3"] = entry(us, int2_b + M * C * 8)
+    us = graph_time([lambda c=c: F.int2_topk(x, c[0], c[1], V, C, sorted=False) for c in copies], 10)
+    out["E_int2_coarse_plus_top512_set_M3"] = entry(us, int2_b + M * C * 8)
     # the exact rescore of 3 x 512 candidate rows, over n_x activation sets and their candidates
     xs = [torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_x)]
-    pairs = [F.int2_topk(xx, P, S, V, C) for xx in xs]
+    pairs = [F.int2_topk(xx, P, S, V, C, sorted=False) for xx in xs]
     ref_b = M * C * (K + K // 32 + 8) + M * K * 2 + M * C * 2
     us = graph_time([lambda i=i: F.refine_mx8_(pairs[i][0], xs[i], pairs[i][1], q, s) for i in range(n_x)], 5)
     out["E_refine_mx8_3x512_M3"] = dict(entry(us, ref_b), activation_sets=n_x)
 
     def head(xx, c):
-        co, ix = F.int2_topk(xx, c[0], c[1], V, C)
+        co, ix = F.int2_topk(xx, c[0], c[1], V, C, sorted=False)
         F.refine_mx8_(co, xx, ix, q, s)
     us = graph_time([lambda i=i: head(xs[i], copies[i % 3]) for i in range(n_x)], 3)
     out["E_fast_head_total_M3"] = {"us": round(us, 3), "activation_sets": n_x}
@@ -295,7 +298,7 @@ def bench_head(F, torch, dev, out, vectors=1000, n_x=128):
     for b0 in range(1000, 1000 + vectors, M):
         rng = torch.Generator(device=dev).manual_seed(b0)
         xs_ = torch.randn((M, K), generator=rng, device=dev).to(torch.bfloat16)
-        co, ix = F.int2_topk(xs_, P, S, V, C)
+        co, ix = F.int2_topk(xs_, P, S, V, C, sorted=False)
         fast = F.refine_mx8_(co, xs_, ix, q, s)
         full = F.mx8_linear(xs_, q, s, (32, 512, 1, 4))
         m = min(M, 1000 + vectors - b0)
@@ -327,7 +330,7 @@ def bench_draft(F, torch, dev, out):
     copies = [dict(st, c=(st["c"][0].clone(), st["c"][1].clone())) for _ in range(ncp)]
     us = graph_time([lambda c=c: fp4patch._draft_logits(F, x, c, V, DC) for c in copies], 10)
     out["F_draft_head_65k_int2_top64_nv4_M3"] = entry(us, int2_b + M * DC * (K // 2 + K // 16 + 8) + M * V * 2)
-    cand = F.int2_topk(x, *st["c"], NS, DC)[1]
+    cand = F.int2_topk(x, *st["c"], NS, DC, sorted=False)[1]
     us = graph_time([lambda: F.refine_nv4(x, cand, st["w"], st["s"], st["gs"])] * 4, 10)
     out["F_refine_nv4_3x64_M3"] = entry(us, M * DC * (K // 2 + K // 16 + 8) + M * K * 2 + M * DC * 4)
     nv4_b = NS * (K // 2 + K // 16) + M * K * 2 + M * NS * 2
@@ -548,7 +551,7 @@ def head_parity(F, torch, dev, head, batches):
     for b in range(batches):
         gx = torch.Generator(device=dev).manual_seed(5000 + b)
         x = torch.randn((M, K), generator=gx, device=dev).to(torch.bfloat16)
-        co, ix = F.int2_topk(x, P, S, V, C)
+        co, ix = F.int2_topk(x, P, S, V, C, sorted=False)
         out = F.refine_mx8_(co, x, ix, q, s)
         xs.append(x.view(torch.int16).cpu().numpy().view(np.uint16))
         sel.append(ix.cpu().numpy())

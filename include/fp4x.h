@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 8
+#define FP4X_ABI_VERSION 9
 
 enum {
   FP4X_OK = 0,
@@ -135,12 +135,16 @@ int64_t fp4x_topk_workspace_size(int M, int V);
  * target head, FP4X_DT_F32 for the draft head; 16-byte aligned rows of
  * coarse_stride elements), then fp4x_topk_rows of it into idx_out [M, C],
  * with the top-k's slice maxima written by the coarse kernel's epilogue where
- * it streams.  Results equal the two calls made separately.
+ * it streams.  Results equal the two calls made separately.  set_only != 0:
+ * the caller needs the selected set only (both heads scatter exact logits at
+ * these indices, so their order does not reach any result); the row's C
+ * indices then come in increasing index order for bf16 coarse logits, which
+ * skips the sort, and in fp4x_topk_rows' order for fp32 ones.
  * [int2_logits then torch.topk(coarse, C), x/fp4patch.py:371-377 (bf16);
  *  x/fp4patch.py:313-314 (fp32, the draft head)] */
 int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
                    void* coarse, int coarse_dtype, int64_t coarse_stride, int M, int N, int K, int G, int C,
-                   int64_t* idx_out, void* workspace, int64_t ws_bytes, void* stream);
+                   int64_t* idx_out, int set_only, void* workspace, int64_t ws_bytes, void* stream);
 
 /* fp4x_int2_topk with its workspace (the top-k's slice maxima) in a static
  * device array of the library, fp4x_int2_topk_noalloc_limit() = 1 MiB per
@@ -152,7 +156,7 @@ int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S
  * calls on one device share it, so calls that overlap in time race. */
 int fp4x_int2_topk_noalloc(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
                            void* coarse, int coarse_dtype, int64_t coarse_stride, int M, int N, int K, int G, int C,
-                           int64_t* idx_out, void* stream);
+                           int64_t* idx_out, int set_only, void* stream);
 int64_t fp4x_int2_topk_noalloc_limit(void);
 
 /* In place: out[m, idx[m, c]] = cast(sum_k float(e4m3(w)*2^(s-127)) * float(x[m, k])).

@@ -32,8 +32,8 @@ _SIGS = {
     "fp4x_int2_logits": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P], _I),
     "fp4x_topk_rows": ([_P, _I, _I64, _I, _I, _I, _P, _P, _I64, _P], _I),
     "fp4x_topk_workspace_size": ([_I, _I], _I64),
-    "fp4x_int2_topk": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I64, _I, _I, _I, _I, _I, _P, _P, _I64, _P], _I),
-    "fp4x_int2_topk_noalloc": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I64, _I, _I, _I, _I, _I, _P, _P], _I),
+    "fp4x_int2_topk": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I64, _I, _I, _I, _I, _I, _P, _I, _P, _I64, _P], _I),
+    "fp4x_int2_topk_noalloc": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I64, _I, _I, _I, _I, _I, _P, _I, _P], _I),
     "fp4x_int2_topk_noalloc_limit": ([], _I64),
     "fp4x_refine_mx8": ([_P, _I, _I64, _P, _P, _I, _I, _P, _P, _I, _I, _P], _I),
     "fp4x_refine_nv4": ([_P, _P, _P, _I, _I, _P, _P, ctypes.c_float, _I, _I, _P], _I),
@@ -51,7 +51,7 @@ _SIGS = {
     "fp4x_reload_env": ([], _I),
     "fp4x_read_ceiling": ([_P, _I64, _I, _I, _P, _P], _I),
 }
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _LIB = None
 

@@ -23,7 +23,7 @@ bool launch_mx8_stream_entry(GemvLaunch p, hipStream_t st);
 int topk_check(const void* logits, int dtype, int64_t stride, int M, int V, int C, void* workspace,
                int64_t ws_bytes);
 int topk_launch(const void* lg, int dtype, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
-                bool have_smax, hipStream_t st);
+                bool have_smax, bool set_only, hipStream_t st);
 int topk_slice_len(int V);
 int64_t topk_smax_stride(int V);
 template <bool F16S, class Epi> bool launch_w8_ktile(GemvLaunch p, hipStream_t st);
@@ -346,7 +346,7 @@ int fp4x_int2_logits(const void* x, int64_t x_stride, const void* P, const void*
 
 int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
                    void* coarse, int coarse_dtype, int64_t coarse_stride, int M, int N, int K, int G, int C,
-                   int64_t* idx_out, void* workspace, int64_t ws_bytes, void* stream) {
+                   int64_t* idx_out, int set_only, void* workspace, int64_t ws_bytes, void* stream) {
   int rc = topk_check(coarse, coarse_dtype, coarse_stride, M, N, C, workspace, ws_bytes);
   if (rc) return rc;
   if (M == 0) return FP4X_OK;
@@ -358,7 +358,7 @@ int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S
   rc = int2_coarse(x, x_stride, P, S, s_fmt, rs, coarse, coarse_dtype, coarse_stride, M, N, K, G,
                    fuse ? smax : nullptr, topk_smax_stride(N), st);
   if (rc < 0) return rc;
-  return topk_launch(coarse, coarse_dtype, coarse_stride, M, N, C, idx_out, smax, rc == 1, st);
+  return topk_launch(coarse, coarse_dtype, coarse_stride, M, N, C, idx_out, smax, rc == 1, set_only != 0, st);
 }
 
 }  // extern "C"

@@ -594,6 +594,26 @@ __device__ int rs_rank256(const uint32_t* a, int n, int* part) {
   return rank;
 }
 
+// The C largest of n_c (C <= n_c <= kRsThreads) bf16 candidates, for callers
+// that need the set only, in candidate (index) order: the C-th largest key16
+// T by radix select (one key per thread), then every candidate above T and
+// the first C - (count above T) at T, placed by two workgroup scans (the
+// first packs the counts above T and at T into one word).  Candidate t's
+// key16 is ck[t] >> 16; every thread of the workgroup calls it.
+__device__ void tk_select_set(const uint32_t* ck, const int* cidx, int n_c, int C, uint32_t* wh, TkHist& h,
+                              uint32_t* ext, int* slots, int64_t* out) {
+  const int t = threadIdx.x;
+  const uint32_t key[1] = {t < n_c ? ck[t] >> 16 : 0u};   // candidates' keys are >= T0 >= 1
+  const uint32_t T = rs_kth<1>(key, C, wh, h, ext);
+  const int above = key[0] > T ? 1 : 0, tie = key[0] != 0 && key[0] == T ? 1 : 0;
+  int tot;
+  const int pre = rs_scan(above | (tie << 16), slots, &tot);
+  const bool in = above || (tie && (pre >> 16) < C - (tot & 0xffff));
+  int n_in;
+  const int pos = rs_scan(in ? 1 : 0, slots, &n_in);
+  if (in) out[pos] = (int64_t)cidx[t];
+}
+
 // VPT: 8-slice vectors of the row's slice maxima per thread (1, 2 or 4, the
 // fewest that cover the row), so short rows run fewer register slots.  E:
 // the row's element type (Elem16 for bf16 logits, Elem32 for fp32).  The
@@ -602,7 +622,7 @@ __device__ int rs_rank256(const uint32_t* a, int n, int* part) {
 template <int VPT, class E>
 __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename E::T* logits, int64_t stride, int V,
                                                                  int C, const uint16_t* smax, int64_t sstride,
-                                                                 int64_t* idx_out) {
+                                                                 int64_t* idx_out, int set_only) {
   constexpr bool F32 = E::BITS == 32;
   constexpr int EPI = E::PER16;         // elements per 16-byte item
   // (the 64 entries past kTkCap of cand, ck, cidx and slist take the writes
@@ -749,6 +769,10 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
     tk_finish(cand, n_c, C, out);       // (full key, index) composites
     return;
   }
+  if (set_only && n_c <= kRsThreads) {             // the set in index order: no sort
+    tk_select_set(ck, cidx, n_c, C, wh, h, ext, slots, out);
+    return;
+  }
   // sort the candidates (positions follow the index order, so ties sort by index)
   if (n_c <= 256) {
     const int r = rs_rank256(ck, n_c, reinterpret_cast<int*>(wh));
@@ -864,7 +888,7 @@ int topk_check(const void* logits, int dtype, int64_t stride, int M, int V, int 
 // B (and A unless the slice maxima are already in the workspace).
 template <class E>
 static int topk_launch_t(const typename E::T* lg, int64_t stride, int M, int V, int C, int64_t* idx_out,
-                         uint16_t* smax, bool have_smax, hipStream_t st) {
+                         uint16_t* smax, bool have_smax, bool set_only, hipStream_t st) {
   const int S = tk_slice(V), ns = (V + S - 1) / S;
   const int64_t ss = tk_smax_stride(V);
   if (V > kTkCap && ns >= C && !have_smax)
@@ -872,15 +896,17 @@ static int topk_launch_t(const typename E::T* lg, int64_t stride, int M, int V, 
   const int nv = (ns + 7) / 8;
   auto kern = nv <= kRsThreads ? topk_rowsel_kernel<1, E> : nv <= 2 * kRsThreads ? topk_rowsel_kernel<2, E>
                                                                                : topk_rowsel_kernel<kRsVptMax, E>;
-  hipLaunchKernelGGL(kern, dim3(M), dim3(kRsThreads), 0, st, lg, stride, V, C, smax, ss, idx_out);
+  hipLaunchKernelGGL(kern, dim3(M), dim3(kRsThreads), 0, st, lg, stride, V, C, smax, ss, idx_out, set_only ? 1 : 0);
   return check_launch("topk");
 }
 
 int topk_launch(const void* lg, int dtype, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
-                bool have_smax, hipStream_t st) {
+                bool have_smax, bool set_only, hipStream_t st) {
   if (dtype == FP4X_DT_F32)
-    return topk_launch_t<Elem32>(static_cast<const uint32_t*>(lg), stride, M, V, C, idx_out, smax, have_smax, st);
-  return topk_launch_t<Elem16>(static_cast<const uint16_t*>(lg), stride, M, V, C, idx_out, smax, have_smax, st);
+    return topk_launch_t<Elem32>(static_cast<const uint32_t*>(lg), stride, M, V, C, idx_out, smax, have_smax,
+                                 set_only, st);
+  return topk_launch_t<Elem16>(static_cast<const uint16_t*>(lg), stride, M, V, C, idx_out, smax, have_smax,
+                               set_only, st);
 }
 }  // namespace fp4x
 
@@ -890,7 +916,7 @@ int fp4x_topk_rows(const void* logits, int dtype, int64_t stride, int M, int V, 
                    void* workspace, int64_t ws_bytes, void* stream) {
   int rc = topk_check(logits, dtype, stride, M, V, C, workspace, ws_bytes);
   if (rc || M == 0) return rc;
-  return topk_launch(logits, dtype, stride, M, V, C, idx_out, static_cast<uint16_t*>(workspace), false,
+  return topk_launch(logits, dtype, stride, M, V, C, idx_out, static_cast<uint16_t*>(workspace), false, false,
                      (hipStream_t)stream);
 }
 

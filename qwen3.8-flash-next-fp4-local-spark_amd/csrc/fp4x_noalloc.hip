@@ -66,7 +66,7 @@ int64_t fp4x_int2_topk_noalloc_limit(void) { return kScratchBytes; }
 
 int fp4x_int2_topk_noalloc(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
                            void* coarse, int coarse_dtype, int64_t coarse_stride, int M, int N, int K, int G, int C,
-                           int64_t* idx_out, void* stream) {
+                           int64_t* idx_out, int set_only, void* stream) {
   const int64_t need = fp4x_topk_workspace_size(M, N);
   if (need > kScratchBytes) {
     fp4x::set_error("int2_topk_noalloc: M rows of N logits need " + std::to_string(need) +
@@ -75,8 +75,8 @@ int fp4x_int2_topk_noalloc(const void* x, int64_t x_stride, const void* P, const
   }
   void* ws = scratch_on_current_device();
   if (!ws) return FP4X_ERR_LAUNCH;
-  return fp4x_int2_topk(x, x_stride, P, S, s_fmt, rs, coarse, coarse_dtype, coarse_stride, M, N, K, G, C, idx_out, ws,
-                        kScratchBytes, stream);
+  return fp4x_int2_topk(x, x_stride, P, S, s_fmt, rs, coarse, coarse_dtype, coarse_stride, M, N, K, G, C, idx_out,
+                        set_only, ws, kScratchBytes, stream);
 }
 
 }  // extern "C"

@@ -408,7 +408,7 @@ class _FastHead:
         if self.int2:
             P, S = self.coarse
             # int2_logits + top-C in one call (the coarse kernel also yields the top-k's slice maxima)
-            coarse, idx = F.int2_topk(h, P, S, self.w.shape[0], self.C)
+            coarse, idx = F.int2_topk(h, P, S, self.w.shape[0], self.C, sorted=False)
         else:
             P, S, gs = self.coarse
             coarse = F.nv4_linear(h, P, S, gs, (32, 256, 4))
@@ -468,7 +468,7 @@ def _draft_logits(F, h, st, vocab, dc, cfg=(32, 256, 4), inv_t=None):
     import torch
     if dc and h.shape[0] <= MAX_ROWS:
         # the top dc of the fp32 coarse logits (int2_logits' default dtype, as x/fp4patch.py:313-314 selects)
-        _, cand = F.int2_topk(h, *st["c"], st["idx"].numel(), dc, out_dtype=torch.float32)
+        _, cand = F.int2_topk(h, *st["c"], st["idx"].numel(), dc, out_dtype=torch.float32, sorted=False)
         vals = F.refine_nv4(h, cand, st["w"], st["s"], st["gs"])
         return F.scatter_draft(vals, cand, st["idx"], vocab, inv_t)
     sub = F.nv4_linear(h, st["w"], st["s"], st["gs"], cfg)

@@ -210,11 +210,14 @@ def int2_logits(x, P, S, N, BN=64, BK=512, nw=4, RS=None, out_dtype=torch.float3
     return out
 
 
-def int2_topk(x, P, S, N, C, RS=None, out_dtype=torch.bfloat16):
+def int2_topk(x, P, S, N, C, RS=None, out_dtype=torch.bfloat16, sorted=True):
     """The coarse stage of the fast head (bf16) or of the draft head (fp32):
     (coarse [M, N], idx int64 [M, C]) = (int2_logits(x, P, S, N, RS=RS,
     out_dtype=out_dtype), topk_rows(coarse, C)), in one call that lets the
-    coarse kernel produce the top-k's slice maxima."""
+    coarse kernel produce the top-k's slice maxima.  sorted=False: the same
+    index set per row, for callers that only scatter at these indices, in
+    increasing index order for bf16 logits (no sort) and in topk_rows' order
+    for fp32 ones."""
     _need_cuda(x, P, S)
     x = x.to(torch.bfloat16).contiguous()
     m, k = x.shape
@@ -233,7 +236,8 @@ def int2_topk(x, P, S, N, C, RS=None, out_dtype=torch.bfloat16):
         ws = _topk_workspace(x.device, nbytes)
         _L.check(_L.lib().fp4x_int2_topk(_ptr(x[m0:]), k, _ptr(P), _ptr(S), sfmt,
                                          _ptr(RS) if RS is not None else None, _ptr(coarse[m0:]), _dt(out_dtype), ld,
-                                         mb, N, k, G, C, _ptr(idx[m0:]), _ptr(ws), nbytes, st), "int2_topk")
+                                         mb, N, k, G, C, _ptr(idx[m0:]), 0 if sorted else 1, _ptr(ws), nbytes, st),
+                 "int2_topk")
     return coarse, idx
 
 

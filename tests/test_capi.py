@@ -71,8 +71,8 @@ def test_argument_errors_without_gpu(lib):
     # one u16 maximum per 16-element slice, rows padded to 8 slices
     assert L.fp4x_topk_workspace_size(3, 248320) == 3 * 15520 * 2
     assert L.fp4x_topk_workspace_size(1, 1 << 20) == (1 << 20) // 32 * 2     # 32-element slices past 2^19
-    assert L.fp4x_int2_topk(None, 2560, None, None, 2, None, None, 0, 100, 1, 248320, 2560, 16, 512, None, None, 0,
-                            None) == _fp4x.ERR_ARG                             # coarse stride < N
+    assert L.fp4x_int2_topk(None, 2560, None, None, 2, None, None, 0, 100, 1, 248320, 2560, 16, 512, None, 0, None,
+                            0, None) == _fp4x.ERR_ARG                          # coarse stride < N
     assert b"topk" in L.fp4x_last_error()
     assert L.fp4x_hc_up(None, 640, None, None, 1, None, 10240, None, 1, 640, 2560, 4, 3, None) == _fp4x.ERR_ARG
     # the whole mixer: shapes it cannot take reach the down projection's checks (M = 17; split-K without scratch)

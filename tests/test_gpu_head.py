@@ -239,7 +239,7 @@ def test_fast_head_full_size_32_batches(gpu, F):
     coarse_bits, sel, outs, full_am = [], [], [], []
     for x, _ in xs:
         xt = bf16_dev(x)
-        coarse, idx = F.int2_topk(xt, P, S, V, C)
+        coarse, idx = F.int2_topk(xt, P, S, V, C, sorted=False)
         coarse_bits.append(bf16_bits(coarse))
         sel.append(idx.cpu().numpy())
         outs.append(bf16_bits(F.refine_mx8_(coarse, xt, idx, q, s)))
@@ -265,8 +265,9 @@ def test_fast_head_full_size_32_batches(gpu, F):
     print(f"coarse bf16 flips against the rounded exact sums: {int(diff.sum())} of {diff.size} "
           f"(max |d| / bound {worst:.3g})")
     assert diff.mean() <= 1e-3
-    # selection: exact on the GPU's coarse; the oracle's set up to flipped entries
-    assert np.array_equal(sel, oh.topk_total_order(coarse_bits, C))
+    # selection (the set, in index order): exact on the GPU's coarse; the
+    # oracle's set up to flipped entries
+    assert np.array_equal(sel, np.sort(oh.topk_total_order(coarse_bits, C), 1))
     o_idx = oh.topk_total_order(o_coarse, C)
     same_set = 0
     for r in range(B * M):
@@ -357,6 +358,15 @@ def test_int2_topk_fused_equals_separate(gpu, F, V, M, rs, C, f32):
     assert torch.equal(idx, idx2)
     host = coarse.cpu().numpy() if f32 else bf16_bits(coarse)
     assert np.array_equal(idx.cpu().numpy(), oh.topk_total_order(host, C))
+    # sorted=False (the heads scatter at the indices): the same set per row, in
+    # increasing index order for bf16 logits, the sorted order for fp32 ones
+    coarse3, idx3 = F.int2_topk(xt, P, S, V, C, RS=R, out_dtype=dt, sorted=False)
+    assert torch.equal(coarse3.view(torch.int16 if not f32 else torch.int32),
+                       coarse.view(torch.int16 if not f32 else torch.int32))
+    if f32:
+        assert torch.equal(idx3, idx)
+    else:
+        assert torch.equal(idx3, torch.sort(idx, dim=1).values)
 
 
 # ------------------------------------------------------------------ draft head (NVFP4 rescore)

@@ -17,7 +17,7 @@ def _call(L, x, P, S, N, C, coarse, idx):
     m, k = x.shape
     return L.fp4x_int2_topk_noalloc(ctypes.c_void_p(x.data_ptr()), k, ctypes.c_void_p(P.data_ptr()),
                                     ctypes.c_void_p(S.data_ptr()), 2, None, ctypes.c_void_p(coarse.data_ptr()), 0,
-                                    coarse.stride(0), m, N, k, k // S.shape[1], C, ctypes.c_void_p(idx.data_ptr()),
+                                    coarse.stride(0), m, N, k, k // S.shape[1], C, ctypes.c_void_p(idx.data_ptr()), 0,
                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
 
 
@@ -45,5 +45,5 @@ def test_int2_topk_noalloc_matches_workspace_path(gpu):
         assert torch.equal(idx, want_i), (V, M)
     # 17 rows of a 2^20-element head need more than the static array: rejected, nothing launched
     rc = L.fp4x_int2_topk_noalloc(None, 2560, None, None, 2, None, None, 0, 1 << 20, 17, 1 << 20, 2560, 16, 64, None,
-                                  None)
+                                  0, None)
     assert rc == _fp4x.ERR_ARG and b"static workspace" in L.fp4x_last_error()
