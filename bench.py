@@ -267,9 +267,12 @@ def bench_head(F, torch, dev, out, vectors=1000, n_x=128):
     x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
     us = graph_time([lambda c=c: F.int2_logits(x, c[0], c[1], V, out_dtype=torch.bfloat16) for c in copies], 10)
     out["E_int2_coarse_248320x2560_M3"] = entry(us, int2_b)
-    coarse = F.int2_logits(x, P, S, V, out_dtype=torch.bfloat16)
-    us = graph_time([lambda: F.topk_rows(coarse, C)] * 4, 10)
-    out["E_topk512_M3"] = entry(us, M * V * 2 + M * C * 8)
+    # the top-C alone over 16 coarse outputs of different activations, one graph
+    coarses = [F.int2_logits(torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16), P, S, V,
+                             out_dtype=torch.bfloat16) for _ in range(16)]
+    us = graph_time([lambda co=co: F.topk_rows(co, C) for co in coarses], 10)
+    out["E_topk512_M3"] = dict(entry(us, M * V * 2 + M * C * 8), coarse_sets=len(coarses))
+    del coarses
     # the coarse pass and the top-C in one call (slice maxima from the coarse kernel);
     # the fast head asks for the set only (it scatters exact logits at the indices)
     us = graph_time([lambda c=c: F.int2_topk(x, c[0], c[1], V, C) for c in copies], 10)
@@ -330,9 +333,15 @@ def bench_draft(F, torch, dev, out):
     copies = [dict(st, c=(st["c"][0].clone(), st["c"][1].clone())) for _ in range(ncp)]
     us = graph_time([lambda c=c: fp4patch._draft_logits(F, x, c, V, DC) for c in copies], 10)
     out["F_draft_head_65k_int2_top64_nv4_M3"] = entry(us, int2_b + M * DC * (K // 2 + K // 16 + 8) + M * V * 2)
-    cand = F.int2_topk(x, *st["c"], NS, DC, sorted=False)[1]
-    us = graph_time([lambda: F.refine_nv4(x, cand, st["w"], st["s"], st["gs"])] * 4, 10)
-    out["F_refine_nv4_3x64_M3"] = entry(us, M * DC * (K // 2 + K // 16 + 8) + M * K * 2 + M * DC * 4)
+    # the exact rescore alone, over n_x activation sets and their own candidates
+    # (rows not read by the previous call), one graph
+    n_x = 64
+    xs = [torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_x)]
+    cands = [F.int2_topk(xx, *st["c"], NS, DC, sorted=False)[1] for xx in xs]
+    us = graph_time([lambda i=i: F.refine_nv4(xs[i], cands[i], st["w"], st["s"], st["gs"]) for i in range(n_x)], 5)
+    out["F_refine_nv4_3x64_M3"] = dict(entry(us, M * DC * (K // 2 + K // 16 + 8) + M * K * 2 + M * DC * 4),
+                                       activation_sets=n_x)
+    del xs, cands
     nv4_b = NS * (K // 2 + K // 16) + M * K * 2 + M * NS * 2
     ncp = copies_for(nv4_b)
     wc = [(st["w"].clone(), st["s"].clone()) for _ in range(ncp)]
