@@ -626,8 +626,12 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   // (Contiguous equal ranges per wave left the waves of one SIMD finishing
   // one after another - the SIMD favours its oldest wave - so the last
   // quarter of the kernel ran on a quarter of the waves.)
+  // A wave whose first tile T0 + w is past T1 (a workgroup of fewer tiles
+  // than waves) issues and computes nothing; it only helps stage the
+  // activations.
   const int64_t nw = (int64_t)gridDim.x * W, g0 = (int64_t)blockIdx.x * W;
-  const int T0 = (int)(g0 * tiles / nw), T1 = (int)((g0 + W) * tiles / nw);   // T1 - T0 >= W (host condition)
+  const int T0 = (int)(g0 * tiles / nw), T1 = (int)((g0 + W) * tiles / nw);   // T1 - T0 >= W / 2 - 1 (host condition)
+  const bool act = T0 + wave < T1;
   __shared__ int s_next;
   if (threadIdx.x == 0) s_next = T0 + W;              // (visible after the staging barrier below)
   const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
@@ -641,8 +645,8 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   // issuer: the tile whose units go out (ij: next unit; a new tile is taken
   // when its first unit is issued, never before the staging barrier since
   // D <= J), the tiles taken so far (ngot), the last two of them (fifo)
-  int ij = 0, is = 0, issued = 0, ngot = 1;
-  bool need = false, idone = false;
+  int ij = 0, is = 0, issued = 0, ngot = act ? 1 : 0;
+  bool need = false, idone = !act;
   int fifo[2] = {T0 + wave, 0};
   const uint8_t* iw = nullptr;
   const uint8_t* isb = nullptr;
@@ -657,7 +661,7 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
     o1 = (uint32_t)(rB * cb + cB * 16);
     os = (uint32_t)(rS * sbr + sp * 16);
   };
-  set_tile(T0 + wave);
+  set_tile(act ? T0 + wave : T0);
   auto issue_next = [&]() {
     if (need) {
       int t = 0;
@@ -685,8 +689,10 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   };
   // D units of the first tile go out first, then the activations are staged
   // while they fly.
+  if (act) {
 #pragma unroll
-  for (int u = 0; u < D; ++u) issue_next();
+    for (int u = 0; u < D; ++u) issue_next();
+  }
   {
     const int per_row = K / 16, total = p.M * per_row;
     const uint4* xg4 = reinterpret_cast<const uint4*>(p.x);
@@ -771,8 +777,8 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
 }
 
 // The INT2 head (fp16 scales, G = 16) through the streaming kernel when the
-// matrix has at least one tile per wave of the grid and a tile's units fill
-// the ring (the 65k-token draft subset: 4075 tiles over 8 waves per CU);
+// matrix has at least one tile per two waves of the grid and a tile's units
+// fill the ring (the 65k-token draft subset: 4075 tiles over 16 waves per CU);
 // false otherwise (or when FP4X_INT2_STREAM=0).  16 waves per CU (ring depth
 // 3) when the staged activations leave room, else 8 waves with the deepest
 // ring that fits.
@@ -803,7 +809,7 @@ inline bool launch_int2_stream(GemvLaunch p, hipStream_t st) {
   const size_t xb = (size_t)StreamGeom::xbuf_bytes(p.M, K);
   const int64_t cus = device_cus();
   auto fits = [&](int W, int D) {
-    return xb + (size_t)W * D * kInt2Unit <= (size_t)kInt2DynLds && K / 512 >= D && tiles >= cus * W;
+    return xb + (size_t)W * D * kInt2Unit <= (size_t)kInt2DynLds && K / 512 >= D && 2 * tiles >= cus * W;
   };
   if (fits(16, 3)) return launch_int2_stream_wd<16, 3>(p, xb + (size_t)16 * 3 * kInt2Unit, st);
   if (fits(8, 6)) return launch_int2_stream_wd<8, 6>(p, xb + (size_t)8 * 6 * kInt2Unit, st);
