@@ -289,17 +289,19 @@ def test_fast_head_full_size_32_batches(gpu, F):
 
 
 # ------------------------------------------------------------------ INT2 streaming kernel
-@pytest.mark.parametrize("M,rs,one,K", [(3, False, False, 2560), (16, False, False, 2560), (3, True, False, 2560),
-                                        (3, False, True, 2560), (3, False, False, 1536)])
+@pytest.mark.parametrize("M,rs,one,K", [(3, False, 0, 2560), (16, False, 0, 2560), (3, True, 0, 2560),
+                                        (3, False, 1, 2560), (3, False, 2, 2560), (3, False, 0, 1536)])
 def test_int2_stream(gpu, F, M, rs, one, K, monkeypatch):
-    """Heads of at least 2 tiles per wave of the grid take the streaming kernel
-    (one wave per tile, LDS ring of direct loads); N tail of 40 rows.  one:
-    between 1 and 2 tiles per wave at 8 waves per CU (the 65,197-row draft
-    subset on 256 CUs), 3 rows past the last full tile; K = 1536: three units
-    per tile instead of five."""
+    """Heads of at least one tile per two waves of the grid take the streaming
+    kernel (16 waves per CU, LDS ring of direct loads); N tail of 40 rows.
+    one = 1: just under one tile per wave (the 65,197-row draft subset on 256
+    CUs: some workgroups have a wave with no tile), 3 rows past the last full
+    tile; one = 2: 10 tiles per CU (six waves of a workgroup without a tile),
+    5 rows past the last full tile; K = 1536: three units per tile instead of
+    five."""
     rng = np.random.default_rng(77 + M + rs + 5 * one + K)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    V = 16 * (16 * cus - 21) - 3 if one else 4 * 8 * 16 * cus + 40
+    V = {0: 4 * 8 * 16 * cus + 40, 1: 16 * (16 * cus - 21) - 3, 2: 16 * 10 * cus - 5}[one]
     w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
     P, S = oq.quantize_int2(w, group=16)
     del w
