@@ -196,7 +196,9 @@ struct HcMixArgs {
 constexpr int kMixMaxHc = 4;                     // streams the single-launch mixer takes
 constexpr int kMixOutPer = 2;                    // epilogue outputs per thread
 
-template <bool F16S, int KW, int CPS>
+// SPLIT: the up tiles have workgroups of their own (grid = D + up
+// workgroups).
+template <bool F16S, int KW, int CPS, bool SPLIT>
 __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   using F = FmtW8<F16S>;
   constexpr int DP = 4 * KW;
@@ -235,6 +237,15 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
       }
     }
   }
+
+  // SPLIT: a down item's workgroup is done here; it would only recompute the
+  // last up tile as padding, and wait and read the bottleneck for it
+  // (measured: the served mixer 11.4 -> 11.1 us).  Its flag still advances,
+  // unread.  (With up tiles in the down items' workgroups, the same exit for
+  // the workgroups past the up tiles made the synthetic mixer slower, 12.6 ->
+  // 12.8 us, and so did the test alone compiled into its kernel.)
+  if constexpr (SPLIT)
+    if ((int)blockIdx.x < a.D) return;
 
   // 2. the up tiles' weights (one batch per lane) stream during the wait (at
   //    once in a workgroup without a down item)
@@ -327,9 +338,9 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
 // The plan keeps the dynamic LDS within 150 KB (the kernel also has a few
 // bytes of static LDS); a failed attribute call is cleared so that the
 // two-launch fallback does not report it.
-template <bool F16S, int KW>
+template <bool F16S, int KW, bool SPLIT>
 static bool launch_hc_mix(const HcMixArgs& a, int P, size_t lds, hipStream_t st) {
-  auto kern = hc_mix_kernel<F16S, KW, 1>;
+  auto kern = hc_mix_kernel<F16S, KW, 1, SPLIT>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -496,7 +507,8 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   const int R = 8 / WT, ntu = H / bj, D = tiles_d * C, cus = device_cus();
   if (hc > kMixMaxHc || R * M * bj > kMixOutPer * 512) return two();
   const int need_u = (ntu + R - 1) / R;
-  const int P = D + need_u <= cus ? D + need_u : (D > need_u ? D : need_u);
+  const bool split = D + need_u <= cus;
+  const int P = split ? D + need_u : (D > need_u ? D : need_u);
   if (P > cus) return two();
   const size_t lds_u = (((size_t)M * lr * 2 + 15) & ~(size_t)15) + (size_t)R * (T / 16) * (KW - 1) * 1024 +
                        (size_t)R * M * T * 4;
@@ -522,11 +534,19 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   hipStream_t st = (hipStream_t)stream;
   bool launched;
   if (s_dtype == FP4X_DT_F16)
-    launched = KW == 1 ? launch_hc_mix<true, 1>(a, P, lds, st) : KW == 2 ? launch_hc_mix<true, 2>(a, P, lds, st)
-                                                                    : launch_hc_mix<true, 4>(a, P, lds, st);
+    launched = split ? (KW == 1   ? launch_hc_mix<true, 1, true>(a, P, lds, st)
+                        : KW == 2 ? launch_hc_mix<true, 2, true>(a, P, lds, st)
+                                  : launch_hc_mix<true, 4, true>(a, P, lds, st))
+                     : (KW == 1   ? launch_hc_mix<true, 1, false>(a, P, lds, st)
+                        : KW == 2 ? launch_hc_mix<true, 2, false>(a, P, lds, st)
+                                  : launch_hc_mix<true, 4, false>(a, P, lds, st));
   else
-    launched = KW == 1 ? launch_hc_mix<false, 1>(a, P, lds, st) : KW == 2 ? launch_hc_mix<false, 2>(a, P, lds, st)
-                                                                     : launch_hc_mix<false, 4>(a, P, lds, st);
+    launched = split ? (KW == 1   ? launch_hc_mix<false, 1, true>(a, P, lds, st)
+                        : KW == 2 ? launch_hc_mix<false, 2, true>(a, P, lds, st)
+                                  : launch_hc_mix<false, 4, true>(a, P, lds, st))
+                     : (KW == 1   ? launch_hc_mix<false, 1, false>(a, P, lds, st)
+                        : KW == 2 ? launch_hc_mix<false, 2, false>(a, P, lds, st)
+                                  : launch_hc_mix<false, 4, false>(a, P, lds, st));
   if (!launched) return two();
   return check_launch("hc_mix");
 }
