@@ -243,7 +243,7 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   // (measured: the served mixer 11.4 -> 11.1 us).  Its flag still advances,
   // unread.  (With up tiles in the down items' workgroups, the same exit for
   // the workgroups past the up tiles made the synthetic mixer slower, 12.6 ->
-  // 12.8 us, and so did the test alone compiled into its kernel.)
+  // 12.8 us, also as an instance of its own.)
   if constexpr (SPLIT)
     if ((int)blockIdx.x < a.D) return;
 
