@@ -267,6 +267,19 @@ def bench_head(F, torch, dev, out, vectors=1000, n_x=128):
     x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
     us = graph_time([lambda c=c: F.int2_logits(x, c[0], c[1], V, out_dtype=torch.bfloat16) for c in copies], 10)
     out["E_int2_coarse_248320x2560_M3"] = entry(us, int2_b)
+    # the variant with e4m3 group scales and an fp32 scale per row (the MFMA core: the streaming kernel
+    # takes fp16 scales); its copy from the torch quantizer, three copies rotated
+    wf = F.mx8_dequant(q, s)
+    P8, S8, R8 = F.quantize_int2(wf, scale_fmt="e4m3", group=16)
+    del wf
+    torch.cuda.empty_cache()
+    copies8 = [(P8.clone(), S8.clone(), R8.clone()) for _ in range(2)] + [(P8, S8, R8)]
+    us = graph_time([lambda c=c: F.int2_logits(x, c[0], c[1], V, RS=c[2], out_dtype=torch.bfloat16)
+                     for c in copies8], 10)
+    out["E_int2_e4m3_rowscale_coarse_248320x2560_M3"] = entry(us, V * K // 4 + V * (K // 16) + V * 4 + M * K * 2 +
+                                                               M * V * 2)
+    del copies8, P8, S8, R8
+    torch.cuda.empty_cache()
     # the top-C alone over 16 coarse outputs of different activations, one graph
     coarses = [F.int2_logits(torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16), P, S, V,
                              out_dtype=torch.bfloat16) for _ in range(16)]

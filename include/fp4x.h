@@ -59,7 +59,7 @@ enum {
 
 /* weight-preparation sources and targets (fp4x_quantize, fp4x_absmax) */
 enum { FP4X_SRC_F32 = 0, FP4X_SRC_BF16 = 1, FP4X_SRC_MX8 = 2, FP4X_SRC_NV4 = 3 };
-enum { FP4X_Q_W8 = 0, FP4X_Q_W6 = 1, FP4X_Q_NV4 = 2, FP4X_Q_INT2 = 3 };
+enum { FP4X_Q_W8 = 0, FP4X_Q_W6 = 1, FP4X_Q_NV4 = 2, FP4X_Q_INT2 = 3, FP4X_Q_INT2_E4M3 = 4 };
 
 const char* fp4x_last_error(void);
 int fp4x_abi_version(void);
@@ -193,10 +193,12 @@ int fp4x_scatter_draft(void* out, int64_t out_stride, const float* vals, const i
  *   FP4X_Q_W6   out0 L [N, K/2], out1 H [N, K/4], out2 fp16 S [N, K/32]; qmax 1..31
  *   FP4X_Q_NV4  out0 P [N, K/2], out1 e4m3fn S [N, K/16]; dst_gs the global scale
  *   FP4X_Q_INT2 out0 P [N, K/4], out1 fp16 S [N, K/G]; G = 16, 32 or 64
+ *   FP4X_Q_INT2_E4M3 out0 P [N, K/4], out1 e4m3fn S [N, K/G], out2 fp32 row
+ *               scales [N]; G = 16, 32 or 64 (scale_fmt "e4m3")
  * Results equal the reference's torch quantizers evaluated in fp32 with IEEE
  * division.  16-byte aligned sources and out0.
  * [quantize_w8 :138-144, quantize_w6 :179-202 (clip_search = 0), quantize_nv4
- *  :277-300, quantize_int2 :330-351 (fp16 scales); the weight preparation of
+ *  :277-300, quantize_int2 :330-351 (fp16 or e4m3 scales); the weight preparation of
  *  x/fp4patch.py:61-83, :179-182, :211-214, :357-359] */
 int fp4x_quantize(int src, const void* src_a, const void* src_b, float src_gs, int64_t N, int K, int dst, int G,
                   int qmax, float dst_gs, void* out0, void* out1, void* out2, void* stream);

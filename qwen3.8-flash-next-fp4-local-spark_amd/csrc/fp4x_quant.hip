@@ -1,7 +1,7 @@
 // Weight preparation on the device: the reference's pure-torch quantizers
 // (x/fp4x_kernels.py: quantize_w8 :138-144, quantize_w6 :179-202 without the
-// clip search, quantize_nv4 :277-300, quantize_int2 :330-351 with fp16 scales)
-// as one thread per quantization group.
+// clip search, quantize_nv4 :277-300, quantize_int2 :330-351 with fp16 scales,
+// or e4m3 scales under an fp32 row scale) as one thread per quantization group.
 //
 // The source rows are fp32, bf16, or packed MXFP8 / NVFP4 rows decoded in
 // registers with the exact dequant of mx8_dequant (:261-267) or dequant_nv4
@@ -112,7 +112,8 @@ struct SrcNV4 {
 
 __device__ __forceinline__ float f16_round(float v) { return (float)(_Float16)v; }
 
-// Positive fp32 v in [2^-9, 448] -> e4m3fn code, round to nearest even.
+// Non-negative fp32 v < 464 -> e4m3fn code, round to nearest even (below
+// 2^-6 the subnormal step 2^-9; below 2^-10, and at it, code 0).
 __device__ __forceinline__ uint32_t e4m3_code(float v) {
   int e = (int)((__float_as_uint(v) >> 23) & 0xff) - 127;
   if (e < -6) e = -6;                                  // subnormal step 2^-9
@@ -214,9 +215,27 @@ struct QNV4 {
   }
 };
 
-// INT2 with fp16 group scales: s = fp16(max(amax, 1e-8) / 1.5), code =
-// clamp(floor(w / s) + 2, 0, 3) (0 where w / s is NaN: a zero group whose
-// scale underflows fp16), element j of a 4-group in bit pair (0, 2, 1, 3)[j].
+// The G 2-bit codes clamp(floor(w / sf) + 2, 0, 3) of one INT2 group (0 where
+// w / sf is NaN: a zero element of a group whose scale underflows), element j
+// of a 4-group in bit pair (0, 2, 1, 3)[j], stored at o (G / 4 bytes).
+template <int G>
+__device__ __forceinline__ void put_int2_codes(const float (&f)[G], float sf, uint8_t* o) {
+  uint32_t b[G / 16];
+#pragma unroll
+  for (int i = 0; i < G / 16; ++i) b[i] = 0;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const uint32_t c = (uint32_t)fminf(fmaxf(floorf(f[i] / sf) + 2.0f, 0.0f), 3.0f);
+    const int pair = (i & 3) == 1 ? 2 : (i & 3) == 2 ? 1 : (i & 3);
+    b[i >> 4] |= c << (2 * pair + 8 * ((i >> 2) & 3));
+  }
+  uint32_t* o32 = reinterpret_cast<uint32_t*>(o);
+#pragma unroll
+  for (int i = 0; i < G / 16; ++i) o32[i] = b[i];
+}
+
+// INT2 with fp16 group scales: s = fp16(max(amax, 1e-8) / 1.5) (a zero group's
+// scale underflows fp16 to 0, and its codes are 0).
 template <int GG>
 struct QInt2 {
   static constexpr int G = GG;
@@ -224,20 +243,27 @@ struct QInt2 {
   uint16_t* S;
   __device__ void put(int64_t row, int gi, int K, const float (&f)[G]) const {
     const _Float16 s16 = (_Float16)(fmaxf(group_amax(f), 1e-8f) / 1.5f);
-    const float sf = (float)s16;
-    uint32_t b[G / 16];
-#pragma unroll
-    for (int i = 0; i < G / 16; ++i) b[i] = 0;
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const uint32_t c = (uint32_t)fminf(fmaxf(floorf(f[i] / sf) + 2.0f, 0.0f), 3.0f);
-      const int pair = (i & 3) == 1 ? 2 : (i & 3) == 2 ? 1 : (i & 3);
-      b[i >> 4] |= c << (2 * pair + 8 * ((i >> 2) & 3));
-    }
-    uint32_t* o = reinterpret_cast<uint32_t*>(P + row * (K / 4) + gi * (G / 4));
-#pragma unroll
-    for (int i = 0; i < G / 16; ++i) o[i] = b[i];
+    put_int2_codes(f, (float)s16, P + row * (K / 4) + gi * (G / 4));
     S[row * (K / G) + gi] = __builtin_bit_cast(uint16_t, s16);
+  }
+};
+
+// INT2 with e4m3fn group scales under an fp32 row scale rs = R[row] (written
+// by int2e_rows_kernel first): S = e4m3(s / rs) for s = max(amax, 1e-8) / 1.5,
+// codes against sf = float(S) * rs.  A group whose s / rs rounds to e4m3 0
+// (amax below about 2^-10 / 448 of the row's largest) has sf = 0: its codes
+// are 3, 0 and 0 for positive, negative and zero elements.
+template <int GG>
+struct QInt2E {
+  static constexpr int G = GG;
+  uint8_t* P;
+  uint8_t* S;
+  const float* R;
+  __device__ void put(int64_t row, int gi, int K, const float (&f)[G]) const {
+    const float rs = R[row];
+    const uint32_t code = e4m3_code((fmaxf(group_amax(f), 1e-8f) / 1.5f) / rs);
+    put_int2_codes(f, e4m3_value(code) * rs, P + row * (K / 4) + gi * (G / 4));
+    S[row * (K / G) + gi] = (uint8_t)code;
   }
 };
 
@@ -271,6 +297,25 @@ __global__ __launch_bounds__(256) void absmax_kernel(Src src, int64_t N, int K, 
   if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(m));
 }
 
+// Row scales of the e4m3 INT2 target, one wave per row: R[row] =
+// (max(row amax, 1e-8) / 1.5) / 448, the largest group scale of the row over
+// 448 (the rounded quotient max(a, 1e-8) / 1.5 is monotonic in a, so the row
+// maximum of the group scales is the scale of the row's amax).
+template <class Src>
+__global__ __launch_bounds__(256) void int2e_rows_kernel(Src src, int64_t N, int K, float* R) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= N) return;                                  // uniform over the wave
+  float m = 0.0f;
+  for (int g = threadIdx.x & 63; g < K / 16; g += 64) {
+    float f[16];
+    src.template load<16>(row, g * 16, f);
+    m = fmaxf(m, group_amax(f));
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  if ((threadIdx.x & 63) == 0) R[row] = (fmaxf(m, 1e-8f) / 1.5f) / 448.0f;
+}
+
 static bool al(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 template <class Src, class Q>
@@ -292,6 +337,18 @@ static int dispatch_q(const Src& src, int64_t N, int K, int dst, int G, int qmax
                       N, K, st);
     case FP4X_Q_NV4:
       return launch_q(src, QNV4{static_cast<uint8_t*>(o0), static_cast<uint8_t*>(o1), gs}, N, K, st);
+    case FP4X_Q_INT2_E4M3: {
+      uint8_t* P = static_cast<uint8_t*>(o0);
+      uint8_t* S = static_cast<uint8_t*>(o1);
+      float* R = static_cast<float*>(o2);
+      if (N == 0) return FP4X_OK;
+      hipLaunchKernelGGL(int2e_rows_kernel<Src>, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, src, N, K, R);
+      int rc = check_launch("quantize (row scales)");
+      if (rc) return rc;
+      if (G == 16) return launch_q(src, QInt2E<16>{P, S, R}, N, K, st);
+      if (G == 32) return launch_q(src, QInt2E<32>{P, S, R}, N, K, st);
+      return launch_q(src, QInt2E<64>{P, S, R}, N, K, st);
+    }
     default:
       if (G == 16) return launch_q(src, QInt2<16>{static_cast<uint8_t*>(o0), static_cast<uint16_t*>(o1)}, N, K, st);
       if (G == 32) return launch_q(src, QInt2<32>{static_cast<uint8_t*>(o0), static_cast<uint16_t*>(o1)}, N, K, st);
@@ -319,12 +376,14 @@ int fp4x_quantize(int src, const void* src_a, const void* src_b, float src_gs, i
                   int qmax, float dst_gs, void* out0, void* out1, void* out2, void* stream) {
   int rc = src_check(src, src_a, src_b, N, K);
   if (rc) return rc;
-  if (dst < FP4X_Q_W8 || dst > FP4X_Q_INT2 || (dst == FP4X_Q_INT2 && G != 16 && G != 32 && G != 64) ||
+  const bool int2 = dst == FP4X_Q_INT2 || dst == FP4X_Q_INT2_E4M3;
+  if (dst < FP4X_Q_W8 || dst > FP4X_Q_INT2_E4M3 || (int2 && G != 16 && G != 32 && G != 64) ||
       (dst == FP4X_Q_W6 && (qmax < 1 || qmax > 31)) || (dst == FP4X_Q_NV4 && !(dst_gs > 0.0f))) {
     set_error("quantize: bad target (INT2 group 16, 32 or 64; W6 qmax 1..31; NVFP4 gs > 0)");
     return FP4X_ERR_ARG;
   }
-  if (!al(out0, 16) || !out1 || (dst == FP4X_Q_W6 && !out2)) {
+  if (!al(out0, 16) || !out1 || ((dst == FP4X_Q_W6 || dst == FP4X_Q_INT2_E4M3) && !out2) ||
+      (dst == FP4X_Q_INT2_E4M3 && !al(out2, 4))) {
     set_error("quantize: the packed output must be 16-byte aligned, and every output plane given");
     return FP4X_ERR_ARG;
   }

@@ -499,7 +499,7 @@ _E2M1 = {}
 
 # HIP weight preparation
 _SRC_F32, _SRC_BF16, _SRC_MX8, _SRC_NV4 = 0, 1, 2, 3
-_Q_W8, _Q_W6, _Q_NV4, _Q_INT2 = 0, 1, 2, 3
+_Q_W8, _Q_W6, _Q_NV4, _Q_INT2, _Q_INT2_E4M3 = 0, 1, 2, 3, 4
 
 
 def _hip_src(w):
@@ -519,7 +519,8 @@ def _hip_quantize(src, n, k, dst, G=16, qmax=31, gs=0.0):
     shapes = {_Q_W8: [(k, torch.int8), (k // 64, torch.float32)],
               _Q_W6: [(k // 2, torch.uint8), (k // 4, torch.uint8), (k // 32, torch.float16)],
               _Q_NV4: [(k // 2, torch.uint8), (k // 16, torch.float8_e4m3fn)],
-              _Q_INT2: [(k // 4, torch.uint8), (k // G, torch.float16)]}[dst]
+              _Q_INT2: [(k // 4, torch.uint8), (k // G, torch.float16)],
+              _Q_INT2_E4M3: [(k // 4, torch.uint8), (k // G, torch.float8_e4m3fn), (1, torch.float32)]}[dst]
     outs = [torch.empty((n, c), dtype=dt, device=dev) for c, dt in shapes]
     o = [_ptr(t) for t in outs] + [None] * (3 - len(outs))
     _L.check(_L.lib().fp4x_quantize(kind, _ptr(a), None if b is None else _ptr(b), float(sgs), n, k, dst, G, qmax,
@@ -662,10 +663,14 @@ def quantize_nv4(w, rows=2048):
 @torch.no_grad()
 def quantize_int2(weight, scale_fmt="fp16", group=16):
     """INT2 per group (levels -1.5..1.5 x s): fp16 -> (P, S); e4m3 -> (P, S_e4m3, row_scale fp32).
-    HIP kernel for device fp32/bf16 matrices with fp16 scales and G = 16, 32, 64."""
+    HIP kernels for device fp32/bf16 matrices and G = 16, 32, 64 (any scale_fmt
+    other than "fp16" is the e4m3 form, as in the reference)."""
     src = _hip_src(weight)
-    if src is not None and scale_fmt == "fp16" and group in (16, 32, 64):
-        return tuple(_hip_quantize(src, weight.shape[0], weight.shape[1], _Q_INT2, G=group))
+    if src is not None and group in (16, 32, 64):
+        if scale_fmt == "fp16":
+            return tuple(_hip_quantize(src, weight.shape[0], weight.shape[1], _Q_INT2, G=group))
+        P, S, R = _hip_quantize(src, weight.shape[0], weight.shape[1], _Q_INT2_E4M3, G=group)
+        return P, S, R.view(-1)
     n, k = weight.shape
     P = torch.empty((n, k // 4), dtype=torch.uint8, device=weight.device)
     S = torch.empty((n, k // group), dtype=torch.float16 if scale_fmt == "fp16" else torch.float8_e4m3fn,

@@ -1,6 +1,6 @@
 """Weight preparation on the GPU (csrc/fp4x_quant.hip): the HIP quantizers
 equal the oracle's quantizers bit for bit (codes, scales, the NVFP4 global
-scale) for fp32, bf16, MXFP8 and NVFP4 sources, on the reference's golden
+scale, the e4m3 INT2 row scales) for fp32, bf16, MXFP8 and NVFP4 sources, on the reference's golden
 vectors, on random matrices with degenerate groups, and on the NVFP4
 midpoint case where fp32 and fp64 evaluation differ."""
 import numpy as np
@@ -38,7 +38,8 @@ def same(a, b):
 
 
 def check(fmt, got, w, group=16, qmax=31):
-    """got (device tuple) against the oracle quantizer of fp32 weights w."""
+    """got (device tuple) against the oracle quantizer of fp32 weights w
+    (fmt "int2e": INT2 with e4m3 group scales and fp32 row scales)."""
     if fmt == "w8":
         want = oq.quantize_w8(w)
     elif fmt == "w6":
@@ -47,8 +48,11 @@ def check(fmt, got, w, group=16, qmax=31):
         want = oq.quantize_nv4(w)
         assert got[2] == want[2], (got[2], want[2])                # gs, the python float
         got, want = got[:2], want[:2]
+    elif fmt == "int2e":
+        want = oq.quantize_int2(w, scale_fmt="e4m3", group=group)
     else:
         want = oq.quantize_int2(w, group=group)
+    assert len(got) == len(want)
     for i, (g, t) in enumerate(zip(got, want)):
         assert same(np_(g), t), (fmt, i, int((np_(g).reshape(-1) != np.asarray(t).reshape(-1)).sum()))
 
@@ -63,6 +67,9 @@ def test_golden_vectors(gpu, F, golden):
     for grp in (16, 32):
         P, S = F.quantize_int2(dev(golden["int2_w"]), group=grp)
         assert same(np_(P), golden[f"int2g{grp}_P"]) and same(np_(S), golden[f"int2g{grp}_S"])
+    P, S, R = F.quantize_int2(dev(golden["int2_w"]), scale_fmt="e4m3", group=16)
+    assert S.dtype == torch.float8_e4m3fn and R.dtype == torch.float32 and R.shape == (golden["int2_w"].shape[0],)
+    assert same(np_(P), golden["int2e_P"]) and same(np_(S), golden["int2e_S"]) and same(np_(R), golden["int2e_R"])
 
 
 def weights(seed, n=384, k=2560):
@@ -84,7 +91,7 @@ def weights(seed, n=384, k=2560):
     return w
 
 
-@pytest.mark.parametrize("fmt", ["w8", "w6", "nv4", "int2"])
+@pytest.mark.parametrize("fmt", ["w8", "w6", "nv4", "int2", "int2e"])
 @pytest.mark.parametrize("src", ["f32", "bf16"])
 def test_dense_sources(gpu, F, fmt, src):
     w = weights(11)
@@ -100,11 +107,39 @@ def test_dense_sources(gpu, F, fmt, src):
         check("w6", F.quantize_w6(t, 15), w, qmax=15)
     elif fmt == "nv4":
         got = F.quantize_nv4(t)
+    elif fmt == "int2e":
+        for grp in (32, 64):
+            check(fmt, F.quantize_int2(t, scale_fmt="e4m3", group=grp), w, group=grp)
+        got = F.quantize_int2(t, scale_fmt="e4m3", group=16)
     else:
         for grp in (32, 64):
             check("int2", F.quantize_int2(t, group=grp), w, group=grp)
         got = F.quantize_int2(t, group=16)
     check(fmt, got, w)
+
+
+def test_int2e_scale_edges(gpu, F):
+    """e4m3 INT2 groups at the ends of the scale range: groups 2^-20 and
+    2^-21 times the row's largest (s / rs rounds to e4m3 0: sf = 0, codes
+    3 / 0 / 0 for positive, negative and zero elements), groups whose s / rs
+    sits near the e4m3 subnormal ties (i + 1/2) 2^-9, zero groups beside 0.5,
+    a zero row, and each row's largest group (s / rs = 448 up to one fp32
+    rounding)."""
+    k = 256
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((8, k)) * 0.02).astype(np.float32)
+    w[0, :16] = 1.0
+    w[0, 16:32] = np.float32(2.0 ** -20) * np.sign(rng.standard_normal(16)).astype(np.float32)
+    w[0, 32:48] = 0
+    w[0, 40] = np.float32(2.0 ** -21)
+    for i in range(8):                                  # amax / row amax = (i + 1/2) 2^-9 / 448
+        g = w[1, 16 * (i + 1):16 * (i + 2)]
+        w[1, 16 * (i + 1):16 * (i + 2)] = g * (np.float32((i + 0.5) * 2.0 ** -9 / 448) / np.abs(g).max())
+    w[1, :16] = 1.0
+    w[2] = np.where(rng.random(k) < 0.5, np.float32(0.0), np.float32(-0.0))
+    w[2, 100] = 0.5
+    w[3] = 0
+    check("int2e", F.quantize_int2(dev(w), scale_fmt="e4m3"), w)
 
 
 @pytest.mark.parametrize("fmt", ["w8", "w6", "nv4", "int2"])
@@ -142,3 +177,5 @@ def test_head_sized_int2_from_mx8(gpu, F):
     rows = torch.randperm(248320, generator=g, device=gpu)[:256].sort().values
     Po, So = oq.quantize_int2(wf[rows].cpu().numpy(), group=16)
     assert same(np_(P[rows]), Po) and same(np_(S[rows]), So)
+    P, S, R = F.quantize_int2(wf, scale_fmt="e4m3", group=16)         # the row-scaled e4m3 form
+    check("int2e", (P[rows], S[rows], R[rows]), wf[rows].cpu().numpy())
