@@ -17,6 +17,7 @@ template <bool F16S> bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t 
 extern template bool launch_w8_stream<false>(GemvLaunch, int, hipStream_t);
 extern template bool launch_w8_stream<true>(GemvLaunch, int, hipStream_t);
 bool launch_int2_stream_f16(GemvLaunch p, hipStream_t st);
+bool launch_int2_stream_e4m3(GemvLaunch p, hipStream_t st);
 bool launch_nv4_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_w6_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_mx8_stream_entry(GemvLaunch p, hipStream_t st);
@@ -327,6 +328,10 @@ static int int2_coarse(const void* x, int64_t x_stride, const void* P, const voi
                    : launch_gemv_mfma<FmtInt2<false, 0>, EpiStore>(p, 1, st);
     }
     return rc;
+  }
+  if (G == 16 && launch_int2_stream_e4m3(p, st)) {     // large heads
+    rc = check_launch("int2_stream");
+    return rc ? rc : (smax ? 1 : 0);
   }
   p.smax = nullptr;
   if (G == 16) return launch_gemv_mfma<FmtInt2<true, 16>, EpiStore>(p, 1, st);

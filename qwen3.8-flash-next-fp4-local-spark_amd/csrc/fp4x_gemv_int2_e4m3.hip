@@ -1,9 +1,11 @@
 // Explicit GEMV instantiations (one translation unit per weight format, so
 // the library compiles in parallel).
 #include "fp4x_mfma.h"
+#include "fp4x_stream.h"
 
 namespace fp4x {
 template int launch_gemv_mfma<FmtInt2<true, 16>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 template int launch_gemv_mfma<FmtInt2<true, 32>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 template int launch_gemv_mfma<FmtInt2<true, 0>, EpiStore>(const GemvLaunch&, int, hipStream_t);
+bool launch_int2_stream_e4m3(GemvLaunch p, hipStream_t st) { return launch_int2_stream<true>(p, st); }
 }  // namespace fp4x

@@ -515,21 +515,27 @@ bool launch_w8_ktile(GemvLaunch p, hipStream_t st) {
 namespace fp4x {
 
 // ---------------------------------------------------------------------------
-// Streaming INT2 coarse head (2-bit codes, one fp16 scale per 16 K values):
-// logits[m, n] = sum_k x[m, k] * bf16((code - 1.5) * s) (x/fp4x_kernels.py:304-325),
-// optionally times rs[n].
+// Streaming INT2 coarse head (2-bit codes, one fp16 or e4m3 scale per 16 K
+// values): logits[m, n] = sum_k x[m, k] * bf16((code - 1.5) * s)
+// (x/fp4x_kernels.py:304-325), optionally times rs[n] (the e4m3 form's row scale).
 //
 // One wave per 16-row tile, no cross-wave reduction: the tiles of the matrix
 // are split into contiguous, equal (+-1) ranges over every wave of the grid
 // (one workgroup of W waves per CU), and each wave streams its tiles' units
 // through a private LDS ring of D buffers.  A unit is 128 bytes of codes
-// (512 weights) and the 64 bytes of their scales, for each of the 16 rows:
-// two 16-byte direct loads per lane for the codes (the W8 lane pattern) and
-// one for the scales (lane l: row l >> 2, 16-byte piece (l & 3) ^ ((row >> 2) & 3),
-// so that the 8-byte scale reads of a quarter-wave hit distinct banks).  The
+// (512 weights) and the 64 (fp16) or 32 (e4m3) bytes of their scales, for each
+// of the 16 rows: two 16-byte direct loads per lane for the codes (the W8 lane
+// pattern) and one for the scales (fp16: lane l: row l >> 2, 16-byte piece
+// (l & 3) ^ ((row >> 2) & 3), so that the 8-byte scale reads of a quarter-wave
+// hit distinct banks; e4m3: lanes 0..31, row l >> 1, piece (l & 1) ^ (row >> 3),
+// so that the 4-byte scale reads of a wave hit 64 distinct banks).  The
 // activations are staged once per workgroup in the 4x4-transposed k order of
 // FmtInt2::deq16t (one byte permute per weight).
-constexpr int kInt2Unit = 2048 + 1024;
+template <bool E4M3>
+struct Int2Unit {
+  static constexpr int scale_row = E4M3 ? 32 : 64;    // scale bytes of one row in a unit
+  static constexpr int bytes = 2048 + 16 * scale_row;
+};
 
 __device__ __forceinline__ void int2_read_unit(uint32_t wa, uint32_t wb, uint32_t sa, uint32_t sb, uint4& q0,
                                                uint4& q1, uint2& s0, uint2& s1) {
@@ -595,6 +601,38 @@ __device__ __forceinline__ void int2_read_unit_x(uint32_t wa, uint32_t wb, uint3
       : "v"(wa), "v"(wb), "v"(sa), "v"(sb), "v"(xa)
       : "memory");
 }
+// int2_read_unit_x with e4m3 scales: 4 bytes per half (s0.y, s1.y untouched).
+__device__ __forceinline__ void int2_read_unit_x_e4m3(uint32_t wa, uint32_t wb, uint32_t sa, uint32_t sb,
+                                                      uint32_t xa, uint4& q0, uint4& q1, uint32_t& s0, uint32_t& s1,
+                                                      i2x_u32x4 (&x)[8], i2x_u32x4 (&y)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %20\n\t"
+      "ds_read_b128 %1, %21\n\t"
+      "ds_read_b32 %2, %22\n\t"
+      "ds_read_b32 %3, %23\n\t"
+      "ds_read_b128 %4, %24\n\t"
+      "ds_read_b128 %5, %24 offset:16\n\t"
+      "ds_read_b128 %6, %24 offset:32\n\t"
+      "ds_read_b128 %7, %24 offset:48\n\t"
+      "ds_read_b128 %8, %24 offset:64\n\t"
+      "ds_read_b128 %9, %24 offset:80\n\t"
+      "ds_read_b128 %10, %24 offset:96\n\t"
+      "ds_read_b128 %11, %24 offset:112\n\t"
+      "ds_read_b128 %12, %24 offset:512\n\t"
+      "ds_read_b128 %13, %24 offset:528\n\t"
+      "ds_read_b128 %14, %24 offset:544\n\t"
+      "ds_read_b128 %15, %24 offset:560\n\t"
+      "ds_read_b128 %16, %24 offset:576\n\t"
+      "ds_read_b128 %17, %24 offset:592\n\t"
+      "ds_read_b128 %18, %24 offset:608\n\t"
+      "ds_read_b128 %19, %24 offset:624\n\t"
+      "s_waitcnt lgkmcnt(8)"
+      : "=&v"(q0), "=&v"(q1), "=&v"(s0), "=&v"(s1), "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]),
+        "=&v"(x[4]), "=&v"(x[5]), "=&v"(x[6]), "=&v"(x[7]), "=&v"(y[0]), "=&v"(y[1]), "=&v"(y[2]), "=&v"(y[3]),
+        "=&v"(y[4]), "=&v"(y[5]), "=&v"(y[6]), "=&v"(y[7])
+      : "v"(wa), "v"(wb), "v"(sa), "v"(sb), "v"(xa)
+      : "memory");
+}
 // The second half's activations are in registers after this (tied to them so
 // that no use moves above the wait, and to the accumulator so that the first
 // half's MFMAs stay above it).
@@ -612,9 +650,10 @@ __device__ __forceinline__ void lds_put_u128(uint32_t a, uint4 v) {
 }
 __device__ __forceinline__ void wait_lgkm0_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <int W, int D>
+template <bool E4M3, int W, int D>
 __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
-  using F = FmtInt2<false, 16>;
+  using F = FmtInt2<E4M3, 16>;
+  using U = Int2Unit<E4M3>;
   extern __shared__ __align__(16) uint16_t lds[];
   char* base = reinterpret_cast<char*>(lds);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -635,13 +674,14 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   __shared__ int s_next;
   if (threadIdx.x == 0) s_next = T0 + W;              // (visible after the staging barrier below)
   const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
-  char* ring = base + xbuf + wave * D * kInt2Unit;
-  const int cb = K / 4, sbr = K / 8;                 // code and scale bytes per row
+  char* ring = base + xbuf + wave * D * U::bytes;
+  const int cb = K / 4, sbr = K / 16 * (E4M3 ? 1 : 2);   // code and scale bytes per row
 
   // DMA lanes (codes as in the W8 kernel; scales: row l >> 2, piece (l & 3) ^ ((row >> 2) & 3))
   const int dr = lane >> 3, dc = lane & 7;
   const int cA = dc ^ (dr >> 1), cB = dc ^ (4 + (dr >> 1));
-  const int sr = lane >> 2, sp = (lane & 3) ^ ((sr >> 2) & 3);
+  const int sr = E4M3 ? lane >> 1 : lane >> 2;
+  const int sp = E4M3 ? (lane & 1) ^ (sr >> 3) : (lane & 3) ^ ((sr >> 2) & 3);
   // issuer: the tile whose units go out (ij: next unit; a new tile is taken
   // when its first unit is issued, never before the staging barrier since
   // D <= J), the tiles taken so far (ngot), the last two of them (fifo)
@@ -676,10 +716,10 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
       ++ngot;
       set_tile(t);
     }
-    char* l = ring + is * kInt2Unit;
+    char* l = ring + is * U::bytes;
     dma_b128(iw + ij * 128 + o0, l);
     dma_b128(iw + ij * 128 + o1, l + 1024);
-    dma_b128(isb + ij * 64 + os, l + 2048);
+    if (!E4M3 || lane < 32) dma_b128(isb + ij * U::scale_row + os, l + 2048);
     if (++is == D) is = 0;
     ++issued;
     if (++ij == J) {
@@ -719,9 +759,12 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   const int xr = n < p.M ? n : 0;
   const uint32_t rl = lds_addr(ring);
   const uint32_t wlA = rl + n * 128 + ((g ^ (n >> 1)) * 16), wlB = rl + n * 128 + (((g + 4) ^ (n >> 1)) * 16);
-  const int sx = (n >> 2) & 3;
-  const uint32_t slA = rl + 2048 + n * 64 + (((g >> 1) ^ sx) * 16) + (g & 1) * 8;
-  const uint32_t slB = rl + 2048 + n * 64 + (((2 + (g >> 1)) ^ sx) * 16) + (g & 1) * 8;
+  // lane (n, g): the scales of chunks g (A) and g + 4 (B) of row n
+  const int sx = E4M3 ? n >> 3 : (n >> 2) & 3;
+  const uint32_t slA = E4M3 ? rl + 2048 + n * 32 + (sx * 16) + g * 4
+                            : rl + 2048 + n * 64 + (((g >> 1) ^ sx) * 16) + (g & 1) * 8;
+  const uint32_t slB = E4M3 ? rl + 2048 + n * 32 + ((1 ^ sx) * 16) + g * 4
+                            : rl + 2048 + n * 64 + (((2 + (g >> 1)) ^ sx) * 16) + (g & 1) * 8;
   const uint32_t xl = lds_addr(base) + xr * xrow + g * 128;   // chunk g of unit 0
   int cs = 0, u = 0;
   for (int q = 0; q < ngot; ++q) {                   // (ngot grows while tiles are taken)
@@ -730,11 +773,17 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
     for (int j = 0; j < J; ++j, ++u) {
       if (issued - 1 - u >= D - 1) wait_vmcnt<3 * (D - 1)>();
       else wait_vmcnt<0>();
-      const uint32_t so = cs * kInt2Unit;
+      const uint32_t so = cs * U::bytes;
       typename F::Chunk ch[2];
       i2x_u32x4 xh[2][8];
-      int2_read_unit_x(wlA + so, wlB + so, slA + so, slB + so, xl + j * 1024, ch[0].q, ch[1].q, ch[0].s, ch[1].s,
-                       xh[0], xh[1]);
+      if constexpr (E4M3) {
+        ch[0].s.y = ch[1].s.y = 0;
+        int2_read_unit_x_e4m3(wlA + so, wlB + so, slA + so, slB + so, xl + j * 1024, ch[0].q, ch[1].q, ch[0].s.x,
+                              ch[1].s.x, xh[0], xh[1]);
+      } else {
+        int2_read_unit_x(wlA + so, wlB + so, slA + so, slB + so, xl + j * 1024, ch[0].q, ch[1].q, ch[0].s, ch[1].s,
+                         xh[0], xh[1]);
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         if (h == 1) int2_wait_x(xh[1], acc);
@@ -776,17 +825,17 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   wait_vmcnt<0>();                                   // no load of the prologue outlives the wave
 }
 
-// The INT2 head (fp16 scales, G = 16) through the streaming kernel when the
-// matrix has at least one tile per two waves of the grid and a tile's units
-// fill the ring (the 65k-token draft subset: 4075 tiles over 16 waves per CU);
-// false otherwise (or when FP4X_INT2_STREAM=0).  16 waves per CU (ring depth
-// 3) when the staged activations leave room, else 8 waves with the deepest
-// ring that fits.
+// The INT2 head (G = 16, fp16 or e4m3 scales) through the streaming kernel
+// when the matrix has at least one tile per two waves of the grid and a tile's
+// units fill the ring (the 65k-token draft subset: 4075 tiles over 16 waves
+// per CU); false otherwise (or when FP4X_INT2_STREAM=0).  16 waves per CU
+// (ring depth 3) when the staged activations leave room, else 8 waves with
+// the deepest ring that fits.
 constexpr int kInt2DynLds = 160 * 1024 - 256;      // room for the kernel's static LDS (the tile counter)
 
-template <int W, int D>
+template <bool E4M3, int W, int D>
 bool launch_int2_stream_wd(GemvLaunch p, size_t lds, hipStream_t st) {
-  auto kern = int2_stream_kernel<W, D>;
+  auto kern = int2_stream_kernel<E4M3, W, D>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -800,6 +849,7 @@ bool launch_int2_stream_wd(GemvLaunch p, size_t lds, hipStream_t st) {
   return true;
 }
 
+template <bool E4M3>
 inline bool launch_int2_stream(GemvLaunch p, hipStream_t st) {
   if (!switches().int2_stream) return false;
   const int K = p.pa.K;
@@ -808,13 +858,14 @@ inline bool launch_int2_stream(GemvLaunch p, hipStream_t st) {
   const int64_t tiles = (p.N + 15) / 16;
   const size_t xb = (size_t)StreamGeom::xbuf_bytes(p.M, K);
   const int64_t cus = device_cus();
+  constexpr size_t ub = Int2Unit<E4M3>::bytes;
   auto fits = [&](int W, int D) {
-    return xb + (size_t)W * D * kInt2Unit <= (size_t)kInt2DynLds && K / 512 >= D && 2 * tiles >= cus * W;
+    return xb + (size_t)W * D * ub <= (size_t)kInt2DynLds && K / 512 >= D && 2 * tiles >= cus * W;
   };
-  if (fits(16, 3)) return launch_int2_stream_wd<16, 3>(p, xb + (size_t)16 * 3 * kInt2Unit, st);
-  if (fits(8, 6)) return launch_int2_stream_wd<8, 6>(p, xb + (size_t)8 * 6 * kInt2Unit, st);
-  if (fits(8, 4)) return launch_int2_stream_wd<8, 4>(p, xb + (size_t)8 * 4 * kInt2Unit, st);
-  if (fits(8, 3)) return launch_int2_stream_wd<8, 3>(p, xb + (size_t)8 * 3 * kInt2Unit, st);
+  if (fits(16, 3)) return launch_int2_stream_wd<E4M3, 16, 3>(p, xb + 16 * 3 * ub, st);
+  if (fits(8, 6)) return launch_int2_stream_wd<E4M3, 8, 6>(p, xb + 8 * 6 * ub, st);
+  if (fits(8, 4)) return launch_int2_stream_wd<E4M3, 8, 4>(p, xb + 8 * 4 * ub, st);
+  if (fits(8, 3)) return launch_int2_stream_wd<E4M3, 8, 3>(p, xb + 8 * 3 * ub, st);
   return false;
 }
 

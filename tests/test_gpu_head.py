@@ -289,25 +289,34 @@ def test_fast_head_full_size_32_batches(gpu, F):
 
 
 # ------------------------------------------------------------------ INT2 streaming kernel
-@pytest.mark.parametrize("M,rs,one,K", [(3, False, 0, 2560), (16, False, 0, 2560), (3, True, 0, 2560),
-                                        (3, False, 1, 2560), (3, False, 2, 2560), (3, False, 0, 1536)])
-def test_int2_stream(gpu, F, M, rs, one, K, monkeypatch):
+@pytest.mark.parametrize("M,rs,one,K,e4m3", [(3, False, 0, 2560, False), (16, False, 0, 2560, False),
+                                              (3, True, 0, 2560, False), (3, False, 1, 2560, False),
+                                              (3, False, 2, 2560, False), (3, False, 0, 1536, False),
+                                              (3, True, 0, 2560, True), (16, True, 1, 2560, True),
+                                              (3, True, 2, 1536, True)])
+def test_int2_stream(gpu, F, M, rs, one, K, e4m3, monkeypatch):
     """Heads of at least one tile per two waves of the grid take the streaming
     kernel (16 waves per CU, LDS ring of direct loads); N tail of 40 rows.
     one = 1: just under one tile per wave (the 65,197-row draft subset on 256
     CUs: some workgroups have a wave with no tile), 3 rows past the last full
     tile; one = 2: 10 tiles per CU (six waves of a workgroup without a tile),
     5 rows past the last full tile; K = 1536: three units per tile instead of
-    five."""
-    rng = np.random.default_rng(77 + M + rs + 5 * one + K)
+    five.  e4m3: the row-scaled form (e4m3 group scales, the quantizer's fp32
+    row scales as rs)."""
+    rng = np.random.default_rng(77 + M + rs + 5 * one + K + 3 * e4m3)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     V = {0: 4 * 8 * 16 * cus + 40, 1: 16 * (16 * cus - 21) - 3, 2: 16 * 10 * cus - 5}[one]
     w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
-    P, S = oq.quantize_int2(w, group=16)
+    if e4m3:
+        P, S, R = oq.quantize_int2(w, scale_fmt="e4m3", group=16)
+        Sd = dev(S).view(torch.float8_e4m3fn)
+    else:
+        P, S = oq.quantize_int2(w, group=16)
+        R = (rng.random(V) + 0.5).astype(np.float32) if rs else None
+        Sd = dev(S)
     del w
-    R = (rng.random(V) + 0.5).astype(np.float32) if rs else None
     x, xb = act(rng, M, K)
-    args = (bf16_dev(x), dev(P), dev(S), V)
+    args = (bf16_dev(x), dev(P), Sd, V)
     kw = {"RS": dev(R)} if rs else {}
     y = F.int2_logits(*args, **kw).cpu().numpy()
     with path_switch(monkeypatch, "FP4X_INT2_STREAM"):
@@ -316,7 +325,7 @@ def test_int2_stream(gpu, F, M, rs, one, K, monkeypatch):
     worst = 0.0
     for r0 in range(0, V, 16384):
         r1 = min(V, r0 + 16384)
-        wop = og.operand("int2", P[r0:r1], S[r0:r1])
+        wop = og.operand("int2", P[r0:r1], S[r0:r1], **({"scale_fmt": "e4m3"} if e4m3 else {}))
         exact = ordered.exact_sum(x, wop)
         bound = ordered.mfma_bound(x, wop)
         if rs:
@@ -325,7 +334,7 @@ def test_int2_stream(gpu, F, M, rs, one, K, monkeypatch):
         for got in (y[:, r0:r1], y_core[:, r0:r1]):
             assert np.all(np.abs(got - exact) <= bound), float((np.abs(got - exact) / bound).max())
         worst = max(worst, float((np.abs(y[:, r0:r1] - exact) / bound).max()))
-    print(f"int2 stream V={V} M={M} rs={rs}: max |y - exact| / bound = {worst:.3g}")
+    print(f"int2 stream V={V} M={M} rs={rs} e4m3={e4m3}: max |y - exact| / bound = {worst:.3g}")
     # bf16 logits round the same sums
     yb = F.int2_logits(*args, out_dtype=torch.bfloat16, **kw)
     assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
@@ -336,18 +345,23 @@ def test_int2_stream(gpu, F, M, rs, one, K, monkeypatch):
                                           (200040, 3, True, 512, False), (50000, 3, False, 512, False),
                                           (65197, 3, False, 64, False), (20000, 3, False, 64, False),
                                           (65197, 3, False, 64, True), (248320, 3, False, 512, True),
-                                          (20000, 16, False, 256, True)])
+                                          (20000, 16, False, 256, True), (248320, 3, "e4m3", 512, False),
+                                          (65197, 3, "e4m3", 64, True)])
 def test_int2_topk_fused_equals_separate(gpu, F, V, M, rs, C, f32):
     """int2_topk (slice maxima from the streaming coarse kernel's epilogue where
     it streams, else a slice-max launch) equals int2_logits + topk_rows bit for
-    bit, and its selection is the oracle's total order on its own logits."""
+    bit, and its selection is the oracle's total order on its own logits; for
+    fp16 and for e4m3 (row-scaled) group scales."""
     K = 2560
     g = torch.Generator(device=gpu).manual_seed(V + M)
     w = torch.randn((V, K), generator=g, device=gpu) * 0.02
     w[torch.randperm(V, generator=g, device=gpu)[:64]] *= 4
-    P, S = F.quantize_int2(w, group=16)
+    if rs == "e4m3":                                  # the row-scaled form: its own row scales as RS
+        P, S, R = F.quantize_int2(w, scale_fmt="e4m3", group=16)
+    else:
+        P, S = F.quantize_int2(w, group=16)
+        R = (torch.rand(V, generator=g, device=gpu) + 0.5) if rs else None
     del w
-    R = (torch.rand(V, generator=g, device=gpu) + 0.5) if rs else None
     rng = np.random.default_rng(V + M)
     x, _ = act(rng, M, K)
     xt = bf16_dev(x)
