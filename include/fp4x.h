@@ -202,6 +202,17 @@ int fp4x_scatter_draft(void* out, int64_t out_stride, const float* vals, const i
  *  x/fp4patch.py:61-83, :179-182, :211-214, :357-359] */
 int fp4x_quantize(int src, const void* src_a, const void* src_b, float src_gs, int64_t N, int K, int dst, int G,
                   int qmax, float dst_gs, void* out0, void* out1, void* out2, void* stream);
+/* W6 g32 with the clip search: per group, the scale among s = max(fp16(amax /
+ * qmax), 6.2e-5) and max(fp16(s * c_i), 6.2e-5), c_i = torch.linspace(0.70,
+ * 0.98, clip_search) in fp32, with the strictly smallest squared error (fp32,
+ * summed in the order of torch's CPU sum over the group's 32 squares); then
+ * the codes and planes of FP4X_Q_W6.  Sources as fp4x_quantize; qmax 1..31,
+ * clip_search 0..64 (0: the plain W6 target).  L [N, K/2] 16-byte aligned,
+ * H [N, K/4] 8-byte aligned, S fp16 [N, K/32].
+ * [quantize_w6 with clip_search, x/fp4x_kernels.py:179-202; the dense layer
+ *  preparation under FP4X_DENSE_CLIP, x/fp4patch.py:66-83] */
+int fp4x_quantize_w6_clip(int src, const void* src_a, const void* src_b, float src_gs, int64_t N, int K, int qmax,
+                          int clip_search, void* L, void* H, void* S, void* stream);
 /* max |w| of a source matrix (as fp4x_quantize reads it) into *out, a device
  * float the caller zeroes first.  [quantize_nv4's global amax, x/fp4x_kernels.py:284-287] */
 int fp4x_absmax(int src, const void* src_a, const void* src_b, float src_gs, int64_t N, int K, float* out,

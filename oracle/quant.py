@@ -41,8 +41,10 @@ def _w6_scale(f, qmax):
 
 def quantize_w6(w, qmax=31, clip_search=0):
     """(L u8 [N,K/2], H u8 [N,K/4], S fp16 [N,K/32]).  [x/fp4x_kernels.py:179-202]
-    clip_search > 0 picks, per group, the scale with the smallest squared
-    error over the reference's clip grid (sums in fp32, sequential)."""
+    clip_search > 0 picks, per group, the first scale with the strictly
+    smallest squared error over the reference's clip grid: the factors of
+    torch.linspace(0.70, 0.98, n) in fp32 (clip_grid), each error summed in
+    fp32 in the order of torch's CPU sum over a 32-element row (sum_sq32)."""
     w = np.asarray(w, dtype=F32)
     n, k = w.shape
     f = _groups(w, 32)
@@ -50,10 +52,10 @@ def quantize_w6(w, qmax=31, clip_search=0):
     if clip_search:
         def err(sc):
             d = np.clip(np.rint(f / sc), -qmax - 1, qmax) * sc - f
-            return np.add.reduce((d * d).astype(F32), axis=-1, keepdims=True, dtype=F32)
+            return sum_sq32(d)
         best, bs = err(s), s
-        for c in np.linspace(0.70, 0.98, clip_search).tolist():
-            sc = np.maximum(f16_round(s * F32(c)), F32(6.2e-5))
+        for c in clip_grid(clip_search):
+            sc = np.maximum(f16_round(s * c), F32(6.2e-5))
             e = err(sc)
             m = e < best
             best = np.where(m, e, best)
@@ -65,6 +67,33 @@ def quantize_w6(w, qmax=31, clip_search=0):
     H = (hi[:, 0::4] | (hi[:, 2::4] << 2) | (hi[:, 1::4] << 4) | (hi[:, 3::4] << 6)).astype(np.uint8)
     S = s[..., 0].astype(np.float16)
     return L, H, S
+
+
+def clip_grid(n):
+    """torch.linspace(0.70, 0.98, n) as fp32 values: step = fp32((0.98 - 0.70)
+    / (n - 1)) from the fp32 ends, then c_i = start + step * i below n // 2
+    and end - step * (n - 1 - i) from there, each rounded once (a fused
+    multiply-add; the float64 expression below is exact before its rounding)."""
+    s, e = F32(0.70), F32(0.98)
+    if n == 1:
+        return [s]
+    st = F32((e - s) / F32(n - 1))
+    return [F32(float(s) + float(st) * i) if i < n // 2 else F32(float(e) - float(st) * (n - 1 - i))
+            for i in range(n)]
+
+
+def sum_sq32(d):
+    """fp32 sum of the squares of the last axis (32 values) in the order of
+    torch's CPU sum over a 32-element row: lane j adds elements j, j + 8,
+    j + 16, j + 24 in turn, then lanes 0..7 are added in turn; keeps the axis."""
+    d2 = (d * d).astype(F32)
+    lane = [d2[..., j] for j in range(8)]
+    for i in range(8, 32, 8):
+        lane = [(lane[j] + d2[..., i + j]).astype(F32) for j in range(8)]
+    acc = lane[0]
+    for j in range(1, 8):
+        acc = (acc + lane[j]).astype(F32)
+    return acc[..., None]
 
 
 def w6_codes(L, H):

@@ -39,6 +39,7 @@ _SIGS = {
     "fp4x_refine_nv4": ([_P, _P, _P, _I, _I, _P, _P, ctypes.c_float, _I, _I, _P], _I),
     "fp4x_scatter_draft": ([_P, _I64, _P, _P, _P, _I64, _P, _I, _I, _I64, _P], _I),
     "fp4x_quantize": ([_I, _P, _P, ctypes.c_float, _I64, _I, _I, _I, _I, ctypes.c_float, _P, _P, _P, _P], _I),
+    "fp4x_quantize_w6_clip": ([_I, _P, _P, ctypes.c_float, _I64, _I, _I, _I, _P, _P, _P, _P], _I),
     "fp4x_absmax": ([_I, _P, _P, ctypes.c_float, _I64, _I, _P, _P], _I),
     "fp4x_hc_down": ([_P, _I64, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "fp4x_hc_up": ([_P, _I64, _P, _P, _I, _P, _I64, _P, _I, _I, _I, _I, _I, _P], _I),

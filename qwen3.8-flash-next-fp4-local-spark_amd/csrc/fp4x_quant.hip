@@ -1,6 +1,6 @@
 // Weight preparation on the device: the reference's pure-torch quantizers
-// (x/fp4x_kernels.py: quantize_w8 :138-144, quantize_w6 :179-202 without the
-// clip search, quantize_nv4 :277-300, quantize_int2 :330-351 with fp16 scales,
+// (x/fp4x_kernels.py: quantize_w8 :138-144, quantize_w6 :179-202 with or
+// without the clip search, quantize_nv4 :277-300, quantize_int2 :330-351 with fp16 scales,
 // or e4m3 scales under an fp32 row scale) as one thread per quantization group.
 //
 // The source rows are fp32, bf16, or packed MXFP8 / NVFP4 rows decoded in
@@ -11,6 +11,8 @@
 // semantics of its torch ops on CPU tensors (where its golden vectors were
 // taken): torch's GPU division by a Python scalar multiplies by the
 // reciprocal instead, which can move a result by one fp32 ulp.
+#include <cmath>
+
 #include "fp4x_kernels.h"
 #include "../../include/fp4x.h"
 
@@ -169,8 +171,11 @@ struct QW6 {
   uint8_t* H;
   uint16_t* S;
   int qmax;
-  __device__ void put(int64_t row, int gi, int K, const float (&f)[G]) const {
-    const float sc = fmaxf(f16_round(group_amax(f) / (float)qmax), 6.2e-5f);
+  __device__ static float base_scale(const float (&f)[G], int qmax) {
+    return fmaxf(f16_round(group_amax(f) / (float)qmax), 6.2e-5f);
+  }
+  // codes clamp(rint(w / sc), -qmax - 1, qmax) + 32 into the two planes, fp16(sc) into S
+  __device__ void put_scaled(int64_t row, int gi, int K, const float (&f)[G], float sc) const {
     uint32_t c[G];
 #pragma unroll
     for (int i = 0; i < G; ++i)
@@ -187,6 +192,59 @@ struct QW6 {
     *reinterpret_cast<uint4*>(L + row * (K / 2) + gi * 16) = make_uint4(l[0], l[1], l[2], l[3]);
     *reinterpret_cast<uint2*>(H + row * (K / 4) + gi * 8) = make_uint2(h[0], h[1]);
     S[row * (K / G) + gi] = __builtin_bit_cast(uint16_t, (_Float16)sc);
+  }
+  __device__ void put(int64_t row, int gi, int K, const float (&f)[G]) const {
+    put_scaled(row, gi, K, f, base_scale(f, qmax));
+  }
+};
+
+// W6 with the clip search: the group's scale is the first of s, sc_1 .. sc_n
+// (sc_i = max(fp16(s * c_i), 6.2e-5), c_i the fp32 factors of the clip grid)
+// whose squared error sum((clamp(rint(w / sc), -qmax - 1, qmax) * sc - w)^2)
+// is strictly the smallest.  Every operation is rounded to fp32 on its own
+// (no fused multiply-add); the 32 squares are summed as 8 lanes of 4
+// (lane j: elements j, j + 8, j + 16, j + 24 in turn), then lanes 0..7 in
+// turn: the order of torch's CPU sum over a 32-element row.
+constexpr int kW6MaxClip = 64;
+struct W6Clip {
+  int n;
+  float c[kW6MaxClip];
+};
+__device__ __forceinline__ float w6_sq_err(const float (&f)[32], float sc, int qmax) {
+#pragma clang fp contract(off)
+  float lane[8];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float d = fminf(fmaxf(rintf(f[i] / sc), (float)(-qmax - 1)), (float)qmax) * sc - f[i];
+    const float d2 = d * d;
+    if (i < 8) lane[i] = d2;
+    else lane[i & 7] = lane[i & 7] + d2;
+  }
+  float e = lane[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) e = e + lane[j];
+  return e;
+}
+struct QW6Clip : QW6 {
+  W6Clip clip;
+  __device__ void put(int64_t row, int gi, int K, const float (&f)[G]) const {
+#pragma clang fp contract(off)
+    const float s = base_scale(f, qmax);
+    float best = w6_sq_err(f, s, qmax), bs = s;
+    for (int i = 0; i < clip.n; ++i) {
+      // the fp32 product is rounded before its fp16 rounding: without the
+      // register barrier the compiler fuses both into one v_fma_mixlo_f16,
+      // a single rounding that differs at fp16 midpoints of the fp32 product
+      float p = s * clip.c[i];
+      asm volatile("" : "+v"(p));
+      const float sc = fmaxf(f16_round(p), 6.2e-5f);
+      const float e = w6_sq_err(f, sc, qmax);
+      if (e < best) {
+        best = e;
+        bs = sc;
+      }
+    }
+    put_scaled(row, gi, K, f, bs);
   }
 };
 
@@ -400,6 +458,46 @@ int fp4x_quantize(int src, const void* src_a, const void* src_b, float src_gs, i
     default:
       return dispatch_q(SrcNV4{static_cast<const uint8_t*>(src_a), static_cast<const uint8_t*>(src_b), src_gs, K}, N,
                         K, dst, G, qmax, dst_gs, out0, out1, out2, st);
+  }
+}
+
+int fp4x_quantize_w6_clip(int src, const void* src_a, const void* src_b, float src_gs, int64_t N, int K, int qmax,
+                          int clip_search, void* L, void* H, void* S, void* stream) {
+  int rc = src_check(src, src_a, src_b, N, K);
+  if (rc) return rc;
+  if (qmax < 1 || qmax > 31 || clip_search < 0 || clip_search > kW6MaxClip) {
+    set_error("quantize_w6_clip: need qmax 1..31 and clip_search 0..64");
+    return FP4X_ERR_ARG;
+  }
+  if (!al(L, 16) || !al(H, 8) || !S) {
+    set_error("quantize_w6_clip: L must be 16-byte and H 8-byte aligned, and S given");
+    return FP4X_ERR_ARG;
+  }
+  // the clip grid as torch.linspace(0.70, 0.98, n) in fp32: step = (0.98f - 0.70f) / (n - 1),
+  // c_i = fma(step, i, 0.70f) below n / 2, else fma(-step, n - 1 - i, 0.98f)
+  QW6Clip q;
+  q.L = static_cast<uint8_t*>(L);
+  q.H = static_cast<uint8_t*>(H);
+  q.S = static_cast<uint16_t*>(S);
+  q.qmax = qmax;
+  q.clip.n = clip_search;
+  const float c0 = 0.70f, c1 = 0.98f;
+  const float step = clip_search > 1 ? (c1 - c0) / (float)(clip_search - 1) : 0.0f;
+  for (int i = 0; i < clip_search; ++i)
+    q.clip.c[i] = i < clip_search / 2 || clip_search == 1 ? std::fma(step, (float)i, c0)
+                                                          : std::fma(-step, (float)(clip_search - 1 - i), c1);
+  for (int i = clip_search; i < kW6MaxClip; ++i) q.clip.c[i] = 0.0f;
+  hipStream_t st = (hipStream_t)stream;
+  switch (src) {
+    case FP4X_SRC_F32:
+      return launch_q(SrcF32{static_cast<const float*>(src_a), K}, q, N, K, st);
+    case FP4X_SRC_BF16:
+      return launch_q(SrcBF16{static_cast<const uint16_t*>(src_a), K}, q, N, K, st);
+    case FP4X_SRC_MX8:
+      return launch_q(SrcMX8{static_cast<const uint8_t*>(src_a), static_cast<const uint8_t*>(src_b), K}, q, N, K, st);
+    default:
+      return launch_q(SrcNV4{static_cast<const uint8_t*>(src_a), static_cast<const uint8_t*>(src_b), src_gs, K}, q, N,
+                      K, st);
   }
 }
 

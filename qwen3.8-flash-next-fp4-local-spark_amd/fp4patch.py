@@ -119,10 +119,8 @@ class _DenseDecode:
             F = self.F
             if self.low_bit_format(*w.shape) != "w6":
                 planes = F.requantize_mx8(w, s, "nv4")              # read from the packed rows directly
-            elif not self.clip:
-                planes = F.requantize_mx8(w, s, "w6", qmax=self.qmax)
-            else:                                                    # the clip search stays on the torch formulas
-                planes = F.quantize_w6(F.mx8_dequant(w, s), self.qmax, self.clip)
+            else:                                                    # with the clip search when one is set
+                planes = F.requantize_mx8(w, s, "w6", qmax=self.qmax, clip_search=self.clip)
             self.copies[id(layer)] = planes
             if len(self.copies) in (1, 200):
                 _say(f"dense {self.mode}: {len(self.copies)} layers have their low-bit copy")

@@ -528,6 +528,17 @@ def _hip_quantize(src, n, k, dst, G=16, qmax=31, gs=0.0):
     return outs
 
 
+def _hip_w6_clip(src, n, k, qmax, clip_search):
+    """One fp4x_quantize_w6_clip call: (L, H, S)."""
+    kind, a, b, sgs = src
+    dev = a.device
+    outs = [torch.empty((n, c), dtype=dt, device=dev)
+            for c, dt in ((k // 2, torch.uint8), (k // 4, torch.uint8), (k // 32, torch.float16))]
+    _L.check(_L.lib().fp4x_quantize_w6_clip(kind, _ptr(a), None if b is None else _ptr(b), float(sgs), n, k, qmax,
+                                            clip_search, *[_ptr(t) for t in outs], _L.stream_of(a)), "quantize_w6_clip")
+    return tuple(outs)
+
+
 def _hip_nv4(src, n, k):
     """NVFP4 of a source: the global amax on the device (one host read, as the
     reference's .item()), gs = max(amax / 6 / 448, 1e-30), then the groups."""
@@ -540,18 +551,18 @@ def _hip_nv4(src, n, k):
     return P, S, gs
 
 
-def requantize_mx8(w8, s_u8, fmt, group=16, qmax=31):
+def requantize_mx8(w8, s_u8, fmt, group=16, qmax=31, clip_search=0):
     """quantize_<fmt>(mx8_dequant(w8, s_u8)) for fmt in w8, w6, nv4, int2, read
     from the packed MXFP8 rows without their fp32 copy (the plugin's layer and
-    LM-head preparation, x/fp4patch.py:61-83, :357-359)."""
+    LM-head preparation, x/fp4patch.py:61-83, :357-359); clip_search for w6."""
     _need_cuda(w8, s_u8)
     n, k = w8.shape
-    if k % 64 or (fmt == "int2" and group not in (16, 32, 64)):
+    if k % 64 or (fmt == "int2" and group not in (16, 32, 64)) or clip_search > 64:
         wf = mx8_dequant(w8, s_u8)
-        return {"w8": quantize_w8, "w6": lambda t: quantize_w6(t, qmax), "nv4": quantize_nv4,
+        return {"w8": quantize_w8, "w6": lambda t: quantize_w6(t, qmax, clip_search), "nv4": quantize_nv4,
                 "int2": lambda t: quantize_int2(t, group=group)}[fmt](wf)
     src = (_SRC_MX8, w8.contiguous(), s_u8.contiguous().view(torch.uint8), 0.0)
-    return _requantize(src, n, k, fmt, group, qmax)
+    return _requantize(src, n, k, fmt, group, qmax, clip_search)
 
 
 def requantize_nv4(P, S, gs, fmt, group=16, qmax=31):
@@ -567,9 +578,11 @@ def requantize_nv4(P, S, gs, fmt, group=16, qmax=31):
     return _requantize(src, n, k, fmt, group, qmax)
 
 
-def _requantize(src, n, k, fmt, group, qmax):
+def _requantize(src, n, k, fmt, group, qmax, clip_search=0):
     if fmt == "w8":
         return tuple(_hip_quantize(src, n, k, _Q_W8))
+    if fmt == "w6" and clip_search:
+        return _hip_w6_clip(src, n, k, qmax, clip_search)
     if fmt == "w6":
         return tuple(_hip_quantize(src, n, k, _Q_W6, qmax=qmax))
     if fmt == "nv4":
@@ -603,11 +616,13 @@ def _w6_pack(codes):
 @torch.no_grad()
 def quantize_w6(w, qmax=31, clip_search=0):
     """W6 g32 two-plane layout: (L [N, K/2], H [N, K/4], S fp16 [N, K/32]).
-    qmax < 31 quantizes to fewer levels in the same layout.  HIP kernel for
-    device fp32/bf16 matrices without a clip search."""
+    qmax < 31 quantizes to fewer levels in the same layout.  HIP kernels for
+    device fp32/bf16 matrices (the clip search for up to 64 clip factors)."""
     src = _hip_src(w)
     if src is not None and not clip_search:
         return tuple(_hip_quantize(src, w.shape[0], w.shape[1], _Q_W6, qmax=qmax))
+    if src is not None and 0 < clip_search <= 64:
+        return _hip_w6_clip(src, w.shape[0], w.shape[1], qmax, clip_search)
     n, k = w.shape
     L = torch.empty((n, k // 2), dtype=torch.uint8, device=w.device)
     H = torch.empty((n, k // 4), dtype=torch.uint8, device=w.device)

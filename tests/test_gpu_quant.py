@@ -62,6 +62,8 @@ def test_golden_vectors(gpu, F, golden):
     assert same(np_(q), golden["w8_q"]) and same(np_(s), golden["w8_s"])
     L, H, S = F.quantize_w6(dev(golden["w6_w"]))
     assert same(np_(L), golden["w6_L"]) and same(np_(H), golden["w6_H"]) and same(np_(S), golden["w6_S"])
+    L, H, S = F.quantize_w6(dev(golden["w6_w"]), 15, 3)                   # with the clip search
+    assert same(np_(L), golden["w6c_L"]) and same(np_(H), golden["w6c_H"]) and same(np_(S), golden["w6c_S"])
     P, S, gs = F.quantize_nv4(dev(golden["nv4_w"]))
     assert same(np_(P), golden["nv4_P"]) and same(np_(S), golden["nv4_S"]) and gs == float(golden["nv4_gs"])
     for grp in (16, 32):
@@ -153,6 +155,27 @@ def test_packed_sources(gpu, F, fmt):
     P, S, gs = oq.quantize_nv4(w)
     got = F.requantize_nv4(dev(P), dev(S).view(torch.float8_e4m3fn), gs, fmt)
     check(fmt, got, oq.dequant_nv4(P, S, gs))
+
+
+@pytest.mark.parametrize("qmax,clip", [(31, 3), (15, 7), (31, 16)])
+def test_w6_clip_search(gpu, F, qmax, clip):
+    """quantize_w6 with the clip search equals the oracle's bit for bit, from
+    fp32 and bf16 rows and from packed MXFP8 rows (the plugin's dense layer
+    preparation under FP4X_DENSE_CLIP)."""
+    w = weights(13 + clip)
+    w[8:16, ::32] *= 20                                     # one outlier per group: the search clips it
+    got = F.quantize_w6(dev(w), qmax, clip)
+    want = oq.quantize_w6(w, qmax, clip)
+    for i, (g, t) in enumerate(zip(got, want)):
+        assert same(np_(g), t), ("w6 clip", i, int((np_(g).reshape(-1) != np.asarray(t).reshape(-1)).sum()))
+    wb = fm.round_bf16(w)
+    got = F.quantize_w6(dev(fm.bf16_bits(wb).view(np.int16)).view(torch.bfloat16), qmax, clip)
+    for g, t in zip(got, oq.quantize_w6(wb, qmax, clip)):
+        assert same(np_(g), t)
+    q8, s8 = oq.quantize_mx8(w)
+    got = F.requantize_mx8(dev(q8), dev(s8), "w6", qmax=qmax, clip_search=clip)
+    for g, t in zip(got, oq.quantize_w6(oq.mx8_dequant(q8, s8), qmax, clip)):
+        assert same(np_(g), t)
 
 
 def test_nv4_midpoints(gpu, F):

@@ -33,6 +33,44 @@ def test_w6_clip_search_golden(golden):
     assert np.array_equal(S.view(np.uint16), golden["w6c_S"].view(np.uint16))
 
 
+def test_w6_clip_grid_and_sum_order():
+    """The clip search's two fp32 details, pinned against torch's own CPU
+    results: clip_grid(n) is torch.linspace(0.70, 0.98, n) for n = 1..64
+    (numpy's float64 linspace rounded to fp32 differs from n = 3 on), and
+    sum_sq32 is torch's fp32 sum of the squares over a 32-element row, here on
+    magnitudes over 12 decades (a sequential or pairwise sum differs on most
+    such rows)."""
+    for n in range(1, 65):
+        want = np.array(torch.linspace(0.70, 0.98, n).tolist(), np.float32)
+        assert np.array_equal(np.array(oq.clip_grid(n), np.float32), want), n
+    rng = np.random.default_rng(9)
+    d = (rng.standard_normal((4096, 32)) * 10.0 ** rng.uniform(-6, 6, (4096, 32))).astype(np.float32)
+    want = (torch.from_numpy(d) ** 2).sum(-1, keepdim=True).numpy()
+    assert np.array_equal(oq.sum_sq32(d).view(np.uint32), want.view(np.uint32))
+    seq = (d * d)[:, :1].copy()
+    for i in range(1, 32):
+        seq = seq + (d * d)[:, i:i + 1]
+    assert (seq != want).mean() > 0.3                     # the order matters on these rows
+
+
+@pytest.mark.parametrize("qmax,clip", [(31, 3), (15, 7), (31, 16), (7, 1)])
+def test_w6_clip_search_torch_formulas(qmax, clip):
+    """The oracle's clip search equals the reference's torch formulas (the
+    product's CPU fallback of quantize_w6) bit for bit on N(0, 0.02) rows,
+    rows with one outlier per group, and rows of values on the W6 grid."""
+    import fp4x_kernels as F
+    rng = np.random.default_rng(qmax + clip)
+    w = (rng.standard_normal((64, 256)) * 0.02).astype(np.float32)
+    w[:8, ::32] *= 20
+    w[8:16] = (rng.integers(-qmax, qmax + 1, (8, 256)) * np.float32(2.0 ** -7)).astype(np.float32)
+    got = F.quantize_w6(torch.from_numpy(w), qmax, clip)
+    want = oq.quantize_w6(w, qmax, clip)
+    for g, t in zip(got, want):
+        assert np.array_equal(g.numpy().view(np.uint8), np.asarray(t).view(np.uint8))
+    plain = oq.quantize_w6(w, qmax)
+    assert not np.array_equal(want[2], plain[2])          # the search moved some scales
+
+
 def test_mx8_dequant_golden(golden):
     got = oq.mx8_dequant(golden["mx8_w"], golden["mx8_s"])
     assert np.array_equal(got.view(np.uint32), golden["mx8_deq"].view(np.uint32))
