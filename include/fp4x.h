@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 9
+#define FP4X_ABI_VERSION 10
 
 enum {
   FP4X_OK = 0,

@@ -52,7 +52,7 @@ _SIGS = {
     "fp4x_reload_env": ([], _I),
     "fp4x_read_ceiling": ([_P, _I64, _I, _I, _P, _P], _I),
 }
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _LIB = None
 
