@@ -306,8 +306,8 @@ struct QInt2 {
   }
 };
 
-// INT2 with e4m3fn group scales under an fp32 row scale rs = R[row] (written
-// by int2e_rows_kernel first): S = e4m3(s / rs) for s = max(amax, 1e-8) / 1.5,
+// INT2 with e4m3fn group scales under an fp32 row scale rs (R[row], written by
+// int2e_kernel): S = e4m3(s / rs) for s = max(amax, 1e-8) / 1.5,
 // codes against sf = float(S) * rs.  A group whose s / rs rounds to e4m3 0
 // (amax below about 2^-10 / 448 of the row's largest) has sf = 0: its codes
 // are 3, 0 and 0 for positive, negative and zero elements.
@@ -316,9 +316,9 @@ struct QInt2E {
   static constexpr int G = GG;
   uint8_t* P;
   uint8_t* S;
-  const float* R;
-  __device__ void put(int64_t row, int gi, int K, const float (&f)[G]) const {
-    const float rs = R[row];
+  float* R;
+  __device__ void put(int64_t row, int gi, int K, const float (&f)[G]) const { put_rs(row, gi, K, f, R[row]); }
+  __device__ void put_rs(int64_t row, int gi, int K, const float (&f)[G], float rs) const {
     const uint32_t code = e4m3_code((fmaxf(group_amax(f), 1e-8f) / 1.5f) / rs);
     put_int2_codes(f, e4m3_value(code) * rs, P + row * (K / 4) + gi * (G / 4));
     S[row * (K / G) + gi] = (uint8_t)code;
@@ -355,23 +355,32 @@ __global__ __launch_bounds__(256) void absmax_kernel(Src src, int64_t N, int K, 
   if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(m));
 }
 
-// Row scales of the e4m3 INT2 target, one wave per row: R[row] =
+// The e4m3 INT2 target, one wave per row: the row scale R[row] =
 // (max(row amax, 1e-8) / 1.5) / 448, the largest group scale of the row over
 // 448 (the rounded quotient max(a, 1e-8) / 1.5 is monotonic in a, so the row
-// maximum of the group scales is the scale of the row's amax).
-template <class Src>
-__global__ __launch_bounds__(256) void int2e_rows_kernel(Src src, int64_t N, int K, float* R) {
+// maximum of the group scales is the scale of the row's amax), then the
+// row's groups against it.  The second read of the row comes from the caches
+// the first one filled.
+template <class Src, int G>
+__global__ __launch_bounds__(256) void int2e_kernel(Src src, QInt2E<G> q, int64_t N, int K) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= N) return;                                  // uniform over the wave
+  const int lane = threadIdx.x & 63;
   float m = 0.0f;
-  for (int g = threadIdx.x & 63; g < K / 16; g += 64) {
+  for (int g = lane; g < K / 16; g += 64) {
     float f[16];
     src.template load<16>(row, g * 16, f);
     m = fmaxf(m, group_amax(f));
   }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
-  if ((threadIdx.x & 63) == 0) R[row] = (fmaxf(m, 1e-8f) / 1.5f) / 448.0f;
+  const float rs = (fmaxf(m, 1e-8f) / 1.5f) / 448.0f;
+  if (lane == 0) q.R[row] = rs;
+  for (int gi = lane; gi < K / G; gi += 64) {
+    float f[G];
+    src.template load<G>(row, gi * G, f);
+    q.put_rs(row, gi, K, f, rs);
+  }
 }
 
 static bool al(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -400,12 +409,11 @@ static int dispatch_q(const Src& src, int64_t N, int K, int dst, int G, int qmax
       uint8_t* S = static_cast<uint8_t*>(o1);
       float* R = static_cast<float*>(o2);
       if (N == 0) return FP4X_OK;
-      hipLaunchKernelGGL(int2e_rows_kernel<Src>, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, src, N, K, R);
-      int rc = check_launch("quantize (row scales)");
-      if (rc) return rc;
-      if (G == 16) return launch_q(src, QInt2E<16>{P, S, R}, N, K, st);
-      if (G == 32) return launch_q(src, QInt2E<32>{P, S, R}, N, K, st);
-      return launch_q(src, QInt2E<64>{P, S, R}, N, K, st);
+      const dim3 grid((unsigned)((N + 3) / 4));
+      if (G == 16) hipLaunchKernelGGL((int2e_kernel<Src, 16>), grid, dim3(256), 0, st, src, QInt2E<16>{P, S, R}, N, K);
+      else if (G == 32) hipLaunchKernelGGL((int2e_kernel<Src, 32>), grid, dim3(256), 0, st, src, QInt2E<32>{P, S, R}, N, K);
+      else hipLaunchKernelGGL((int2e_kernel<Src, 64>), grid, dim3(256), 0, st, src, QInt2E<64>{P, S, R}, N, K);
+      return check_launch("quantize (INT2 e4m3)");
     }
     default:
       if (G == 16) return launch_q(src, QInt2<16>{static_cast<uint8_t*>(o0), static_cast<uint16_t*>(o1)}, N, K, st);
