@@ -551,34 +551,36 @@ def _hip_nv4(src, n, k):
     return P, S, gs
 
 
-def requantize_mx8(w8, s_u8, fmt, group=16, qmax=31, clip_search=0):
+def requantize_mx8(w8, s_u8, fmt, group=16, qmax=31, clip_search=0, scale_fmt="fp16"):
     """quantize_<fmt>(mx8_dequant(w8, s_u8)) for fmt in w8, w6, nv4, int2, read
     from the packed MXFP8 rows without their fp32 copy (the plugin's layer and
-    LM-head preparation, x/fp4patch.py:61-83, :357-359); clip_search for w6."""
+    LM-head preparation, x/fp4patch.py:61-83, :357-359); clip_search for w6,
+    scale_fmt for int2."""
     _need_cuda(w8, s_u8)
     n, k = w8.shape
     if k % 64 or (fmt == "int2" and group not in (16, 32, 64)) or clip_search > 64:
         wf = mx8_dequant(w8, s_u8)
         return {"w8": quantize_w8, "w6": lambda t: quantize_w6(t, qmax, clip_search), "nv4": quantize_nv4,
-                "int2": lambda t: quantize_int2(t, group=group)}[fmt](wf)
+                "int2": lambda t: quantize_int2(t, scale_fmt, group)}[fmt](wf)
     src = (_SRC_MX8, w8.contiguous(), s_u8.contiguous().view(torch.uint8), 0.0)
-    return _requantize(src, n, k, fmt, group, qmax, clip_search)
+    return _requantize(src, n, k, fmt, group, qmax, clip_search, scale_fmt)
 
 
-def requantize_nv4(P, S, gs, fmt, group=16, qmax=31):
+def requantize_nv4(P, S, gs, fmt, group=16, qmax=31, scale_fmt="fp16"):
     """quantize_<fmt>(dequant_nv4(P, S, gs)) read from the packed NVFP4 rows
-    without their fp32 copy (the draft head's INT2 copy, x/fp4patch.py:303-306)."""
+    without their fp32 copy (the draft head's INT2 copy, x/fp4patch.py:303-306);
+    scale_fmt for int2."""
     _need_cuda(P, S)
     n, k = P.shape[0], P.shape[1] * 2
     if k % 64 or (fmt == "int2" and group not in (16, 32, 64)):
         wf = dequant_nv4(P, S, gs)
         return {"w8": quantize_w8, "w6": lambda t: quantize_w6(t, qmax), "nv4": quantize_nv4,
-                "int2": lambda t: quantize_int2(t, group=group)}[fmt](wf)
+                "int2": lambda t: quantize_int2(t, scale_fmt, group)}[fmt](wf)
     src = (_SRC_NV4, P.contiguous(), S.contiguous().view(torch.uint8), float(gs))
-    return _requantize(src, n, k, fmt, group, qmax)
+    return _requantize(src, n, k, fmt, group, qmax, scale_fmt=scale_fmt)
 
 
-def _requantize(src, n, k, fmt, group, qmax, clip_search=0):
+def _requantize(src, n, k, fmt, group, qmax, clip_search=0, scale_fmt="fp16"):
     if fmt == "w8":
         return tuple(_hip_quantize(src, n, k, _Q_W8))
     if fmt == "w6" and clip_search:
@@ -587,6 +589,9 @@ def _requantize(src, n, k, fmt, group, qmax, clip_search=0):
         return tuple(_hip_quantize(src, n, k, _Q_W6, qmax=qmax))
     if fmt == "nv4":
         return _hip_nv4(src, n, k)
+    if fmt == "int2" and scale_fmt != "fp16":
+        P, S, R = _hip_quantize(src, n, k, _Q_INT2_E4M3, G=group)
+        return P, S, R.view(-1)
     if fmt == "int2":
         return tuple(_hip_quantize(src, n, k, _Q_INT2, G=group))
     raise ValueError(f"fp4x: unknown format {fmt!r}")

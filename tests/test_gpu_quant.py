@@ -144,16 +144,19 @@ def test_int2e_scale_edges(gpu, F):
     check("int2e", F.quantize_int2(dev(w), scale_fmt="e4m3"), w)
 
 
-@pytest.mark.parametrize("fmt", ["w8", "w6", "nv4", "int2"])
+@pytest.mark.parametrize("fmt", ["w8", "w6", "nv4", "int2", "int2e"])
 def test_packed_sources(gpu, F, fmt):
     """requantize_mx8 / requantize_nv4 equal the quantizer of the packed rows'
-    exact dequant (the plugin's layer, LM-head and draft-head preparation)."""
+    exact dequant (the plugin's layer, LM-head and draft-head preparation;
+    int2e: INT2 with e4m3 group scales and fp32 row scales)."""
     w = weights(12)
+    kw = {"scale_fmt": "e4m3"} if fmt == "int2e" else {}
+    f = "int2" if fmt == "int2e" else fmt
     q8, s8 = oq.quantize_mx8(w)
-    got = F.requantize_mx8(dev(q8), dev(s8), fmt)
+    got = F.requantize_mx8(dev(q8), dev(s8), f, **kw)
     check(fmt, got, oq.mx8_dequant(q8, s8))
     P, S, gs = oq.quantize_nv4(w)
-    got = F.requantize_nv4(dev(P), dev(S).view(torch.float8_e4m3fn), gs, fmt)
+    got = F.requantize_nv4(dev(P), dev(S).view(torch.float8_e4m3fn), gs, f, **kw)
     check(fmt, got, oq.dequant_nv4(P, S, gs))
 
 
