@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 10
+#define FP4X_ABI_VERSION 11
 
 enum {
   FP4X_OK = 0,
@@ -138,8 +138,8 @@ int64_t fp4x_topk_workspace_size(int M, int V);
  * it streams.  Results equal the two calls made separately.  set_only != 0:
  * the caller needs the selected set only (both heads scatter exact logits at
  * these indices, so their order does not reach any result); the row's C
- * indices then come in increasing index order for bf16 coarse logits, which
- * skips the sort, and in fp4x_topk_rows' order for fp32 ones.
+ * indices are then the same set in an unspecified order (where the selection
+ * can skip the sort it writes them in increasing index order).
  * [int2_logits then torch.topk(coarse, C), x/fp4patch.py:371-377 (bf16);
  *  x/fp4patch.py:313-314 (fp32, the draft head)] */
 int fp4x_int2_topk(const void* x, int64_t x_stride, const void* P, const void* S, int s_fmt, const float* rs,
@@ -279,6 +279,14 @@ int fp4x_mx8_dequant(const void* w, const void* s, int N, int K, float* out, voi
  * if the data fold to one particular word.  No counterpart in the reference:
  * the benchmark's measured ceiling of a one-shot read of a GEMV's bytes. */
 int fp4x_read_ceiling(const void* src, int64_t bytes, int unroll, int wgs_per_cu, uint32_t* sink, void* stream);
+
+/* Launch `wgs` one-wave workgroups on `stream` that each hold a CU for
+ * `microseconds` of wall-clock time (at most 100 ms) and then end; each
+ * takes lds_kb KB of LDS (up to 160, a whole CU's), which keeps workgroups
+ * that need LDS off its CU meanwhile.  No counterpart in the reference: a
+ * test utility, with which the mixer's tests make its workgroups start late,
+ * as when another kernel holds part of the GPU. */
+int fp4x_hold_cus(int wgs, int64_t microseconds, int lds_kb, uint32_t* sink, void* stream);
 
 /* Re-read the path switches from the environment (they are read once, when
  * first needed, never per launch): FP4X_W8_STREAM, FP4X_INT2_STREAM,

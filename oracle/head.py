@@ -91,6 +91,22 @@ def fast_head(x_bits, P, S, G, w_codes, s_u8, C, lpr_mx8):
     return coarse, idx, out
 
 
+def fast_head_argmax(x_bits, P, S, G, w_codes, s_u8, C, lpr_mx8, block=96):
+    """Per row, the argmax (first index of the largest value) of fast_head's
+    output, for many rows: the coarse pass runs over the head once for all
+    rows, the top-C and the rescore per block of rows, so 1,000 rows of a
+    248,320-row head stay within a few GB."""
+    coarse = bf16_bits(int2_coarse(x_bits, P, S, G))
+    am = np.empty(coarse.shape[0], np.int64)
+    for b0 in range(0, coarse.shape[0], block):
+        cb = coarse[b0:b0 + block]
+        idx = topk_total_order(cb, C)
+        out = cb.copy()
+        np.put_along_axis(out, idx, bf16_bits(mx8_rows(x_bits[b0:b0 + block], w_codes, s_u8, idx, lpr_mx8)), 1)
+        am[b0:b0 + block] = np.argmax(bf16_to_f32(out), -1)
+    return am
+
+
 def full_mx8_logits(x_bits, w_codes, s_u8):
     """Exact-weight full-vocabulary logits (fp32, numpy order) for argmax
     agreement checks."""

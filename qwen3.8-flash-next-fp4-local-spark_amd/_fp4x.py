@@ -51,8 +51,9 @@ _SIGS = {
     "fp4x_mx8_dequant": ([_P, _P, _I, _I, _P, _P], _I),
     "fp4x_reload_env": ([], _I),
     "fp4x_read_ceiling": ([_P, _I64, _I, _I, _P, _P], _I),
+    "fp4x_hold_cus": ([_I, _I64, _I, _P, _P], _I),
 }
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _LIB = None
 

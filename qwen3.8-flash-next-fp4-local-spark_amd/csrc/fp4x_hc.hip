@@ -167,29 +167,38 @@ static bool al(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & 
 //     loads and lengthen the critical path.)
 //   * The workgroup whose count completes the down tiles re-arms the count
 //     and advances every workgroup's flag by one (a fetch-add per 128-byte
-//     flag line).  Each workgroup read its own flag when it started, and one
-//     lane waits until the flag differs from that value (s_sleep between
-//     reads, at most spin_limit reads); the workgroup then stages the
-//     bottleneck with device-coherent loads and runs its up tiles.  (200
-//     workgroups polling one shared counter instead made a hot spot that cost
-//     about 13 us per mixer.)
-//   * The flags are generation counters, never lowered: a call waits for the
-//     advance that follows its own start, so an advance that comes late (after
-//     its waiter gave up) can never satisfy the next call, whose waiters read
-//     the flag afresh.
-//   * The down items sit in the lowest workgroup indices, which the hardware
-//     dispatches first, so the wait never depends on a workgroup that could
-//     not get a CU; the grid is at most one workgroup per CU.
+//     flag line).  One lane of each workgroup waits until its flag reaches
+//     the call's generation (s_sleep between reads, at most spin_limit
+//     reads); the workgroup then stages the bottleneck with device-coherent
+//     loads and runs its up tiles.  (200 workgroups polling one shared
+//     counter instead made a hot spot that cost about 13 us per mixer.)
+//   * Generations: beside its flag, on the same line, workgroup w keeps the
+//     number of calls whose grid held a workgroup w (its ack word).  Every
+//     such call advances flag w exactly once (every down item always runs,
+//     so the last tile is always counted), and its workgroup w adds one to
+//     ack w when it starts, so flag w == ack w between calls.  A workgroup
+//     therefore waits for flag == ack + 1 (the ack read at its start): the
+//     target does not depend on when the workgroup starts.  A workgroup
+//     that only gets a CU after the advance (another kernel holding CUs)
+//     finds its flag there already; one whose wait gave up still counts its
+//     call, so the late advance cannot satisfy the next call.
+//   * The down items sit in the lowest workgroup indices, which each XCD
+//     dispatches in order, so every down item was dispatched before any
+//     workgroup that waits on the same XCD, and a wait never depends on a
+//     workgroup that waits behind it for a CU; the grid is at most one
+//     workgroup per CU.
 //   * A wait that reaches spin_limit (which would need another kernel
 //     holding the CUs for about a second) writes NaN to that workgroup's
 //     outputs and sets bit 0 of the status word sync[1].
 constexpr int kMixFlagStride = 32;               // int32 between flags: one 128-byte line each
+constexpr int kMixAckAt = 16;                    // a workgroup's ack word, 64 bytes after its flag
 
 struct HcMixArgs {
   GemvLaunch d;          // down: x, q, s, di (out), bot (out2), lr, hc, split-K slots and tickets
   HcUpArgs u;            // up: bot [M, lr] contiguous, interleaved q/s, normalized, out
   int* sync;             // [0] down tiles done (zero between calls), [1] status (bit 0: a wait gave up),
-                         // [kMixFlagStride * (w + 1)] generation flag of workgroup w
+                         // [kMixFlagStride * (w + 1)] generation flag of workgroup w,
+                         // [kMixFlagStride * (w + 1) + kMixAckAt] its ack word (calls it has started)
   int C, D, tiles_d, R, spin_limit;
 };
 
@@ -218,8 +227,11 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   const int J = ((nch + CPS - 1) / CPS + DP - 1) / DP;
   const int64_t urow = (int64_t)tuc * T + grp * 16 + n;
   int* flag = a.sync + kMixFlagStride * (blockIdx.x + 1);
-  int gen0 = 0;                                     // this workgroup's flag before the call's advance
-  if (threadIdx.x == 0) gen0 = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int gen = 0;                                      // the value this call's advance gives the flag
+  if (threadIdx.x == 0) {
+    gen = __hip_atomic_load(flag + kMixAckAt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    __hip_atomic_store(flag + kMixAckAt, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // 1. one down item in each of the first D workgroups (the critical path:
   //    its loads go out first)
@@ -268,14 +280,14 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   }
   __syncthreads();
 
-  // 3. wait for this workgroup's flag to advance past its value at the start
+  // 3. wait for this workgroup's flag to reach the call's generation
   if (threadIdx.x == 0) {
     int f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int it = 0; f == gen0 && it < a.spin_limit; ++it) {
+    for (int it = 0; f != gen && it < a.spin_limit; ++it) {
       __builtin_amdgcn_s_sleep(4);
       f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    s_ok = f != gen0;
+    s_ok = f == gen;
     if (!s_ok) __hip_atomic_fetch_or(a.sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();

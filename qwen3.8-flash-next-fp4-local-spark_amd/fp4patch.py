@@ -30,19 +30,28 @@ weights are prepared) back to the method it replaced.
 import os
 import sys
 
-# Tile tables keyed by weight shape (N, K): (BN, BK, KSPLIT, warps).  The
-# MI355X kernels choose their own tiling; KSPLIT (how many K slices are
-# summed, in order) and the shape assertion on (K, KSPLIT, BK) are what these
-# entries still decide.  The values are the reference's (x/fp4patch.py:11-21).
-CFG_MX8 = {(16384, 2560): (32, 512, 1, 4), (96, 2560): (16, 128, 4, 2), (13312, 2560): (32, 512, 1, 4),
-           (640, 2560): (16, 512, 1, 4), (1280, 2560): (16, 512, 1, 4), (2560, 6144): (32, 512, 1, 4),
-           (2560, 640): (32, 128, 1, 4)}
-CFG_W6 = {(16384, 2560): (32, 256, 1, 4), (96, 2560): (16, 256, 2, 4), (13312, 2560): (32, 256, 1, 4),
-          (640, 2560): (16, 256, 1, 4), (1280, 2560): (16, 256, 1, 4), (2560, 6144): (32, 256, 1, 4),
-          (2560, 640): (32, 128, 1, 4)}
+# Tile tables keyed by weight shape (N, K): (BN, BK, KSPLIT, warps), or
+# (BN, BK, warps, KSPLIT) for NVFP4.  The MI355X kernels choose their own
+# tiling; KSPLIT (how many K slices are summed, in order) and the shape
+# assertion on (K, KSPLIT, BK) are what these entries still decide.  The values
+# are the reference's (x/fp4patch.py:11-21) except two K splits:
+#   * CFG_W8[(336, 10240)] sums 8 K slices (the reference: 4) so that the
+#     unfused mixer's down projection takes the fused one's decomposition
+#     (HC_DOWN_CFG) and the two paths give the same bits;
+#   * CFG_BG[(336, 10240)] sums 4 K slices (the reference: 1).  With one slice
+#     this 21-tile bf16 GEMV has 21 workgroups for 256 CUs; four ordered slices
+#     spread it over 84, and fix its summation order as any split does.  (On
+#     the reference's GPU the same table entry takes one slice because its
+#     split-K adds partials with fp32 atomics in no fixed order.)
+CFG_MX8 = {(16384, 2560): (16, 512, 1, 4), (96, 2560): (16, 128, 4, 2), (13312, 2560): (32, 512, 1, 4),
+           (640, 2560): (16, 512, 1, 2), (1280, 2560): (16, 256, 1, 4), (2560, 6144): (32, 512, 1, 4),
+           (2560, 640): (64, 128, 1, 4)}
+CFG_W6 = {(16384, 2560): (32, 256, 1, 4), (96, 2560): (16, 256, 2, 4), (13312, 2560): (16, 256, 1, 4),
+          (640, 2560): (16, 256, 1, 2), (1280, 2560): (16, 256, 1, 2), (2560, 6144): (32, 256, 1, 4),
+          (2560, 640): (32, 128, 1, 2)}
 CFG_NV4 = {}
 CFG_BG = {(336, 10240): (16, 512, 4, 4), (10240, 320): (32, 64, 1, 4), (512, 2560): (16, 256, 1, 4)}
-CFG_HC_NV4 = {(336, 10240): (16, 128, 2, 4), (10240, 320): (32, 64, 4, 1)}
+CFG_HC_NV4 = {(336, 10240): (16, 128, 2, 20), (10240, 320): (32, 64, 4, 1)}
 CFG_W8 = {(336, 10240): (32, 256, 8, 4), (10240, 320): (32, 64, 1, 8), (512, 2560): (16, 512, 1, 4)}
 # The fused mixer's down projection and the unfused one (CFG_W8[(336, 10240)])
 # use the same KSPLIT, so both give the same bits.
@@ -72,6 +81,24 @@ def _mx8_cfg(n, k):
     """The MXFP8 linear's cfg for an (N, K) weight: the table's, else one
     K slice with the largest K tile dividing K."""
     return CFG_MX8.get((n, k)) or (32, _k_tile(k), 1, 4)
+
+
+class _Stats:
+    """Call counts of the hooks, logged every `every` counted calls (the
+    reference logs its dense-linear counts every 20,000 calls,
+    x/fp4patch.py:22, :122-123, :135-136)."""
+
+    def __init__(self, every=20000):
+        self.every, self.n, self.total = every, {}, 0
+
+    def count(self, key):
+        self.n[key] = self.n.get(key, 0) + 1
+        self.total += 1
+        if self.total % self.every == 0:
+            _say(f"stats {dict(sorted(self.n.items()))}")
+
+
+STATS = _Stats()
 
 
 class _Milestones:
@@ -143,7 +170,9 @@ class _DenseDecode:
     def run(self, layer, source, bias):
         rows = self.packed_rows(layer, source, bias)
         if rows is None:
+            STATS.count("mx8_skip")
             return self.original(layer, source, bias)
+        STATS.count("mx8")
         w, s = rows
         n, k = w.shape
         F = self.F
@@ -231,7 +260,17 @@ class _Projection:
 
 
 class _Mixer:
-    """State of the GatedResidual._mix_normalized hook (x/fp4patch.py:197-249)."""
+    """State of the GatedResidual._mix_normalized hook (x/fp4patch.py:197-249).
+
+    The fused mixer runs as one launch (HCFused.mix), whose up workgroups wait
+    for the bottleneck with a bounded wait; a wait that gives up leaves NaN in
+    that call's block_input and sets a status bit.  check_waits() reads that bit
+    without blocking, from eager calls (every CHECK_EVERY-th eager mixer call,
+    and every eager call of the fast head); after a give-up the hook logs and
+    counts it and runs each mixer as two launches (down, then up), which wait
+    for nothing.  Graphs captured before keep the launches they recorded."""
+
+    CHECK_EVERY = 64
 
     def __init__(self, torch, F, HC, op, fused):
         self.torch, self.F, self.HC, self.op, self.fused = torch, F, HC, op, fused
@@ -239,6 +278,22 @@ class _Mixer:
         self.scratch = None                                           # one HCFused for every mixer
         self.down = {}                                                # (data_ptr, shape) -> (q, s)
         self.up = {}                                                  # (data_ptr, shape) -> interleaved (q, s)
+        self.single = True                                            # one launch per fused mixer
+        self.timeouts = 0
+        self.eager_calls = 0
+
+    def check_waits(self):
+        """Poll the single-launch mixer's status word (non-blocking, eager only);
+        on a give-up, log, count and switch to two launches per mixer."""
+        if self.scratch is None or not self.single or _capturing(self.torch):
+            return
+        if self.scratch.poll_timeouts():
+            self.timeouts += 1
+            self.single = False
+            STATS.count("mix_timeout")
+            _say(f"fused mixers: a single-launch mixer gave up waiting for its bottleneck ({self.timeouts} so far; "
+                 "its block_input held NaN); each mixer now runs as two launches (graphs captured before keep "
+                 "the single launch)")
 
     def _prepared(self, res, normalized):
         """The layer's (down, up) W8 copies and the shared scratch, prepared on
@@ -268,14 +323,25 @@ class _Mixer:
         (qd, sd), (qi, si) = planes
         x = normalized.contiguous()
         # down then up, as HCFused.down + HCFused.up (x/fp4patch.py:217-218), one launch where the shapes allow
-        di, _, block_input = self.scratch.mix(x, qd, sd, res.lora_rank, res.hc_count, qi, si, x, HC_DOWN_CFG,
-                                              HC_UP_CFG)
+        if self.single:
+            STATS.count("mix_single")
+            di, _, block_input = self.scratch.mix(x, qd, sd, res.lora_rank, res.hc_count, qi, si, x, HC_DOWN_CFG,
+                                                  HC_UP_CFG)
+        else:
+            STATS.count("mix_two")
+            di, bot = self.scratch.down(x, qd, sd, res.lora_rank, res.hc_count, HC_DOWN_CFG)
+            block_input = self.F.HCFused.up(bot, qi, si, x, res.hc_count, HC_UP_CFG)
         injection = di[:, res.lora_rank: res.lora_rank + res.hc_count] if res.use_combine else None
         return block_input, injection
 
     def mix(self, res, normalized, original):
         if res.tp_size > 1:
+            STATS.count("mix_skip")
             return original(res, normalized)
+        if self.scratch is not None and not _capturing(self.torch):
+            self.eager_calls += 1
+            if self.eager_calls % self.CHECK_EVERY == 0:
+                self.check_waits()
         quantized = "mtp" not in (res._preparation_prefix or "") or self.w8_mtp
         decode = normalized.shape[0] <= MAX_ROWS
         if self.fused and quantized and decode:
@@ -295,7 +361,11 @@ class _Mixer:
         gate_logits = self.op(bottleneck, res.input_mix_weight_up.weight, quantized)
         block_input = (self.F.hc_gate_mean(normalized, gate_logits, hc) if on_gpu
                        else self.HC.hc_gate_mix(normalized, gate_logits, hc))
+        STATS.count("mix_unfused")
         return block_input, injection
+
+
+MIXERS = []              # the installed mixer hooks, whose status the fast head's eager calls also check
 
 
 def _patch_linears(torch, op, mtp_w8, gate_mode):
@@ -349,6 +419,7 @@ def _patch_hc():
     op = torch.ops.vllm.fp4x_bf16_linear
     original = HC.GatedResidual._mix_normalized
     mixer = _Mixer(torch, F, HC, op, fused=projection.w8 and _on("FP4X_HC_FUSED"))
+    MIXERS.append(mixer)
 
     def _mix_normalized(self, normalized):
         return mixer.mix(self, normalized, original)
@@ -415,7 +486,10 @@ class _FastHead:
 
     def compute(self, model, hidden_states):
         h = hidden_states
+        for mixer in MIXERS:                          # once per step: the head runs eagerly
+            mixer.check_waits()
         if self.disabled or h.dim() != 2 or not 0 < h.shape[0] <= MAX_ROWS:
+            STATS.count("head_skip")
             return self.original(model, hidden_states)
         if not self.ready:
             if _capturing(self.torch):
@@ -423,6 +497,7 @@ class _FastHead:
             self.build(model, h.contiguous())
             if self.disabled:
                 return self.original(model, hidden_states)
+        STATS.count("head")
         return self.logits(h.contiguous())
 
 

@@ -12,8 +12,11 @@ summed (in slice order, deterministically), and the reference's shape
 assertion on (K, KSPLIT, BK) is kept.  Tile sizes and warp counts are GB10
 Triton knobs; the HIP kernels choose their own gfx950 layout.
 
-Weight preparation (quantize_*, dequant_int2, dequant_nv4, interleave_up)
-stays in torch, as in the reference; it runs once per weight at load time.
+Weight preparation: quantize_* and requantize_* run as HIP kernels on device
+tensors (libfp4x.so's quantizers, bit-exact with the reference's fp32 torch
+expressions) and as those torch expressions on CPU tensors; mx8_dequant is a
+HIP kernel; dequant_int2, dequant_nv4 and interleave_up are torch
+expressions.  Each runs once per weight at load time.
 """
 import torch
 
@@ -215,9 +218,9 @@ def int2_topk(x, P, S, N, C, RS=None, out_dtype=torch.bfloat16, sorted=True):
     (coarse [M, N], idx int64 [M, C]) = (int2_logits(x, P, S, N, RS=RS,
     out_dtype=out_dtype), topk_rows(coarse, C)), in one call that lets the
     coarse kernel produce the top-k's slice maxima.  sorted=False: the same
-    index set per row, for callers that only scatter at these indices, in
-    increasing index order for bf16 logits (no sort) and in topk_rows' order
-    for fp32 ones."""
+    index set per row in an unspecified order, for callers that only scatter
+    at these indices (where the selection can skip its sort, increasing index
+    order)."""
     _need_cuda(x, P, S)
     x = x.to(torch.bfloat16).contiguous()
     m, k = x.shape
@@ -289,7 +292,10 @@ def _topk_workspace(device, nbytes):
 
 
 def refine_mx8_(out, x, idx, w8, s_u8, BC=16, BK=256, nw=4):
-    """In place: out[m, idx[m, c]] = exact MXFP8 row idx[m, c] . x[m] (fp32 accumulate)."""
+    """Rescore the candidates in place and return out: for each row m and
+    candidate c, out[m, idx[m, c]] becomes the dot product of x[m] with the
+    dequantized MXFP8 weight row idx[m, c] (products exact in fp32, summed
+    with fp32 fma in the rescore kernel's fixed order), cast to out's dtype."""
     _need_cuda(out, x, idx, w8, s_u8)
     x = x.to(torch.bfloat16).contiguous()
     idx = idx.to(torch.int64).contiguous()
@@ -303,7 +309,10 @@ def refine_mx8_(out, x, idx, w8, s_u8, BC=16, BK=256, nw=4):
 
 
 def refine_nv4(x, idx, wp, s, gs, BC=16, BK=256, nw=4):
-    """[M, C] exact NVFP4 logits for candidate rows idx[m, c] (fp32 accumulate, times gs)."""
+    """fp32 [M, C]: for each row m and candidate c, gs times the dot product of
+    x[m] with the dequantized NVFP4 weight row idx[m, c] (exact products,
+    fp32 fma in the rescore kernel's fixed order); NaN for a candidate
+    outside [0, V)."""
     _need_cuda(x, idx, wp, s)
     x = x.to(torch.bfloat16).contiguous()
     idx = idx.to(torch.int64).contiguous()
@@ -355,6 +364,8 @@ class HCFused:
         cus = torch.cuda.get_device_properties(device).multi_processor_count
         self.tickets = torch.zeros(2 * max(n_down, 16) + 64 + 32 * (cus + 1), dtype=torch.int32, device=device)
         self._status_at = (self.tickets.numel() - 32 * (cus + 1)) // 32 * 32 + 1
+        self._poll_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self._poll_event = None
 
     def down(self, x, q, s, lr, hc, cfg=(32, 512, 4, 4)):
         """(di bf16 [M, N], bot bf16 [M, lr]) = split-K W8 GEMV + cast + scaled SiLU."""
@@ -413,9 +424,32 @@ class HCFused:
             self.tickets[at].zero_()
         return hit
 
+    def poll_timeouts(self):
+        """wait_timeouts without blocking: True if the status word copied by an
+        earlier poll showed a give-up.  Each poll whose previous copy has
+        arrived queues, on the current stream after the work already there, a
+        copy of the word to pinned host memory and the word's clear; so a
+        give-up is reported by the first poll after its copy arrives.  Eager
+        use only (the copy and the clear must not be captured)."""
+        if not getattr(self, "_mixed", False):
+            return False
+        hit = False
+        if self._poll_event is not None:
+            if not self._poll_event.query():
+                return False                                   # the last copy is still in flight
+            hit = bool(int(self._poll_host[0]) & 1)
+        at = self._status_at
+        self._poll_host.copy_(self.tickets[at:at + 1], non_blocking=True)
+        self.tickets[at:at + 1].zero_()
+        self._poll_event = torch.cuda.Event()
+        self._poll_event.record()
+        return hit
+
     @staticmethod
     def interleave_up(q, s, hc, bj):
-        """Reorder up-projection rows [HC*H, K] so each BJ-column tile holds its HC stream rows contiguously."""
+        """Permute the up projection's rows [hc*H, K] (and their scales): stored
+        row t*(hc*bj) + s*bj + j holds original row s*H + t*bj + j, so the hc
+        stream rows of output columns t*bj .. t*bj + bj - 1 are one block."""
         n = q.shape[0]
         h = n // hc
         idx = torch.arange(n, device=q.device).view(hc, h // bj, bj).permute(1, 0, 2).reshape(-1)

@@ -98,6 +98,10 @@ def test_argument_errors_without_gpu(lib):
     assert b"bad target" in L.fp4x_last_error()
     assert Q(2, None, None, 0.0, 8, 128, 0, 16, 31, 0.0, None, None, None, None) == _fp4x.ERR_ARG
     assert L.fp4x_absmax(1, None, None, 0.0, 8, 100, None, None) == _fp4x.ERR_ARG
+    # the CU-holding test kernel: bounded time and LDS
+    assert L.fp4x_hold_cus(8, 200000, 160, None, None) == _fp4x.ERR_ARG
+    assert L.fp4x_hold_cus(8, 100, 161, None, None) == _fp4x.ERR_ARG
+    assert b"hold_cus" in L.fp4x_last_error()
     # empty problems are no-ops
     assert L.fp4x_mx8_linear(None, 2560, None, None, None, 0, 0, 64, 2560, 1, None, None, None) == _fp4x.OK
 

@@ -17,8 +17,13 @@
   input;
 * a single-launch call whose flag wait gives up (forced from the host with
   FP4X_HC_SPIN_LIMIT=0) writes NaN and sets the status word, and the next
-  call is bit-identical to the two-launch path.
+  call is bit-identical to the two-launch path;
+* single-launch calls whose up workgroups get a CU only after the bottleneck
+  is ready (a kernel on another stream holds most CUs) are bit-identical to
+  the two-launch path, with no NaN and no status bit.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -226,4 +231,53 @@ def test_mix_wait_give_up_then_recovers(gpu, F, monkeypatch):
         for a, b in zip(again, ref):
             assert torch.equal(a, b)
         assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
+    assert not fx.wait_timeouts()
+
+
+@pytest.mark.parametrize("nd,lr,ks", [(ND, LR, KS), (336, 320, 8)])
+def test_mix_late_workgroups(gpu, F, monkeypatch, nd, lr, ks):
+    """Workgroups that start after the bottleneck's flag advance.  A kernel on a
+    second stream holds most CUs for 4 ms (one workgroup filling a CU's LDS on
+    each), and the single-launch mixers issued meanwhile on the current stream
+    run on the CUs left free: their up workgroups are dispatched as down items
+    end, many after the last down tile has advanced the flags.  Each must find
+    its generation reached instead of waiting for another advance: no NaN, no
+    status bit, every call bit-identical to the two-launch path.  The flag
+    wait is limited to 2^18 reads (tens of ms, set from the host), so a
+    workgroup waiting for an advance that never comes ends its call with NaN
+    instead of stalling the test."""
+    import _fp4x as L
+    rng = np.random.default_rng(91 + nd)
+    (qd, sd), (qu, su) = layer(rng, nd=nd, lr=lr)
+    qd, sd = dev(qd), dev(sd)
+    qi, si = F.HCFused.interleave_up(dev(qu), dev(su), HC, 8)
+    fx = F.HCFused(gpu, n_down=nd, max_ksplit=ks)
+    x_t = bf16_dev(act(rng, 3, HC * H)[0])
+    cfg = (32, 256, ks, 4)
+    with path_switch(monkeypatch, "FP4X_HC_MIX"):
+        ref = fx.mix(x_t, qd, sd, lr, HC, qi, si, x_t, cfg)
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    sink = torch.zeros(1, dtype=torch.int32, device=gpu)
+    side = torch.cuda.Stream(gpu)
+    with path_switch(monkeypatch, "FP4X_HC_SPIN_LIMIT", str(1 << 18)):
+        for free in (cus // 8, cus // 4, cus // 2):
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            L.check(L.lib().fp4x_hold_cus(cus - free, 4000, 160, L.ptr(sink), ctypes.c_void_p(side.cuda_stream)),
+                    "hold_cus")
+            t0.record()
+            outs = [fx.mix(x_t, qd, sd, lr, HC, qi, si, x_t, cfg) for _ in range(8)]
+            t1.record()
+            torch.cuda.synchronize()
+            print(f"{nd}x{HC * H} mixers with {free} of {cus} CUs free: "
+                  f"{t0.elapsed_time(t1) * 1e3 / 8:.1f} us per call", flush=True)
+            for i, o in enumerate(outs):
+                assert not torch.isnan(o[2].float()).any(), (free, i)
+                for a, b in zip(o, ref):
+                    assert torch.equal(a, b), (free, i)
+            assert not fx.wait_timeouts(), free
+            assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
+    again = fx.mix(x_t, qd, sd, lr, HC, qi, si, x_t, cfg)
+    for a, b in zip(again, ref):
+        assert torch.equal(a, b)
     assert not fx.wait_timeouts()

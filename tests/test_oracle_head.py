@@ -87,3 +87,24 @@ def test_int2_coarse_is_rounded_exact_sum():
         for v in range(V):
             ex = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(x[m], op[v]))
             assert Fraction(float(got[m, v])) == er.f32(ex), (m, v)
+
+
+def test_fast_head_argmax_blocks():
+    """fast_head_argmax (one coarse pass, top-C and rescore per block of rows)
+    equals the argmax of fast_head's output row by row, with blocks that split
+    the rows unevenly; a planted winner row is every row's argmax."""
+    rng = np.random.default_rng(15)
+    V, K, C, M = 2000, 256, 32, 7
+    w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    q, s = oq.quantize_mx8(w)
+    P, S = oq.quantize_int2(oq.mx8_dequant(q, s), group=16)
+    xb = fm.bf16_bits(fm.round_bf16(rng.standard_normal((M, K)).astype(np.float32)))
+    _, _, out = oh.fast_head(xb, P, S, 16, q, s, C, 4)
+    want = np.argmax(fm.bf16_to_f32(out), -1)
+    assert np.array_equal(oh.fast_head_argmax(xb, P, S, 16, q, s, C, 4, block=3), want)
+    # a row aligned with x[0] wins row 0 by a wide margin
+    w2 = w.copy()
+    w2[123] = fm.bf16_to_f32(xb[0]) * 0.5
+    q2, s2 = oq.quantize_mx8(w2)
+    P2, S2 = oq.quantize_int2(oq.mx8_dequant(q2, s2), group=16)
+    assert oh.fast_head_argmax(xb[:1], P2, S2, 16, q2, s2, C, 4)[0] == 123
