@@ -573,6 +573,78 @@ __device__ uint32_t rs_kth(const uint32_t (&key)[N], int k, uint32_t* wh, TkHist
   return lo + sel;
 }
 
+// k-th largest (k >= 1) of the keys held N per thread (0 = none) in one
+// histogram round over the kRsThreads key values at and below the largest key
+// hi: thread b's bin counts the keys equal to hi - b, and one workgroup scan
+// over the bins finds the key.  Returns 0 when fewer than k keys lie in that
+// window (the caller then takes rs_kth); else the key, with *hi_out = hi and
+// *above_out = the number of keys strictly above it.  hist (kRsThreads words)
+// must be zero and visible on entry.  Logit maxima span far fewer than 1024
+// bf16 key values above their C-th largest, so one round decides.
+template <int N>
+__device__ uint32_t rs_kth_window(const uint32_t (&key)[N], int k, uint32_t* hist, int* slots, uint32_t* ext,
+                                  uint32_t* hi_out, int* above_out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t hi = 0;
+#pragma unroll
+  for (int j = 0; j < N; ++j) hi = max(hi, key[j]);
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) hi = max(hi, rs_xor_lane(hi, d));
+  if (lane == 0) ext[wave] = hi;
+  __syncthreads();
+  hi = 0;
+#pragma unroll
+  for (int w = 0; w < kRsWaves; ++w) hi = max(hi, ext[w]);
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const uint32_t off = hi - key[j];
+    if (key[j] != 0 && off < (uint32_t)kRsThreads) atomicAdd(&hist[off], 1u);
+  }
+  __syncthreads();
+  const int c = (int)hist[threadIdx.x];
+  int tot;
+  const int pre = rs_scan(c, slots, &tot);
+  if (pre < k && pre + c >= k) {
+    ext[2 * kRsWaves] = hi - threadIdx.x;
+    ext[2 * kRsWaves + 1] = (uint32_t)pre;
+  }
+  __syncthreads();
+  if (tot < k) return 0;                           // (the same in every thread)
+  *hi_out = hi;
+  *above_out = (int)ext[2 * kRsWaves + 1];
+  return ext[2 * kRsWaves];
+}
+
+// The C largest of n_c (C <= n_c <= kRsThreads) bf16 candidates, for callers
+// that need the set only: T, the C-th largest key16, by one window round (the
+// candidates' keys lie within the window of the row's maxima, so it always
+// decides), then every candidate above T and the first C - (count above T) at
+// T in candidate (index) order, ranked by ballots and per-wave counts, and
+// placed the same way, so the set comes out in increasing index order.
+// hist must be zero and visible on entry.  Candidate t's key16 is ck[t] >> 16.
+__device__ void tk_select_set_window(const uint32_t* ck, const int* cidx, int n_c, int C, uint32_t* hist, int* slots,
+                                     uint32_t* ext, int64_t* out) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const uint32_t key[1] = {t < n_c ? ck[t] >> 16 : 0u};
+  uint32_t hi;
+  int above;
+  const uint32_t T = rs_kth_window<1>(key, C, hist, slots, ext, &hi, &above);
+  const bool up = key[0] > T, tie = key[0] != 0 && key[0] == T;
+  const uint64_t below = (1ull << lane) - 1ull;
+  const uint64_t bt = __ballot(tie);
+  if (lane == 0) slots[wave] = __popcll(bt);
+  __syncthreads();
+  int before = 0;
+  for (int w = 0; w < wave; ++w) before += slots[w];
+  const bool in = up || (tie && before + __popcll(bt & below) < C - above);
+  const uint64_t bi = __ballot(in);
+  if (lane == 0) ext[wave] = __popcll(bi);          // (the window round's reads of ext[0, kRsWaves) are done)
+  __syncthreads();
+  int pos = 0;
+  for (int w = 0; w < wave; ++w) pos += (int)ext[w];
+  if (in) out[pos + __popcll(bi & below)] = (int64_t)cidx[t];
+}
+
 // Descending ranks of n <= 256 distinct keys a[0, n) in LDS: thread (t, q)
 // counts the keys above a[t] among a quarter (n2 = 256), an eighth (128) or a
 // sixteenth (<= 64) of them; the partial counts meet in part[1024].  Returns
@@ -632,9 +704,10 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
   __shared__ int cidx[kTkCap + 64];       // bf16 candidate element indices, increasing
   __shared__ int slist[kTkCap + 64];      // candidate slices, increasing
   __shared__ uint32_t wh[kRsWaves * 256];
+  __shared__ uint32_t hist[kRsThreads];   // the window round's bins (zero before each use)
   __shared__ TkHist h;
   __shared__ int slots[kRsWaves];
-  __shared__ uint32_t ext[2 * kRsWaves];
+  __shared__ uint32_t ext[2 * kRsWaves + 2];
   __shared__ int n_x;
   const int m = blockIdx.x;
   const typename E::T* row = logits + (int64_t)m * stride;
@@ -647,8 +720,9 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
   }
   const int S = tk_slice(V), ns = (V + S - 1) / S;
   int n_c = 0;
-  bool exact = ns < C;
+  bool exact = ns < C, windowed = false;
   if (!exact) {
+    hist[threadIdx.x] = 0;                          // (visible after the first barrier of the T0 round)
     // thread t holds the 8-slice vectors [t * VPT, t * VPT + VPT) of the row's
     // slice maxima (the padding past ns is never written: masked)
     const int nv = (ns + 7) / 8;
@@ -667,97 +741,109 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
       }
     }
     // T0: the C-th largest maximum of 4-slice groups (a lower bound of the
-    // C-th largest element: C groups each hold an element >= T0)
+    // C-th largest element: C groups each hold an element >= T0), in one
+    // window round when the groups' top C lie within 1024 key values of the
+    // largest (then every candidate's key does too), else by rs_kth
     uint32_t key[VPT * 2];
 #pragma unroll
     for (int j = 0; j < VPT * 2; ++j)
       key[j] = max(max(sk[4 * j], sk[4 * j + 1]), max(sk[4 * j + 2], sk[4 * j + 3]));
     const int ng = (ns + 3) / 4;
-    const uint32_t T0 = ng >= C ? rs_kth(key, C, wh, h, ext) : 1u;
-    // candidate slices (maximum >= T0), in increasing order: one scan.  Waves
-    // past the row's vectors (short rows) hold no slices and skip the work.
+    uint32_t T0 = 1u;
+    if (ng >= C) {
+      uint32_t hi;
+      int above;
+      T0 = rs_kth_window(key, C, hist, slots, ext, &hi, &above);
+      windowed = T0 != 0;
+      if (!windowed) T0 = rs_kth(key, C, wh, h, ext);
+    }
+    hist[threadIdx.x] = 0;                          // for the final round (the T0 round has read its bin)
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const bool live = wv * 64 * VPT < nv;
-    int cc = 0;
-    if (live) {
+    {
+      // candidate slices in increasing order: one scan.  Waves past the row's
+      // vectors (short rows) hold no slices and skip the work.
+      const bool live = wv * 64 * VPT < nv;
+      int cc = 0;
+      if (live) {
 #pragma unroll
-      for (int j = 0; j < VPT * 8; ++j) cc += sk[j] >= T0 ? 1 : 0;
-    }
-    int nsl;
-    int pos = rs_scan(cc, slots, &nsl);
-    nsl = __builtin_amdgcn_readfirstlane(nsl);
-    if (live) {
-      const int dummy = kTkCap + (threadIdx.x & 63);
-#pragma unroll
-      for (int j = 0; j < VPT * 8; ++j) {
-        const bool in = sk[j] >= T0;
-        slist[in && pos < kTkCap ? pos : dummy] = (threadIdx.x * VPT + (j >> 3)) * 8 + (j & 7);
-        pos += in ? 1 : 0;
+        for (int j = 0; j < VPT * 8; ++j) cc += sk[j] >= T0 ? 1 : 0;
       }
-    }
-    __syncthreads();
-    exact = nsl > kTkCap;
-    if (!exact) {
-      // their elements whose key16 >= T0, in increasing index order: thread t
-      // takes contiguous 16-byte items (8 bf16 or 4 fp32 elements) of a round,
-      // one scan per round; waves holding no item of the round skip to the
-      // scan, and the second item slot is skipped when the round has at most
-      // one item per thread
-      const int per = S / EPI, tot = nsl * per;
-      for (int r0 = 0; r0 < tot; r0 += kRsThreads * kRsIpt) {
-        const int nr = min(tot - r0, kRsThreads * kRsIpt);
-        const int ipt = (nr + kRsThreads - 1) / kRsThreads;
-        const bool wlive = wv * 64 * ipt < nr;
-        uint32_t k8[kRsIpt * EPI];        // key16 (0: no element)
-        uint32_t raw[kRsIpt * EPI];       // the elements (fp32 rows: for the full key)
-        int e[kRsIpt];
-        int cnt = 0;
-        if (wlive) {
-          uint4 v[kRsIpt];
+      int nsl;
+      int pos = rs_scan(cc, slots, &nsl);
+      nsl = __builtin_amdgcn_readfirstlane(nsl);
+      if (live) {
+        const int dummy = kTkCap + (threadIdx.x & 63);
 #pragma unroll
-          for (int j = 0; j < kRsIpt; ++j) {
-            // every slot loads (a dead one reads the row's first item), so no
-            // load waits at a branch's join; the row's last item is read whole
-            // (rows are readable to a whole item past V), its elements past V
-            // masked below
-            const int it = r0 + threadIdx.x * ipt + j;
-            const bool ok = j < ipt && it < r0 + nr;
-            e[j] = ok ? slist[it / per] * S + (it % per) * EPI : -1;
-            v[j] = *reinterpret_cast<const uint4*>(row + (ok ? e[j] : 0));
-          }
-#pragma unroll
-          for (int j = 0; j < kRsIpt; ++j) {
-#pragma unroll
-            for (int q = 0; q < EPI; ++q) {
-              raw[j * EPI + q] = E::at(v[j], q);
-              const uint32_t kq = E::key16((typename E::T)raw[j * EPI + q]);
-              k8[j * EPI + q] = e[j] >= 0 && e[j] + q < V ? kq : 0u;
-              cnt += k8[j * EPI + q] >= T0 ? 1 : 0;
-            }
-          }
+        for (int j = 0; j < VPT * 8; ++j) {
+          const bool in = sk[j] >= T0;
+          slist[in && pos < kTkCap ? pos : dummy] = (threadIdx.x * VPT + (j >> 3)) * 8 + (j & 7);
+          pos += in ? 1 : 0;
         }
-        int step;
-        int p2 = n_c + rs_scan(cnt, slots, &step);
-        if (wlive) {
-          const int dummy = kTkCap + (threadIdx.x & 63);
-#pragma unroll
-          for (int j = 0; j < kRsIpt * EPI; ++j) {
-            const bool in = k8[j] >= T0;
-            const int at = in && p2 < kTkCap ? p2 : dummy;
-            const int ei = e[j / EPI] + (j % EPI);
-            if constexpr (F32) {
-              cand[at] = tk_comp(E::key((typename E::T)raw[j]), (uint32_t)ei);
-            } else {
-              ck[at] = (k8[j] << 16) | (uint32_t)(0xffff - p2);
-              cidx[at] = ei;
-            }
-            p2 += in ? 1 : 0;
-          }
-        }
-        n_c += __builtin_amdgcn_readfirstlane(step);
       }
       __syncthreads();
-      exact = n_c > kTkCap;
+      exact = nsl > kTkCap;
+      if (!exact) {
+        // their elements whose key16 >= T0, in increasing index order: thread t
+        // takes contiguous 16-byte items (8 bf16 or 4 fp32 elements) of a round,
+        // one scan per round; waves holding no item of the round skip to the
+        // scan, and the second item slot is skipped when the round has at most
+        // one item per thread
+        const int per = S / EPI, tot = nsl * per;
+        for (int r0 = 0; r0 < tot; r0 += kRsThreads * kRsIpt) {
+          const int nr = min(tot - r0, kRsThreads * kRsIpt);
+          const int ipt = (nr + kRsThreads - 1) / kRsThreads;
+          const bool wlive = wv * 64 * ipt < nr;
+          uint32_t k8[kRsIpt * EPI];        // key16 (0: no element)
+          uint32_t raw[kRsIpt * EPI];       // the elements (fp32 rows: for the full key)
+          int e[kRsIpt];
+          int cnt = 0;
+          if (wlive) {
+            uint4 v[kRsIpt];
+#pragma unroll
+            for (int j = 0; j < kRsIpt; ++j) {
+              // every slot loads (a dead one, or an item starting past V, reads
+              // the row's first item), so no load waits at a branch's join; the
+              // item holding element V - 1 is read whole (rows are readable to
+              // the 16-byte boundary after V), its elements past V masked below
+              const int it = r0 + threadIdx.x * ipt + j;
+              const bool ok = j < ipt && it < r0 + nr;
+              e[j] = ok ? slist[it / per] * S + (it % per) * EPI : -1;
+              v[j] = *reinterpret_cast<const uint4*>(row + (ok && e[j] < V ? e[j] : 0));
+            }
+#pragma unroll
+            for (int j = 0; j < kRsIpt; ++j) {
+#pragma unroll
+              for (int q = 0; q < EPI; ++q) {
+                raw[j * EPI + q] = E::at(v[j], q);
+                const uint32_t kq = E::key16((typename E::T)raw[j * EPI + q]);
+                k8[j * EPI + q] = e[j] >= 0 && e[j] + q < V ? kq : 0u;
+                cnt += k8[j * EPI + q] >= T0 ? 1 : 0;
+              }
+            }
+          }
+          int step;
+          int p2 = n_c + rs_scan(cnt, slots, &step);
+          if (wlive) {
+            const int dummy = kTkCap + (threadIdx.x & 63);
+#pragma unroll
+            for (int j = 0; j < kRsIpt * EPI; ++j) {
+              const bool in = k8[j] >= T0;
+              const int at = in && p2 < kTkCap ? p2 : dummy;
+              const int ei = e[j / EPI] + (j % EPI);
+              if constexpr (F32) {
+                cand[at] = tk_comp(E::key((typename E::T)raw[j]), (uint32_t)ei);
+              } else {
+                ck[at] = (k8[j] << 16) | (uint32_t)(0xffff - p2);
+                cidx[at] = ei;
+              }
+              p2 += in ? 1 : 0;
+            }
+          }
+          n_c += __builtin_amdgcn_readfirstlane(step);
+        }
+        __syncthreads();
+        exact = n_c > kTkCap;
+      }
     }
   }
   if (exact) {
@@ -769,8 +855,9 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
     tk_finish(cand, n_c, C, out);       // (full key, index) composites
     return;
   }
-  if (set_only && n_c <= kRsThreads) {             // the set in index order: no sort
-    tk_select_set(ck, cidx, n_c, C, wh, h, ext, slots, out);
+  if (set_only && n_c <= kRsThreads) {             // the set only: no sort
+    if (windowed) tk_select_set_window(ck, cidx, n_c, C, hist, slots, ext, out);
+    else tk_select_set(ck, cidx, n_c, C, wh, h, ext, slots, out);
     return;
   }
   // sort the candidates (positions follow the index order, so ties sort by index)
