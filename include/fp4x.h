@@ -241,12 +241,17 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
  * afterwards.  The single launch keeps one tile ticket per 128-byte line,
  * ticket t at 32 t, and at S = (n_tickets - 32 * (CUs + 1)) rounded down to
  * a multiple of 32 the down-tile count (S), a status word (S + 1) and one
- * 128-byte generation-flag line per workgroup, so it needs S >= 32 *
- * ceil(N / 16); with fewer it makes the two calls.  (S depends on the buffer
- * alone: calls of any shape on one buffer agree on it.)  A workgroup whose flag wait gives up (only
- * possible when other work holds the GPU's CUs for about a second) writes NaN
- * to its outputs and sets bit 0 of the status word; the next call is not
- * affected.  FP4X_HC_MIX=0 forces the two calls.
+ * 128-byte line per workgroup (its generation flag, its ack word and a down
+ * tile's generation), so it needs S >= 32 * ceil(N / 16); with fewer it
+ * makes the two calls.  (S depends on the buffer alone: calls of any shape on
+ * one buffer agree on it.)  part: the down partials of the single launch sit
+ * in one XCD's L2 per tile, followed by one tag line per partial.  A
+ * workgroup whose flag wait gives up (only possible when other work holds the
+ * GPU's CUs for about a second) writes NaN to its outputs and sets bit 0 of
+ * the status word; a down tile whose partials were not all on its closer's
+ * XCD writes NaN and sets bit 1; the next call is not affected.
+ * FP4X_HC_MIX=0 forces the two calls, FP4X_HC_XCD=0 device-coherent
+ * partials.
  * [HCFused.down then HCFused.up as the plugin's fused mixer calls them,
  *  x/fp4patch.py:217-218 (_mix_fused); x/fp4x_kernels.py:503-526] */
 int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, int s_dtype, void* di, void* bot,
@@ -291,7 +296,9 @@ int fp4x_hold_cus(int wgs, int64_t microseconds, int lds_kb, uint32_t* sink, voi
 /* Re-read the path switches from the environment (they are read once, when
  * first needed, never per launch): FP4X_W8_STREAM, FP4X_INT2_STREAM,
  * FP4X_NV4_STREAM, FP4X_W6_STREAM, FP4X_MX8_STREAM and FP4X_HC_MIX ("0"
- * selects the MFMA core or the two-call mixer), FP4X_WAVES_PER_CU.  Not
+ * selects the MFMA core or the two-call mixer), FP4X_HC_XCD ("0": the
+ * single-launch mixer's down partials device-coherent rather than in one
+ * XCD's L2), FP4X_ROWS, FP4X_WAVES_PER_CU, FP4X_HC_SPIN_LIMIT.  Not
  * thread-safe against concurrent launches.  No counterpart in the reference
  * (its Triton launches take no such switches). */
 int fp4x_reload_env(void);

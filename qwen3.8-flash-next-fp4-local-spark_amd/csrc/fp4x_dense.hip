@@ -69,6 +69,7 @@ void reload_switches() {
   w.mx8_stream = on("FP4X_MX8_STREAM");
   w.hc_mix = on("FP4X_HC_MIX");
   w.rows = on("FP4X_ROWS");
+  w.hc_xcd = on("FP4X_HC_XCD");
   const char* e = getenv("FP4X_WAVES_PER_CU");
   const int v = e ? atoi(e) : 0;
   w.waves_per_cu = v >= 1 && v <= 64 ? v : 0;

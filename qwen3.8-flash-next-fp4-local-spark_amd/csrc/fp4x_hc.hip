@@ -12,6 +12,8 @@
 // with the same split, scaled-SiLU kernel, W8 GEMV, gate-mean kernel.  Both
 // paths share the GEMV core, the K split and every epilogue function, so they
 // agree bit for bit.
+#include <type_traits>
+
 #include "fp4x_mfma.h"
 #include "fp4x_stream.h"
 #include "../../include/fp4x.h"
@@ -192,13 +194,17 @@ static bool al(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & 
 //     outputs and sets bit 0 of the status word sync[1].
 constexpr int kMixFlagStride = 32;               // int32 between flags: one 128-byte line each
 constexpr int kMixAckAt = 16;                    // a workgroup's ack word, 64 bytes after its flag
+constexpr int kMixGenAt = 8;                     // a down tile's generation word, on the flag lines
 
 struct HcMixArgs {
   GemvLaunch d;          // down: x, q, s, di (out), bot (out2), lr, hc, split-K slots and tickets
   HcUpArgs u;            // up: bot [M, lr] contiguous, interleaved q/s, normalized, out
-  int* sync;             // [0] down tiles done (zero between calls), [1] status (bit 0: a wait gave up),
+  int* sync;             // [0] down tiles done (zero between calls), [1] status (bit 0: a wait gave up,
+                         // bit 1: a down tile's partials were not all on its closer's XCD),
                          // [kMixFlagStride * (w + 1)] generation flag of workgroup w,
-                         // [kMixFlagStride * (w + 1) + kMixAckAt] its ack word (calls it has started)
+                         // [kMixFlagStride * (w + 1) + kMixAckAt] its ack word (calls it has started),
+                         // [kMixFlagStride * (t + 1) + kMixGenAt] down tile t's generation (XCD-local slots)
+  SplitLocal loc;        // XCD-local slots: generations, tags, status
   int C, D, tiles_d, R, spin_limit;
 };
 
@@ -206,8 +212,11 @@ constexpr int kMixMaxHc = 4;                     // streams the single-launch mi
 constexpr int kMixOutPer = 2;                    // epilogue outputs per thread
 
 // SPLIT: the up tiles have workgroups of their own (grid = D + up
-// workgroups).
-template <bool F16S, int KW, int CPS, bool SPLIT>
+// workgroups).  LOCAL: the down items of a tile are the workgroups i < D with
+// one residue i mod 8, so they run on one XCD and keep their partials in its
+// L2 (w8_splitk_item's LOCAL form); tile counts per residue differ by at most
+// one, and the workgroups past a residue's items hold no down item.
+template <bool F16S, int KW, int CPS, bool SPLIT, bool LOCAL>
 __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   using F = FmtW8<F16S>;
   constexpr int DP = 4 * KW;
@@ -235,9 +244,21 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
 
   // 1. one down item in each of the first D workgroups (the critical path:
   //    its loads go out first)
+  int t = -1, c = 0;
   if ((int)blockIdx.x < a.D) {
-    const int t = blockIdx.x / a.C, c = blockIdx.x - t * a.C;
-    if (w8_splitk_item<F16S, 8, 2, EpiHcDownShared>(a.d, a.C, t, c, base)) {
+    if constexpr (LOCAL) {
+      const int r = blockIdx.x & 7, k = blockIdx.x >> 3, q = a.tiles_d >> 3, rem = a.tiles_d & 7;
+      if (k < (q + (r < rem ? 1 : 0)) * a.C) {
+        t = r * q + (r < rem ? r : rem) + k / a.C;
+        c = k % a.C;
+      }
+    } else {
+      t = blockIdx.x / a.C;
+      c = blockIdx.x - t * a.C;
+    }
+  }
+  if (t >= 0) {
+    if (w8_splitk_item<F16S, 8, 2, EpiHcDownShared, LOCAL>(a.d, a.C, t, c, base, a.loc)) {
       wait_vmcnt<0>();                              // the tile's bottleneck stores have completed
       int old = 0;
       if (lane == 0) old = __hip_atomic_fetch_add(a.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -350,9 +371,9 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
 // The plan keeps the dynamic LDS within 150 KB (the kernel also has a few
 // bytes of static LDS); a failed attribute call is cleared so that the
 // two-launch fallback does not report it.
-template <bool F16S, int KW, bool SPLIT>
+template <bool F16S, int KW, bool SPLIT, bool LOCAL>
 static bool launch_hc_mix(const HcMixArgs& a, int P, size_t lds, hipStream_t st) {
-  auto kern = hc_mix_kernel<F16S, KW, 1, SPLIT>;
+  auto kern = hc_mix_kernel<F16S, KW, 1, SPLIT, LOCAL>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -516,7 +537,15 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   // all up tiles (which load them at once); otherwise max(D, up workgroups),
   // the up tiles sharing workgroups with down items (measured: spreading only
   // part of the up tiles to extra workgroups is slower than not at all)
-  const int R = 8 / WT, ntu = H / bj, D = tiles_d * C, cus = device_cus();
+  const int cus = device_cus();
+  // XCD-local down partials (w8_splitk_item's LOCAL form): at most 8 parts per
+  // tile, a generation word per tile on the flag lines, and the tags after the
+  // slots in the caller's slot buffer; the down items then span 8 residues x
+  // the most tiles a residue holds x C workgroups
+  const int64_t slot_floats = ((int64_t)tiles_d * C * M * 16 + 15) & ~(int64_t)15;
+  const bool local = switches().hc_xcd && C <= 8 && tiles_d <= cus &&
+                     slot_floats + (int64_t)tiles_d * C * 16 <= (int64_t)ksplit * 16 * N;
+  const int R = 8 / WT, ntu = H / bj, D = local ? 8 * ((tiles_d + 7) / 8) * C : tiles_d * C;
   if (hc > kMixMaxHc || R * M * bj > kMixOutPer * 512) return two();
   const int need_u = (ntu + R - 1) / R;
   const bool split = D + need_u <= cus;
@@ -538,27 +567,29 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   a.u.out = static_cast<uint16_t*>(out);
   a.u.M = M; a.u.K = lr; a.u.H = H; a.u.hc = hc; a.u.bj = bj;
   a.sync = tickets + sync_at;
+  a.loc.gen = a.sync + kMixFlagStride + kMixGenAt;
+  a.loc.gstride = kMixFlagStride;
+  a.loc.tags = reinterpret_cast<int*>(part + slot_floats);
+  a.loc.status = a.sync + 1;
   a.C = C;
   a.D = D;
   a.tiles_d = tiles_d;
   a.R = R;
   a.spin_limit = switches().hc_spin_limit;
   hipStream_t st = (hipStream_t)stream;
-  bool launched;
-  if (s_dtype == FP4X_DT_F16)
-    launched = split ? (KW == 1   ? launch_hc_mix<true, 1, true>(a, P, lds, st)
-                        : KW == 2 ? launch_hc_mix<true, 2, true>(a, P, lds, st)
-                                  : launch_hc_mix<true, 4, true>(a, P, lds, st))
-                     : (KW == 1   ? launch_hc_mix<true, 1, false>(a, P, lds, st)
-                        : KW == 2 ? launch_hc_mix<true, 2, false>(a, P, lds, st)
-                                  : launch_hc_mix<true, 4, false>(a, P, lds, st));
-  else
-    launched = split ? (KW == 1   ? launch_hc_mix<false, 1, true>(a, P, lds, st)
-                        : KW == 2 ? launch_hc_mix<false, 2, true>(a, P, lds, st)
-                                  : launch_hc_mix<false, 4, true>(a, P, lds, st))
-                     : (KW == 1   ? launch_hc_mix<false, 1, false>(a, P, lds, st)
-                        : KW == 2 ? launch_hc_mix<false, 2, false>(a, P, lds, st)
-                                  : launch_hc_mix<false, 4, false>(a, P, lds, st));
+  auto go = [&](auto f16s, auto loc) {
+    constexpr bool F = decltype(f16s)::value, L = decltype(loc)::value;
+    if (split) return KW == 1 ? launch_hc_mix<F, 1, true, L>(a, P, lds, st)
+                      : KW == 2 ? launch_hc_mix<F, 2, true, L>(a, P, lds, st)
+                                : launch_hc_mix<F, 4, true, L>(a, P, lds, st);
+    return KW == 1 ? launch_hc_mix<F, 1, false, L>(a, P, lds, st)
+           : KW == 2 ? launch_hc_mix<F, 2, false, L>(a, P, lds, st)
+                     : launch_hc_mix<F, 4, false, L>(a, P, lds, st);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  const bool launched = s_dtype == FP4X_DT_F16 ? (local ? go(T_{}, T_{}) : go(T_{}, F_{}))
+                                               : (local ? go(F_{}, T_{}) : go(F_{}, F_{}));
   if (!launched) return two();
   return check_launch("hc_mix");
 }

@@ -88,14 +88,15 @@ int check_launch(const char* what);
 // single-launch mixer off (the MFMA core or the two-call mixer runs instead):
 // FP4X_W8_STREAM, FP4X_INT2_STREAM, FP4X_NV4_STREAM, FP4X_W6_STREAM,
 // FP4X_MX8_STREAM, FP4X_HC_MIX, FP4X_ROWS (the few-rows kernel of small
-// matrices).  FP4X_WAVES_PER_CU (1..64) caps the MFMA
+// matrices), FP4X_HC_XCD (the single-launch mixer's XCD-local down
+// partials).  FP4X_WAVES_PER_CU (1..64) caps the MFMA
 // core's resident waves per CU (0: no cap).  FP4X_HC_SPIN_LIMIT (>= 0)
 // bounds the single-launch mixer's flag wait (reads, default 2^22, about a
 // second); 0 makes every wait that is not already satisfied give up, which
 // lets tests exercise the give-up path from the host.
 struct Switches {
   bool w8_stream = true, int2_stream = true, nv4_stream = true, w6_stream = true, mx8_stream = true;
-  bool hc_mix = true, rows = true;
+  bool hc_mix = true, rows = true, hc_xcd = true;
   int waves_per_cu = 0;
   int hc_spin_limit = 1 << 22;
 };

@@ -279,11 +279,51 @@ __device__ __forceinline__ void stream_read_x(uint32_t xa, uint4& x0a, uint4& x0
 //     no cache-wide write-back or invalidate is needed because every access to
 //     the slots and the ticket is device-coherent.
 //
+// XCD-local slots (LOCAL, the single-launch mixer): when the caller places
+// every item of a tile on one XCD (workgroups whose indices are congruent
+// mod 8: the dispatcher hands consecutive workgroups to the XCDs in turn), the
+// partials are stored plainly into that XCD's L2 and the closer reads them
+// from there (L1 bypassed), instead of through the device's coherence point:
+// each of those round trips is several hundred ns shorter.  The ticket stays
+// device-scope, so arrivals are always counted exactly.  Each partial carries
+// a tag, the tile's call generation (gen, device-coherent, read by every item
+// at its start and advanced by the closer); a closer that finds a tag other
+// than its own generation (an item ran on another XCD, so its partial is in
+// another L2) writes NaN for the tile and sets bit 1 of *status, and the
+// generation still advances, so the next call starts clean.
+struct SplitLocal {
+  int* gen;            // per-tile generation words, gstride ints apart
+  int gstride;
+  int* tags;           // [tiles][C] tags, 16 ints (one 64-byte line) apart
+  int* status;
+};
+
+// Eight floats (a[i]) and one int (at) from this XCD's L2 (sc0: the L1 is
+// bypassed), all issued before one wait.
+__device__ __forceinline__ void ld_l2_8x1(const float* const (&a)[8], const int* at, float (&v)[8], int& tv) {
+  asm volatile(
+      "global_load_dword %0, %9, off sc0\n\t"
+      "global_load_dword %1, %10, off sc0\n\t"
+      "global_load_dword %2, %11, off sc0\n\t"
+      "global_load_dword %3, %12, off sc0\n\t"
+      "global_load_dword %4, %13, off sc0\n\t"
+      "global_load_dword %5, %14, off sc0\n\t"
+      "global_load_dword %6, %15, off sc0\n\t"
+      "global_load_dword %7, %16, off sc0\n\t"
+      "global_load_dword %8, %17, off sc0\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]),
+        "=&v"(tv)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]), "v"(at)
+      : "memory");
+}
+
 // w8_splitk_item runs one (tile t, part c) item with the workgroup's WPG waves
 // and LDS at base; it returns true in the wave that ran the tile's epilogue
 // (wave 0 of the last-arriving workgroup), false elsewhere.
-template <bool F16S, int WPG, int JW, class Epi>
-__device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t, int c, char* base) {
+template <bool F16S, int WPG, int JW, class Epi, bool LOCAL = false>
+__device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t, int c, char* base,
+                                               const SplitLocal& loc = SplitLocal{}) {
   constexpr int UW = WPG * JW;                       // units per workgroup
   constexpr int XR = UW * 256 + 64;                  // LDS bytes per activation row
   static_assert(UW % 4 == 0, "activation slice in whole 1 KB pieces");
@@ -298,6 +338,9 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
     const int m = i / PPR, u = i - m * PPR;
     dma_b128(p.x + (int64_t)m * p.x_stride + (int64_t)(c * UW + u * 4) * 128 + lane * 8, base + m * XR + u * 1024);
   }
+  int gen = 0;                                       // LOCAL: the tile's generation before this call
+  if constexpr (LOCAL)
+    if (wave == 0) gen = __hip_atomic_load(loc.gen + (int64_t)t * loc.gstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int lim = p.N - 1 - t * 16;                  // rows past N read row N - 1
   const int64_t row = (int64_t)t * 16 + (n < lim ? n : lim);
   const int u0 = c * UW + wave * JW;
@@ -353,16 +396,52 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
   }
   // wave 0: slot c of tile t holds [M][16] fp32 partials
   float* slots = p.part + (int64_t)t * C * p.M * 16;
+  const int want = __builtin_amdgcn_readfirstlane(gen) + 1;   // LOCAL: this call's generation
+  if constexpr (LOCAL) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (g * 4 + i < p.M)
-      __hip_atomic_store(slots + (c * p.M + g * 4 + i) * 16 + n, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < 4; ++i)
+      if (g * 4 + i < p.M) slots[(c * p.M + g * 4 + i) * 16 + n] = acc[i];
+    if (lane == 0) loc.tags[((int64_t)t * C + c) * 16] = want;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (g * 4 + i < p.M)
+        __hip_atomic_store(slots + (c * p.M + g * 4 + i) * 16 + n, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   wait_vmcnt<0>();                                   // the slot stores have completed
   int tk = 0;
   int* const ticket = p.tickets + (int64_t)t * p.tstride;
   if (lane == 0) tk = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   tk = __builtin_amdgcn_readfirstlane(tk);
   if (tk != C - 1) return false;
+  if constexpr (LOCAL) {
+    // every element e = m * 16 + n of the tile: its C partials in slot order;
+    // lane cc < C also checks item cc's tag (C <= 8, checked by the host)
+    bool ok = true;
+    for (int e0 = 0; e0 < p.M * 16; e0 += 64) {
+      const int e = e0 + lane;
+      const int ec = e < p.M * 16 ? e : 0;
+      const float* a[8];
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) a[cc] = slots + (cc < C ? cc : 0) * p.M * 16 + ec;
+      float v[8];
+      int tv;
+      ld_l2_8x1(a, loc.tags + ((int64_t)t * C + (lane < C ? lane : 0)) * 16, v, tv);
+      if (e0 == 0) ok = __ballot(lane < C && tv != want) == 0;
+      float tot = v[0];
+#pragma unroll
+      for (int cc = 1; cc < 8; ++cc)
+        if (cc < C) tot += v[cc];
+      const int64_t orow = (int64_t)t * 16 + (e & 15);
+      if (e < p.M * 16 && orow < p.N) Epi::apply(p, 0, e >> 4, orow, ok ? tot * p.gs : __builtin_nanf(""));
+    }
+    if (lane == 0) {
+      if (!ok) __hip_atomic_fetch_or(loc.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(loc.gen + (int64_t)t * loc.gstride, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ticket_reset(ticket);
+    }
+    return true;
+  }
   for (int e = lane; e < p.M * 16; e += 64) {        // e = m * 16 + n
     const float* src = slots + e;
     float tot = ld_coherent(src);

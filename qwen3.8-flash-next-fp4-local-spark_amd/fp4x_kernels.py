@@ -414,12 +414,13 @@ class HCFused:
 
     def wait_timeouts(self, clear=True):
         """True if a single-launch mixer call since the last check gave up
-        waiting for its bottleneck (its outputs then hold NaN).  Reads the
-        device status word: synchronizes the stream."""
+        waiting for its bottleneck (bit 0 of the device status word), or found
+        a down tile's partials off its closer's XCD (bit 1); that call's
+        outputs hold NaN.  Reads the status word: synchronizes the stream."""
         at = self._status_at
         if not getattr(self, "_mixed", False):
             return False
-        hit = bool(int(self.tickets[at].item()) & 1)
+        hit = bool(int(self.tickets[at].item()) & 3)
         if clear and hit:
             self.tickets[at].zero_()
         return hit
@@ -437,7 +438,7 @@ class HCFused:
         if self._poll_event is not None:
             if not self._poll_event.query():
                 return False                                   # the last copy is still in flight
-            hit = bool(int(self._poll_host[0]) & 1)
+            hit = bool(int(self._poll_host[0]) & 3)
         at = self._status_at
         self._poll_host.copy_(self.tickets[at:at + 1], non_blocking=True)
         self.tickets[at:at + 1].zero_()
