@@ -23,7 +23,7 @@ and the 48-gate launch with fp16 and with the reference's fp32 scales, the
 97-layer mixer at the synthetic and the served shape, the 248,320-row fast
 LM head and the exact MXFP8 head it replaces, the 65k-token draft head),
 timed as HIP-graph replays, and the load-time weight preparation (group G,
-eager).  `read_ceiling` times a plain coalesced read of each kernel's bytes
+eager), and the MTP layer's int8 linears (H).  `read_ceiling` times a plain coalesced read of each kernel's bytes
 under the same protocol (the fastest of a sweep of load depths and grids);
 each kernel row carries `frac_of_ceiling`, that read's time over the
 kernel's.  `cpu_baseline` times the reference math as PyTorch CPU ops
@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E,F,G")
+    ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E,F,G,H")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ceiling", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -151,6 +151,26 @@ def bench_dense(F, torch, dev, out):
             us = graph_time([lambda p=p: fn(x, p) for p in copies] * 2)
             out[f"{name}_M{M}"] = entry(us, wbytes + M * k * 2 + M * n * 2)
         del copies, planes, w
+        torch.cuda.empty_cache()
+
+
+def bench_mtp(F, torch, dev, out):
+    """The MTP layer's linears as FP4X_MTP_W8=1 serves them (int8 g64 copies of its bf16 weights, fp32
+    scales, bf16 out, the plugin's CFG_W8 K split or one slice): attention qkv [13312 x 2560], output
+    [2560 x 6144], shared-expert gate/up [1280 x 2560] and down [2560 x 640] (the shapes the reference's
+    MTP weight patch names, x/fp4patch.py:513-525), at M = 3 (1 target + 2 draft rows).  Its router gate
+    [512 x 2560] and its mixers take the B and D rows' kernels."""
+    import fp4patch
+    for n, k in ((13312, 2560), (2560, 6144), (1280, 2560), (2560, 640)):
+        g = torch.Generator(device=dev).manual_seed(7)
+        q, s = F.quantize_w8(torch.randn((n, k), generator=g, device=dev) * 0.02)
+        cfg = fp4patch.CFG_W8.get((n, k)) or (32, fp4patch._k_tile(k, (256, 64)), 1, 4)
+        wbytes = n * k + n * (k // 64) * 4
+        copies = [(q.clone(), s.clone()) for _ in range(copies_for(wbytes))]
+        x = torch.randn((3, k), generator=g, device=dev).to(torch.bfloat16)
+        us = graph_time([lambda c=c: F.w8_linear(x, c[0], c[1], cfg) for c in copies] * 2)
+        out[f"H_mtp_w8_{n}x{k}_M3"] = entry(us, wbytes + 3 * k * 2 + 3 * n * 2)
+        del copies, q, s
         torch.cuda.empty_cache()
 
 
@@ -687,7 +707,7 @@ def main():
 
     kernels = {}
     kernels["B_w8_gates_48_layers_M3"] = entry(ms_step * 1e3, step_bytes)
-    sel = set("ABCDEFG") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
+    sel = set("ABCDEFGH") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
     def done(what):
         print(f"[bench] {what} done", file=sys.stderr, flush=True)
 
@@ -717,6 +737,10 @@ def main():
         bench_prep(F, torch, dev, kernels)
         torch.cuda.empty_cache()
         done("G")
+    if "H" in sel:
+        bench_mtp(F, torch, dev, kernels)
+        torch.cuda.empty_cache()
+        done("H")
 
     ceil = {}
     if not args.no_ceiling:

@@ -21,6 +21,8 @@ bool launch_int2_stream_e4m3(GemvLaunch p, hipStream_t st);
 bool launch_nv4_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_w6_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_mx8_stream_entry(GemvLaunch p, hipStream_t st);
+bool launch_w8_single_stream_f16(GemvLaunch p, hipStream_t st);
+bool launch_w8_single_stream_f32(GemvLaunch p, hipStream_t st);
 int topk_check(const void* logits, int dtype, int64_t stride, int M, int V, int C, void* workspace,
                int64_t ws_bytes);
 int topk_launch(const void* lg, int dtype, int64_t stride, int M, int V, int C, int64_t* idx_out, uint16_t* smax,
@@ -238,18 +240,21 @@ int fp4x_w8_linear_layers(const void* x, int64_t x_stride, int64_t x_lstride, co
   // long runs of tiles (layer-batched gates) stream through LDS; split-K calls of
   // few tiles spread each tile's K over several workgroups (or over the waves
   // of one workgroup), the mixer's down projection taking the same path; other
-  // matrices of few rows (a router gate) take the few-rows kernels; other
-  // shapes use the MFMA core
+  // matrices of few rows (a router gate) or of short rows take the few-rows
+  // kernels; other single matrices of at least half a tile per CU stream
+  // through LDS; other shapes use the MFMA core
   hipStream_t st = (hipStream_t)stream;
   if (fmt == FP4X_FMT_W8_F16) {
     if (launch_w8_stream<true>(p, layers, st)) return check_launch("w8_stream");
     if (layers == 1 && launch_w8_ktile<true, EpiStore>(p, st)) return check_launch("w8_ktile");
     if (launch_rows_gemv<FmtW8<true>>(p, layers, st)) return check_launch("w8_rows");   // few rows (a router gate)
+    if (layers == 1 && launch_w8_single_stream_f16(p, st)) return check_launch("w8_single_stream");
     return launch_gemv_mfma<FmtW8<true>, EpiStore>(p, layers, st);
   }
   if (launch_w8_stream<false>(p, layers, st)) return check_launch("w8_stream");
   if (layers == 1 && launch_w8_ktile<false, EpiStore>(p, st)) return check_launch("w8_ktile");
   if (launch_rows_gemv<FmtW8<false>>(p, layers, st)) return check_launch("w8_rows");
+  if (layers == 1 && launch_w8_single_stream_f32(p, st)) return check_launch("w8_single_stream");
   return launch_gemv_mfma<FmtW8<false>, EpiStore>(p, layers, st);
 }
 

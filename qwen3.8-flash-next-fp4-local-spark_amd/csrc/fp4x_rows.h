@@ -339,6 +339,52 @@ inline bool rows_shape_ok(int N, int M, int cus) {
   return M >= 1 && M <= 16 && N >= 1 && tiles * 2 < cus && rows_per_wg(N, cus) > 0;
 }
 
+// Workgroups of rows_fma_kernel<F, MT> of `threads` threads one CU holds at
+// once (its registers decide: the NVFP4 and W6 kernels at M >= 3 hold fewer).
+template <class F, int MT>
+int rows_fma_resident(int threads) {
+  static int cache[kRowsFmaMaxThreads / 64 + 1];
+  const int key = threads / 64;
+  int occ = cache[key];
+  if (occ <= 0) {
+    const size_t lds = (size_t)key * MT * sizeof(float);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(rows_fma_kernel<F, MT>),
+                                                     threads, lds) != hipSuccess ||
+        occ < 1)
+      occ = 1;
+    cache[key] = occ;
+  }
+  return occ;
+}
+
+// The fma kernel beyond few-rows shapes: wider matrices of short rows (the MTP
+// shared expert's [1280 x 2560] and its down projection [2560 x 640]), whose
+// tiles leave the MFMA core and the streaming kernels one memory round trip
+// per tile with few loads in flight, while one row per workgroup puts every
+// load of the matrix in flight at once.  Two limits: every workgroup resident
+// in one round, and under 2^17 fp32 products per lane slot of a CU
+// (N * threads * M * KPC / CUs), beyond which the fma work outlasts the
+// loads.  Measured as graph replays from HBM, fma kernel against the
+// previous path, us at M = 1 / 3 / 4: W8 [1280 x 2560] 3.3 / 4.1 / 4.4
+// against 6.5 / 6.7 / 7.5 (MFMA core); W8 [2048 x 2560] 3.7 / 4.8 / 5.3
+// against 5.4 / 5.9 / 6.1 (streaming); W8 [2560 x 640] 3.0 / 3.6 / 3.8
+// against 5.0 / 5.2 / 5.4; MXFP8 [2048 x 2560] 3.6 / 4.6 / 5.1 against 6.3 /
+// 6.7 / 6.9; NVFP4 [4096 x 2560] 5.1 / - / - against 6.2 / 6.5 / 6.9 (at
+// M = 2 the products limit: 6.5 against 6.4).
+constexpr int64_t kRowsFmaProductsPerCu = int64_t(1) << 17;
+
+template <class F>
+bool rows_fma_shape_ok(int N, int M, int threads, int cus) {
+  if (M < 1 || M > 4 || N < 1 || threads > kRowsFmaMaxThreads) return false;
+  if (rows_shape_ok(N, M, cus)) return true;
+  if ((int64_t)N * threads * M * F::KPC >= kRowsFmaProductsPerCu * cus) return false;
+  const int res = M == 1   ? rows_fma_resident<F, 1>(threads)
+                  : M == 2 ? rows_fma_resident<F, 2>(threads)
+                  : M == 3 ? rows_fma_resident<F, 3>(threads)
+                           : rows_fma_resident<F, 4>(threads);
+  return N <= (int64_t)res * cus;
+}
+
 // Launch a few-rows kernel when the call fits one: one matrix, no per-row
 // scale, strides within int32, a few-rows shape, and (M <= 4, at most 256
 // chunks per row) the fma kernel or else an MFMA plan of at most 8 waves;
@@ -350,8 +396,11 @@ bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
   if (!switches().rows || batch != 1 || p.rs) return false;
   if (p.x_stride > INT32_MAX || p.out_stride > INT32_MAX) return false;
   const int cus = device_cus();
-  if (!rows_shape_ok(p.N, p.M, cus) || p.pa.K % F::KPC) return false;
+  if (p.pa.K % F::KPC) return false;
   const int nch = p.pa.K / F::KPC;
+  const int threads = (nch + 63) / 64 * 64;
+  const bool fma = rows_fma_shape_ok<F>(p.N, p.M, threads, cus);
+  if (!fma && !rows_shape_ok(p.N, p.M, cus)) return false;
   RowsLaunch a;
   a.pa = p.pa;
   a.x = p.x;
@@ -362,8 +411,7 @@ bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
   a.M = p.M;
   a.out_dtype = p.out_dtype;
   a.gs = p.gs;
-  const int threads = (nch + 63) / 64 * 64;
-  if (p.M <= 4 && threads <= kRowsFmaMaxThreads) {
+  if (fma) {
     a.R = 1;
     const size_t lds = (size_t)(threads / 64) * p.M * sizeof(float);
     const dim3 grid((unsigned)p.N), block((unsigned)threads);

@@ -500,7 +500,7 @@ bool launch_w8_stream_cfg(GemvLaunch p, size_t lds, int gx, hipStream_t st) {
 // the LDS plan within the CU's 160 KB.
 struct StreamW8H;
 template <class U, int T, int KW, int D>
-bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st);
+bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st, int64_t min_items = -1);
 
 template <bool F16S>
 bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
@@ -1225,6 +1225,71 @@ struct StreamW8H {
   }
 };
 
+// W8 g64 unit with fp32 scales (the reference's _w8 layout): StreamW8H's
+// 16 rows x 256 bytes of int8, then 16 rows x 4 fp32 scales, lane l loading
+// the scale of row l >> 2, group l & 3 (one 4-byte load), so row r's four
+// scales are the 16 bytes at 4096 + 16 r.
+struct StreamW8F {
+  static constexpr int UK = 256, BYTES = 4096 + 256, NDMA = 5, XG = 32;
+  static constexpr bool BATCHED = true;
+  const uint8_t* w;
+  const uint8_t* s;
+  uint32_t o[4], os;
+  __device__ void set(const GemvLaunch& p, int K, int b, int64_t t, int ku, int lane, int lim) {
+    const int sr = lane >> 2;
+    w = p.pa.w0 + b * p.w0_bstride + t * 16 * K + ku * 256;
+    s = p.pa.s + b * p.s_bstride + (t * 16 * (K / 64) + ku * 4) * 4;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int r = 4 * h + (lane >> 4);
+      o[h] = (uint32_t)((r < lim ? r : lim) * K + ((lane & 15) ^ r) * 16);
+    }
+    os = (uint32_t)((sr < lim ? sr : lim) * (K / 64) * 4 + (lane & 3) * 4);
+  }
+  __device__ void issue(char* d, int ij) const {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) dma_b128(w + ij * 256 + o[h], d + h * 1024);
+    dma_b32(s + ij * 16 + os, d + 4096);
+  }
+  __device__ static void consume(uint32_t u, uint32_t xa, int n, int g, f32x4_t& acc) {
+    uint4 q[4], x[8], sc;
+    asm volatile(
+        "ds_read_b128 %0, %13\n\t"
+        "ds_read_b128 %1, %14\n\t"
+        "ds_read_b128 %2, %15\n\t"
+        "ds_read_b128 %3, %16\n\t"
+        "ds_read_b128 %4, %17\n\t"
+        "ds_read_b128 %5, %18\n\t"
+        "ds_read_b128 %6, %18 offset:16\n\t"
+        "ds_read_b128 %7, %18 offset:128\n\t"
+        "ds_read_b128 %8, %18 offset:144\n\t"
+        "ds_read_b128 %9, %18 offset:256\n\t"
+        "ds_read_b128 %10, %18 offset:272\n\t"
+        "ds_read_b128 %11, %18 offset:384\n\t"
+        "ds_read_b128 %12, %18 offset:400\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(sc), "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]),
+          "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]), "=&v"(x[6]), "=&v"(x[7])
+        : "v"(u + n * 256 + ((g ^ n) * 16)), "v"(u + n * 256 + (((g + 4) ^ n) * 16)),
+          "v"(u + n * 256 + (((g + 8) ^ n) * 16)), "v"(u + n * 256 + (((g + 12) ^ n) * 16)),
+          "v"(u + 4096 + n * 16), "v"(xa)
+        : "memory");
+    uint32_t w[8];
+    w8_chunk_bf16(q[0], __uint_as_float(sc.x), w);
+    acc = mfma16(x[0], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[1], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    w8_chunk_bf16(q[1], __uint_as_float(sc.y), w);
+    acc = mfma16(x[2], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[3], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    w8_chunk_bf16(q[2], __uint_as_float(sc.z), w);
+    acc = mfma16(x[4], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[5], make_uint4(w[4], w[5], w[6], w[7]), acc);
+    w8_chunk_bf16(q[3], __uint_as_float(sc.w), w);
+    acc = mfma16(x[6], make_uint4(w[0], w[1], w[2], w[3]), acc);
+    acc = mfma16(x[7], make_uint4(w[4], w[5], w[6], w[7]), acc);
+  }
+};
+
 template <class U, int T, int KW, int D, int KC>
 __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p) {
   load_launch_once(p);
@@ -1354,7 +1419,7 @@ bool launch_dense_stream_k(const GemvLaunch& p, size_t lds, unsigned gx, hipStre
 // false (and nothing launched) otherwise, or when `env` is set to 0.  (The
 // second weight plane, W6's H, must be 16-byte aligned.)
 template <class U, int T, int KW, int D>
-bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st) {
+bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st, int64_t min_items) {
   if (!on) return false;                              // the format's switch is off: the MFMA core runs
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
   if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / U::UK) % KW != 0 || batch < 1) return false;
@@ -1364,7 +1429,7 @@ bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st) {
     return false;
   if (batch > 1 && ((p.w0_bstride & 15) || (p.w1_bstride & 15) || (p.s_bstride & 3))) return false;
   const int64_t cus = device_cus(), items = (int64_t)batch * tiles;
-  if (items < cus * T) return false;
+  if (items < (min_items >= 0 ? min_items : cus * T)) return false;
   const int64_t per = (items + cus * T - 1) / (cus * T) * T;
   // batch entries one workgroup can span (its first and last item), each with its activations
   const int64_t span = batch > 1 ? (per + tiles - 1) / tiles + 1 : 1;
@@ -1405,6 +1470,24 @@ inline bool launch_mx8_stream(GemvLaunch p, hipStream_t st) {
 // / 10.2 / 12.4.
 inline bool launch_w6_stream(GemvLaunch p, hipStream_t st) {
   return launch_dense_stream<StreamW6, 2, 2, 2>(p, 1, switches().w6_stream, st);
+}
+// Single W8 matrices without split-K (fp16 or fp32 scales), as the NVFP4, W6
+// and MXFP8 kernels by tiles per CU: 4 slots x 2 waves, 2 x 2, and one tile
+// per workgroup (down to half a tile per CU) with its K over KW waves of two
+// 256-K units each (K = 2560: 5 waves; K = 6144, the MTP attention output:
+// 12).  Other shapes take the MFMA core.
+template <class U>
+inline bool launch_w8_single_stream(const GemvLaunch& p, hipStream_t st) {
+  const bool on = switches().w8_stream;
+  const int64_t tiles = (p.N + 15) / 16, cus = device_cus();
+  const int units = p.pa.K / 256;
+  if (tiles >= 4 * cus) return launch_dense_stream<U, 4, 2, 2>(p, 1, on, st);
+  if (tiles >= 2 * cus) return launch_dense_stream<U, 2, 2, 2>(p, 1, on, st);
+  if (2 * tiles < cus) return false;
+  if (units % 12 == 0) return launch_dense_stream<U, 1, 12, 2>(p, 1, on, st, cus / 2);
+  if (units % 10 == 0) return launch_dense_stream<U, 1, 5, 2>(p, 1, on, st, cus / 2);
+  if (units % 8 == 0) return launch_dense_stream<U, 1, 4, 2>(p, 1, on, st, cus / 2);
+  return false;
 }
 
 }  // namespace fp4x

@@ -151,13 +151,16 @@ def test_gemv_parity(gpu, F, fmt, M):
 
 
 @pytest.mark.parametrize("fmt", ["mx8", "w8", "w8_f16", "w6", "nv4", "bf16"])
-@pytest.mark.parametrize("N,M", [(512, 3), (512, 1), (512, 16), (96, 3), (1000, 4), (480, 8), (1024, 4), (200, 16)])
+@pytest.mark.parametrize("N,M", [(512, 3), (512, 1), (512, 16), (96, 3), (1000, 4), (480, 8), (1024, 4), (200, 16),
+                                 (1280, 3), (2048, 1), (1536, 4)])
 def test_rows_gemv(gpu, F, fmt, N, M, monkeypatch):
     """Matrices whose 16-row tiles fill under half of the CUs (a router gate's
     512 x 2560) take the few-rows kernel (R rows per workgroup, one chunk per
-    thread): fp32 sums within the accumulation bound of the exact sums, equal
-    to the MFMA core's (FP4X_ROWS=0) within the two bounds, repeated calls bit
-    for bit, bf16 outputs the same sums rounded."""
+    thread), and so do wider ones at M <= 4 whose one-row workgroups are all
+    resident at once (1280, 2048 and 1536 rows): fp32 sums within the
+    accumulation bound of the exact sums, equal to the other path's
+    (FP4X_ROWS=0) within the two bounds, repeated calls bit for bit, bf16
+    outputs the same sums rounded."""
     rng = np.random.default_rng(4000 + N + M)
     k = 2560
     base = "w8" if fmt == "w8_f16" else fmt
@@ -273,6 +276,49 @@ def _dense_stream_case(F, fmt, slots, parts, env, M, tail, k, monkeypatch):
 
 
 @pytest.mark.parametrize("case", [
+    # tiles as a multiple of the CUs (or N), K, M, scale dtype, waves per tile
+    ((4, 40), 2560, 3, np.float32, 2),    # 4 tile slots x 2 waves, a 40-row tail
+    ((4, 0), 2560, 16, np.float16, 2),
+    (13312, 2560, 3, np.float32, 2),       # the MTP attention qkv: 2 slots x 2 waves
+    (13312, 2560, 1, np.float16, 2),
+    ((1, 40), 2560, 3, np.float32, 5),    # one tile per workgroup, 5 waves of 2 units
+    ((1, 0), 2560, 16, np.float16, 5),
+    (2560, 6144, 3, np.float32, 12),       # the MTP attention output: 12 waves of 2 units
+    (2048, 4096, 5, np.float16, 4),        # K = 4096 (run-time K): 4 waves of 4 units
+])
+def test_w8_single_stream(gpu, F, case, monkeypatch):
+    """Single W8 matrices without split-K of at least half a tile per CU stream
+    through LDS (fp32 or fp16 scales): fp32 sums within the MFMA bound of the
+    exact sum (the tile's K over `parts` waves), a different K decomposition
+    than the MFMA core's (FP4X_W8_STREAM=0), repeated calls bit for bit, bf16
+    outputs the same sums rounded."""
+    size, k, M, s_dtype, parts = case
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n = 16 * size[0] * cus + size[1] if isinstance(size, tuple) else size
+    rng = np.random.default_rng(5000 + n + k + M)
+    q, s = oq.quantize_w8(weights(rng, n, k))
+    s = s.astype(s_dtype)
+    x, _ = act(rng, M, k)
+    qd, sd, xd = dev(q), dev(s), bf16_dev(x)
+    w_op = og.operand("w8", q, s.astype(np.float32))
+    y = to_f32(F.w8_linear(xd, qd, sd, (32, 256, 1, 4), torch.float32))
+    with path_switch(monkeypatch, "FP4X_W8_STREAM"):
+        y_core = to_f32(F.w8_linear(xd, qd, sd, (32, 256, 1, 4), torch.float32))
+    assert not np.array_equal(y.view(np.uint32), y_core.view(np.uint32)), "streaming kernel not taken"
+    exact = ordered.exact_sum(x, w_op)
+    bound = ordered.mfma_bound(x, w_op, parts)
+    for got in (y, y_core):
+        assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
+    assert_tol(y, og.matmul_f32(x, w_op), what=f"w8 single stream N={n} K={k} M={M}")
+    y2 = to_f32(F.w8_linear(xd, qd, sd, (32, 256, 1, 4), torch.float32))
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    yb = F.w8_linear(xd, qd, sd, (32, 256, 1, 4))
+    assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
+    print(f"N={n} K={k} M={M} {np.dtype(s_dtype).name}: max |y - exact| / bound = "
+          f"{(np.abs(y - exact) / bound).max():.3g}")
+
+
+@pytest.mark.parametrize("case", [
     # N, K, M, ksplit, scale dtype, split over workgroups
     (640, 10240, 3, 4, np.float16, True),    # the mixer's down projection: 5 workgroups per tile
     (640, 10240, 1, 4, np.float32, True),
@@ -333,6 +379,30 @@ def test_gemv_shape_errors(gpu, F):
         F.mx8_linear(x.float(), *planes, (32, 64, 1, 4))
     y = F.mx8_linear(x[:0], *planes, (32, 64, 1, 4))
     assert y.shape == (0, 64)
+
+
+@pytest.mark.parametrize("N,K,M", [(2560, 640, 3), (2560, 640, 1), (4096, 640, 4), (2560, 1280, 2)])
+def test_rows_gemv_short_rows(gpu, F, N, K, M, monkeypatch):
+    """W8 matrices of short rows (the MTP shared expert's down projection,
+    [2560 x 640]) take the fma few-rows kernel, one row per workgroup: the same
+    checks as above against the MFMA core (FP4X_ROWS=0)."""
+    rng = np.random.default_rng(4100 + N + K + M)
+    q, s = oq.quantize_w8(weights(rng, N, K))
+    x, _ = act(rng, M, K)
+    xd, qd, sd = bf16_dev(x), dev(q), dev(s)
+    w_op = og.operand("w8", q, s)
+    cfg = (32, 64, 1, 4)
+    y = to_f32(F.w8_linear(xd, qd, sd, cfg, torch.float32))
+    with path_switch(monkeypatch, "FP4X_ROWS"):
+        y_core = to_f32(F.w8_linear(xd, qd, sd, cfg, torch.float32))
+    assert not np.array_equal(y.view(np.uint32), y_core.view(np.uint32)), "few-rows kernel not taken"
+    exact = ordered.exact_sum(x, w_op)
+    bound = ordered.mfma_bound(x, w_op)
+    for got in (y, y_core):
+        assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
+    assert_tol(y, og.matmul_f32(x, w_op), what=f"w8 rows N={N} K={K} M={M}")
+    assert np.array_equal(y.view(np.uint32), to_f32(F.w8_linear(xd, qd, sd, cfg, torch.float32)).view(np.uint32))
+    assert np.array_equal(bf16_bits(F.w8_linear(xd, qd, sd, cfg)), fm.bf16_bits(y))
 
 
 def test_w8_fp16_scales_and_layers(gpu, F):
