@@ -9,9 +9,11 @@
 //   * M <= 4 (rows_fma_kernel): one weight row per workgroup, thread c
 //     owning chunk c (the format's 16-byte unit of the main plane, with its
 //     scale), dequantized to the bf16 operand and multiplied with the M
-//     activation rows by fp32 fma (each product exact, one rounding per
-//     step).  Each wave sums its partials with DPP steps, lane 63 stores the
-//     wave's sums, and thread m adds the waves' sums in wave order.
+//     activation rows by v_dot2_f32_bf16 (two bf16 products and the running
+//     fp32 sum per step: half the instructions of an fma per product, which
+//     took the 512 x 2560 gate at M = 3 from 3.3 to 3.0 us).  Each wave sums
+//     its partials with DPP steps, lane 63 stores the wave's sums, and thread
+//     m adds the waves' sums in wave order.
 //   * 4 < M <= 16 (rows_mfma_kernel): R <= 4 weight rows per workgroup,
 //     products on v_mfma_f32_4x4x4bf16_1k: 16 independent blocks of
 //     D[4 x 4] += A[4 x 4] B[4 x 4].  Lane 4b + q of a wave holds, for block
@@ -68,6 +70,14 @@ __device__ __forceinline__ float wave_sum_lane63(float v) {
   return v;
 }
 
+// c + (the two bf16 products of a and b) in fp32, one v_dot2_f32_bf16 (the
+// two products' sum is not always rounded once; the few-rows sums are checked
+// against the accumulation bound, and repeat bit for bit)
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
 template <class F, int MT>
 __global__ __launch_bounds__(kRowsFmaMaxThreads) void rows_fma_kernel(RowsLaunch p) {
   extern __shared__ float red[];                       // [waves][MT]
@@ -110,10 +120,7 @@ __global__ __launch_bounds__(kRowsFmaMaxThreads) void rows_fma_kernel(RowsLaunch
       const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
       float t = acc[m];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        t = __builtin_fmaf(bf16_lo(w[i]), bf16_lo(xv[i]), t);
-        t = __builtin_fmaf(bf16_hi(w[i]), bf16_hi(xv[i]), t);
-      }
+      for (int i = 0; i < 8; ++i) t = dot2_bf16(w[i], xv[i], t);
       acc[m] = t;
     }
   }
@@ -362,22 +369,23 @@ int rows_fma_resident(int threads) {
 // tiles leave the MFMA core and the streaming kernels one memory round trip
 // per tile with few loads in flight, while one row per workgroup puts every
 // load of the matrix in flight at once.  Two limits: every workgroup resident
-// in one round, and under 2^17 fp32 products per lane slot of a CU
-// (N * threads * M * KPC / CUs), beyond which the fma work outlasts the
-// loads.  Measured as graph replays from HBM, fma kernel against the
-// previous path, us at M = 1 / 3 / 4: W8 [1280 x 2560] 3.3 / 4.1 / 4.4
-// against 6.5 / 6.7 / 7.5 (MFMA core); W8 [2048 x 2560] 3.7 / 4.8 / 5.3
-// against 5.4 / 5.9 / 6.1 (streaming); W8 [2560 x 640] 3.0 / 3.6 / 3.8
-// against 5.0 / 5.2 / 5.4; MXFP8 [2048 x 2560] 3.6 / 4.6 / 5.1 against 6.3 /
-// 6.7 / 6.9; NVFP4 [4096 x 2560] 5.1 / - / - against 6.2 / 6.5 / 6.9 (at
-// M = 2 the products limit: 6.5 against 6.4).
+// in one round, and at most 2^17 fp32 products per lane slot of a CU
+// (N * threads * M * KPC / CUs), beyond which the dot work outlasts the
+// loads.  Measured as graph replays from HBM, this kernel against the path
+// the shape takes without it, us at M = 1 / 2 / 3 / 4: W8 [2560 x 2560] 3.8 /
+// 4.4 / 4.9 / 5.5 against 5.5 / 5.8 / 6.0 / 6.3 (streaming); W8 [8192 x 640]
+// 4.0 / 4.3 / 4.9 / 5.4 against 5.9 / 6.0 / 6.1 / 6.3 (MFMA core); MXFP8
+// [2048 x 2560] 3.4 / 3.9 / 4.3 / 4.7 against 6.3 / 6.5 / 6.7 / 6.9; W6 [2048
+// x 2560] 3.9 / 4.6 / 5.4 / 6.1 against 7.1 / 7.2 / 7.4 / 8.0; NVFP4 [4096 x
+// 2560] 4.5 / 6.0 against 6.3 / 6.4 at M = 1 / 2, and 7.5 against 6.5 at
+// M = 3, past the limit.
 constexpr int64_t kRowsFmaProductsPerCu = int64_t(1) << 17;
 
 template <class F>
 bool rows_fma_shape_ok(int N, int M, int threads, int cus) {
   if (M < 1 || M > 4 || N < 1 || threads > kRowsFmaMaxThreads) return false;
   if (rows_shape_ok(N, M, cus)) return true;
-  if ((int64_t)N * threads * M * F::KPC >= kRowsFmaProductsPerCu * cus) return false;
+  if ((int64_t)N * threads * M * F::KPC > kRowsFmaProductsPerCu * cus) return false;
   const int res = M == 1   ? rows_fma_resident<F, 1>(threads)
                   : M == 2 ? rows_fma_resident<F, 2>(threads)
                   : M == 3 ? rows_fma_resident<F, 3>(threads)
