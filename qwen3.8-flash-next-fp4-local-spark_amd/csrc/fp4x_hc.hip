@@ -299,6 +299,13 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
 #pragma unroll
     for (int s = 0; s < kMixMaxHc; ++s) nrv[q][s] = nm[(int64_t)(s < u.hc ? s : u.hc - 1) * u.H];
   }
+  // the up weights' bf16 operands, made while the bottleneck is outstanding
+  // (the plan gives every lane one full batch of kNJ single chunks), so that
+  // only the MFMAs follow the flag
+  static_assert(CPS == 1 && F::SUB == 1, "one 16-weight chunk per batch slot");
+  uint32_t wq[kNJ][8];
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j) F::deq16(cb.ch[j][0], 0, wq[j]);
   __syncthreads();
 
   // 3. wait for this workgroup's flag to reach the call's generation
@@ -331,7 +338,14 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   const bool xon = n < u.M;
   const uint16_t* xl0 = lds + (xon ? n : 0) * K + CPS * cw * F::KPC;
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  mfma_compute<F, DP, CPS, true, false>(cb, xl0, 0, J, cw, nch, acc);
+  // the MFMA order of mfma_compute's full path (hc_up_mfma_kernel), on the
+  // operands made above
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j) {
+    const uint4* xp = reinterpret_cast<const uint4*>(xl0 + j * DP * F::KPC);
+    acc = mfma16(xp[0], make_uint4(wq[j][0], wq[j][1], wq[j][2], wq[j][3]), acc);
+    acc = mfma16(xp[1], make_uint4(wq[j][4], wq[j][5], wq[j][6], wq[j][7]), acc);
+  }
   float* gred = red + ((size_t)slot * (T / 16) + grp) * (KW > 1 ? KW - 1 : 0) * 256;
   if (wv > 0) reinterpret_cast<f32x4_t*>(gred)[(wv - 1) * 64 + lane] = acc;
   __syncthreads();

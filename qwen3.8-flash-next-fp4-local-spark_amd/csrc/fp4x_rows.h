@@ -368,13 +368,16 @@ int rows_fma_resident(int threads) {
 // shared expert's [1280 x 2560] and its down projection [2560 x 640]), whose
 // tiles leave the MFMA core and the streaming kernels one memory round trip
 // per tile with few loads in flight, while one row per workgroup puts every
-// load of the matrix in flight at once.  Two limits: the workgroups resident
-// in at most two rounds, and at most 2^17 fp32 products per lane slot of a CU
-// (N * threads * M * KPC / CUs), beyond which the dot work outlasts the
-// loads.  Measured as graph replays from HBM, this kernel against the path
-// the shape takes without it, us at M = 1 / 2 / 3 / 4: W8 [4096 x 2560] (two
-// rounds) 4.6 / 5.4 against 6.1 / 6.3 (streaming) at M = 1 / 2; NVFP4 [8192
-// x 2560] 6.6 / 7.9 against 7.7 / 8.0 (MFMA core); W8 [2560 x 2560] 3.8 /
+// load of the matrix in flight at once.  Three limits: at most 2^17 fp32
+// products per lane slot of a CU (N * threads * M * KPC / CUs), beyond which
+// the dot work outlasts the loads; every workgroup resident in one round; and
+// at most 32 waves per CU whatever the occupancy, so that the mixer's up
+// projection [10240 x 320 or 640] (one wave per row, 40 per CU) stays on the
+// MFMA core, whose sums the single-launch mixer's up tiles reproduce bit for
+// bit.  (Two resident rounds were faster for W8 [4096 x 2560] at M = 1, 4.6
+// against 6.1 us, but would take that projection.)  Measured as graph replays
+// from HBM, this kernel against the path the shape takes without it, us at
+// M = 1 / 2 / 3 / 4: W8 [2560 x 2560] 3.8 /
 // 4.4 / 4.9 / 5.5 against 5.5 / 5.8 / 6.0 / 6.3 (streaming); W8 [8192 x 640]
 // 4.0 / 4.3 / 4.9 / 5.4 against 5.9 / 6.0 / 6.1 / 6.3 (MFMA core); MXFP8
 // [2048 x 2560] 3.4 / 3.9 / 4.3 / 4.7 against 6.3 / 6.5 / 6.7 / 6.9; W6 [2048
@@ -388,11 +391,12 @@ bool rows_fma_shape_ok(int N, int M, int threads, int cus) {
   if (M < 1 || M > 4 || N < 1 || threads > kRowsFmaMaxThreads) return false;
   if (rows_shape_ok(N, M, cus)) return true;
   if ((int64_t)N * threads * M * F::KPC > kRowsFmaProductsPerCu * cus) return false;
+  if ((int64_t)N * (threads / 64) > 32 * (int64_t)cus) return false;
   const int res = M == 1   ? rows_fma_resident<F, 1>(threads)
                   : M == 2 ? rows_fma_resident<F, 2>(threads)
                   : M == 3 ? rows_fma_resident<F, 3>(threads)
                            : rows_fma_resident<F, 4>(threads);
-  return N <= 2 * (int64_t)res * cus;
+  return N <= (int64_t)res * cus;
 }
 
 // Launch a few-rows kernel when the call fits one: one matrix, no per-row

@@ -381,28 +381,19 @@ def test_gemv_shape_errors(gpu, F):
     assert y.shape == (0, 64)
 
 
-@pytest.mark.parametrize("fmt,N,M", [("w8", 4096, 1), ("w8", 4096, 2), ("nv4", 8192, 1)])
-def test_rows_gemv_two_rounds(gpu, F, fmt, N, M, monkeypatch):
-    """Matrices whose one-row workgroups fill the CUs twice (W8 [4096 x 2560],
-    NVFP4 [8192 x 2560]) still take the fma few-rows kernel at small M: fp32
-    sums within the bound, unlike the path taken with FP4X_ROWS=0 (the
-    streaming kernel, the MFMA core) in the last bits, repeated calls bit for
-    bit."""
-    rng = np.random.default_rng(4200 + N + M)
-    k = 2560
-    planes, w_op, gs = prep(fmt, rng, N, k)
-    x, _ = act(rng, M, k)
-    xd = bf16_dev(x)
-    y = to_f32(run(F, fmt, xd, planes, 1, torch.float32))
+@pytest.mark.parametrize("N,K,M", [(10240, 320, 3), (10240, 640, 3), (10240, 320, 1)])
+def test_mixer_up_shape_takes_the_core(gpu, F, N, K, M, monkeypatch):
+    """The mixer's up projection [10240 x 320 or 640] through w8_linear (the
+    unfused mixer's gate logits) stays on the MFMA core, bit for bit with
+    FP4X_ROWS=0, so that the unfused mixer equals the single-launch one."""
+    rng = np.random.default_rng(4300 + N + K + M)
+    q, s = oq.quantize_w8(weights(rng, N, K))
+    x, _ = act(rng, M, K)
+    xd, qd, sd = bf16_dev(x), dev(q), dev(s)
+    y = F.w8_linear(xd, qd, sd, (32, 64, 1, 4), torch.float32)
     with path_switch(monkeypatch, "FP4X_ROWS"):
-        y_other = to_f32(run(F, fmt, xd, planes, 1, torch.float32))
-    assert not np.array_equal(y.view(np.uint32), y_other.view(np.uint32)), "few-rows kernel not taken"
-    exact = ordered.exact_sum(x, w_op) * gs
-    bound = ordered.mfma_bound(x, w_op, 5) * abs(gs)
-    for got in (y, y_other):
-        assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
-    assert_tol(y, og.matmul_f32(x, w_op) * np.float32(gs), what=f"{fmt} rows N={N} M={M}")
-    assert np.array_equal(y.view(np.uint32), to_f32(run(F, fmt, xd, planes, 1, torch.float32)).view(np.uint32))
+        y_core = F.w8_linear(xd, qd, sd, (32, 64, 1, 4), torch.float32)
+    assert torch.equal(y, y_core)
 
 
 @pytest.mark.parametrize("N,K,M", [(2560, 640, 3), (2560, 640, 1), (4096, 640, 4), (2560, 1280, 2)])
