@@ -240,7 +240,7 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
  * int32, zero before the first call and never touched by the caller
  * afterwards.  The single launch keeps one tile ticket per 128-byte line,
  * ticket t at 32 t, and at S = (n_tickets - 32 * (CUs + 1)) rounded down to
- * a multiple of 32 the down-tile count (S), a status word (S + 1) and one
+ * a multiple of 32 an unused word (S), a status word (S + 1) and one
  * 128-byte line per workgroup (its generation flag, its ack word and a down
  * tile's generation), so it needs S >= 32 * ceil(N / 16); with fewer it
  * makes the two calls.  (S depends on the buffer alone: calls of any shape on

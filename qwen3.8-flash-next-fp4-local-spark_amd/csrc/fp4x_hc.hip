@@ -162,28 +162,31 @@ static bool al(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & 
 // projection runs.
 //   * Workgroups 0..D-1 (D = down tiles x C) run one down item each.  The
 //     last arriver of a down tile stores di and, device-coherently, the
-//     bottleneck, waits for those stores and counts the tile in sync[0].
+//     bottleneck, waits for those stores and then advances every
+//     workgroup's flag by one (a fetch-add per 128-byte flag line).  (A
+//     shared tile count whose last increment advanced the flags cost one more
+//     device round trip per mixer: the served mixer 9.9 -> 9.5 us without it.)
 //   * Every workgroup (8 waves) then issues the weight loads of its R up
 //     tiles (R = 8 / waves per up tile), which stream while it waits.
 //     (Issued first, they would share each CU's bandwidth with the down
 //     loads and lengthen the critical path.)
-//   * The workgroup whose count completes the down tiles re-arms the count
-//     and advances every workgroup's flag by one (a fetch-add per 128-byte
-//     flag line).  One lane of each workgroup waits until its flag reaches
-//     the call's generation (s_sleep between reads, at most spin_limit
-//     reads); the workgroup then stages the bottleneck with device-coherent
-//     loads and runs its up tiles.  (200 workgroups polling one shared
-//     counter instead made a hot spot that cost about 13 us per mixer.)
+//   * One lane of each workgroup waits until its flag reaches the call's
+//     generation (s_sleep between reads, at most spin_limit reads); the
+//     workgroup then stages the bottleneck with device-coherent loads and
+//     runs its up tiles.  (200 workgroups polling one shared counter instead
+//     made a hot spot that cost about 13 us per mixer.)
 //   * Generations: beside its flag, on the same line, workgroup w keeps the
-//     number of calls whose grid held a workgroup w (its ack word).  Every
-//     such call advances flag w exactly once (every down item always runs,
-//     so the last tile is always counted), and its workgroup w adds one to
-//     ack w when it starts, so flag w == ack w between calls.  A workgroup
-//     therefore waits for flag == ack + 1 (the ack read at its start): the
-//     target does not depend on when the workgroup starts.  A workgroup
-//     that only gets a CU after the advance (another kernel holding CUs)
-//     finds its flag there already; one whose wait gave up still counts its
-//     call, so the late advance cannot satisfy the next call.
+//     number of tile advances of the calls whose grid held a workgroup w
+//     (its ack word).  Every such call advances flag w once per down tile
+//     (every down item always runs, so every tile has a closer), and its
+//     workgroup w adds the call's tile count to ack w when it starts, so
+//     flag w == ack w between calls.  A workgroup therefore waits for flag ==
+//     ack + tiles (the ack read at its start): the target does not depend on
+//     when the workgroup starts.  A workgroup that only gets a CU after the
+//     advances (another kernel holding CUs) finds its flag there already;
+//     one whose wait gave up still counts its call, so the late advances
+//     cannot satisfy the next call.  (The words wrap modulo 2^32 and are
+//     only compared for equality.)
 //   * The down items sit in the lowest workgroup indices, which each XCD
 //     dispatches in order, so every down item was dispatched before any
 //     workgroup that waits on the same XCD, and a wait never depends on a
@@ -199,10 +202,11 @@ constexpr int kMixGenAt = 8;                     // a down tile's generation wor
 struct HcMixArgs {
   GemvLaunch d;          // down: x, q, s, di (out), bot (out2), lr, hc, split-K slots and tickets
   HcUpArgs u;            // up: bot [M, lr] contiguous, interleaved q/s, normalized, out
-  int* sync;             // [0] down tiles done (zero between calls), [1] status (bit 0: a wait gave up,
+  int* sync;             // [0] unused (zero), [1] status (bit 0: a wait gave up,
                          // bit 1: a down tile's partials were not all on its closer's XCD),
                          // [kMixFlagStride * (w + 1)] generation flag of workgroup w,
-                         // [kMixFlagStride * (w + 1) + kMixAckAt] its ack word (calls it has started),
+                         // [kMixFlagStride * (w + 1) + kMixAckAt] its ack word (tile advances of the
+                         // calls it has started),
                          // [kMixFlagStride * (t + 1) + kMixGenAt] down tile t's generation (XCD-local slots)
   SplitLocal loc;        // XCD-local slots: generations, tags, status
   int C, D, tiles_d, R, spin_limit;
@@ -236,9 +240,10 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   const int J = ((nch + CPS - 1) / CPS + DP - 1) / DP;
   const int64_t urow = (int64_t)tuc * T + grp * 16 + n;
   int* flag = a.sync + kMixFlagStride * (blockIdx.x + 1);
-  int gen = 0;                                      // the value this call's advance gives the flag
+  int gen = 0;                                      // the value this call's advances give the flag
   if (threadIdx.x == 0) {
-    gen = __hip_atomic_load(flag + kMixAckAt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    gen = (int)((uint32_t)__hip_atomic_load(flag + kMixAckAt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
+                (uint32_t)a.tiles_d);
     __hip_atomic_store(flag + kMixAckAt, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
@@ -260,14 +265,10 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   if (t >= 0) {
     if (w8_splitk_item<F16S, 8, 2, EpiHcDownShared, LOCAL>(a.d, a.C, t, c, base, a.loc)) {
       wait_vmcnt<0>();                              // the tile's bottleneck stores have completed
-      int old = 0;
-      if (lane == 0) old = __hip_atomic_fetch_add(a.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      old = __builtin_amdgcn_readfirstlane(old);
-      if (old == a.tiles_d - 1) {                   // the last down tile: re-arm the count, advance every flag
-        if (lane == 0) __hip_atomic_store(a.sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int w = lane; w < (int)gridDim.x; w += 64)
-          __hip_atomic_fetch_add(a.sync + kMixFlagStride * (w + 1), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      // this tile's advance of every workgroup's flag (the flags reach the
+      // call's generation when every tile has advanced them)
+      for (int w = lane; w < (int)gridDim.x; w += 64)
+        __hip_atomic_fetch_add(a.sync + kMixFlagStride * (w + 1), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
@@ -528,7 +529,7 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   const int tiles_d = (N + 15) / 16;
   // tile tickets one 128-byte line apart from the start of the buffer (the
   // 200 items' ticket atomics of a mixer would otherwise queue on two lines);
-  // the count, the status word and the flags in its last 32 * (cus + 1) ints,
+  // the status word and the flags in its last 32 * (cus + 1) ints,
   // at the same place for every shape the buffer serves
   d.tstride = kMixFlagStride;
   const int64_t sync_at =
