@@ -141,9 +141,11 @@ def all_finite_bf16():
     return b[(b & 0x7F80) != 0x7F80]
 
 
-@pytest.mark.parametrize("hc", [4, 3])
+@pytest.mark.parametrize("hc", [4, 3, 1])
 def test_scaled_silu_kernel_every_bf16(gpu, F, hc):
-    """fp4x_hc_scaled_silu on every finite bf16 input equals the oracle bit for bit."""
+    """fp4x_hc_scaled_silu on every finite bf16 input equals the oracle bit for
+    bit (hc = 1: the output is bf16(sc * sigmoid(sc)) itself, for every bf16
+    sc)."""
     bits = all_finite_bf16()
     n = bits.size // 64 * 64
     d = fm.bf16_to_f32(bits[:n]).reshape(64, -1)
@@ -164,6 +166,19 @@ def test_gate_mean_kernel_every_bf16(gpu, F):
     got = F.hc_gate_mean(bf16_dev(nrm), bf16_dev(g), HC)
     want = ohc.gate_mean(nrm, g, HC)
     assert np.array_equal(bf16_bits(got), fm.bf16_bits(want))
+
+
+def test_gate_every_bf16_logit(gpu, F):
+    """One stream (hc = 1) and normalized inputs of 1: the gate-mean output is
+    bf16(sigmoid(g)) itself, for every finite bf16 gate logit, bit for bit with
+    the oracle."""
+    bits = all_finite_bf16()
+    g = fm.bf16_to_f32(bits).reshape(2, -1)
+    nrm = np.ones_like(g)
+    got = F.hc_gate_mean(bf16_dev(nrm), bf16_dev(g), 1)
+    want = ohc.gate_mean(nrm, g, 1)
+    assert np.array_equal(bf16_bits(got), fm.bf16_bits(want))
+    assert np.array_equal(fm.bf16_bits(want), fm.bf16_bits(ohc.round_bf16(ohc.sigmoid32(g))))
 
 
 def f16_w8(w):
