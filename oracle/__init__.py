@@ -3,7 +3,7 @@
 A restatement, in numpy (and C for the order-exact sums), of the reference
 plugin's quantize / dequantize / GEMV / mixer / fast-head semantics
 (x/fp4x_kernels.py, x/fp4patch.py).  Only tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg use it, as the checker; the product path never
+bench.py's cpu_baseline leg use it, to check results; the product path never
 imports it.
 
 Modules

@@ -599,8 +599,9 @@ def _patch_draft_vocab():
 
 
 # ----------------------------------------------------------------- entry point
-# Switches of reference patches outside this build (disk PLE embeddings, the
-# drafter weight swap, MoE ablations, graph debugging): reported, not acted on.
+# Switches of reference patches this plugin does not implement (disk PLE
+# embeddings, the drafter weight swap, MoE ablations, graph debugging):
+# reported, not acted on.
 _NOT_BUILT = ("FP4X_KEEP_GRAPH", "FP4X_MOE_ZERO", "FP4X_MOE_TAU", "FP4X_MTP_PATCH", "FP4X_PLE_SPIN",
               "FP4X_PLE_EARLY", "FP4X_PLE_QD")
 
@@ -619,7 +620,7 @@ def register():
     optional piece never stops the server."""
     for flag in _NOT_BUILT:
         if _env(flag):
-            _say(f"{flag}: that reference patch is not part of this build; ignored")
+            _say(f"{flag}: that reference patch is not implemented by this plugin; ignored")
     for flag, wanted, install in _PATCHES:
         if not wanted(flag):
             continue

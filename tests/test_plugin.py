@@ -1,6 +1,6 @@
 """The plugin's registration logic on the CPU (x/fp4patch.py:604-647): the
 entry point, which FP4X_* switches install which class patches on the
-stand-in vLLM modules, the switches outside this build, and that a patch
+stand-in vLLM modules, the switches the plugin does not implement, and that a patch
 that cannot install only logs."""
 import os
 
@@ -55,7 +55,7 @@ def test_every_switch_installs_its_hook(plugin, monkeypatch, tmp_path, capfd):
     err = capfd.readouterr().err
     for line in ("b12x MXFP8 linears of up to 16 rows", "hyper-connection mixers of up to 16 rows",
                  "unquantized linears hooked", "target LM head of up to 16 rows", "MTP draft head restricted",
-                 "FP4X_MOE_ZERO: that reference patch is not part of this build; ignored"):
+                 "FP4X_MOE_ZERO: that reference patch is not implemented by this plugin; ignored"):
         assert line in err, line
     import torch
     assert hasattr(torch.ops.vllm, "fp4x_bf16_linear")            # the plugin's custom op
