@@ -580,21 +580,24 @@ __device__ uint32_t rs_kth(const uint32_t (&key)[N], int k, uint32_t* wh, TkHist
 // window (the caller then takes rs_kth); else the key, with *hi_out = hi and
 // *above_out = the number of keys strictly above it.  hist (kRsThreads words)
 // must be zero and visible on entry.  Logit maxima span far fewer than 1024
-// bf16 key values above their C-th largest, so one round decides.
+// bf16 key values above their C-th largest, so one round decides.  A caller
+// that knows the largest key passes it as hi_known (0: computed here).
 template <int N>
 __device__ uint32_t rs_kth_window(const uint32_t (&key)[N], int k, uint32_t* hist, int* slots, uint32_t* ext,
-                                  uint32_t* hi_out, int* above_out) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t hi = 0;
+                                  uint32_t* hi_out, int* above_out, uint32_t hi_known = 0) {
+  uint32_t hi = hi_known;
+  if (hi == 0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int j = 0; j < N; ++j) hi = max(hi, key[j]);
+    for (int j = 0; j < N; ++j) hi = max(hi, key[j]);
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) hi = max(hi, rs_xor_lane(hi, d));
-  if (lane == 0) ext[wave] = hi;
-  __syncthreads();
-  hi = 0;
+    for (int d = 1; d < 64; d <<= 1) hi = max(hi, rs_xor_lane(hi, d));
+    if (lane == 0) ext[wave] = hi;
+    __syncthreads();
+    hi = 0;
 #pragma unroll
-  for (int w = 0; w < kRsWaves; ++w) hi = max(hi, ext[w]);
+    for (int w = 0; w < kRsWaves; ++w) hi = max(hi, ext[w]);
+  }
 #pragma unroll
   for (int j = 0; j < N; ++j) {
     const uint32_t off = hi - key[j];
@@ -621,14 +624,15 @@ __device__ uint32_t rs_kth_window(const uint32_t (&key)[N], int k, uint32_t* his
 // decides), then every candidate above T and the first C - (count above T) at
 // T in candidate (index) order, ranked by ballots and per-wave counts, and
 // placed the same way, so the set comes out in increasing index order.
-// hist must be zero and visible on entry.  Candidate t's key16 is ck[t] >> 16.
+// hist must be zero and visible on entry.  Candidate t's key16 is ck[t] >> 16;
+// row_hi is the row's largest key16, which the largest candidate holds.
 __device__ void tk_select_set_window(const uint32_t* ck, const int* cidx, int n_c, int C, uint32_t* hist, int* slots,
-                                     uint32_t* ext, int64_t* out) {
+                                     uint32_t* ext, int64_t* out, uint32_t row_hi) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const uint32_t key[1] = {t < n_c ? ck[t] >> 16 : 0u};
   uint32_t hi;
   int above;
-  const uint32_t T = rs_kth_window<1>(key, C, hist, slots, ext, &hi, &above);
+  const uint32_t T = rs_kth_window<1>(key, C, hist, slots, ext, &hi, &above, row_hi);
   const bool up = key[0] > T, tie = key[0] != 0 && key[0] == T;
   const uint64_t below = (1ull << lane) - 1ull;
   const uint64_t bt = __ballot(tie);
@@ -721,6 +725,7 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
   const int S = tk_slice(V), ns = (V + S - 1) / S;
   int n_c = 0;
   bool exact = ns < C, windowed = false;
+  uint32_t row_hi = 0;                              // the row's largest key16, from the window round
   if (!exact) {
     hist[threadIdx.x] = 0;                          // (visible after the first barrier of the T0 round)
     // thread t holds the 8-slice vectors [t * VPT, t * VPT + VPT) of the row's
@@ -755,6 +760,7 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
       int above;
       T0 = rs_kth_window(key, C, hist, slots, ext, &hi, &above);
       windowed = T0 != 0;
+      row_hi = hi;
       if (!windowed) T0 = rs_kth(key, C, wh, h, ext);
     }
     hist[threadIdx.x] = 0;                          // for the final round (the T0 round has read its bin)
@@ -856,7 +862,7 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
     return;
   }
   if (set_only && n_c <= kRsThreads) {             // the set only: no sort
-    if (windowed) tk_select_set_window(ck, cidx, n_c, C, hist, slots, ext, out);
+    if (windowed) tk_select_set_window(ck, cidx, n_c, C, hist, slots, ext, out, row_hi);
     else tk_select_set(ck, cidx, n_c, C, wh, h, ext, slots, out);
     return;
   }
