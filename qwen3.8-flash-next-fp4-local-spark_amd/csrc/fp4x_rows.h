@@ -47,6 +47,7 @@ struct RowsLaunch {
 // ------------------------------------------------------------------ M <= 4
 
 constexpr int kRowsFmaMaxThreads = 256;              // K up to 256 chunks (4096 int8, 8192 NVFP4 weights)
+constexpr int kRowsMultiMaxThreads = 512;            // several rows per workgroup: up to 512 chunks
 
 // Sum over each row of 16 lanes, every lane of the row receiving it: DPP
 // xor-partner additions with partners 1, 2 (quad permutes), 4 (half-row
@@ -78,9 +79,9 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-template <class F, int MT>
-__global__ __launch_bounds__(kRowsFmaMaxThreads) void rows_fma_kernel(RowsLaunch p) {
-  extern __shared__ float red[];                       // [waves][MT]
+template <class F, int MT, int R>
+__global__ __launch_bounds__(R == 1 ? kRowsFmaMaxThreads : kRowsMultiMaxThreads) void rows_fma_kernel(RowsLaunch p) {
+  extern __shared__ float red[];                       // [waves][R][MT]
   // every argument read up front (the empty asm needs each value in a
   // register), so no scalar load waits between the main loads and the store
   const PlaneArgs pa = p.pa;
@@ -92,57 +93,81 @@ __global__ __launch_bounds__(kRowsFmaMaxThreads) void rows_fma_kernel(RowsLaunch
                "s"(N), "s"(M), "s"(odt), "s"(gs));
   const int nch = pa.K / F::KPC;
   const int c = threadIdx.x;
-  const int64_t row = blockIdx.x;
+  const int64_t row0 = (int64_t)blockIdx.x * R;
   // Lanes past the row's chunks load the last chunk (their sums are zeroed
-  // below); loads under a branch would each be waited for at its join.
+  // below), rows past N load row N - 1 (never stored); loads under a branch
+  // would each be waited for at its join.
   const int cc = c < nch ? c : nch - 1;
-  const typename F::Chunk ch = F::load(pa, row, cc);
+  typename F::Chunk ch[R];
   uint4 xr[F::SUB][MT][2];
+  auto load_x = [&]() {
 #pragma unroll
-  for (int sub = 0; sub < F::SUB; ++sub)
+    for (int sub = 0; sub < F::SUB; ++sub)
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const uint4* xp = reinterpret_cast<const uint4*>(xg + (int64_t)m * xs + cc * F::KPC + sub * 16);
-      xr[sub][m][0] = xp[0];
-      xr[sub][m][1] = xp[1];
-    }
-  __builtin_amdgcn_sched_barrier(0);                   // every load above issues before any use below
-  float acc[MT];
+      for (int m = 0; m < MT; ++m) {
+        const uint4* xp = reinterpret_cast<const uint4*>(xg + (int64_t)m * xs + cc * F::KPC + sub * 16);
+        xr[sub][m][0] = xp[0];
+        xr[sub][m][1] = xp[1];
+      }
+  };
+  if constexpr (R == 1) {
+    ch[0] = F::load(pa, row0, cc);
+    load_x();
+  } else {
+    // the activations first, then the rows in order, so that row r's sums
+    // wait only for the loads up to its own
+    load_x();
 #pragma unroll
-  for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-#pragma unroll
-  for (int sub = 0; sub < F::SUB; ++sub) {
-    uint32_t w[8];
-    F::deq16(ch, sub, w);
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const uint4 xa = xr[sub][m][0], xb = xr[sub][m][1];
-      const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-      float t = acc[m];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) t = dot2_bf16(w[i], xv[i], t);
-      acc[m] = t;
-    }
+    for (int r = 0; r < R; ++r) ch[r] = F::load(pa, row0 + r < N ? row0 + r : (int64_t)N - 1, cc);
   }
+  __builtin_amdgcn_sched_barrier(0);                   // every load above issues before any use below
+  float acc[R][MT];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int sub = 0; sub < F::SUB; ++sub) {
+      uint32_t w[8];
+      F::deq16(ch[r], sub, w);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const uint4 xa = xr[sub][m][0], xb = xr[sub][m][1];
+        const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        float t = acc[r][m];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t = dot2_bf16(w[i], xv[i], t);
+        acc[r][m] = t;
+      }
+    }
   if (c >= nch) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nwaves = (nch + 63) >> 6;
-  float sums[MT];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) sums[m] = wave_sum_lane63(acc[m]);
-  if (lane == 63) {
+  for (int r = 0; r < R; ++r) {
+    float sums[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) red[wave * MT + m] = sums[m];
+    for (int m = 0; m < MT; ++m) sums[m] = wave_sum_lane63(acc[r][m]);
+    if (lane == 63) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) red[(wave * R + r) * MT + m] = sums[m];
+    }
   }
   __syncthreads();
-  const int m = threadIdx.x;
-  if (m < MT) {
-    float v = red[m];
-    for (int j = 1; j < nwaves; ++j) v += red[j * MT + m];
-    store_out(out, (int64_t)m * os + row, odt, v * gs);
+  const int o = threadIdx.x;
+  if (o < R * MT) {
+    const int r = o / MT, m = o % MT;
+    float v = red[r * MT + m];
+    for (int j = 1; j < nwaves; ++j) v += red[(j * R + r) * MT + m];
+    const int64_t row = row0 + r;
+    if (row < N) store_out(out, (int64_t)m * os + row, odt, v * gs);
   }
 }
 
@@ -346,22 +371,31 @@ inline bool rows_shape_ok(int N, int M, int cus) {
   return M >= 1 && M <= 16 && N >= 1 && tiles * 2 < cus && rows_per_wg(N, cus) > 0;
 }
 
-// Workgroups of rows_fma_kernel<F, MT> of `threads` threads one CU holds at
-// once (its registers decide: the NVFP4 and W6 kernels at M >= 3 hold fewer).
-template <class F, int MT>
+// Workgroups of rows_fma_kernel<F, MT, R> of `threads` threads one CU holds
+// at once (its registers decide: the NVFP4 and W6 kernels at M >= 3 hold
+// fewer).
+template <class F, int MT, int R>
 int rows_fma_resident(int threads) {
-  static int cache[kRowsFmaMaxThreads / 64 + 1];
+  static int cache[kRowsMultiMaxThreads / 64 + 1];
   const int key = threads / 64;
   int occ = cache[key];
   if (occ <= 0) {
-    const size_t lds = (size_t)key * MT * sizeof(float);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(rows_fma_kernel<F, MT>),
+    const size_t lds = (size_t)key * R * MT * sizeof(float);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(rows_fma_kernel<F, MT, R>),
                                                      threads, lds) != hipSuccess ||
         occ < 1)
       occ = 1;
     cache[key] = occ;
   }
   return occ;
+}
+
+template <class F, int R>
+int rows_fma_resident_m(int M, int threads) {
+  return M == 1   ? rows_fma_resident<F, 1, R>(threads)
+         : M == 2 ? rows_fma_resident<F, 2, R>(threads)
+         : M == 3 ? rows_fma_resident<F, 3, R>(threads)
+                  : rows_fma_resident<F, 4, R>(threads);
 }
 
 // The fma kernel beyond few-rows shapes: wider matrices of short rows (the MTP
@@ -392,30 +426,70 @@ bool rows_fma_shape_ok(int N, int M, int threads, int cus) {
   if (rows_shape_ok(N, M, cus)) return true;
   if ((int64_t)N * threads * M * F::KPC > kRowsFmaProductsPerCu * cus) return false;
   if ((int64_t)N * (threads / 64) > 32 * (int64_t)cus) return false;
-  const int res = M == 1   ? rows_fma_resident<F, 1>(threads)
-                  : M == 2 ? rows_fma_resident<F, 2>(threads)
-                  : M == 3 ? rows_fma_resident<F, 3>(threads)
-                           : rows_fma_resident<F, 4>(threads);
-  return N <= (int64_t)res * cus;
+  return N <= (int64_t)rows_fma_resident_m<F, 1>(M, threads) * cus;
 }
 
-// Launch a few-rows kernel when the call fits one: one matrix, no per-row
-// scale, strides within int32, a few-rows shape, and (M <= 4, at most 256
-// chunks per row) the fma kernel or else an MFMA plan of at most 8 waves;
-// false (nothing launched) otherwise, or when FP4X_ROWS=0.  The split count
-// of the call is a shape precondition only: these kernels sum each row over
-// its whole K inside one workgroup, in a fixed order.
+// Rows per workgroup R of the fma kernel for a matrix of M <= 4 activation
+// rows that is not a few-rows shape, or 0 for none.  With R > 1 a workgroup
+// loads its activations once and then every chunk of its R rows, so the
+// activation reads (M * K * 2 bytes per workgroup, from L2) shrink R-fold,
+// at R times the registers and 1/R of the workgroups.  Only for rows longer
+// than one wave's chunks (the mixer's up projection, 20 or 40 chunks, stays
+// on the MFMA core) and of at most 512 chunks, with every workgroup resident
+// in one round:
+//   * M >= 2 and N >= 8 rows per CU: R = 2;
+//   * else R = 1 where rows_fma_shape_ok takes the matrix (at M = 1, and
+//     for under 8 rows per CU, the one-row kernel's extra workgroups pay
+//     more than its activation reads cost);
+//   * else R = 2 (rows of over 256 chunks, or past the one-row limits).
+// Measured as graph replays from HBM (us at M = 1 / 2 / 3 / 4), R = 1 / 2:
+// W6 [2048 x 2560] 3.9 / 4.6 / 5.4 / 6.1 against 4.2 / 4.5 / 5.0 / 5.4;
+// NVFP4 [2048 x 2560] 3.5 / 4.3 / 5.0 / 5.8 against 3.6 / 4.0 / 4.4 / 4.7;
+// W8 [2560 x 2560] 3.8 / 4.4 / 5.0 / 5.5 against 4.0 / 4.4 / 4.7 / 5.1;
+// MXFP8 [2048 x 2560] 3.5 / 3.9 / 4.3 / 4.8 against 3.8 / 4.0 / 4.4 / 4.8;
+// W6 [1280 x 2560] 3.4 / 3.9 / 4.4 / 4.9 against 3.9 / 4.3 / 4.7 / 5.1.  Against
+// the path these shapes took before (MFMA core, or W8's single-matrix
+// stream): W6 [2560 x 6144] (the attention output projection) 5.4 (R = 1) /
+// 6.7 / 8.1 / 9.5 against 14.0 / 14.3 / 14.6 / 16.2 (R = 4 at M = 2..4: 7.6
+// / 8.7 / 9.7; R = 8: 9.8 / 11.1 / 12.4); NVFP4 [2560 x 6144] 4.7 / 5.7 / 7.1
+// / 8.6 against 10.7 / 11.0 / 11.3 / 12.7; MXFP8, W8 and bf16 [2560 x 6144]
+// (384 chunks, past the one-row kernel, R = 2): 5.5 / 6.5 / 7.5 / 8.4, 5.6 /
+// 6.6 / 7.6 / 8.4 and 7.8 / 7.9 / 8.7 / 9.6 against 11.7 / 12.0 / 12.3 / 13.6,
+// 7.9 / 8.3 / 8.7 / 14.3 and 12.5 / 12.6 / 12.8 / 14.3; W6 [4096 x 2560] 5.1
+// / 6.0 / 6.7 / 7.6 against 7.5 / 7.6 / 7.8 / 8.3; NVFP4 [8192 x 2560] 5.9 /
+// 7.2 at M = 1 / 2 against 7.6 / 7.8.  Larger matrices stay on the streaming
+// kernels or the MFMA core (W6 [8192 x 2560] at M = 3: 7.4 streaming against
+// 10.5 / 9.9 at R = 2 / 4).
 template <class F>
-bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
+int rows_fma_pick(int N, int M, int nch, int threads, int cus) {
+  if (M < 1 || M > 4 || N < 1) return 0;
+  if (rows_shape_ok(N, M, cus)) return threads <= kRowsFmaMaxThreads ? 1 : 0;
+  const bool r2 = nch > 64 && threads <= kRowsMultiMaxThreads &&
+                  (N + 1) / 2 <= (int64_t)rows_fma_resident_m<F, 2>(M, threads) * cus;
+  if (M >= 2 && N >= 8 * cus && r2) return 2;
+  if (rows_fma_shape_ok<F>(N, M, threads, cus)) return 1;
+  return r2 ? 2 : 0;
+}
+
+template <class F, int R>
+inline bool rows_fma_launch(const RowsLaunch& a, int threads, hipStream_t st) {
+  const size_t lds = (size_t)(threads / 64) * R * a.M * sizeof(float);
+  const dim3 grid((unsigned)((a.N + R - 1) / R)), block((unsigned)threads);
+  switch (a.M) {
+    case 1: hipLaunchKernelGGL((rows_fma_kernel<F, 1, R>), grid, block, lds, st, a); return true;
+    case 2: hipLaunchKernelGGL((rows_fma_kernel<F, 2, R>), grid, block, lds, st, a); return true;
+    case 3: hipLaunchKernelGGL((rows_fma_kernel<F, 3, R>), grid, block, lds, st, a); return true;
+    case 4: hipLaunchKernelGGL((rows_fma_kernel<F, 4, R>), grid, block, lds, st, a); return true;
+  }
+  return false;
+}
+
+// The few-rows launch block of a call, false when the call's layout does not
+// fit the few-rows kernels (several matrices, a per-row scale, strides past
+// int32, K not a whole number of chunks, FP4X_ROWS=0).
+inline bool rows_launch_args(const GemvLaunch& p, int batch, int kpc, RowsLaunch& a) {
   if (!switches().rows || batch != 1 || p.rs) return false;
-  if (p.x_stride > INT32_MAX || p.out_stride > INT32_MAX) return false;
-  const int cus = device_cus();
-  if (p.pa.K % F::KPC) return false;
-  const int nch = p.pa.K / F::KPC;
-  const int threads = (nch + 63) / 64 * 64;
-  const bool fma = rows_fma_shape_ok<F>(p.N, p.M, threads, cus);
-  if (!fma && !rows_shape_ok(p.N, p.M, cus)) return false;
-  RowsLaunch a;
+  if (p.x_stride > INT32_MAX || p.out_stride > INT32_MAX || p.pa.K % kpc) return false;
   a.pa = p.pa;
   a.x = p.x;
   a.out = p.out;
@@ -423,24 +497,67 @@ bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
   a.out_stride = (int)p.out_stride;
   a.N = p.N;
   a.M = p.M;
+  a.R = 1;
   a.out_dtype = p.out_dtype;
   a.gs = p.gs;
-  if (fma) {
-    a.R = 1;
-    const size_t lds = (size_t)(threads / 64) * p.M * sizeof(float);
-    const dim3 grid((unsigned)p.N), block((unsigned)threads);
-    switch (p.M) {
-      case 1: hipLaunchKernelGGL((rows_fma_kernel<F, 1>), grid, block, lds, st, a); return true;
-      case 2: hipLaunchKernelGGL((rows_fma_kernel<F, 2>), grid, block, lds, st, a); return true;
-      case 3: hipLaunchKernelGGL((rows_fma_kernel<F, 3>), grid, block, lds, st, a); return true;
-      case 4: hipLaunchKernelGGL((rows_fma_kernel<F, 4>), grid, block, lds, st, a); return true;
-    }
-    return false;
+  return true;
+}
+
+template <class F>
+inline bool rows_fma_go(RowsLaunch& a, int R, int threads, hipStream_t st) {
+  a.R = R;
+  switch (R) {
+    case 1: return rows_fma_launch<F, 1>(a, threads, st);
+    case 2: return rows_fma_launch<F, 2>(a, threads, st);
+    case 4: return rows_fma_launch<F, 4>(a, threads, st);
   }
+  return false;
+}
+
+// Launch a few-rows kernel when the call fits one: one matrix, no per-row
+// scale, strides within int32, and either the fma kernel (M <= 4, R rows per
+// workgroup as rows_fma_pick decides) or, for a few-rows shape, an MFMA plan
+// of at most 8 waves; false (nothing launched) otherwise, or when
+// FP4X_ROWS=0.  The split count of the call is a shape precondition only:
+// these kernels sum each row over its whole K inside one workgroup, in a
+// fixed order.
+template <class F>
+bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
+  RowsLaunch a;
+  if (!rows_launch_args(p, batch, F::KPC, a)) return false;
+  const int cus = device_cus();
+  const int nch = p.pa.K / F::KPC;
+  const int threads = (nch + 63) / 64 * 64;
+  const int R = rows_fma_pick<F>(p.N, p.M, nch, threads, cus);
+  if (R) return rows_fma_go<F>(a, R, threads, st);
+  if (!rows_shape_ok(p.N, p.M, cus)) return false;
   RowsPlan pl;
   if (!rows_mfma_plan<F>(nch, p.M, pl)) return false;
   a.R = rows_per_wg(p.N, cus);
   return rows_dispatch<F>(pl, RowsGemvBody<F>{a, pl, st});
+}
+
+// MXFP8 matrices of 16 to 32 rows per CU at M <= 2 (shapes its streaming
+// kernel takes): the fma kernel with 2 rows per workgroup up to 8 workgroups
+// per CU, else 4, when every workgroup is resident.  Measured as graph
+// replays from HBM, us at M = 1 / 2, this against the streaming kernel:
+// [4096 x 2560] (R = 2) 4.4 / 5.0 against 4.7 / 5.3; [8192 x 2560] (R = 4)
+// 6.2 / 6.8 against 6.3 / 7.1.  Larger matrices gain nothing ([13312 x 2560]
+// 9.4 / 9.6 against 9.3 / 9.4, [16384 x 2560] 10.3 / 10.9 against 10.3 /
+// 10.6), and at M = 3 the streaming kernel is as fast or faster (5.4 against
+// 5.6 at [4096 x 2560]).
+template <class F>
+bool launch_rows_wide(const GemvLaunch& p, hipStream_t st) {
+  RowsLaunch a;
+  if (p.M < 1 || p.M > 2 || !rows_launch_args(p, 1, F::KPC, a)) return false;
+  const int cus = device_cus();
+  const int nch = p.pa.K / F::KPC;
+  const int threads = (nch + 63) / 64 * 64;
+  if (p.N < 16 * cus || p.N > 32 * cus || nch <= 64 || threads > kRowsMultiMaxThreads) return false;
+  const int R = (p.N + 1) / 2 <= 8 * cus ? 2 : 4;
+  const int res = R == 2 ? rows_fma_resident_m<F, 2>(p.M, threads) : rows_fma_resident_m<F, 4>(p.M, threads);
+  if ((p.N + R - 1) / R > (int64_t)res * cus) return false;
+  return rows_fma_go<F>(a, R, threads, st);
 }
 
 }  // namespace fp4x

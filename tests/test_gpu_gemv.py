@@ -262,16 +262,17 @@ def _dense_stream_case(F, fmt, slots, parts, env, M, tail, k, monkeypatch):
     n = 16 * slots * cus + tail
     planes, w_op, gs = prep(fmt, rng, n, k)
     x, _ = act(rng, M, k)
-    y = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
-    with path_switch(monkeypatch, env):
-        y_core = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
+    with path_switch(monkeypatch, "FP4X_ROWS"):        # MXFP8 at M <= 2 takes the few-rows kernel first
+        y = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
+        with path_switch(monkeypatch, env):
+            y_core = to_f32(run(F, fmt, bf16_dev(x), planes, 1, torch.float32))
+        yb = run(F, fmt, bf16_dev(x), planes, 1)                    # bf16 output: the same sums rounded
     assert not np.array_equal(y.view(np.uint32), y_core.view(np.uint32)), "streaming kernel not taken"
     exact = ordered.exact_sum(x, w_op) * gs
     bound = ordered.mfma_bound(x, w_op, parts) * abs(gs)              # parts: K slices of a tile
     for got in (y, y_core):
         assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
     assert_tol(y, og.matmul_f32(x, w_op) * np.float32(gs), what=f"{fmt} stream M={M}")
-    yb = run(F, fmt, bf16_dev(x), planes, 1)                        # bf16 output: the same sums rounded
     assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
 
 
@@ -288,10 +289,11 @@ def _dense_stream_case(F, fmt, slots, parts, env, M, tail, k, monkeypatch):
 ])
 def test_w8_single_stream(gpu, F, case, monkeypatch):
     """Single W8 matrices without split-K of at least half a tile per CU stream
-    through LDS (fp32 or fp16 scales): fp32 sums within the MFMA bound of the
-    exact sum (the tile's K over `parts` waves), a different K decomposition
-    than the MFMA core's (FP4X_W8_STREAM=0), repeated calls bit for bit, bf16
-    outputs the same sums rounded."""
+    through LDS (fp32 or fp16 scales), with the few-rows kernels off
+    (FP4X_ROWS=0; at M <= 4 they take some of these shapes first): fp32 sums
+    within the MFMA bound of the exact sum (the tile's K over `parts` waves),
+    a different K decomposition than the MFMA core's (FP4X_W8_STREAM=0),
+    repeated calls bit for bit, bf16 outputs the same sums rounded."""
     size, k, M, s_dtype, parts = case
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     n = 16 * size[0] * cus + size[1] if isinstance(size, tuple) else size
@@ -301,18 +303,19 @@ def test_w8_single_stream(gpu, F, case, monkeypatch):
     x, _ = act(rng, M, k)
     qd, sd, xd = dev(q), dev(s), bf16_dev(x)
     w_op = og.operand("w8", q, s.astype(np.float32))
-    y = to_f32(F.w8_linear(xd, qd, sd, (32, 256, 1, 4), torch.float32))
-    with path_switch(monkeypatch, "FP4X_W8_STREAM"):
-        y_core = to_f32(F.w8_linear(xd, qd, sd, (32, 256, 1, 4), torch.float32))
+    with path_switch(monkeypatch, "FP4X_ROWS"):
+        y = to_f32(F.w8_linear(xd, qd, sd, (32, 256, 1, 4), torch.float32))
+        with path_switch(monkeypatch, "FP4X_W8_STREAM"):
+            y_core = to_f32(F.w8_linear(xd, qd, sd, (32, 256, 1, 4), torch.float32))
+        y2 = to_f32(F.w8_linear(xd, qd, sd, (32, 256, 1, 4), torch.float32))
+        yb = F.w8_linear(xd, qd, sd, (32, 256, 1, 4))
     assert not np.array_equal(y.view(np.uint32), y_core.view(np.uint32)), "streaming kernel not taken"
     exact = ordered.exact_sum(x, w_op)
     bound = ordered.mfma_bound(x, w_op, parts)
     for got in (y, y_core):
         assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
     assert_tol(y, og.matmul_f32(x, w_op), what=f"w8 single stream N={n} K={k} M={M}")
-    y2 = to_f32(F.w8_linear(xd, qd, sd, (32, 256, 1, 4), torch.float32))
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
-    yb = F.w8_linear(xd, qd, sd, (32, 256, 1, 4))
     assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
     print(f"N={n} K={k} M={M} {np.dtype(s_dtype).name}: max |y - exact| / bound = "
           f"{(np.abs(y - exact) / bound).max():.3g}")
@@ -418,6 +421,50 @@ def test_rows_gemv_short_rows(gpu, F, N, K, M, monkeypatch):
     assert_tol(y, og.matmul_f32(x, w_op), what=f"w8 rows N={N} K={K} M={M}")
     assert np.array_equal(y.view(np.uint32), to_f32(F.w8_linear(xd, qd, sd, cfg, torch.float32)).view(np.uint32))
     assert np.array_equal(bf16_bits(F.w8_linear(xd, qd, sd, cfg)), fm.bf16_bits(y))
+
+
+@pytest.mark.parametrize("fmt", ["mx8", "w8", "w8_f16", "w6", "nv4", "bf16"])
+@pytest.mark.parametrize("rows,K,M", [
+    # rows as (multiple of the CUs, extra rows)
+    ((10, 0), 6144, 3),      # the attention output projection [2560 x 6144]: 2 rows per workgroup
+    ((10, 0), 6144, 1),      # M = 1: W6 / NVFP4 one row per workgroup, the 384-chunk formats 2
+    ((8, 1), 2560, 4),       # an odd N: the last workgroup's second row lies past N
+    ((16, 1), 2560, 2),      # MXFP8: 4 rows per workgroup ahead of its streaming kernel, N % 4 = 1
+    ((16, 0), 2560, 1),      # MXFP8 [4096 x 2560] at M = 1: 2 rows per workgroup
+])
+def test_rows_gemv_multi(gpu, F, fmt, rows, K, M, monkeypatch):
+    """Matrices of at least 8 rows per CU at M = 2..4, and of rows past the
+    one-row kernel's limits, take the fma few-rows kernel with R = 2 (MXFP8 at
+    M <= 2 and 16 rows per CU or more: 2 or 4) rows per workgroup: fp32 sums
+    within the accumulation bound of the exact sums and different from the
+    other path's (FP4X_ROWS=0; both within the bound), repeated calls bit for
+    bit, bf16 outputs the same sums rounded."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    N = rows[0] * cus + rows[1]
+    rng = np.random.default_rng(4500 + N + K + M)
+    base = "w8" if fmt == "w8_f16" else fmt
+    planes, w_op, gs = prep(base, rng, N, K)
+    if fmt == "w8_f16":
+        q, s = planes
+        s16 = s.half()
+        planes = (q, s16)
+        w_op = og.operand("w8", q.cpu().numpy(), s16.float().cpu().numpy())
+    x, _ = act(rng, M, K)
+    xd = bf16_dev(x)
+    print(f"{fmt} N={N} K={K} M={M}", flush=True)
+    y = to_f32(run(F, base, xd, planes, 1, torch.float32))
+    with path_switch(monkeypatch, "FP4X_ROWS"):
+        y_other = to_f32(run(F, base, xd, planes, 1, torch.float32))
+    assert not np.array_equal(y.view(np.uint32), y_other.view(np.uint32)), "few-rows kernel not taken"
+    exact = ordered.exact_sum(x, w_op) * gs
+    for got, parts in ((y, 1), (y_other, 12)):
+        bound = ordered.mfma_bound(x, w_op, parts) * abs(gs)
+        assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
+    assert_tol(y, og.matmul_f32(x, w_op) * np.float32(gs), what=f"{fmt} rows N={N} K={K} M={M}")
+    y2 = to_f32(run(F, base, xd, planes, 1, torch.float32))
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    yb = run(F, base, xd, planes, 1)
+    assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
 
 
 def test_w8_fp16_scales_and_layers(gpu, F):
