@@ -23,7 +23,8 @@ and the 48-gate launch with fp16 and with the reference's fp32 scales, the
 97-layer mixer at the synthetic and the served shape, the 248,320-row fast
 LM head and the exact MXFP8 head it replaces, the 65k-token draft head),
 timed as HIP-graph replays, and the load-time weight preparation (group G,
-eager), and the MTP layer's int8 linears (H).  `read_ceiling` times a plain coalesced read of each kernel's bytes
+eager), the MTP layer's int8 linears (H), and the served model's dense
+linears at M = 3 in W6 and MXFP8 (I).  `read_ceiling` times a plain coalesced read of each kernel's bytes
 under the same protocol (the fastest of a sweep of load depths and grids);
 each kernel row carries `frac_of_ceiling`, that read's time over the
 kernel's.  `cpu_baseline` times the reference math as PyTorch CPU ops
@@ -50,7 +51,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E,F,G,H")
+    ap.add_argument("--kernels", default="all", help="all | none | comma list of A,B,C,D,E,F,G,H,I")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ceiling", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -172,6 +173,38 @@ def bench_mtp(F, torch, dev, out):
         out[f"H_mtp_w8_{n}x{k}_M3"] = entry(us, wbytes + 3 * k * 2 + 3 * n * 2)
         del copies, q, s
         torch.cuda.empty_cache()
+
+
+def bench_shapes(F, torch, dev, out):
+    """The served model's dense linears as the plugin calls them: every (N, K)
+    of its tile tables (x/fp4patch.py:11-18) at M = 3 (1 target + 2 draft
+    rows), in W6 (the shipped FP4X_DENSE=w6, CFG_W6's K split) and in MXFP8
+    (the plugin's default dense mode, _mx8_cfg), bf16 out, the attention
+    output projection [2560 x 6144] at M = 1 as well; weights rotate from
+    HBM."""
+    import fp4patch
+    shapes = sorted(set(fp4patch.CFG_W6) | set(fp4patch.CFG_MX8))
+    for fmt in ("w6", "mx8"):
+        for n, k in shapes:
+            g = torch.Generator(device=dev).manual_seed(11)
+            w = torch.randn((n, k), generator=g, device=dev) * 0.02
+            if fmt == "w6":
+                planes = F.quantize_w6(w)
+                wbytes = n * k // 2 + n * k // 4 + n * (k // 32) * 2
+                cfg = fp4patch.CFG_W6.get((n, k)) or (32, 256, 1, 4)
+                fn = lambda x, p, cfg=cfg: F.w6_linear(x, *p, cfg)
+            else:
+                planes = F.quantize_mx8(w)
+                wbytes = n * k + n * (k // 32)
+                cfg = fp4patch._mx8_cfg(n, k)
+                fn = lambda x, p, cfg=cfg: F.mx8_linear(x, *p, cfg)
+            copies = [tuple(t.clone() for t in planes) for _ in range(copies_for(wbytes))]
+            for M in ((1, 3) if (n, k) == (2560, 6144) else (3,)):
+                x = torch.randn((M, k), generator=g, device=dev).to(torch.bfloat16)
+                us = graph_time([lambda p=p: fn(x, p) for p in copies] * 2)
+                out[f"I_{fmt}_{n}x{k}_M{M}"] = entry(us, wbytes + M * k * 2 + M * n * 2)
+            del copies, planes, w
+            torch.cuda.empty_cache()
 
 
 def bench_gates_single(F, torch, dev, out, q, s):
@@ -707,7 +740,7 @@ def main():
 
     kernels = {}
     kernels["B_w8_gates_48_layers_M3"] = entry(ms_step * 1e3, step_bytes)
-    sel = set("ABCDEFGH") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
+    sel = set("ABCDEFGHI") if args.kernels == "all" else set() if args.kernels == "none" else set(args.kernels.split(","))
     def done(what):
         print(f"[bench] {what} done", file=sys.stderr, flush=True)
 
@@ -741,6 +774,10 @@ def main():
         bench_mtp(F, torch, dev, kernels)
         torch.cuda.empty_cache()
         done("H")
+    if "I" in sel:
+        bench_shapes(F, torch, dev, kernels)
+        torch.cuda.empty_cache()
+        done("I")
 
     ceil = {}
     if not args.no_ceiling:

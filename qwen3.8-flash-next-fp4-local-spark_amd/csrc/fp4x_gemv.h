@@ -209,6 +209,15 @@ struct FmtW6 {
     ch.s = ld_u16(a.s + (row * (a.K / 32) + c) * 2);
     return ch;
   }
+  // Half h of chunk c (16 weights) in the sub-0 position of a chunk.
+  __device__ static Chunk load_half(const PlaneArgs& a, int64_t row, int c, int h) {
+    Chunk ch;
+    const uint2 l = ld_u64(a.w0 + row * (a.K / 2) + c * 16 + h * 8);
+    ch.lo = make_uint4(l.x, l.y, 0, 0);
+    ch.hi = make_uint2(ld_u32(a.w1 + row * (a.K / 4) + c * 8 + h * 4), 0);
+    ch.s = ld_u16(a.s + (row * (a.K / 32) + c) * 2);
+    return ch;
+  }
   __device__ static Chunk zero() {
     Chunk ch; ch.lo = make_uint4(0, 0, 0, 0); ch.hi = make_uint2(0, 0); ch.s = 0; return ch;
   }
@@ -279,6 +288,14 @@ struct FmtNV4 {
     Chunk ch;
     ch.q = ld_u128(a.w0 + row * (a.K / 2) + c * 16);
     ch.s = ld_u16(a.s + row * (a.K / 16) + c * 2);
+    return ch;
+  }
+  // Half h of chunk c (16 weights) in the sub-0 position of a chunk.
+  __device__ static Chunk load_half(const PlaneArgs& a, int64_t row, int c, int h) {
+    Chunk ch;
+    const uint2 q = ld_u64(a.w0 + row * (a.K / 2) + c * 16 + h * 8);
+    ch.q = make_uint4(q.x, q.y, 0, 0);
+    ch.s = ld_u8(a.s + row * (a.K / 16) + c * 2 + h);
     return ch;
   }
   __device__ static Chunk zero() { Chunk ch; ch.q = make_uint4(0, 0, 0, 0); ch.s = 0; return ch; }

@@ -6,14 +6,16 @@
 // issues every memory load before using any, so a lane waits for one memory
 // round trip.  Two kernels:
 //
-//   * M <= 4 (rows_fma_kernel): one weight row per workgroup, thread c
-//     owning chunk c (the format's 16-byte unit of the main plane, with its
-//     scale), dequantized to the bf16 operand and multiplied with the M
+//   * M <= 4 (rows_fma_kernel): R = 1, 2 or 4 weight rows per workgroup,
+//     thread c owning chunk c (the format's 16-byte unit of the main plane,
+//     with its scale) of each row, or, for the 32-weight chunks of W6 and
+//     NVFP4, half c & 1 of chunk c >> 1 (half the serial dequant work per
+//     lane); dequantized to the bf16 operand and multiplied with the M
 //     activation rows by v_dot2_f32_bf16 (two bf16 products and the running
 //     fp32 sum per step: half the instructions of an fma per product, which
 //     took the 512 x 2560 gate at M = 3 from 3.3 to 3.0 us).  Each wave sums
 //     its partials with DPP steps, lane 63 stores the wave's sums, and thread
-//     m adds the waves' sums in wave order.
+//     r M + m adds the waves' sums of row r in wave order.
 //   * 4 < M <= 16 (rows_mfma_kernel): R <= 4 weight rows per workgroup,
 //     products on v_mfma_f32_4x4x4bf16_1k: 16 independent blocks of
 //     D[4 x 4] += A[4 x 4] B[4 x 4].  Lane 4b + q of a wave holds, for block
@@ -47,7 +49,10 @@ struct RowsLaunch {
 // ------------------------------------------------------------------ M <= 4
 
 constexpr int kRowsFmaMaxThreads = 256;              // K up to 256 chunks (4096 int8, 8192 NVFP4 weights)
-constexpr int kRowsMultiMaxThreads = 512;            // several rows per workgroup: up to 512 chunks
+constexpr int kRowsMultiMaxThreads = 512;            // several rows, or half chunks, per workgroup: 512 lanes
+constexpr int rows_fma_max_threads(int R, int LPC) {
+  return R == 1 && LPC == 1 ? kRowsFmaMaxThreads : kRowsMultiMaxThreads;
+}
 
 // Sum over each row of 16 lanes, every lane of the row receiving it: DPP
 // xor-partner additions with partners 1, 2 (quad permutes), 4 (half-row
@@ -79,8 +84,9 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-template <class F, int MT, int R>
-__global__ __launch_bounds__(R == 1 ? kRowsFmaMaxThreads : kRowsMultiMaxThreads) void rows_fma_kernel(RowsLaunch p) {
+template <class F, int MT, int R, int LPC>
+__global__ __launch_bounds__(rows_fma_max_threads(R, LPC)) void rows_fma_kernel(
+    RowsLaunch p) {
   extern __shared__ float red[];                       // [waves][R][MT]
   // every argument read up front (the empty asm needs each value in a
   // register), so no scalar load waits between the main loads and the store
@@ -91,34 +97,43 @@ __global__ __launch_bounds__(R == 1 ? kRowsFmaMaxThreads : kRowsMultiMaxThreads)
   const float gs = p.gs;
   asm volatile("" ::"s"(pa.w0), "s"(pa.w1), "s"(pa.s), "s"(pa.K), "s"(pa.G), "s"(xg), "s"(out), "s"(xs), "s"(os),
                "s"(N), "s"(M), "s"(odt), "s"(gs));
-  const int nch = pa.K / F::KPC;
+  // LPC lanes per chunk: with 2, lane c takes half c & 1 (16 weights) of
+  // chunk c >> 1, loaded as the sub-0 half of a chunk
+  static_assert(LPC == 1 || (LPC == 2 && F::SUB == 2), "half chunks of two-half formats only");
+  constexpr int SUBL = LPC == 2 ? 1 : F::SUB;          // 16-weight halves per lane
+  const int nch = pa.K / F::KPC, nl = nch * LPC;
   const int c = threadIdx.x;
   const int64_t row0 = (int64_t)blockIdx.x * R;
-  // Lanes past the row's chunks load the last chunk (their sums are zeroed
+  // Lanes past the row's chunks load the last one (their sums are zeroed
   // below), rows past N load row N - 1 (never stored); loads under a branch
   // would each be waited for at its join.
-  const int cc = c < nch ? c : nch - 1;
+  const int cl = c < nl ? c : nl - 1;
+  const int cc = cl / LPC, hf = LPC == 2 ? (cl & 1) : 0;
+  auto load_row = [&](int64_t row) {
+    if constexpr (LPC == 2) return F::load_half(pa, row, cc, hf);
+    else return F::load(pa, row, cc);
+  };
   typename F::Chunk ch[R];
-  uint4 xr[F::SUB][MT][2];
+  uint4 xr[SUBL][MT][2];
   auto load_x = [&]() {
 #pragma unroll
-    for (int sub = 0; sub < F::SUB; ++sub)
+    for (int sub = 0; sub < SUBL; ++sub)
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const uint4* xp = reinterpret_cast<const uint4*>(xg + (int64_t)m * xs + cc * F::KPC + sub * 16);
+        const uint4* xp = reinterpret_cast<const uint4*>(xg + (int64_t)m * xs + cc * F::KPC + (hf + sub) * 16);
         xr[sub][m][0] = xp[0];
         xr[sub][m][1] = xp[1];
       }
   };
   if constexpr (R == 1) {
-    ch[0] = F::load(pa, row0, cc);
+    ch[0] = load_row(row0);
     load_x();
   } else {
     // the activations first, then the rows in order, so that row r's sums
     // wait only for the loads up to its own
     load_x();
 #pragma unroll
-    for (int r = 0; r < R; ++r) ch[r] = F::load(pa, row0 + r < N ? row0 + r : (int64_t)N - 1, cc);
+    for (int r = 0; r < R; ++r) ch[r] = load_row(row0 + r < N ? row0 + r : (int64_t)N - 1);
   }
   __builtin_amdgcn_sched_barrier(0);                   // every load above issues before any use below
   float acc[R][MT];
@@ -129,7 +144,7 @@ __global__ __launch_bounds__(R == 1 ? kRowsFmaMaxThreads : kRowsMultiMaxThreads)
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int sub = 0; sub < F::SUB; ++sub) {
+    for (int sub = 0; sub < SUBL; ++sub) {
       uint32_t w[8];
       F::deq16(ch[r], sub, w);
 #pragma unroll
@@ -142,14 +157,14 @@ __global__ __launch_bounds__(R == 1 ? kRowsFmaMaxThreads : kRowsMultiMaxThreads)
         acc[r][m] = t;
       }
     }
-  if (c >= nch) {
+  if (c >= nl) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nwaves = (nch + 63) >> 6;
+  const int nwaves = (nl + 63) >> 6;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     float sums[MT];
@@ -371,18 +386,18 @@ inline bool rows_shape_ok(int N, int M, int cus) {
   return M >= 1 && M <= 16 && N >= 1 && tiles * 2 < cus && rows_per_wg(N, cus) > 0;
 }
 
-// Workgroups of rows_fma_kernel<F, MT, R> of `threads` threads one CU holds
-// at once (its registers decide: the NVFP4 and W6 kernels at M >= 3 hold
-// fewer).
-template <class F, int MT, int R>
+// Workgroups of rows_fma_kernel<F, MT, R, LPC> of `threads` threads one CU
+// holds at once (its registers decide: the NVFP4 and W6 kernels at M >= 3
+// hold fewer).
+template <class F, int MT, int R, int LPC>
 int rows_fma_resident(int threads) {
   static int cache[kRowsMultiMaxThreads / 64 + 1];
   const int key = threads / 64;
   int occ = cache[key];
   if (occ <= 0) {
     const size_t lds = (size_t)key * R * MT * sizeof(float);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(rows_fma_kernel<F, MT, R>),
-                                                     threads, lds) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &occ, reinterpret_cast<const void*>(rows_fma_kernel<F, MT, R, LPC>), threads, lds) != hipSuccess ||
         occ < 1)
       occ = 1;
     cache[key] = occ;
@@ -390,12 +405,12 @@ int rows_fma_resident(int threads) {
   return occ;
 }
 
-template <class F, int R>
+template <class F, int R, int LPC>
 int rows_fma_resident_m(int M, int threads) {
-  return M == 1   ? rows_fma_resident<F, 1, R>(threads)
-         : M == 2 ? rows_fma_resident<F, 2, R>(threads)
-         : M == 3 ? rows_fma_resident<F, 3, R>(threads)
-                  : rows_fma_resident<F, 4, R>(threads);
+  return M == 1   ? rows_fma_resident<F, 1, R, LPC>(threads)
+         : M == 2 ? rows_fma_resident<F, 2, R, LPC>(threads)
+         : M == 3 ? rows_fma_resident<F, 3, R, LPC>(threads)
+                  : rows_fma_resident<F, 4, R, LPC>(threads);
 }
 
 // The fma kernel beyond few-rows shapes: wider matrices of short rows (the MTP
@@ -420,13 +435,13 @@ int rows_fma_resident_m(int M, int threads) {
 // M = 3, past the limit.
 constexpr int64_t kRowsFmaProductsPerCu = int64_t(1) << 17;
 
-template <class F>
+template <class F, int LPC>
 bool rows_fma_shape_ok(int N, int M, int threads, int cus) {
-  if (M < 1 || M > 4 || N < 1 || threads > kRowsFmaMaxThreads) return false;
+  if (M < 1 || M > 4 || N < 1 || threads > rows_fma_max_threads(1, LPC)) return false;
   if (rows_shape_ok(N, M, cus)) return true;
-  if ((int64_t)N * threads * M * F::KPC > kRowsFmaProductsPerCu * cus) return false;
-  if ((int64_t)N * (threads / 64) > 32 * (int64_t)cus) return false;
-  return N <= (int64_t)rows_fma_resident_m<F, 1>(M, threads) * cus;
+  if ((int64_t)N * threads * M * F::KPC / LPC > kRowsFmaProductsPerCu * cus) return false;
+  if ((int64_t)N * (threads / 64) / LPC > 32 * (int64_t)cus) return false;
+  return N <= (int64_t)rows_fma_resident_m<F, 1, LPC>(M, threads) * cus;
 }
 
 // Rows per workgroup R of the fma kernel for a matrix of M <= 4 activation
@@ -460,26 +475,26 @@ bool rows_fma_shape_ok(int N, int M, int threads, int cus) {
 // 7.2 at M = 1 / 2 against 7.6 / 7.8.  Larger matrices stay on the streaming
 // kernels or the MFMA core (W6 [8192 x 2560] at M = 3: 7.4 streaming against
 // 10.5 / 9.9 at R = 2 / 4).
-template <class F>
+template <class F, int LPC>
 int rows_fma_pick(int N, int M, int nch, int threads, int cus) {
   if (M < 1 || M > 4 || N < 1) return 0;
-  if (rows_shape_ok(N, M, cus)) return threads <= kRowsFmaMaxThreads ? 1 : 0;
+  if (rows_shape_ok(N, M, cus)) return threads <= rows_fma_max_threads(1, LPC) ? 1 : 0;
   const bool r2 = nch > 64 && threads <= kRowsMultiMaxThreads &&
-                  (N + 1) / 2 <= (int64_t)rows_fma_resident_m<F, 2>(M, threads) * cus;
+                  (N + 1) / 2 <= (int64_t)rows_fma_resident_m<F, 2, LPC>(M, threads) * cus;
   if (M >= 2 && N >= 8 * cus && r2) return 2;
-  if (rows_fma_shape_ok<F>(N, M, threads, cus)) return 1;
+  if (rows_fma_shape_ok<F, LPC>(N, M, threads, cus)) return 1;
   return r2 ? 2 : 0;
 }
 
-template <class F, int R>
+template <class F, int R, int LPC>
 inline bool rows_fma_launch(const RowsLaunch& a, int threads, hipStream_t st) {
   const size_t lds = (size_t)(threads / 64) * R * a.M * sizeof(float);
   const dim3 grid((unsigned)((a.N + R - 1) / R)), block((unsigned)threads);
   switch (a.M) {
-    case 1: hipLaunchKernelGGL((rows_fma_kernel<F, 1, R>), grid, block, lds, st, a); return true;
-    case 2: hipLaunchKernelGGL((rows_fma_kernel<F, 2, R>), grid, block, lds, st, a); return true;
-    case 3: hipLaunchKernelGGL((rows_fma_kernel<F, 3, R>), grid, block, lds, st, a); return true;
-    case 4: hipLaunchKernelGGL((rows_fma_kernel<F, 4, R>), grid, block, lds, st, a); return true;
+    case 1: hipLaunchKernelGGL((rows_fma_kernel<F, 1, R, LPC>), grid, block, lds, st, a); return true;
+    case 2: hipLaunchKernelGGL((rows_fma_kernel<F, 2, R, LPC>), grid, block, lds, st, a); return true;
+    case 3: hipLaunchKernelGGL((rows_fma_kernel<F, 3, R, LPC>), grid, block, lds, st, a); return true;
+    case 4: hipLaunchKernelGGL((rows_fma_kernel<F, 4, R, LPC>), grid, block, lds, st, a); return true;
   }
   return false;
 }
@@ -503,16 +518,17 @@ inline bool rows_launch_args(const GemvLaunch& p, int batch, int kpc, RowsLaunch
   return true;
 }
 
-template <class F>
+template <class F, int LPC>
 inline bool rows_fma_go(RowsLaunch& a, int R, int threads, hipStream_t st) {
   a.R = R;
   switch (R) {
-    case 1: return rows_fma_launch<F, 1>(a, threads, st);
-    case 2: return rows_fma_launch<F, 2>(a, threads, st);
-    case 4: return rows_fma_launch<F, 4>(a, threads, st);
+    case 1: return rows_fma_launch<F, 1, LPC>(a, threads, st);
+    case 2: return rows_fma_launch<F, 2, LPC>(a, threads, st);
+    case 4: return rows_fma_launch<F, 4, LPC>(a, threads, st);
   }
   return false;
 }
+
 
 // Launch a few-rows kernel when the call fits one: one matrix, no per-row
 // scale, strides within int32, and either the fma kernel (M <= 4, R rows per
@@ -520,16 +536,31 @@ inline bool rows_fma_go(RowsLaunch& a, int R, int threads, hipStream_t st) {
 // of at most 8 waves; false (nothing launched) otherwise, or when
 // FP4X_ROWS=0.  The split count of the call is a shape precondition only:
 // these kernels sum each row over its whole K inside one workgroup, in a
-// fixed order.
+// fixed order.  W6 and NVFP4 split each chunk over two lanes, measured
+// against one lane per chunk (us at M = 1 / 3): W6 [1280 x 2560] 3.3 / 3.8
+// against 3.4 / 4.5; [2560 x 640] 3.0 / 3.4 against 3.3 / 4.2; [640 x 2560]
+// 3.0 / 3.4 against 3.1 / 3.7; [4096 x 2560] 4.8 / 6.1 against 5.1 / 6.7;
+// [2560 x 6144] at M = 3 7.7 against 8.1 (at M = 1 5.6 against 5.4, so rows
+// of over 128 chunks keep one lane per chunk at M = 1); NVFP4 [2560 x 640]
+// 2.8 / 3.3 against 3.0 / 3.9; [4096 x 2560] 4.2 / 5.4 against 4.5 / 5.9.
 template <class F>
 bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
   RowsLaunch a;
   if (!rows_launch_args(p, batch, F::KPC, a)) return false;
   const int cus = device_cus();
   const int nch = p.pa.K / F::KPC;
-  const int threads = (nch + 63) / 64 * 64;
-  const int R = rows_fma_pick<F>(p.N, p.M, nch, threads, cus);
-  if (R) return rows_fma_go<F>(a, R, threads, st);
+  if constexpr (F::SUB == 2) {
+    // W6 and NVFP4 chunks (32 weights) split over two lanes: at M >= 2, and
+    // at M = 1 for rows of up to 128 chunks
+    if (p.M >= 2 || 2 * nch <= kRowsFmaMaxThreads) {
+      const int lanes = (2 * nch + 63) / 64 * 64;
+      const int R = rows_fma_pick<F, 2>(p.N, p.M, nch, lanes, cus);
+      if (R) return rows_fma_go<F, 2>(a, R, lanes, st);
+    }
+  }
+  const int lanes = (nch + 63) / 64 * 64;
+  const int R = rows_fma_pick<F, 1>(p.N, p.M, nch, lanes, cus);
+  if (R) return rows_fma_go<F, 1>(a, R, lanes, st);
   if (!rows_shape_ok(p.N, p.M, cus)) return false;
   RowsPlan pl;
   if (!rows_mfma_plan<F>(nch, p.M, pl)) return false;
@@ -555,9 +586,9 @@ bool launch_rows_wide(const GemvLaunch& p, hipStream_t st) {
   const int threads = (nch + 63) / 64 * 64;
   if (p.N < 16 * cus || p.N > 32 * cus || nch <= 64 || threads > kRowsMultiMaxThreads) return false;
   const int R = (p.N + 1) / 2 <= 8 * cus ? 2 : 4;
-  const int res = R == 2 ? rows_fma_resident_m<F, 2>(p.M, threads) : rows_fma_resident_m<F, 4>(p.M, threads);
+  const int res = R == 2 ? rows_fma_resident_m<F, 2, 1>(p.M, threads) : rows_fma_resident_m<F, 4, 1>(p.M, threads);
   if ((p.N + R - 1) / R > (int64_t)res * cus) return false;
-  return rows_fma_go<F>(a, R, threads, st);
+  return rows_fma_go<F, 1>(a, R, threads, st);
 }
 
 }  // namespace fp4x
