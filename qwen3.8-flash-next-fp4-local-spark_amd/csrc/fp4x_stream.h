@@ -1398,18 +1398,63 @@ __global__ __launch_bounds__(64 * T * KW) void dense_stream_kernel(GemvLaunch p)
 constexpr int kStreamKc = 2560;
 
 template <class U, int T, int KW, int D, int KC>
-bool launch_dense_stream_k(const GemvLaunch& p, size_t lds, unsigned gx, hipStream_t st) {
-  auto kern = dense_stream_kernel<U, T, KW, D, KC>;
+bool dense_stream_ready() {
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024) != hipSuccess) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(dense_stream_kernel<U, T, KW, D, KC>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
       (void)hipGetLastError();
       return false;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3(gx), dim3(64 * T * KW), lds, st, p);
+  return true;
+}
+
+// Workgroups of dense_stream_kernel<U, T, KW, D, KC> with `lds` bytes of LDS
+// one CU holds at once, at most 2 (cached per LDS size).
+template <class U, int T, int KW, int D, int KC>
+int dense_stream_resident(size_t lds) {
+  static size_t keys[16];
+  static int vals[16];
+  for (int i = 0; i < 16 && keys[i]; ++i)
+    if (keys[i] == lds) return vals[i];
+  int occ = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &occ, reinterpret_cast<const void*>(dense_stream_kernel<U, T, KW, D, KC>), 64 * T * KW, lds) !=
+          hipSuccess ||
+      occ < 1) {
+    (void)hipGetLastError();
+    occ = 1;
+  }
+  occ = occ < 2 ? occ : 2;
+  for (int i = 0; i < 16; ++i)
+    if (!keys[i]) {
+      keys[i] = lds;
+      vals[i] = occ;
+      break;
+    }
+  return occ;
+}
+
+template <class U, int T, int KW, int D, int KC>
+bool launch_dense_stream_k(GemvLaunch p, int64_t items, size_t lds, bool batched, hipStream_t st) {
+  if (!dense_stream_ready<U, T, KW, D, KC>()) return false;
+  // One round of T tiles per workgroup where two workgroups fit a CU (a
+  // single matrix), instead of rounds of T tiles in one workgroup per CU:
+  // the second workgroup's loads overlap the first's dequant and epilogue.
+  // Measured as graph replays, us at M = 1 / 3: W6 [13312 x 2560] 10.0 /
+  // 10.3 against 10.7-11.1 / 11.0; W6 [16384 x 2560] 10.6 / 11.1 against
+  // 11.0 / 11.4; MXFP8 [8192 x 2560] 6.4 / 6.8 against 6.3-6.5 / 7.2;
+  // MXFP8 [16384 x 2560] 9.9 / 10.2 against 10.0-10.3 / 10.8 (three rounds
+  // of one tile, or one workgroup per tile when more than two would share a
+  // CU, were slower).
+  const int64_t cus = device_cus();
+  const int occ = batched ? 1 : dense_stream_resident<U, T, KW, D, KC>(lds);
+  const int64_t per = (items + cus * T * occ - 1) / (cus * T * occ) * T;
+  p.per_wg = (int)per;
+  const unsigned gx = (unsigned)((items + per - 1) / per);
+  hipLaunchKernelGGL((dense_stream_kernel<U, T, KW, D, KC>), dim3(gx), dim3(64 * T * KW), lds, st, p);
   return true;
 }
 
@@ -1438,11 +1483,11 @@ bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st, int64
                      (size_t)T * KW * D * U::BYTES;
   if (lds > 160 * 1024) return false;
   p.batch = batch;
-  p.per_wg = (int)per;
   p.xbufs = (int)span;
-  const unsigned gx = (unsigned)((items + per - 1) / per);
-  return K == kStreamKc ? launch_dense_stream_k<U, T, KW, D, kStreamKc>(p, lds, gx, st)
-                        : launch_dense_stream_k<U, T, KW, D, 0>(p, lds, gx, st);
+  // layer-batched calls keep one workgroup per CU (their activation buffers
+  // are planned for that many items per workgroup)
+  return K == kStreamKc ? launch_dense_stream_k<U, T, KW, D, kStreamKc>(p, items, lds, batch > 1, st)
+                        : launch_dense_stream_k<U, T, KW, D, 0>(p, items, lds, batch > 1, st);
 }
 
 // Shapes measured as graph replays (T slots, KW waves per tile, D units per

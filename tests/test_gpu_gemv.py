@@ -241,10 +241,20 @@ def test_dense_stream(gpu, F, fmt, slots, parts, env, M, tail, monkeypatch):
     workgroup, a ring of 2 units of 256 K per wave), W6 matrices of at least 2
     (2 slots x 2 waves, 2 units of 256 K) and MXFP8 matrices of at least 1 (1
     slot x 10 waves, 2 units of 128 K) take the streaming kernel: fp32 sums within the MFMA
-    bound of the exact sum, as the core's are; a 40-row tail gives workgroups
-    of two rounds whose last round has idle slots.  K = 2560 runs the
-    instantiation compiled for that row length."""
+    bound of the exact sum, as the core's are; a 40-row tail leaves idle slots
+    in the last workgroup (and, where two workgroups fit a CU, a second
+    workgroup on some CUs).  K = 2560 runs the instantiation compiled for that
+    row length."""
     _dense_stream_case(F, fmt, slots, parts, env, M, tail, 2560, monkeypatch)
+
+
+@pytest.mark.parametrize("fmt,slots,parts,env", [("nv4", 8, 2, "FP4X_NV4_STREAM"), ("w6", 4, 2, "FP4X_W6_STREAM"),
+                                                   ("mx8", 2, 10, "FP4X_MX8_STREAM")])
+def test_dense_stream_rounds(gpu, F, fmt, slots, parts, env, monkeypatch):
+    """Matrices past two workgroups per CU of one round each: workgroups of two
+    rounds of T tiles, the last one's second round partly idle (a 40-row
+    tail), against the same bound."""
+    _dense_stream_case(F, fmt, slots, parts, env, 3, 40, 2560, monkeypatch)
 
 
 @pytest.mark.parametrize("M", [1, 3])
