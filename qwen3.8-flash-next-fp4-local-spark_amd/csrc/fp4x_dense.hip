@@ -21,6 +21,8 @@ bool launch_int2_stream_e4m3(GemvLaunch p, hipStream_t st);
 bool launch_nv4_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_w6_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_mx8_stream_entry(GemvLaunch p, hipStream_t st);
+bool launch_nv4_stream_one_entry(GemvLaunch p, hipStream_t st);
+bool launch_w6_stream_one_entry(GemvLaunch p, hipStream_t st);
 bool launch_w8_single_stream_f16(GemvLaunch p, hipStream_t st);
 bool launch_w8_single_stream_f32(GemvLaunch p, hipStream_t st);
 int topk_check(const void* logits, int dtype, int64_t stride, int M, int V, int C, void* workspace,
@@ -276,7 +278,8 @@ int fp4x_w6_linear(const void* x, int64_t x_stride, const void* L, const void* H
   p.pa.w1 = static_cast<const uint8_t*>(H);
   p.pa.s = static_cast<const uint8_t*>(S);
   if (launch_w6_stream_entry(p, (hipStream_t)stream)) return check_launch("w6_stream");     // many tiles
-  if (launch_rows_gemv<FmtW6>(p, 1, (hipStream_t)stream)) return check_launch("w6_rows");    // few rows
+  if (launch_rows_gemv<FmtW6>(p, 1, (hipStream_t)stream)) return check_launch("w6_rows");    // fewer rows
+  if (launch_w6_stream_one_entry(p, (hipStream_t)stream)) return check_launch("w6_stream");  // 1-2 tiles per CU
   return launch_gemv_mfma<FmtW6, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
@@ -291,7 +294,8 @@ int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* 
   p.pa.s = static_cast<const uint8_t*>(S);
   p.gs = gs;
   if (launch_nv4_stream_entry(p, (hipStream_t)stream)) return check_launch("nv4_stream");   // many tiles
-  if (launch_rows_gemv<FmtNV4>(p, 1, (hipStream_t)stream)) return check_launch("nv4_rows");  // few rows
+  if (launch_rows_gemv<FmtNV4>(p, 1, (hipStream_t)stream)) return check_launch("nv4_rows");  // fewer rows
+  if (launch_nv4_stream_one_entry(p, (hipStream_t)stream)) return check_launch("nv4_stream"); // 1-2 tiles per CU
   return launch_gemv_mfma<FmtNV4, EpiStore>(p, 1, (hipStream_t)stream);
 }
 

@@ -5,4 +5,5 @@
 namespace fp4x {
 template int launch_gemv_mfma<FmtNV4, EpiStore>(const GemvLaunch&, int, hipStream_t);
 bool launch_nv4_stream_entry(GemvLaunch p, hipStream_t st) { return launch_nv4_stream(p, st); }
+bool launch_nv4_stream_one_entry(GemvLaunch p, hipStream_t st) { return launch_nv4_stream_one(p, st); }
 }  // namespace fp4x

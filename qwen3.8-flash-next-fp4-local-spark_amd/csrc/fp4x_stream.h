@@ -1496,9 +1496,34 @@ bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st, int64
 // 8.6 / 9.8; (4, 1, 3) 8.8 / 8.7 / 10.1; (2, 5, 2) 8.7 / 9.4 / 10.3.  With
 // 128-K units (two loads each): (4, 2, 3) 8.8 / 8.9 / 9.9; (4, 4, 3) 9.5 / 9.4
 // / 10.6; (2, 4, 3) 9.0 / 9.2 / 10.1; (2, 5, 2) 9.1 / 9.5 / 10.5; (1, 10, 2)
-// 10.2 / 10.8 / 11.9.  The core: 10.5 / 11.1 / 14.7.
+// 10.2 / 10.8 / 11.9.  The core: 10.5 / 11.1 / 14.7.  With two workgroups
+// of one round per CU (2, 2, 2) is faster at M <= 5 (us at M = 1 / 2 / 3 / 4
+// / 5 / 8: 7.3 / 7.4 / 7.6 / 7.8 / 8.0 / 8.5 against 7.7 / 7.7 / 7.8 / 8.0 /
+// 8.1 / 8.3; M = 16: 10.0 against 8.9), and it takes matrices of 2 to 4
+// tiles per CU, which (4, 2, 2) cannot: [8192 x 2560] 5.7 / 5.7 / 5.9 / 6.2 /
+// 6.1 / 6.4 against 5.8 / 7.1 / 8.0 / 8.6 / 9.4 / 10.0 on the few-rows kernel
+// (M <= 2) or the core; [13312 x 2560] 7.0 / 7.2 / 7.4 / 7.6 / 7.8 / 8.1
+// against the core's 10.0 / 10.4 / 10.9 / 11.9 / 12.8 / 13.3.
 inline bool launch_nv4_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamNV4, 4, 2, 2>(p, 1, switches().nv4_stream, st);
+  const bool on = switches().nv4_stream;
+  const int64_t tiles = (p.N + 15) / 16;
+  if (p.M > 5 && tiles >= 4 * (int64_t)device_cus() && launch_dense_stream<StreamNV4, 4, 2, 2>(p, 1, on, st))
+    return true;
+  return launch_dense_stream<StreamNV4, 2, 2, 2>(p, 1, on, st);
+}
+// Matrices of 1 to 2 tiles per CU that the few-rows kernel does not take
+// (M >= 5, or past its limits): one tile slot per workgroup, two waves, two
+// workgroups per CU.  Us at M = 1 / 3 / 4 / 8 against the path these shapes
+// take without it: NVFP4 [4096 x 2560] 5.0 / 5.5 / 5.8 / 6.3 against 4.1 /
+// 5.4 / 6.0 / 7.9 (the few-rows kernel at M <= 4, then the core); [6144 x
+// 2560] 6.5 / 6.9 / 7.2 / 7.7 against 5.1 / 7.3 / 8.4 / 9.9; W6 [4096 x
+// 2560] 6.2 / 6.7 / 7.0 / 7.5 against 4.8 / 6.1 / 6.6 / 9.3; [6144 x 2560]
+// 8.7 / 9.1 / 9.3 / 9.8 against 6.4 / 9.8 / 10.5 / 12.3.
+inline bool launch_nv4_stream_one(GemvLaunch p, hipStream_t st) {
+  return launch_dense_stream<StreamNV4, 1, 2, 2>(p, 1, switches().nv4_stream, st);
+}
+inline bool launch_w6_stream_one(GemvLaunch p, hipStream_t st) {
+  return launch_dense_stream<StreamW6, 1, 2, 2>(p, 1, switches().w6_stream, st);
 }
 // MXFP8 4096 x 2560 (256 tiles, one per CU; 10 waves of 2 units put a tile's
 // 46 KB in flight at once): (1, 10, 2) 5.1 / 5.8 / 6.6; (1, 5, 3) 5.2 / 6.0 /

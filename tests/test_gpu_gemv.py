@@ -237,10 +237,11 @@ def test_gemv_tile_groups(gpu, F, fmt, M):
 @pytest.mark.parametrize("fmt,slots,parts,env", [("nv4", 4, 2, "FP4X_NV4_STREAM"), ("w6", 2, 2, "FP4X_W6_STREAM"),
                                                    ("mx8", 1, 10, "FP4X_MX8_STREAM")])
 def test_dense_stream(gpu, F, fmt, slots, parts, env, M, tail, monkeypatch):
-    """NVFP4 matrices of at least 4 tiles per CU (4 tile slots x 2 waves per
-    workgroup, a ring of 2 units of 256 K per wave), W6 matrices of at least 2
-    (2 slots x 2 waves, 2 units of 256 K) and MXFP8 matrices of at least 1 (1
-    slot x 10 waves, 2 units of 128 K) take the streaming kernel: fp32 sums within the MFMA
+    """NVFP4 matrices of at least 4 tiles per CU (2 tile slots x 2 waves per
+    workgroup at M <= 5, 4 x 2 above, a ring of 2 units of 256 K per wave), W6
+    matrices of at least 2 (2 slots x 2 waves, 2 units of 256 K) and MXFP8
+    matrices of at least 1 (1 slot x 10 waves, 2 units of 128 K) take the
+    streaming kernel: fp32 sums within the MFMA
     bound of the exact sum, as the core's are; a 40-row tail leaves idle slots
     in the last workgroup (and, where two workgroups fit a CU, a second
     workgroup on some CUs).  K = 2560 runs the instantiation compiled for that
@@ -266,10 +267,24 @@ def test_dense_stream_other_k(gpu, F, fmt, slots, parts, env, M, monkeypatch):
     _dense_stream_case(F, fmt, slots, parts, env, M, 40, 5120, monkeypatch)
 
 
+@pytest.mark.parametrize("fmt,slots,M,env", [
+    ("nv4", 2, 3, "FP4X_NV4_STREAM"),    # 2 to 4 tiles per CU: 2 slots x 2 waves
+    ("nv4", 2, 8, "FP4X_NV4_STREAM"),
+    ("nv4", 1, 8, "FP4X_NV4_STREAM"),    # 1 to 2 tiles per CU: one slot, two workgroups per CU
+    ("w6", 1, 8, "FP4X_W6_STREAM"),
+    ("w6", 1.5, 3, "FP4X_W6_STREAM"),
+])
+def test_dense_stream_mid(gpu, F, fmt, slots, M, env, monkeypatch):
+    """NVFP4 matrices of 2 to 4 tiles per CU, and W6 / NVFP4 matrices of 1 to 2
+    tiles per CU that the few-rows kernel leaves (M >= 5, or past its limits)
+    stream with fewer tile slots per workgroup, against the same bound."""
+    _dense_stream_case(F, fmt, slots, 2, env, M, 40, 2560, monkeypatch)
+
+
 def _dense_stream_case(F, fmt, slots, parts, env, M, tail, k, monkeypatch):
-    rng = np.random.default_rng(500 + M + tail + slots + k)
+    rng = np.random.default_rng(500 + M + tail + int(2 * slots) + k)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    n = 16 * slots * cus + tail
+    n = int(16 * slots * cus) + tail
     planes, w_op, gs = prep(fmt, rng, n, k)
     x, _ = act(rng, M, k)
     with path_switch(monkeypatch, "FP4X_ROWS"):        # MXFP8 at M <= 2 takes the few-rows kernel first
