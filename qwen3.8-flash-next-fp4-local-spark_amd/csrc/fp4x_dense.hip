@@ -23,6 +23,9 @@ bool launch_w6_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_mx8_stream_entry(GemvLaunch p, hipStream_t st);
 bool launch_nv4_stream_one_entry(GemvLaunch p, hipStream_t st);
 bool launch_w6_stream_one_entry(GemvLaunch p, hipStream_t st);
+bool launch_w6_stream_tile_entry(GemvLaunch p, hipStream_t st);
+bool launch_nv4_stream_tile_entry(GemvLaunch p, hipStream_t st);
+bool launch_mx8_stream_tile_entry(GemvLaunch p, hipStream_t st);
 bool launch_w8_single_stream_f16(GemvLaunch p, hipStream_t st);
 bool launch_w8_single_stream_f32(GemvLaunch p, hipStream_t st);
 int topk_check(const void* logits, int dtype, int64_t stride, int M, int V, int C, void* workspace,
@@ -206,6 +209,7 @@ int fp4x_mx8_linear(const void* x, int64_t x_stride, const void* w, const void* 
   if (launch_rows_wide<FmtMX8>(p, (hipStream_t)stream)) return check_launch("mx8_rows");    // many rows, M <= 2
   if (launch_mx8_stream_entry(p, (hipStream_t)stream)) return check_launch("mx8_stream");   // many tiles
   if (launch_rows_gemv<FmtMX8>(p, 1, (hipStream_t)stream)) return check_launch("mx8_rows");  // fewer rows
+  if (launch_mx8_stream_tile_entry(p, (hipStream_t)stream)) return check_launch("mx8_stream"); // 1/2-1 tile per CU
   return launch_gemv_mfma<FmtMX8, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
@@ -280,6 +284,7 @@ int fp4x_w6_linear(const void* x, int64_t x_stride, const void* L, const void* H
   if (launch_w6_stream_entry(p, (hipStream_t)stream)) return check_launch("w6_stream");     // many tiles
   if (launch_rows_gemv<FmtW6>(p, 1, (hipStream_t)stream)) return check_launch("w6_rows");    // fewer rows
   if (launch_w6_stream_one_entry(p, (hipStream_t)stream)) return check_launch("w6_stream");  // 1-2 tiles per CU
+  if (launch_w6_stream_tile_entry(p, (hipStream_t)stream)) return check_launch("w6_stream"); // 1/2-1 tile per CU
   return launch_gemv_mfma<FmtW6, EpiStore>(p, 1, (hipStream_t)stream);
 }
 
@@ -296,6 +301,7 @@ int fp4x_nv4_linear(const void* x, int64_t x_stride, const void* P, const void* 
   if (launch_nv4_stream_entry(p, (hipStream_t)stream)) return check_launch("nv4_stream");   // many tiles
   if (launch_rows_gemv<FmtNV4>(p, 1, (hipStream_t)stream)) return check_launch("nv4_rows");  // fewer rows
   if (launch_nv4_stream_one_entry(p, (hipStream_t)stream)) return check_launch("nv4_stream"); // 1-2 tiles per CU
+  if (launch_nv4_stream_tile_entry(p, (hipStream_t)stream)) return check_launch("nv4_stream"); // 1/2-1 tile per CU
   return launch_gemv_mfma<FmtNV4, EpiStore>(p, 1, (hipStream_t)stream);
 }
 

@@ -5,5 +5,8 @@
 namespace fp4x {
 template int launch_gemv_mfma<FmtW6, EpiStore>(const GemvLaunch&, int, hipStream_t);
 bool launch_w6_stream_entry(GemvLaunch p, hipStream_t st) { return launch_w6_stream(p, st); }
+bool launch_w6_stream_tile_entry(GemvLaunch p, hipStream_t st) {
+  return launch_stream_tile_per_wg<StreamW6>(p, switches().w6_stream, st);
+}
 bool launch_w6_stream_one_entry(GemvLaunch p, hipStream_t st) { return launch_w6_stream_one(p, st); }
 }  // namespace fp4x

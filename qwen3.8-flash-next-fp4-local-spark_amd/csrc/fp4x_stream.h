@@ -1525,6 +1525,25 @@ inline bool launch_nv4_stream_one(GemvLaunch p, hipStream_t st) {
 inline bool launch_w6_stream_one(GemvLaunch p, hipStream_t st) {
   return launch_dense_stream<StreamW6, 1, 2, 2>(p, 1, switches().w6_stream, st);
 }
+// Matrices of half a tile to one tile per CU that the few-rows kernel does
+// not take (M >= 5): one tile per workgroup, its K over 8 waves (K a multiple
+// of 8 units: 6144) or 5 (2560), two units of ring each.  Us at M = 5 / 8
+// (/ 16) against the MFMA core: W6 [2560 x 6144] 8.6 / 9.0 against 16.5 /
+// 16.7 (12 waves: 9.2 / -, the activations of 8 rows then overflow LDS; 6:
+// 9.0 / 9.7); NVFP4 [2560 x 6144] 6.8 / 7.3 against 12.9 / 13.5; MXFP8 [2560
+// x 6144] 7.5 / 8.0 against 13.9 / 15.3; W6 [2048 x 2560] 5.5 / 5.5 / 5.9
+// against 8.3 / 8.9 / 10.9 (10 waves: 5.8 / 5.9 / 6.2; 2: 6.7 / 7.2 / 8.3);
+// NVFP4 [2048 x 2560] 4.5 / 4.6 / 4.9 against 6.9 / 7.6 / 9.7; MXFP8 [2048 x
+// 2560] 4.8 / 4.9 / 5.2 against 7.0 / 7.4 / 8.5.
+template <class U>
+inline bool launch_stream_tile_per_wg(const GemvLaunch& p, bool on, hipStream_t st) {
+  const int64_t tiles = (p.N + 15) / 16, cus = device_cus();
+  if (2 * tiles < cus) return false;
+  const int units = p.pa.K / U::UK;
+  if (units % 8 == 0 && launch_dense_stream<U, 1, 8, 2>(p, 1, on, st, cus / 2)) return true;
+  if (units % 5 == 0 && launch_dense_stream<U, 1, 5, 2>(p, 1, on, st, cus / 2)) return true;
+  return false;
+}
 // MXFP8 4096 x 2560 (256 tiles, one per CU; 10 waves of 2 units put a tile's
 // 46 KB in flight at once): (1, 10, 2) 5.1 / 5.8 / 6.6; (1, 5, 3) 5.2 / 6.0 /
 // 7.0; (1, 5, 4) 5.2 / 5.6 / 6.9; (1, 4, 5) 5.3 / 5.6 / 7.0 (the core: 6.5 /

@@ -281,6 +281,21 @@ def test_dense_stream_mid(gpu, F, fmt, slots, M, env, monkeypatch):
     _dense_stream_case(F, fmt, slots, 2, env, M, 40, 2560, monkeypatch)
 
 
+@pytest.mark.parametrize("fmt,slots,k,M,parts,env", [
+    ("w6", 0.625, 6144, 5, 8, "FP4X_W6_STREAM"),      # [2600 x 6144]: 8 waves of 3 units per tile
+    ("nv4", 0.625, 6144, 8, 8, "FP4X_NV4_STREAM"),
+    ("mx8", 0.625, 6144, 5, 8, "FP4X_MX8_STREAM"),    # 8 waves of 6 128-K units
+    ("w6", 0.5, 2560, 16, 5, "FP4X_W6_STREAM"),       # [2088 x 2560]: 5 waves of 2 units
+    ("nv4", 0.5, 2560, 5, 5, "FP4X_NV4_STREAM"),
+    ("mx8", 0.5, 2560, 8, 5, "FP4X_MX8_STREAM"),
+])
+def test_dense_stream_tile_per_workgroup(gpu, F, fmt, slots, k, M, parts, env, monkeypatch):
+    """Matrices of half a tile to one tile per CU at M >= 5 (the few-rows kernel
+    takes M <= 4): one tile per workgroup, its K over `parts` waves, against
+    the same bound."""
+    _dense_stream_case(F, fmt, slots, parts, env, M, 40, k, monkeypatch)
+
+
 def _dense_stream_case(F, fmt, slots, parts, env, M, tail, k, monkeypatch):
     rng = np.random.default_rng(500 + M + tail + int(2 * slots) + k)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
