@@ -1573,7 +1573,14 @@ inline bool launch_w8_single_stream(const GemvLaunch& p, hipStream_t st) {
   if (tiles >= 4 * cus) return launch_dense_stream<U, 4, 2, 2>(p, 1, on, st);
   if (tiles >= 2 * cus) return launch_dense_stream<U, 2, 2, 2>(p, 1, on, st);
   if (2 * tiles < cus) return false;
-  if (units % 12 == 0) return launch_dense_stream<U, 1, 12, 2>(p, 1, on, st, cus / 2);
+  if (units % 12 == 0) {
+    // K = 6144: 12 waves while the activations leave LDS room for their
+    // rings (M <= 3), then 8 and 4 (us at M = 5 / 8, fp32 scales: 8.9 / - and
+    // - / 10.6 against the MFMA core's 14.6 / 15.2; 6 waves at M = 8: 11.3)
+    if (launch_dense_stream<U, 1, 12, 2>(p, 1, on, st, cus / 2)) return true;
+    if (launch_dense_stream<U, 1, 8, 2>(p, 1, on, st, cus / 2)) return true;
+    return launch_dense_stream<U, 1, 4, 2>(p, 1, on, st, cus / 2);
+  }
   if (units % 10 == 0) return launch_dense_stream<U, 1, 5, 2>(p, 1, on, st, cus / 2);
   if (units % 8 == 0) return launch_dense_stream<U, 1, 4, 2>(p, 1, on, st, cus / 2);
   return false;

@@ -325,6 +325,8 @@ def _dense_stream_case(F, fmt, slots, parts, env, M, tail, k, monkeypatch):
     ((1, 40), 2560, 3, np.float32, 5),    # one tile per workgroup, 5 waves of 2 units
     ((1, 0), 2560, 16, np.float16, 5),
     (2560, 6144, 3, np.float32, 12),       # the MTP attention output: 12 waves of 2 units
+    (2560, 6144, 5, np.float32, 8),        # its activations leave room for 8 waves of 3 units
+    (2560, 6144, 8, np.float16, 4),        # ... and for 4 waves of 6 units
     (2048, 4096, 5, np.float16, 4),        # K = 4096 (run-time K): 4 waves of 4 units
 ])
 def test_w8_single_stream(gpu, F, case, monkeypatch):
