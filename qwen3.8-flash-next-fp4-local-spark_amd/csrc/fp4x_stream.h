@@ -1547,9 +1547,15 @@ inline bool launch_stream_tile_per_wg(const GemvLaunch& p, bool on, hipStream_t 
 // MXFP8 4096 x 2560 (256 tiles, one per CU; 10 waves of 2 units put a tile's
 // 46 KB in flight at once): (1, 10, 2) 5.1 / 5.8 / 6.6; (1, 5, 3) 5.2 / 6.0 /
 // 7.0; (1, 5, 4) 5.2 / 5.6 / 6.9; (1, 4, 5) 5.3 / 5.6 / 7.0 (the core: 6.5 /
-// 6.8 / 8.7).
+// 6.8 / 8.7).  Since the K = 2560 instantiation and two workgroups per CU,
+// 5 waves of 4 units are faster up to one tile per CU and at M <= 3: 4096 x
+// 2560 at M = 3 / 16 5.0 / 5.5 against 5.4 / 5.9; 16384 x 2560 at M = 1 / 3
+// 9.7 / 9.9 against 10.0 / 10.2, but at M = 16 13.3 against 11.7.
 inline bool launch_mx8_stream(GemvLaunch p, hipStream_t st) {
-  return launch_dense_stream<StreamMX8, 1, 10, 2>(p, 1, switches().mx8_stream, st);
+  const bool on = switches().mx8_stream;
+  if ((p.M <= 3 || (p.N + 15) / 16 <= device_cus()) && launch_dense_stream<StreamMX8, 1, 5, 2>(p, 1, on, st))
+    return true;
+  return launch_dense_stream<StreamMX8, 1, 10, 2>(p, 1, on, st);
 }
 // W6 8192 x 2560 (512 tiles, two per CU), 256-K units: (2, 2, 2) 7.9 / 8.2 /
 // 9.5; (2, 2, 3) 8.1 / 8.3 / 9.6; (2, 2, 4) 8.5 / 8.8 / 10.0; (2, 5, 2) 8.9 /
