@@ -281,6 +281,7 @@ int fp4x_w6_linear(const void* x, int64_t x_stride, const void* L, const void* H
   p.pa.w0 = static_cast<const uint8_t*>(L);
   p.pa.w1 = static_cast<const uint8_t*>(H);
   p.pa.s = static_cast<const uint8_t*>(S);
+  if (launch_rows_wide<FmtW6>(p, (hipStream_t)stream)) return check_launch("w6_rows");       // many rows, M = 1
   if (launch_w6_stream_entry(p, (hipStream_t)stream)) return check_launch("w6_stream");     // many tiles
   if (launch_rows_gemv<FmtW6>(p, 1, (hipStream_t)stream)) return check_launch("w6_rows");    // fewer rows
   if (launch_w6_stream_one_entry(p, (hipStream_t)stream)) return check_launch("w6_stream");  // 1-2 tiles per CU

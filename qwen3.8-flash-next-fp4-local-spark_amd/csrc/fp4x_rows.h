@@ -33,6 +33,7 @@
 // (5.6 against 6.8 us).
 #pragma once
 #include "fp4x_mfma.h"
+#include <type_traits>
 
 namespace fp4x {
 
@@ -577,9 +578,23 @@ bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
 // 9.4 / 9.6 against 9.3 / 9.4, [16384 x 2560] 10.3 / 10.9 against 10.3 /
 // 10.6), and at M = 3 the streaming kernel is as fast or faster (5.4 against
 // 5.6 at [4096 x 2560]).
+//
+// W6 at M = 1 from 32 to 52 rows per CU (shapes its streaming kernel takes):
+// 2 rows per workgroup with two lanes per chunk, in as many rounds as it
+// takes, ahead of the streaming kernel (us, two runs: [8192 x 2560] 6.9-7.1
+// against 7.2; [10240 x 2560] 7.7-8.2 against 9.6; [13312 x 2560] 9.6-9.9
+// against 9.9; [16384 x 2560] 11.4 against 10.4-11.0, so larger matrices
+// stream).
 template <class F>
 bool launch_rows_wide(const GemvLaunch& p, hipStream_t st) {
   RowsLaunch a;
+  if constexpr (std::is_same<F, FmtW6>::value) {
+    if (p.M != 1 || !rows_launch_args(p, 1, F::KPC, a)) return false;
+    const int cus = device_cus();
+    const int lanes = (2 * (p.pa.K / F::KPC) + 63) / 64 * 64;
+    if (p.N < 32 * cus || p.N > 52 * cus || lanes > kRowsMultiMaxThreads) return false;
+    return rows_fma_go<F, 2>(a, 2, lanes, st);
+  }
   if (p.M < 1 || p.M > 2 || !rows_launch_args(p, 1, F::KPC, a)) return false;
   const int cus = device_cus();
   const int nch = p.pa.K / F::KPC;

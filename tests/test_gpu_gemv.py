@@ -509,6 +509,30 @@ def test_rows_gemv_multi(gpu, F, fmt, rows, K, M, monkeypatch):
     assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
 
 
+@pytest.mark.parametrize("rows", [(32, 8), (52, 0)])
+def test_rows_w6_wide(gpu, F, rows, monkeypatch):
+    """W6 at M = 1 with 32 to 52 rows per CU takes the few-rows kernel (2 rows
+    per workgroup, two lanes per chunk, several rounds) ahead of the streaming
+    kernel: the same checks as test_rows_gemv_multi."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    N, K, M = rows[0] * cus + rows[1], 2560, 1
+    rng = np.random.default_rng(4700 + N)
+    planes, w_op, gs = prep("w6", rng, N, K)
+    x, _ = act(rng, M, K)
+    xd = bf16_dev(x)
+    print(f"w6 N={N} K={K} M={M}", flush=True)
+    y = to_f32(run(F, "w6", xd, planes, 1, torch.float32))
+    with path_switch(monkeypatch, "FP4X_ROWS"):
+        y_other = to_f32(run(F, "w6", xd, planes, 1, torch.float32))
+    assert not np.array_equal(y.view(np.uint32), y_other.view(np.uint32)), "few-rows kernel not taken"
+    exact = ordered.exact_sum(x, w_op)
+    for got, parts in ((y, 1), (y_other, 2)):
+        bound = ordered.mfma_bound(x, w_op, parts)
+        assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
+    assert_tol(y, og.matmul_f32(x, w_op), what=f"w6 wide rows N={N}")
+    assert np.array_equal(y.view(np.uint32), to_f32(run(F, "w6", xd, planes, 1, torch.float32)).view(np.uint32))
+
+
 def test_w8_fp16_scales_and_layers(gpu, F):
     rng = np.random.default_rng(9)
     Ly, n, k, M = 6, 512, 2560, 3
