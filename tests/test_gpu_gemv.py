@@ -414,6 +414,32 @@ def test_gemv_out_dtypes_and_strided_x(gpu, F):
         assert_tol(to_f32(y), ref, what=str(dt))
 
 
+@pytest.mark.parametrize("fmt,rows,k,M", [
+    ("w6", (10, 0), 6144, 3),      # few-rows kernel, 2 rows per workgroup, two lanes per chunk
+    ("mx8", (10, 0), 6144, 1),     # few-rows kernel, 2 rows per workgroup, rows of 384 chunks
+    ("w6", (32, 8), 2560, 1),      # W6 ahead of its streaming kernel
+    ("mx8", (16, 0), 2560, 3),     # streaming, 5 waves per tile
+    ("nv4", (32, 40), 2560, 3),    # streaming, 2 slots, two workgroups per CU
+    ("w6", (10, 0), 6144, 5),      # one tile per workgroup, 8 waves
+    ("w8", (52, 0), 2560, 3),      # W8 single-matrix streaming, 2 slots
+])
+def test_gemv_strided_x_paths(gpu, F, fmt, rows, k, M):
+    """Activations as an offset column slice of a wider tensor (row stride K +
+    512, 16-byte aligned) on each dispatch path: the same results as from a
+    contiguous copy, bit for bit, and within the tolerance of the oracle."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n = rows[0] * cus + rows[1]
+    rng = np.random.default_rng(6100 + n + k + M)
+    planes, w_op, gs = prep(fmt, rng, n, k)
+    x, _ = act(rng, M, k + 512)
+    wide = bf16_dev(x)
+    xt = wide[:, 256:256 + k]                        # row stride k + 512, offset 512 bytes
+    y = to_f32(run(F, fmt, xt, planes, 1, torch.float32))
+    y_c = to_f32(run(F, fmt, xt.contiguous(), planes, 1, torch.float32))
+    assert np.array_equal(y.view(np.uint32), y_c.view(np.uint32))
+    assert_tol(y, og.matmul_f32(x[:, 256:256 + k], w_op) * np.float32(gs), what=f"{fmt} strided N={n} M={M}")
+
+
 def test_gemv_shape_errors(gpu, F):
     rng = np.random.default_rng(6)
     planes, _, _ = prep("mx8", rng, 64, 512)
