@@ -333,19 +333,14 @@ static int int2_coarse(const void* x, int64_t x_stride, const void* P, const voi
   p.smax = smax;
   p.smax_stride = smax_stride;
   if (fmt == FP4X_FMT_INT2_F16) {
-    if (G == 16) {
-      if (launch_int2_stream_f16(p, st)) {                 // large heads
-        rc = check_launch("int2_stream");
-        return rc ? rc : (smax ? 1 : 0);
-      }
-      p.smax = nullptr;
-      rc = launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(p, 1, st);
-    } else {
-      p.smax = nullptr;
-      rc = G == 32 ? launch_gemv_mfma<FmtInt2<false, 32>, EpiStore>(p, 1, st)
-                   : launch_gemv_mfma<FmtInt2<false, 0>, EpiStore>(p, 1, st);
+    if ((G == 16 || G == 32) && launch_int2_stream_f16(p, st)) {   // large heads
+      rc = check_launch("int2_stream");
+      return rc ? rc : (smax ? 1 : 0);
     }
-    return rc;
+    p.smax = nullptr;
+    return G == 16   ? launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(p, 1, st)
+           : G == 32 ? launch_gemv_mfma<FmtInt2<false, 32>, EpiStore>(p, 1, st)
+                     : launch_gemv_mfma<FmtInt2<false, 0>, EpiStore>(p, 1, st);
   }
   if (G == 16 && launch_int2_stream_e4m3(p, st)) {     // large heads
     rc = check_launch("int2_stream");

@@ -7,5 +7,5 @@ namespace fp4x {
 template int launch_gemv_mfma<FmtInt2<true, 16>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 template int launch_gemv_mfma<FmtInt2<true, 32>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 template int launch_gemv_mfma<FmtInt2<true, 0>, EpiStore>(const GemvLaunch&, int, hipStream_t);
-bool launch_int2_stream_e4m3(GemvLaunch p, hipStream_t st) { return launch_int2_stream<true>(p, st); }
+bool launch_int2_stream_e4m3(GemvLaunch p, hipStream_t st) { return launch_int2_stream<true, 16>(p, st); }
 }  // namespace fp4x

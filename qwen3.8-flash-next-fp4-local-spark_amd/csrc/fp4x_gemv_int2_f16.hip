@@ -7,5 +7,7 @@ namespace fp4x {
 template int launch_gemv_mfma<FmtInt2<false, 16>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 template int launch_gemv_mfma<FmtInt2<false, 32>, EpiStore>(const GemvLaunch&, int, hipStream_t);
 template int launch_gemv_mfma<FmtInt2<false, 0>, EpiStore>(const GemvLaunch&, int, hipStream_t);
-bool launch_int2_stream_f16(GemvLaunch p, hipStream_t st) { return launch_int2_stream<false>(p, st); }
+bool launch_int2_stream_f16(GemvLaunch p, hipStream_t st) {
+  return p.pa.G == 32 ? launch_int2_stream<false, 32>(p, st) : launch_int2_stream<false, 16>(p, st);
+}
 }  // namespace fp4x

@@ -602,17 +602,20 @@ namespace fp4x {
 // are split into contiguous, equal (+-1) ranges over every wave of the grid
 // (one workgroup of W waves per CU), and each wave streams its tiles' units
 // through a private LDS ring of D buffers.  A unit is 128 bytes of codes
-// (512 weights) and the 64 (fp16) or 32 (e4m3) bytes of their scales, for each
-// of the 16 rows: two 16-byte direct loads per lane for the codes (the W8 lane
-// pattern) and one for the scales (fp16: lane l: row l >> 2, 16-byte piece
+// (512 weights) and the 64 (fp16, G = 16) or 32 (e4m3 with G = 16, fp16 with
+// G = 32: a compact scale row, C32) bytes of their scales, for each of the 16
+// rows: two 16-byte direct loads per lane for the codes (the W8 lane pattern)
+// and one for the scales (64-byte rows: lane l: row l >> 2, 16-byte piece
 // (l & 3) ^ ((row >> 2) & 3), so that the 8-byte scale reads of a quarter-wave
-// hit distinct banks; e4m3: lanes 0..31, row l >> 1, piece (l & 1) ^ (row >> 3),
-// so that the 4-byte scale reads of a wave hit 64 distinct banks).  The
-// activations are staged once per workgroup in the 4x4-transposed k order of
-// FmtInt2::deq16t (one byte permute per weight).
-template <bool E4M3>
+// hit distinct banks; 32-byte rows: lanes 0..31, row l >> 1, piece (l & 1) ^
+// (row >> 3), so that the 4-byte scale reads of a wave hit 64 distinct
+// banks).  A 64-weight chunk's scales are 4 bytes of a compact row either way
+// (four e4m3 group scales, or two fp16 ones).  The activations are staged
+// once per workgroup in the 4x4-transposed k order of FmtInt2::deq16t (one
+// byte permute per weight).
+template <bool C32>
 struct Int2Unit {
-  static constexpr int scale_row = E4M3 ? 32 : 64;    // scale bytes of one row in a unit
+  static constexpr int scale_row = C32 ? 32 : 64;     // scale bytes of one row in a unit
   static constexpr int bytes = 2048 + 16 * scale_row;
 };
 
@@ -680,8 +683,8 @@ __device__ __forceinline__ void int2_read_unit_x(uint32_t wa, uint32_t wb, uint3
       : "v"(wa), "v"(wb), "v"(sa), "v"(sb), "v"(xa)
       : "memory");
 }
-// int2_read_unit_x with e4m3 scales: 4 bytes per half (s0.y, s1.y untouched).
-__device__ __forceinline__ void int2_read_unit_x_e4m3(uint32_t wa, uint32_t wb, uint32_t sa, uint32_t sb,
+// int2_read_unit_x with compact scale rows: 4 bytes per half (s0.y, s1.y untouched).
+__device__ __forceinline__ void int2_read_unit_x_c32(uint32_t wa, uint32_t wb, uint32_t sa, uint32_t sb,
                                                       uint32_t xa, uint4& q0, uint4& q1, uint32_t& s0, uint32_t& s1,
                                                       i2x_u32x4 (&x)[8], i2x_u32x4 (&y)[8]) {
   asm volatile(
@@ -729,10 +732,12 @@ __device__ __forceinline__ void lds_put_u128(uint32_t a, uint4 v) {
 }
 __device__ __forceinline__ void wait_lgkm0_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <bool E4M3, int W, int D>
+template <bool E4M3, int GC, int W, int D>
 __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
-  using F = FmtInt2<E4M3, 16>;
-  using U = Int2Unit<E4M3>;
+  static_assert(GC == 16 || (GC == 32 && !E4M3), "G = 16, or fp16 scales at G = 32");
+  constexpr bool C32 = E4M3 || GC == 32;               // 32 scale bytes per row and unit
+  using F = FmtInt2<E4M3, GC>;
+  using U = Int2Unit<C32>;
   extern __shared__ __align__(16) uint16_t lds[];
   char* base = reinterpret_cast<char*>(lds);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -754,13 +759,13 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   if (threadIdx.x == 0) s_next = T0 + W;              // (visible after the staging barrier below)
   const int xrow = StreamGeom::xrow_bytes(K), xbuf = StreamGeom::xbuf_bytes(p.M, K);
   char* ring = base + xbuf + wave * D * U::bytes;
-  const int cb = K / 4, sbr = K / 16 * (E4M3 ? 1 : 2);   // code and scale bytes per row
+  const int cb = K / 4, sbr = K / 16 * (C32 ? 1 : 2);    // code and scale bytes per row
 
   // DMA lanes (codes as in the W8 kernel; scales: row l >> 2, piece (l & 3) ^ ((row >> 2) & 3))
   const int dr = lane >> 3, dc = lane & 7;
   const int cA = dc ^ (dr >> 1), cB = dc ^ (4 + (dr >> 1));
-  const int sr = E4M3 ? lane >> 1 : lane >> 2;
-  const int sp = E4M3 ? (lane & 1) ^ (sr >> 3) : (lane & 3) ^ ((sr >> 2) & 3);
+  const int sr = C32 ? lane >> 1 : lane >> 2;
+  const int sp = C32 ? (lane & 1) ^ (sr >> 3) : (lane & 3) ^ ((sr >> 2) & 3);
   // issuer: the tile whose units go out (ij: next unit; a new tile is taken
   // when its first unit is issued, never before the staging barrier since
   // D <= J), the tiles taken so far (ngot), the last two of them (fifo)
@@ -798,7 +803,7 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
     char* l = ring + is * U::bytes;
     dma_b128(iw + ij * 128 + o0, l);
     dma_b128(iw + ij * 128 + o1, l + 1024);
-    if (!E4M3 || lane < 32) dma_b128(isb + ij * U::scale_row + os, l + 2048);
+    if (!C32 || lane < 32) dma_b128(isb + ij * U::scale_row + os, l + 2048);
     if (++is == D) is = 0;
     ++issued;
     if (++ij == J) {
@@ -839,11 +844,11 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   const uint32_t rl = lds_addr(ring);
   const uint32_t wlA = rl + n * 128 + ((g ^ (n >> 1)) * 16), wlB = rl + n * 128 + (((g + 4) ^ (n >> 1)) * 16);
   // lane (n, g): the scales of chunks g (A) and g + 4 (B) of row n
-  const int sx = E4M3 ? n >> 3 : (n >> 2) & 3;
-  const uint32_t slA = E4M3 ? rl + 2048 + n * 32 + (sx * 16) + g * 4
-                            : rl + 2048 + n * 64 + (((g >> 1) ^ sx) * 16) + (g & 1) * 8;
-  const uint32_t slB = E4M3 ? rl + 2048 + n * 32 + ((1 ^ sx) * 16) + g * 4
-                            : rl + 2048 + n * 64 + (((2 + (g >> 1)) ^ sx) * 16) + (g & 1) * 8;
+  const int sx = C32 ? n >> 3 : (n >> 2) & 3;
+  const uint32_t slA = C32 ? rl + 2048 + n * 32 + (sx * 16) + g * 4
+                           : rl + 2048 + n * 64 + (((g >> 1) ^ sx) * 16) + (g & 1) * 8;
+  const uint32_t slB = C32 ? rl + 2048 + n * 32 + ((1 ^ sx) * 16) + g * 4
+                           : rl + 2048 + n * 64 + (((2 + (g >> 1)) ^ sx) * 16) + (g & 1) * 8;
   const uint32_t xl = lds_addr(base) + xr * xrow + g * 128;   // chunk g of unit 0
   int cs = 0, u = 0;
   for (int q = 0; q < ngot; ++q) {                   // (ngot grows while tiles are taken)
@@ -855,9 +860,9 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
       const uint32_t so = cs * U::bytes;
       typename F::Chunk ch[2];
       i2x_u32x4 xh[2][8];
-      if constexpr (E4M3) {
+      if constexpr (C32) {
         ch[0].s.y = ch[1].s.y = 0;
-        int2_read_unit_x_e4m3(wlA + so, wlB + so, slA + so, slB + so, xl + j * 1024, ch[0].q, ch[1].q, ch[0].s.x,
+        int2_read_unit_x_c32(wlA + so, wlB + so, slA + so, slB + so, xl + j * 1024, ch[0].q, ch[1].q, ch[0].s.x,
                               ch[1].s.x, xh[0], xh[1]);
       } else {
         int2_read_unit_x(wlA + so, wlB + so, slA + so, slB + so, xl + j * 1024, ch[0].q, ch[1].q, ch[0].s, ch[1].s,
@@ -904,7 +909,7 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
   wait_vmcnt<0>();                                   // no load of the prologue outlives the wave
 }
 
-// The INT2 head (G = 16, fp16 or e4m3 scales) through the streaming kernel
+// The INT2 head (G = 16 with fp16 or e4m3 scales, G = 32 with fp16 ones) through the streaming kernel
 // when the matrix has at least one tile per two waves of the grid and a tile's
 // units fill the ring (the 65k-token draft subset: 4075 tiles over 16 waves
 // per CU); false otherwise (or when FP4X_INT2_STREAM=0).  16 waves per CU
@@ -912,9 +917,9 @@ __global__ __launch_bounds__(64 * W) void int2_stream_kernel(GemvLaunch p) {
 // the deepest ring that fits.
 constexpr int kInt2DynLds = 160 * 1024 - 256;      // room for the kernel's static LDS (the tile counter)
 
-template <bool E4M3, int W, int D>
+template <bool E4M3, int GC, int W, int D>
 bool launch_int2_stream_wd(GemvLaunch p, size_t lds, hipStream_t st) {
-  auto kern = int2_stream_kernel<E4M3, W, D>;
+  auto kern = int2_stream_kernel<E4M3, GC, W, D>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -928,23 +933,23 @@ bool launch_int2_stream_wd(GemvLaunch p, size_t lds, hipStream_t st) {
   return true;
 }
 
-template <bool E4M3>
+template <bool E4M3, int GC>
 inline bool launch_int2_stream(GemvLaunch p, hipStream_t st) {
   if (!switches().int2_stream) return false;
   const int K = p.pa.K;
-  if (p.pa.G != 16 || K % 512 != 0 || p.M > 16 || p.ksplit != 1) return false;
+  if (p.pa.G != GC || K % 512 != 0 || p.M > 16 || p.ksplit != 1) return false;
   if ((reinterpret_cast<uintptr_t>(p.pa.w0) & 15) || (reinterpret_cast<uintptr_t>(p.pa.s) & 15)) return false;
   const int64_t tiles = (p.N + 15) / 16;
   const size_t xb = (size_t)StreamGeom::xbuf_bytes(p.M, K);
   const int64_t cus = device_cus();
-  constexpr size_t ub = Int2Unit<E4M3>::bytes;
+  constexpr size_t ub = Int2Unit<E4M3 || GC == 32>::bytes;
   auto fits = [&](int W, int D) {
     return xb + (size_t)W * D * ub <= (size_t)kInt2DynLds && K / 512 >= D && 2 * tiles >= cus * W;
   };
-  if (fits(16, 3)) return launch_int2_stream_wd<E4M3, 16, 3>(p, xb + 16 * 3 * ub, st);
-  if (fits(8, 6)) return launch_int2_stream_wd<E4M3, 8, 6>(p, xb + 8 * 6 * ub, st);
-  if (fits(8, 4)) return launch_int2_stream_wd<E4M3, 8, 4>(p, xb + 8 * 4 * ub, st);
-  if (fits(8, 3)) return launch_int2_stream_wd<E4M3, 8, 3>(p, xb + 8 * 3 * ub, st);
+  if (fits(16, 3)) return launch_int2_stream_wd<E4M3, GC, 16, 3>(p, xb + 16 * 3 * ub, st);
+  if (fits(8, 6)) return launch_int2_stream_wd<E4M3, GC, 8, 6>(p, xb + 8 * 6 * ub, st);
+  if (fits(8, 4)) return launch_int2_stream_wd<E4M3, GC, 8, 4>(p, xb + 8 * 4 * ub, st);
+  if (fits(8, 3)) return launch_int2_stream_wd<E4M3, GC, 8, 3>(p, xb + 8 * 3 * ub, st);
   return false;
 }
 

@@ -306,7 +306,19 @@ def test_int2_stream(gpu, F, M, rs, one, K, e4m3, monkeypatch):
     5 rows past the last full tile; K = 1536: three units per tile instead of
     five.  e4m3: the row-scaled form (e4m3 group scales, the quantizer's fp32
     row scales as rs)."""
-    rng = np.random.default_rng(77 + M + rs + 5 * one + K + 3 * e4m3)
+    _int2_stream_case(F, M, rs, one, K, e4m3, 16, monkeypatch)
+
+
+@pytest.mark.parametrize("M,rs,one,K", [(3, False, 0, 2560), (16, True, 1, 2560), (3, False, 2, 1536)])
+def test_int2_stream_g32(gpu, F, M, rs, one, K, monkeypatch):
+    """fp16 group scales at G = 32 (the plugin's FP4X_HEAD_G=32) stream as
+    e4m3 ones do: 32 scale bytes per row and unit, two fp16 scales per 64-weight
+    chunk; the same checks."""
+    _int2_stream_case(F, M, rs, one, K, False, 32, monkeypatch)
+
+
+def _int2_stream_case(F, M, rs, one, K, e4m3, G, monkeypatch):
+    rng = np.random.default_rng(77 + M + rs + 5 * one + K + 3 * e4m3 + G)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     V = {0: 4 * 8 * 16 * cus + 40, 1: 16 * (16 * cus - 21) - 3, 2: 16 * 10 * cus - 5}[one]
     w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
@@ -314,10 +326,11 @@ def test_int2_stream(gpu, F, M, rs, one, K, e4m3, monkeypatch):
         P, S, R = oq.quantize_int2(w, scale_fmt="e4m3", group=16)
         Sd = dev(S).view(torch.float8_e4m3fn)
     else:
-        P, S = oq.quantize_int2(w, group=16)
+        P, S = oq.quantize_int2(w, group=G)
         R = (rng.random(V) + 0.5).astype(np.float32) if rs else None
         Sd = dev(S)
     del w
+    print(f"int2 stream V={V} K={K} M={M} rs={rs} e4m3={e4m3} G={G}", flush=True)
     x, xb = act(rng, M, K)
     args = (bf16_dev(x), dev(P), Sd, V)
     kw = {"RS": dev(R)} if rs else {}
@@ -337,7 +350,7 @@ def test_int2_stream(gpu, F, M, rs, one, K, e4m3, monkeypatch):
         for got in (y[:, r0:r1], y_core[:, r0:r1]):
             assert np.all(np.abs(got - exact) <= bound), float((np.abs(got - exact) / bound).max())
         worst = max(worst, float((np.abs(y[:, r0:r1] - exact) / bound).max()))
-    print(f"int2 stream V={V} M={M} rs={rs} e4m3={e4m3}: max |y - exact| / bound = {worst:.3g}")
+    print(f"int2 stream V={V} M={M} rs={rs} e4m3={e4m3} G={G}: max |y - exact| / bound = {worst:.3g}")
     # bf16 logits round the same sums
     yb = F.int2_logits(*args, out_dtype=torch.bfloat16, **kw)
     assert np.array_equal(bf16_bits(yb), fm.bf16_bits(y))
@@ -349,18 +362,21 @@ def test_int2_stream(gpu, F, M, rs, one, K, e4m3, monkeypatch):
                                           (65197, 3, False, 64, False), (20000, 3, False, 64, False),
                                           (65197, 3, False, 64, True), (248320, 3, False, 512, True),
                                           (20000, 16, False, 256, True), (248320, 3, "e4m3", 512, False),
-                                          (65197, 3, "e4m3", 64, True)])
+                                          (65197, 3, "e4m3", 64, True), (248320, 3, "g32", 1024, False)])
 def test_int2_topk_fused_equals_separate(gpu, F, V, M, rs, C, f32):
     """int2_topk (slice maxima from the streaming coarse kernel's epilogue where
     it streams, else a slice-max launch) equals int2_logits + topk_rows bit for
     bit, and its selection is the oracle's total order on its own logits; for
-    fp16 and for e4m3 (row-scaled) group scales."""
+    fp16 (G = 16 and 32) and for e4m3 (row-scaled) group scales."""
     K = 2560
     g = torch.Generator(device=gpu).manual_seed(V + M)
     w = torch.randn((V, K), generator=g, device=gpu) * 0.02
     w[torch.randperm(V, generator=g, device=gpu)[:64]] *= 4
     if rs == "e4m3":                                  # the row-scaled form: its own row scales as RS
         P, S, R = F.quantize_int2(w, scale_fmt="e4m3", group=16)
+    elif rs == "g32":                                 # fp16 scales per 32 (FP4X_HEAD_G=32, C = 1024)
+        P, S = F.quantize_int2(w, group=32)
+        R = None
     else:
         P, S = F.quantize_int2(w, group=16)
         R = (torch.rand(V, generator=g, device=gpu) + 0.5) if rs else None
@@ -377,13 +393,14 @@ def test_int2_topk_fused_equals_separate(gpu, F, V, M, rs, C, f32):
     assert torch.equal(idx, idx2)
     host = coarse.cpu().numpy() if f32 else bf16_bits(coarse)
     assert np.array_equal(idx.cpu().numpy(), oh.topk_total_order(host, C))
-    # sorted=False (the heads scatter at the indices): the same set per row (on
-    # this path in increasing index order for bf16 logits, the sorted order for
-    # fp32 ones)
+    # sorted=False (the heads scatter at the indices): the same set per row (in
+    # increasing index order for bf16 logits of at most 1024 candidates, as a
+    # top-512 leaves; the sorted order for fp32 ones and for more candidates,
+    # as a top-1024 has)
     coarse3, idx3 = F.int2_topk(xt, P, S, V, C, RS=R, out_dtype=dt, sorted=False)
     assert torch.equal(coarse3.view(torch.int16 if not f32 else torch.int32),
                        coarse.view(torch.int16 if not f32 else torch.int32))
-    if f32:
+    if f32 or C > 512:
         assert torch.equal(idx3, idx)
     else:
         assert torch.equal(idx3, torch.sort(idx, dim=1).values)
