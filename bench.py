@@ -348,6 +348,9 @@ def bench_head(F, torch, dev, out, vectors=1000, n_x=128):
     copies32 = [(P32.clone(), S32.clone()) for _ in range(2)] + [(P32, S32)]
     us = graph_time([lambda c=c: F.int2_logits(x, c[0], c[1], V, out_dtype=torch.bfloat16) for c in copies32], 10)
     out["E_int2_g32_coarse_248320x2560_M3"] = entry(us, V * K // 4 + V * (K // 32) * 2 + M * K * 2 + M * V * 2)
+    # ... with the top-1024 set the reference pairs with G = 32 (x/fp4patch.py:345)
+    us = graph_time([lambda c=c: F.int2_topk(x, c[0], c[1], V, 1024, sorted=False) for c in copies32], 10)
+    out["E_int2_g32_coarse_plus_top1024_set_M3"] = {"us": round(us, 3)}
     del copies32, P32, S32
     torch.cuda.empty_cache()
     # the top-C alone over 16 coarse outputs of different activations, one graph

@@ -690,6 +690,53 @@ __device__ void tk_select_set(const uint32_t* ck, const int* cidx, int n_c, int 
   if (in) out[pos] = (int64_t)cidx[t];
 }
 
+// The C largest of n_c (kRsThreads < n_c <= 4 kRsThreads) bf16 candidates,
+// for callers that need the set only (a top-1024 leaves more candidates than
+// threads): thread t holds candidates 4t .. 4t + 3; T, the C-th largest key16,
+// by the window round where the row's T0 round was windowed (the candidates'
+// keys then lie within its window), else by rs_kth; then every candidate above
+// T and the first C - (count above T) at T in candidate (index) order, placed
+// by two workgroup scans, so the set comes out in increasing index order, as
+// tk_select_set's.  hist must be zero and visible on entry; every thread of the
+// workgroup calls it.
+__device__ void tk_select_set4(const uint32_t* ck, const int* cidx, int n_c, int C, uint32_t* hist, uint32_t* wh,
+                               TkHist& h, int* slots, uint32_t* ext, int64_t* out, bool windowed, uint32_t row_hi) {
+  const int t = threadIdx.x;
+  uint32_t key[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) key[j] = 4 * t + j < n_c ? ck[4 * t + j] >> 16 : 0u;   // keys >= T0 >= 1
+  uint32_t T = 0;
+  if (windowed) {
+    uint32_t hi;
+    int above;
+    T = rs_kth_window<4>(key, C, hist, slots, ext, &hi, &above, row_hi);
+  }
+  if (T == 0) T = rs_kth<4>(key, C, wh, h, ext);
+  int na = 0, nt = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    na += key[j] > T ? 1 : 0;
+    nt += key[j] != 0 && key[j] == T ? 1 : 0;
+  }
+  int tot;
+  const int pre = rs_scan(na | (nt << 16), slots, &tot);
+  const int quota = C - (tot & 0xffff);              // ties at T that make the set
+  int tb = pre >> 16, nin = 0;
+  bool in[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool tie = key[j] != 0 && key[j] == T;
+    in[j] = key[j] > T || (tie && tb < quota);
+    tb += tie ? 1 : 0;
+    nin += in[j] ? 1 : 0;
+  }
+  int n_in;
+  int pos = rs_scan(nin, slots, &n_in);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (in[j]) out[pos++] = (int64_t)cidx[4 * t + j];
+}
+
 // VPT: 8-slice vectors of the row's slice maxima per thread (1, 2 or 4, the
 // fewest that cover the row), so short rows run fewer register slots.  E:
 // the row's element type (Elem16 for bf16 logits, Elem32 for fp32).  The
@@ -864,6 +911,10 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
   if (set_only && n_c <= kRsThreads) {             // the set only: no sort
     if (windowed) tk_select_set_window(ck, cidx, n_c, C, hist, slots, ext, out, row_hi);
     else tk_select_set(ck, cidx, n_c, C, wh, h, ext, slots, out);
+    return;
+  }
+  if (set_only) {                                  // n_c <= kTkCap = 4 kRsThreads here
+    tk_select_set4(ck, cidx, n_c, C, hist, wh, h, slots, ext, out, windowed, row_hi);
     return;
   }
   // sort the candidates (positions follow the index order, so ties sort by index)

@@ -394,32 +394,40 @@ def test_int2_topk_fused_equals_separate(gpu, F, V, M, rs, C, f32):
     host = coarse.cpu().numpy() if f32 else bf16_bits(coarse)
     assert np.array_equal(idx.cpu().numpy(), oh.topk_total_order(host, C))
     # sorted=False (the heads scatter at the indices): the same set per row (in
-    # increasing index order for bf16 logits of at most 1024 candidates, as a
-    # top-512 leaves; the sorted order for fp32 ones and for more candidates,
-    # as a top-1024 has)
+    # increasing index order for bf16 logits, with up to 1024 candidates, as a
+    # top-512 leaves, or more, as a top-1024 has; the sorted order for fp32
+    # ones)
     coarse3, idx3 = F.int2_topk(xt, P, S, V, C, RS=R, out_dtype=dt, sorted=False)
     assert torch.equal(coarse3.view(torch.int16 if not f32 else torch.int32),
                        coarse.view(torch.int16 if not f32 else torch.int32))
-    if f32 or C > 512:
+    if f32:
         assert torch.equal(idx3, idx)
     else:
         assert torch.equal(idx3, torch.sort(idx, dim=1).values)
 
 
-@pytest.mark.parametrize("case,V", [("short_row", 3000), ("all_tied", 50000), ("wide_tie", 248320)])
-def test_int2_topk_set_only_paths(gpu, F, case, V):
+@pytest.mark.parametrize("case,V,C", [("short_row", 3000, 512), ("all_tied", 50000, 512), ("wide_tie", 248320, 512),
+                                      ("top1024", 248320, 1024), ("tie1024", 248320, 1024)])
+def test_int2_topk_set_only_paths(gpu, F, case, V, C):
     """sorted=False on the selection's other paths: a row of at most 4096
     elements (sorted whole), every row element tied (the exact threshold
-    path), and 2000 identical rows holding the top 512 (more candidates at the
-    threshold than the candidate buffers take).  The set equals the sorted
-    call's, which is the oracle's total order on the same logits."""
-    K, M, C = 2560, 3, 512
-    g = torch.Generator(device=gpu).manual_seed(V)
+    path), 2000 identical rows holding the top 512 (more candidates at the
+    threshold than the candidate buffers take), a top-1024 (more candidates
+    than the workgroup's threads: four per thread) and a top-1024 whose last
+    places are 1500 tied rows.  The set equals the sorted call's, which is the
+    oracle's total order on the same logits; the top-1024 sets come out in
+    increasing index order."""
+    K, M = 2560, 3
+    g = torch.Generator(device=gpu).manual_seed(V + C)
     w = torch.randn((V, K), generator=g, device=gpu) * 0.02
     if case == "all_tied":
         w[:] = w[0]
     elif case == "wide_tie":
         w[torch.randperm(V, generator=g, device=gpu)[:2000]] = w[0] * 4
+    elif case == "tie1024":
+        sel = torch.randperm(V, generator=g, device=gpu)
+        w[sel[:600]] *= 8
+        w[sel[600:2100]] = w[sel[600]] * 4
     P, S = F.quantize_int2(w, group=16)
     del w
     xt = bf16_dev(act(np.random.default_rng(V), M, K)[0])
@@ -430,6 +438,8 @@ def test_int2_topk_set_only_paths(gpu, F, case, V):
     assert torch.equal(torch.sort(idx3, dim=1).values, torch.sort(idx, dim=1).values)
     if case == "all_tied":
         assert torch.equal(torch.sort(idx3, dim=1).values, torch.arange(C, device=gpu).expand(M, C))
+    if C > 512:
+        assert torch.equal(idx3, torch.sort(idx3, dim=1).values)
 
 
 # ------------------------------------------------------------------ draft head (NVFP4 rescore)
