@@ -458,7 +458,8 @@ bool rows_fma_shape_ok(int N, int M, int threads, int cus) {
 //     for under 8 rows per CU, the one-row kernel's extra workgroups pay
 //     more than its activation reads cost);
 //   * else R = 2 (rows of over 256 chunks, or past the one-row limits).
-// Measured as graph replays from HBM (us at M = 1 / 2 / 3 / 4), R = 1 / 2:
+// Measured as graph replays from HBM (us at M = 1 / 2 / 3 / 4; one lane per
+// chunk, before W6 and NVFP4 split chunks over two lanes), R = 1 / 2:
 // W6 [2048 x 2560] 3.9 / 4.6 / 5.4 / 6.1 against 4.2 / 4.5 / 5.0 / 5.4;
 // NVFP4 [2048 x 2560] 3.5 / 4.3 / 5.0 / 5.8 against 3.6 / 4.0 / 4.4 / 4.7;
 // W8 [2560 x 2560] 3.8 / 4.4 / 5.0 / 5.5 against 4.0 / 4.4 / 4.7 / 5.1;
@@ -529,7 +530,6 @@ inline bool rows_fma_go(RowsLaunch& a, int R, int threads, hipStream_t st) {
   }
   return false;
 }
-
 
 // Launch a few-rows kernel when the call fits one: one matrix, no per-row
 // scale, strides within int32, and either the fma kernel (M <= 4, R rows per
