@@ -244,12 +244,15 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
  * 128-byte line per workgroup (its generation flag, its ack word and a down
  * tile's generation), so it needs S >= 32 * ceil(N / 16); with fewer it
  * makes the two calls.  (S depends on the buffer alone: calls of any shape on
- * one buffer agree on it.)  part: the down partials of the single launch sit
- * in one XCD's L2 per tile, followed by one tag line per partial.  A
- * workgroup whose flag wait gives up (only possible when other work holds the
- * GPU's CUs for about a second) writes NaN to its outputs and sets bit 0 of
- * the status word; a down tile whose partials were not all on its closer's
- * XCD writes NaN and sets bit 1; the next call is not affected.
+ * one buffer agree on it.)  part: the single launch keeps the down partials
+ * of each tile on one XCD as 64-bit (partial, generation tag) pairs (8-byte
+ * aligned part; 2 * ceil(N / 16) * 16 * M * (parts per tile) floats, else
+ * device-coherent partials).  A workgroup whose flag wait gives up (only
+ * possible when other work holds the GPU's CUs for about a second) writes NaN
+ * to its outputs and sets bit 0 of the status word; a down tile whose closer
+ * gives up waiting for a part's pairs (a part placed on another XCD, or held
+ * off the CUs as long) writes NaN and sets bit 1; the next call is not
+ * affected.
  * FP4X_HC_MIX=0 forces the two calls, FP4X_HC_XCD=0 device-coherent
  * partials.
  * [HCFused.down then HCFused.up as the plugin's fused mixer calls them,

@@ -161,9 +161,10 @@ static bool al(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & 
 // launch, so a mixer pays one launch and the up weights stream while the down
 // projection runs.
 //   * Workgroups 0..D-1 (D = down tiles x C) run one down item each.  The
-//     last arriver of a down tile stores di and, device-coherently, the
-//     bottleneck, waits for those stores and then advances every
-//     workgroup's flag by one (a fetch-add per 128-byte flag line).  (A
+//     closer of a down tile (the last arriver, or with XCD-local partials its
+//     last part) stores di and, device-coherently, the bottleneck, waits for
+//     those stores and then advances every workgroup's flag by one (a
+//     fetch-add per 128-byte flag line).  (A
 //     shared tile count whose last increment advanced the flags cost one more
 //     device round trip per mixer: the served mixer 9.9 -> 9.5 us without it.)
 //   * Every workgroup (8 waves) then issues the weight loads of its R up
@@ -554,12 +555,11 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   // part of the up tiles to extra workgroups is slower than not at all)
   const int cus = device_cus();
   // XCD-local down partials (w8_splitk_item's LOCAL form): at most 8 parts per
-  // tile, a generation word per tile on the flag lines, and the tags after the
-  // slots in the caller's slot buffer; the down items then span 8 residues x
-  // the most tiles a residue holds x C workgroups
-  const int64_t slot_floats = ((int64_t)tiles_d * C * M * 16 + 15) & ~(int64_t)15;
-  const bool local = switches().hc_xcd && C <= 8 && tiles_d <= cus &&
-                     slot_floats + (int64_t)tiles_d * C * 16 <= (int64_t)ksplit * 16 * N;
+  // tile, a generation word per tile on the flag lines, and the parts' 64-bit
+  // (partial, generation) pairs in the caller's slot buffer; the down items
+  // then span 8 residues x the most tiles a residue holds x C workgroups
+  const bool local = switches().hc_xcd && C <= 8 && tiles_d <= cus && al(part, 8) &&
+                     (int64_t)tiles_d * C * M * 16 * 2 <= (int64_t)ksplit * 16 * N;
   const int R = 8 / WT, ntu = H / bj, D = local ? 8 * ((tiles_d + 7) / 8) * C : tiles_d * C;
   if (hc > kMixMaxHc || R * M * bj > kMixOutPer * 512) return two();
   const int need_u = (ntu + R - 1) / R;
@@ -584,8 +584,8 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   a.sync = tickets + sync_at;
   a.loc.gen = a.sync + kMixFlagStride + kMixGenAt;
   a.loc.gstride = kMixFlagStride;
-  a.loc.tags = reinterpret_cast<int*>(part + slot_floats);
   a.loc.status = a.sync + 1;
+  a.loc.spin_limit = switches().hc_spin_limit;
   a.C = C;
   a.D = D;
   a.tiles_d = tiles_d;

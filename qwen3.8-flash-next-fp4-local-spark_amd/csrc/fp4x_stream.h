@@ -282,39 +282,47 @@ __device__ __forceinline__ void stream_read_x(uint32_t xa, uint4& x0a, uint4& x0
 // XCD-local slots (LOCAL, the single-launch mixer): when the caller places
 // every item of a tile on one XCD (workgroups whose indices are congruent
 // mod 8: the dispatcher hands consecutive workgroups to the XCDs in turn), the
-// partials are stored plainly into that XCD's L2 and the closer reads them
-// from there (L1 bypassed), instead of through the device's coherence point:
-// each of those round trips is several hundred ns shorter.  The ticket stays
-// device-scope, so arrivals are always counted exactly.  Each partial carries
-// a tag, the tile's call generation (gen, device-coherent, read by every item
-// at its start and advanced by the closer); a closer that finds a tag other
-// than its own generation (an item ran on another XCD, so its partial is in
-// another L2) writes NaN for the tile and sets bit 1 of *status, and the
-// generation still advances, so the next call starts clean.
+// partials are stored plainly, with no completion wait and no ticket (their
+// lines stay within the XCD that reads them).  The tile's closer is
+// its last part (c = C - 1, the highest workgroup index of the tile, so every
+// other part was dispatched before it and none of them waits on anything).
+// Parts c < C - 1 store their [M x 16] partials as 64-bit (value, tag) pairs,
+// each pair in one store, and end; the tag is the complement of the tile's
+// call generation (gen, device-coherent, read by every part at its start and
+// advanced by the closer).  The closer reads the pairs from L2 until every
+// tag is its call's (s_sleep between reads), adds them in slot order with its
+// own partial last, runs the epilogue and advances gen.  That replaces the
+// slot stores' completion wait, the device-scope ticket and a separate read
+// of the slots (the served mixer 9.43 -> 9.06 us, the 640-row one 11.91 ->
+// 11.83).  A closer whose reads reach spin_limit (a part that ran on
+// another XCD, so its pairs are in another L2, or one that never got a CU)
+// writes NaN for the tile and sets bit 1 of *status; gen still advances, so
+// the next call starts clean.
 struct SplitLocal {
   int* gen;            // per-tile generation words, gstride ints apart
   int gstride;
-  int* tags;           // [tiles][C] tags, 16 ints (one 64-byte line) apart
   int* status;
+  int spin_limit;      // the closer's reads of the other parts' pairs before it gives up
 };
 
-// Eight floats (a[i]) and one int (at) from this XCD's L2 (sc0: the L1 is
-// bypassed), all issued before one wait.
-__device__ __forceinline__ void ld_l2_8x1(const float* const (&a)[8], const int* at, float (&v)[8], int& tv) {
+// Seven (value, tag) pairs, device-scope loads (sc1), all issued before one
+// wait.  Measured on the mixer: workgroup-scope (sc0) loads kept returning the
+// first value a CU had read, even after a vector L1 invalidate, so the
+// closer never saw a late part; atomic ORs of zero saw it but made the mixer
+// 0.8-1.5 us slower; these loads see it and cost least.  A pair counts only
+// when its tag is this call's, whatever path its line took.
+__device__ __forceinline__ void read_pairs_7(const uint64_t* const (&a)[7], uint64_t (&v)[7]) {
   asm volatile(
-      "global_load_dword %0, %9, off sc0\n\t"
-      "global_load_dword %1, %10, off sc0\n\t"
-      "global_load_dword %2, %11, off sc0\n\t"
-      "global_load_dword %3, %12, off sc0\n\t"
-      "global_load_dword %4, %13, off sc0\n\t"
-      "global_load_dword %5, %14, off sc0\n\t"
-      "global_load_dword %6, %15, off sc0\n\t"
-      "global_load_dword %7, %16, off sc0\n\t"
-      "global_load_dword %8, %17, off sc0\n\t"
+      "global_load_dwordx2 %0, %7, off sc1\n\t"
+      "global_load_dwordx2 %1, %8, off sc1\n\t"
+      "global_load_dwordx2 %2, %9, off sc1\n\t"
+      "global_load_dwordx2 %3, %10, off sc1\n\t"
+      "global_load_dwordx2 %4, %11, off sc1\n\t"
+      "global_load_dwordx2 %5, %12, off sc1\n\t"
+      "global_load_dwordx2 %6, %13, off sc1\n\t"
       "s_waitcnt vmcnt(0)"
-      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]),
-        "=&v"(tv)
-      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]), "v"(at)
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6])
       : "memory");
 }
 
@@ -396,12 +404,65 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
   }
   // wave 0: slot c of tile t holds [M][16] fp32 partials
   float* slots = p.part + (int64_t)t * C * p.M * 16;
-  const int want = __builtin_amdgcn_readfirstlane(gen) + 1;   // LOCAL: this call's generation
   if constexpr (LOCAL) {
+    // slot c of tile t: [M][16] 64-bit pairs (partial bits, tag), each
+    // stored in one single-copy-atomic store; the tag is the complement of
+    // this call's generation (as a float, a negative NaN pattern, so float
+    // slots left in the buffer by the two-launch path do not pass for one).
+    // The closer is the tile's last part, which reads the others' pairs
+    // until every tag is this call's and adds its own partial last (slot order)
+    const int want = __builtin_amdgcn_readfirstlane(gen) + 1;
+    const uint32_t tag = ~(uint32_t)want;
+    uint64_t* pairs = reinterpret_cast<uint64_t*>(p.part) + (int64_t)t * C * p.M * 16;
+    if (c != C - 1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (g * 4 + i < p.M) slots[(c * p.M + g * 4 + i) * 16 + n] = acc[i];
-    if (lane == 0) loc.tags[((int64_t)t * C + c) * 16] = want;
+      for (int i = 0; i < 4; ++i)
+        if (g * 4 + i < p.M)
+          __hip_atomic_store(pairs + (c * p.M + g * 4 + i) * 16 + n,
+                             ((uint64_t)tag << 32) | __float_as_uint(acc[i]), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+      return false;
+    }
+    bool ok = true;
+    for (int e0 = 0; e0 < p.M * 16; e0 += 64) {
+      const int e = e0 + lane;
+      const int ec = e < p.M * 16 ? e : 0, m = ec >> 4, nn = ec & 15;
+      // this part's own partial of element ec: lane nn + 16 (m >> 2), component m & 3
+      const int src = (nn + 16 * (m >> 2)) << 2;
+      float own = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(acc[i])));
+        if ((m & 3) == i) own = v;
+      }
+      const uint64_t* a[7];
+#pragma unroll
+      for (int cc = 0; cc < 7; ++cc) a[cc] = pairs + ((cc < C - 1 ? cc : 0) * p.M + m) * 16 + nn;
+      uint64_t v[7] = {0, 0, 0, 0, 0, 0, 0};
+      for (int it = 0;; ++it) {
+        if (!ok) break;
+        read_pairs_7(a, v);
+        bool have = true;
+#pragma unroll
+        for (int cc = 0; cc < 7; ++cc)
+          if (cc < C - 1 && (uint32_t)(v[cc] >> 32) != tag) have = false;
+        if (__ballot(!have) == 0) break;
+        if (it >= loc.spin_limit) ok = false;        // (a part ran on another XCD, or never ran)
+        else __builtin_amdgcn_s_sleep(1);
+      }
+      float tot = __uint_as_float((uint32_t)v[0]);
+#pragma unroll
+      for (int cc = 1; cc < 7; ++cc)
+        if (cc < C - 1) tot += __uint_as_float((uint32_t)v[cc]);
+      tot = C > 1 ? tot + own : own;
+      const int64_t orow = (int64_t)t * 16 + nn;
+      if (e < p.M * 16 && orow < p.N) Epi::apply(p, 0, m, orow, ok ? tot * p.gs : __builtin_nanf(""));
+    }
+    if (lane == 0) {
+      if (!ok) __hip_atomic_fetch_or(loc.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(loc.gen + (int64_t)t * loc.gstride, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return true;
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -414,34 +475,6 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
   if (lane == 0) tk = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   tk = __builtin_amdgcn_readfirstlane(tk);
   if (tk != C - 1) return false;
-  if constexpr (LOCAL) {
-    // every element e = m * 16 + n of the tile: its C partials in slot order;
-    // lane cc < C also checks item cc's tag (C <= 8, checked by the host)
-    bool ok = true;
-    for (int e0 = 0; e0 < p.M * 16; e0 += 64) {
-      const int e = e0 + lane;
-      const int ec = e < p.M * 16 ? e : 0;
-      const float* a[8];
-#pragma unroll
-      for (int cc = 0; cc < 8; ++cc) a[cc] = slots + (cc < C ? cc : 0) * p.M * 16 + ec;
-      float v[8];
-      int tv;
-      ld_l2_8x1(a, loc.tags + ((int64_t)t * C + (lane < C ? lane : 0)) * 16, v, tv);
-      if (e0 == 0) ok = __ballot(lane < C && tv != want) == 0;
-      float tot = v[0];
-#pragma unroll
-      for (int cc = 1; cc < 8; ++cc)
-        if (cc < C) tot += v[cc];
-      const int64_t orow = (int64_t)t * 16 + (e & 15);
-      if (e < p.M * 16 && orow < p.N) Epi::apply(p, 0, e >> 4, orow, ok ? tot * p.gs : __builtin_nanf(""));
-    }
-    if (lane == 0) {
-      if (!ok) __hip_atomic_fetch_or(loc.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(loc.gen + (int64_t)t * loc.gstride, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ticket_reset(ticket);
-    }
-    return true;
-  }
   for (int e = lane; e < p.M * 16; e += 64) {        // e = m * 16 + n
     const float* src = slots + e;
     float tot = ld_coherent(src);
