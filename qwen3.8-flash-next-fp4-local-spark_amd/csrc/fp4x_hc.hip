@@ -585,7 +585,9 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   a.loc.gen = a.sync + kMixFlagStride + kMixGenAt;
   a.loc.gstride = kMixFlagStride;
   a.loc.status = a.sync + 1;
-  a.loc.spin_limit = switches().hc_spin_limit;
+  // the closer waits only for parts of its tile that were dispatched before it
+  // and wait on nothing, so its reads keep a floor whatever the flag limit
+  a.loc.spin_limit = switches().hc_spin_limit > (1 << 16) ? switches().hc_spin_limit : 1 << 16;
   a.C = C;
   a.D = D;
   a.tiles_d = tiles_d;

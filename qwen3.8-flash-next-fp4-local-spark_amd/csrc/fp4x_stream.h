@@ -290,7 +290,8 @@ __device__ __forceinline__ void stream_read_x(uint32_t xa, uint4& x0a, uint4& x0
 // each pair in one store, and end; the tag is the complement of the tile's
 // call generation (gen, device-coherent, read by every part at its start and
 // advanced by the closer).  The closer reads the pairs from L2 until every
-// tag is its call's (s_sleep between reads), adds them in slot order with its
+// tag is its call's (s_sleep between reads, at most spin_limit reads: the
+// caller's flag limit, but never under 65,536), adds them in slot order with its
 // own partial last, runs the epilogue and advances gen.  That replaces the
 // slot stores' completion wait, the device-scope ticket and a separate read
 // of the slots (the served mixer 9.43 -> 9.06 us, the 640-row one 11.91 ->

@@ -20,7 +20,10 @@
   call is bit-identical to the two-launch path;
 * single-launch calls whose up workgroups get a CU only after the bottleneck
   is ready (a kernel on another stream holds most CUs) are bit-identical to
-  the two-launch path, with no NaN and no status bit.
+  the two-launch path, with no NaN and no status bit;
+* single launches whose down tiles split into 2 and 8 K parts (hidden sizes
+  1024 and 4096), whose closers add 1 and 7 other parts' tagged partials,
+  are bit-identical to the two-launch path.
 """
 import ctypes
 
@@ -238,7 +241,9 @@ def test_mix_wait_give_up_then_recovers(gpu, F, monkeypatch):
     print(f"give-up call: {int(nan.sum())} of {nan.numel()} block_input values NaN")
     assert nan.any()
     assert torch.equal(gave_up[2][~nan], ref[2][~nan])
-    assert torch.equal(gave_up[0], ref[0]) and torch.equal(gave_up[1], ref[1])   # the down half never waits
+    # the down half never gives up: a tile's closer waits only for parts that
+    # were dispatched before it and wait on nothing, with at least 65,536 reads
+    assert torch.equal(gave_up[0], ref[0]) and torch.equal(gave_up[1], ref[1])
     assert fx.wait_timeouts()
     assert not fx.wait_timeouts()                                                  # cleared by the read
     for _ in range(3):
@@ -246,6 +251,37 @@ def test_mix_wait_give_up_then_recovers(gpu, F, monkeypatch):
         for a, b in zip(again, ref):
             assert torch.equal(a, b)
         assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
+    assert not fx.wait_timeouts()
+
+
+def took_single_launch(fx):
+    """True once a single launch has advanced workgroup 0's generation flag
+    (the two-call path never touches the flag lines)."""
+    return int(fx.tickets[fx._status_at - 1 + 32].item()) != 0
+
+
+@pytest.mark.parametrize("h", [1024, 4096])
+def test_mix_parts_per_tile(gpu, F, h):
+    """The single launch at hidden sizes whose down tiles split into 2 (K = 4096)
+    and 8 (K = 16384, the most that keep a tile's parts on one XCD) K parts:
+    the tile's last part adds the others' tagged partials in slot order, so
+    every call equals the two-launch path bit for bit, with no NaN and no
+    status bit."""
+    rng = np.random.default_rng(h)
+    (qd, sd), (qu, su) = layer(rng, nd=336, lr=320, h=h)
+    x, _ = act(rng, 3, HC * h)
+    x_t = bf16_dev(x)
+    fx = F.HCFused(gpu)
+    qd, sd = dev(qd), dev(sd)
+    qi, si = F.HCFused.interleave_up(dev(qu), dev(su), HC, 8)
+    di, bot = fx.down(x_t, qd, sd, 320, HC, (32, 256, 8, 4))
+    bi = F.HCFused.up(bot, qi, si, x_t, HC, (8, 64, 4))
+    for _ in range(3):
+        one = fx.mix(x_t, qd, sd, 320, HC, qi, si, x_t, (32, 256, 8, 4))
+        for a, b in zip(one, (di, bot, bi)):
+            assert torch.equal(a, b), h
+        assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
+    assert took_single_launch(fx), h
     assert not fx.wait_timeouts()
 
 
