@@ -214,7 +214,7 @@ struct HcMixArgs {
 };
 
 constexpr int kMixMaxHc = 4;                     // streams the single-launch mixer takes
-constexpr int kMixOutPer = 2;                    // epilogue outputs per thread
+constexpr int kMixPasses = 8;                    // epilogue passes of 128 outputs (a quad of lanes each)
 
 // SPLIT: the up tiles have workgroups of their own (grid = D + up
 // workgroups).  LOCAL: the down items of a tile are the workgroups i < D with
@@ -286,20 +286,21 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   //    once in a workgroup without a down item)
   MfmaBatch<F, CPS> cb;
   mfma_load_full<F, DP, CPS>(cb, F::lane(u.pa, urow, CPS * cw));
-  // ... and the normalized inputs of this thread's epilogue outputs (at most
-  // kMixOutPer), into registers, so that the epilogue waits for no load
-  // (outputs past the workgroup's read a valid element and are not stored)
-  const int per_slot = u.M * u.bj, nout = a.R * per_slot;
-  uint16_t nrv[kMixOutPer][kMixMaxHc];
+  // ... and the normalized inputs of this lane's epilogue terms, into
+  // registers, so that the epilogue waits for no load: each output has a
+  // quad of lanes, lane s of the quad taking stream s, and a pass covers
+  // blockDim / 4 outputs (outputs past the workgroup's read a valid element
+  // and are not stored)
+  const int per_slot = u.M * u.bj, nout = a.R * per_slot, opp = (int)blockDim.x >> 2;
+  const int qs = (int)threadIdx.x & 3, qsc = qs < u.hc ? qs : u.hc - 1;
+  uint16_t nrv[kMixPasses];
 #pragma unroll
-  for (int q = 0; q < kMixOutPer; ++q) {
-    const int e = (int)threadIdx.x + q * (int)blockDim.x, ec = e < nout ? e : 0;
+  for (int q = 0; q < kMixPasses; ++q) {
+    const int e = ((int)threadIdx.x >> 2) + q * opp, ec = e < nout ? e : 0;
     const int sl = ec / per_slot, r = ec - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
     const int tsl = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + sl;
     const int64_t j = (int64_t)(tsl < ntu ? tsl : ntu - 1) * u.bj + jj;
-    const uint16_t* nm = u.nrm + m * u.nrm_stride + j;
-#pragma unroll
-    for (int s = 0; s < kMixMaxHc; ++s) nrv[q][s] = nm[(int64_t)(s < u.hc ? s : u.hc - 1) * u.H];
+    nrv[q] = q * opp < nout ? u.nrm[m * u.nrm_stride + (int64_t)qsc * u.H + j] : (uint16_t)0;
   }
   // the up weights' bf16 operands, made while the bottleneck is outstanding
   // (the plan gives every lane one full batch of kNJ single chunks), so that
@@ -363,23 +364,29 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
       if (g * 4 + i < u.M) gls[(g * 4 + i) * T + grp * 16 + n] = round_bf16(acc[i]);
   }
   __syncthreads();
+  // the epilogue of x/fp4x_kernels.py:486-493 as hc_gate_mean computes it:
+  // lane s of a quad makes stream s's term bf16(nrm * bf16(sigmoid(g))) (one
+  // sigmoid per lane instead of hc in a row), and the quad's lane 0 adds the
+  // terms in stream order from 0.0f, so every output equals hc_gate_mean's
+  // bit for bit
 #pragma unroll
-  for (int q = 0; q < kMixOutPer; ++q) {
-    const int e = (int)threadIdx.x + q * (int)blockDim.x;
-    const int sl = e / per_slot, r = e - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
+  for (int q = 0; q < kMixPasses; ++q) {
+    if (q * opp >= nout) break;                    // (uniform: the same in every thread)
+    const int e = ((int)threadIdx.x >> 2) + q * opp, ec = e < nout ? e : 0;
+    const int sl = ec / per_slot, r = ec - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
     const int tsl = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + sl;
-    if (e >= nout || tsl >= ntu) continue;
-    const int64_t j = (int64_t)tsl * u.bj + jj;
-    const float* gm = gl + (size_t)sl * u.M * T + m * T + jj;
-    auto nrm_s = [&](int s) {
-      uint16_t v = nrv[q][0];
-#pragma unroll
-      for (int t = 1; t < kMixMaxHc; ++t)
-        if (s == t) v = nrv[q][t];
-      return bf16_to_f32(v);
-    };
-    u.out[(int64_t)m * u.H + j] =
-        ok ? hc_gate_mean([&](int s) { return gm[s * u.bj]; }, nrm_s, u.hc) : (uint16_t)0x7fc0u;
+    const float gv = gl[(size_t)sl * u.M * T + m * T + qsc * u.bj + jj];
+    const float term = round_bf16(bf16_to_f32(nrv[q]) * round_bf16(sigmoid_f32(gv)));
+    const float t1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0x55, 0xF, 0xF, false));
+    const float t2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0xAA, 0xF, 0xF, false));
+    const float t3 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0xFF, 0xF, 0xF, false));
+    if (qs != 0 || e >= nout || tsl >= ntu) continue;
+    float tot = 0.0f;
+    tot += term;
+    if (u.hc > 1) tot += t1;
+    if (u.hc > 2) tot += t2;
+    if (u.hc > 3) tot += t3;
+    u.out[(int64_t)m * u.H + (int64_t)tsl * u.bj + jj] = ok ? f32_to_bf16(tot / (float)u.hc) : (uint16_t)0x7fc0u;
   }
 }
 
@@ -561,7 +568,7 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   const bool local = switches().hc_xcd && C <= 8 && tiles_d <= cus && al(part, 8) &&
                      (int64_t)tiles_d * C * M * 16 * 2 <= (int64_t)ksplit * 16 * N;
   const int R = 8 / WT, ntu = H / bj, D = local ? 8 * ((tiles_d + 7) / 8) * C : tiles_d * C;
-  if (hc > kMixMaxHc || R * M * bj > kMixOutPer * 512) return two();
+  if (hc > kMixMaxHc || R * M * bj > kMixPasses * 128) return two();
   const int need_u = (ntu + R - 1) / R;
   const bool split = D + need_u <= cus;
   const int P = split ? D + need_u : (D > need_u ? D : need_u);
