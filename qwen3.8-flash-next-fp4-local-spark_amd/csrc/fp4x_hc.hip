@@ -32,6 +32,24 @@ __device__ __forceinline__ uint16_t hc_gate_mean(GF g, NF nrm, int hc) {
   return f32_to_bf16(tot / (float)hc);
 }
 
+// The same mean with the hc terms made by a quad of lanes: lane s of each
+// quad passes stream s's term bf16(nrm_s * bf16(sigmoid(g_s))) (any value
+// for s >= hc); lane 0 of the quad gets the bf16 mean, which equals
+// hc_gate_mean's bit for bit (the terms added in stream order from 0.0f).
+// Every lane of the wave must call it (DPP quad broadcasts).
+__device__ __forceinline__ uint16_t hc_quad_mean(float term, int hc) {
+  const float t1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0x55, 0xF, 0xF, false));
+  const float t2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0xAA, 0xF, 0xF, false));
+  const float t3 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0xFF, 0xF, 0xF, false));
+  float tot = 0.0f;
+  tot += term;
+  if (hc > 1) tot += t1;
+  if (hc > 2) tot += t2;
+  if (hc > 3) tot += t3;
+  return f32_to_bf16(tot / (float)hc);
+}
+__device__ __forceinline__ float hc_gate_term(float nrm, float g) { return round_bf16(nrm * round_bf16(sigmoid_f32(g))); }
+
 struct HcUpArgs {
   const uint16_t* bot; int64_t bot_stride;
   PlaneArgs pa;          // interleaved q [hc*H, K], s [hc*H, K/64]
@@ -96,14 +114,17 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
       if (g * 4 + i < p.M) gl[(g * 4 + i) * T + grp * 16 + n] = round_bf16(acc[i]);
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < p.M * p.bj; t += blockDim.x) {
-    const int m = t / p.bj, jj = t - m * p.bj;
+  // the epilogue on quads of lanes (hc_quad_mean): lane s of a quad takes
+  // stream s of one output, blockDim / 4 outputs per pass
+  const int qs = (int)threadIdx.x & 3, qsc = qs < p.hc ? qs : p.hc - 1, opp = (int)blockDim.x >> 2;
+  for (int t0 = 0; t0 < p.M * p.bj; t0 += opp) {
+    const int t = t0 + ((int)threadIdx.x >> 2), tc = t < p.M * p.bj ? t : 0;
+    const int m = tc / p.bj, jj = tc - m * p.bj;
     const int64_t j = (int64_t)blockIdx.x * p.bj + jj;
-    const float* gm = gl + m * T + jj;
-    const uint16_t* nm = p.nrm + m * p.nrm_stride + j;
-    const int64_t H = p.H;
-    p.out[(int64_t)m * p.H + j] =
-        hc_gate_mean([&](int s) { return gm[s * p.bj]; }, [&](int s) { return bf16_to_f32(nm[s * H]); }, p.hc);
+    const float term = hc_gate_term(bf16_to_f32(p.nrm[m * p.nrm_stride + (int64_t)qsc * p.H + j]),
+                                    gl[m * T + qsc * p.bj + jj]);
+    const uint16_t v = hc_quad_mean(term, p.hc);
+    if (qs == 0 && t < p.M * p.bj) p.out[(int64_t)m * p.H + j] = v;
   }
 }
 
@@ -364,29 +385,18 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
       if (g * 4 + i < u.M) gls[(g * 4 + i) * T + grp * 16 + n] = round_bf16(acc[i]);
   }
   __syncthreads();
-  // the epilogue of x/fp4x_kernels.py:486-493 as hc_gate_mean computes it:
-  // lane s of a quad makes stream s's term bf16(nrm * bf16(sigmoid(g))) (one
-  // sigmoid per lane instead of hc in a row), and the quad's lane 0 adds the
-  // terms in stream order from 0.0f, so every output equals hc_gate_mean's
-  // bit for bit
+  // the epilogue of x/fp4x_kernels.py:486-493 on quads of lanes
+  // (hc_quad_mean: one sigmoid per lane instead of hc in a row, the terms
+  // added in stream order, so every output equals hc_gate_mean's bit for bit)
 #pragma unroll
   for (int q = 0; q < kMixPasses; ++q) {
     if (q * opp >= nout) break;                    // (uniform: the same in every thread)
     const int e = ((int)threadIdx.x >> 2) + q * opp, ec = e < nout ? e : 0;
     const int sl = ec / per_slot, r = ec - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
     const int tsl = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + sl;
-    const float gv = gl[(size_t)sl * u.M * T + m * T + qsc * u.bj + jj];
-    const float term = round_bf16(bf16_to_f32(nrv[q]) * round_bf16(sigmoid_f32(gv)));
-    const float t1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0x55, 0xF, 0xF, false));
-    const float t2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0xAA, 0xF, 0xF, false));
-    const float t3 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0xFF, 0xF, 0xF, false));
-    if (qs != 0 || e >= nout || tsl >= ntu) continue;
-    float tot = 0.0f;
-    tot += term;
-    if (u.hc > 1) tot += t1;
-    if (u.hc > 2) tot += t2;
-    if (u.hc > 3) tot += t3;
-    u.out[(int64_t)m * u.H + (int64_t)tsl * u.bj + jj] = ok ? f32_to_bf16(tot / (float)u.hc) : (uint16_t)0x7fc0u;
+    const uint16_t v = hc_quad_mean(hc_gate_term(bf16_to_f32(nrv[q]), gl[(size_t)sl * u.M * T + m * T + qsc * u.bj + jj]),
+                                     u.hc);
+    if (qs == 0 && e < nout && tsl < ntu) u.out[(int64_t)m * u.H + (int64_t)tsl * u.bj + jj] = ok ? v : (uint16_t)0x7fc0u;
   }
 }
 
