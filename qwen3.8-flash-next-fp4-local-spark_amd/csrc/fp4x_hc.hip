@@ -101,8 +101,10 @@ __global__ __launch_bounds__(1024) void hc_up_mfma_kernel(HcUpArgs p) {
   }
   // wave-order reduction within each row group
   float* gred = red + (size_t)grp * (KW > 1 ? KW - 1 : 0) * 256;
-  if (wv > 0) reinterpret_cast<f32x4_t*>(gred)[(wv - 1) * 64 + lane] = acc;
-  __syncthreads();
+  if constexpr (KW > 1) {                          // (one wave per row group: nothing to add)
+    if (wv > 0) reinterpret_cast<f32x4_t*>(gred)[(wv - 1) * 64 + lane] = acc;
+    __syncthreads();
+  }
   if (wv == 0) {
 #pragma unroll
     for (int w = 1; w < KW; ++w) {
@@ -371,8 +373,10 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
     acc = mfma16(xp[1], make_uint4(wq[j][4], wq[j][5], wq[j][6], wq[j][7]), acc);
   }
   float* gred = red + ((size_t)slot * (T / 16) + grp) * (KW > 1 ? KW - 1 : 0) * 256;
-  if (wv > 0) reinterpret_cast<f32x4_t*>(gred)[(wv - 1) * 64 + lane] = acc;
-  __syncthreads();
+  if constexpr (KW > 1) {                          // (one wave per row group: nothing to add)
+    if (wv > 0) reinterpret_cast<f32x4_t*>(gred)[(wv - 1) * 64 + lane] = acc;
+    __syncthreads();
+  }
   if (wv == 0) {
 #pragma unroll
     for (int w = 1; w < KW; ++w) {
