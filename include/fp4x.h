@@ -241,13 +241,16 @@ int fp4x_hc_up(const void* bot, int64_t bot_stride, const void* qi, const void* 
  * afterwards.  The single launch keeps one tile ticket per 128-byte line,
  * ticket t at 32 t, and at S = (n_tickets - 32 * (CUs + 1)) rounded down to
  * a multiple of 32 an unused word (S), a status word (S + 1) and one
- * 128-byte line per workgroup (its generation flag, its ack word and a down
- * tile's generation), so it needs S >= 32 * ceil(N / 16); with fewer it
- * makes the two calls.  (S depends on the buffer alone: calls of any shape on
- * one buffer agree on it.)  part: the single launch keeps the down partials
- * of each tile on one XCD as 64-bit (partial, generation tag) pairs (8-byte
- * aligned part; 2 * ceil(N / 16) * 16 * M * (parts per tile) floats, else
- * device-coherent partials).  A workgroup whose flag wait gives up (only
+ * 128-byte line per workgroup slot (its generation flag, its ack word and
+ * its call count), so it needs S >= 32 * ceil(N / 16); with fewer it makes
+ * the two calls.  (S depends on the buffer alone: calls of any shape on one
+ * buffer agree on it.)  The launch has one workgroup per CU; every call
+ * counts in every slot, so all slots agree on the call's count, which tags
+ * the down partials.  part: zero before the first call; the single launch
+ * keeps the down partials of each tile on one XCD as 64-bit (partial, tag)
+ * pairs after the two calls' slots (8-byte aligned part; 3 * ceil(N / 16) *
+ * 16 * M * (parts per tile) + 2 floats, else device-coherent partials).  A
+ * workgroup whose flag wait gives up (only
  * possible when other work holds the GPU's CUs for about a second) writes NaN
  * to its outputs and sets bit 0 of the status word; a down tile whose closer
  * gives up waiting for a part's pairs (a part placed on another XCD, or held

@@ -221,7 +221,7 @@ static bool al(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & 
 //     outputs and sets bit 0 of the status word sync[1].
 constexpr int kMixFlagStride = 32;               // int32 between flags: one 128-byte line each
 constexpr int kMixAckAt = 16;                    // a workgroup's ack word, 64 bytes after its flag
-constexpr int kMixGenAt = 8;                     // a down tile's generation word, on the flag lines
+constexpr int kMixCountAt = 24;                  // a workgroup slot's call count (every call counts in every slot)
 
 struct HcMixArgs {
   GemvLaunch d;          // down: x, q, s, di (out), bot (out2), lr, hc, split-K slots and tickets
@@ -231,9 +231,10 @@ struct HcMixArgs {
                          // [kMixFlagStride * (w + 1)] generation flag of workgroup w,
                          // [kMixFlagStride * (w + 1) + kMixAckAt] its ack word (tile advances of the
                          // calls it has started),
-                         // [kMixFlagStride * (t + 1) + kMixGenAt] down tile t's generation (XCD-local slots)
-  SplitLocal loc;        // XCD-local slots: generations, tags, status
+                         // [kMixFlagStride * (w + 1) + kMixCountAt] slot w's call count (the pairs' tags)
+  SplitLocal loc;        // XCD-local slots: pairs, status
   int C, D, tiles_d, R, spin_limit;
+  int P;                 // workgroups with work; the grid has one per CU, the rest only count the call
 };
 
 constexpr int kMixMaxHc = 4;                     // streams the single-launch mixer takes
@@ -249,7 +250,7 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   using F = FmtW8<F16S>;
   constexpr int DP = 4 * KW;
   extern __shared__ __align__(16) uint16_t lds[];
-  __shared__ int s_ok;
+  __shared__ int s_ok, s_count;
   char* base = reinterpret_cast<char*>(lds);
   const HcUpArgs& u = a.u;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   const int slot = wave / WT, ws = wave - slot * WT, grp = ws / KW, wv = ws - grp * KW;
   // up tiles fill the workgroups from the last one down, so that workgroups
   // without a down item take them first (they issue the loads at once)
-  const int ntu = u.H / u.bj, tu = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + slot;
+  const int ntu = u.H / u.bj, tu = (a.P - 1 - (int)blockIdx.x) * a.R + slot;
   const int tuc = tu < ntu ? tu : ntu - 1;          // padding slots recompute the last tile, store nothing
   const int nch = u.K / F::KPC, cw = wv * 4 + g;
   const int J = ((nch + CPS - 1) / CPS + DP - 1) / DP;
@@ -266,10 +267,19 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   int* flag = a.sync + kMixFlagStride * (blockIdx.x + 1);
   int gen = 0;                                      // the value this call's advances give the flag
   if (threadIdx.x == 0) {
-    gen = (int)((uint32_t)__hip_atomic_load(flag + kMixAckAt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
-                (uint32_t)a.tiles_d);
-    __hip_atomic_store(flag + kMixAckAt, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the call's count: every call's grid holds every workgroup slot and each
+    // slot counts every call in its own word, so all slots agree on it
+    // whenever they start (it tags the XCD-local partials)
+    const int count = __hip_atomic_load(flag + kMixCountAt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    __hip_atomic_store(flag + kMixCountAt, count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_count = count;
+    if ((int)blockIdx.x < a.P) {
+      gen = (int)((uint32_t)__hip_atomic_load(flag + kMixAckAt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
+                  (uint32_t)a.tiles_d);
+      __hip_atomic_store(flag + kMixAckAt, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
+  if ((int)blockIdx.x >= a.P) return;               // a slot without work: it only counts the call
 
   // 1. one down item in each of the first D workgroups (the critical path:
   //    its loads go out first)
@@ -287,11 +297,11 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
     }
   }
   if (t >= 0) {
-    if (w8_splitk_item<F16S, 8, 2, EpiHcDownShared, LOCAL>(a.d, a.C, t, c, base, a.loc)) {
+    if (w8_splitk_item<F16S, 8, 2, EpiHcDownShared, LOCAL>(a.d, a.C, t, c, base, a.loc, &s_count)) {
       wait_vmcnt<0>();                              // the tile's bottleneck stores have completed
       // this tile's advance of every workgroup's flag (the flags reach the
       // call's generation when every tile has advanced them)
-      for (int w = lane; w < (int)gridDim.x; w += 64)
+      for (int w = lane; w < a.P; w += 64)
         __hip_atomic_fetch_add(a.sync + kMixFlagStride * (w + 1), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -321,7 +331,7 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   for (int q = 0; q < kMixPasses; ++q) {
     const int e = ((int)threadIdx.x >> 2) + q * opp, ec = e < nout ? e : 0;
     const int sl = ec / per_slot, r = ec - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
-    const int tsl = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + sl;
+    const int tsl = (a.P - 1 - (int)blockIdx.x) * a.R + sl;
     const int64_t j = (int64_t)(tsl < ntu ? tsl : ntu - 1) * u.bj + jj;
     nrv[q] = q * opp < nout ? u.nrm[m * u.nrm_stride + (int64_t)qsc * u.H + j] : (uint16_t)0;
   }
@@ -397,7 +407,7 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
     if (q * opp >= nout) break;                    // (uniform: the same in every thread)
     const int e = ((int)threadIdx.x >> 2) + q * opp, ec = e < nout ? e : 0;
     const int sl = ec / per_slot, r = ec - sl * per_slot, m = r / u.bj, jj = r - m * u.bj;
-    const int tsl = ((int)gridDim.x - 1 - (int)blockIdx.x) * a.R + sl;
+    const int tsl = (a.P - 1 - (int)blockIdx.x) * a.R + sl;
     const uint16_t v = hc_quad_mean(hc_gate_term(bf16_to_f32(nrv[q]), gl[(size_t)sl * u.M * T + m * T + qsc * u.bj + jj]),
                                      u.hc);
     if (qs == 0 && e < nout && tsl < ntu) u.out[(int64_t)m * u.H + (int64_t)tsl * u.bj + jj] = ok ? v : (uint16_t)0x7fc0u;
@@ -420,7 +430,7 @@ static bool launch_hc_mix(const HcMixArgs& a, int P, size_t lds, hipStream_t st)
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3(P), dim3(512), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3(device_cus()), dim3(512), lds, st, a);   // P of them have work
   return true;
 }
 
@@ -580,7 +590,7 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   // (partial, generation) pairs in the caller's slot buffer; the down items
   // then span 8 residues x the most tiles a residue holds x C workgroups
   const bool local = switches().hc_xcd && C <= 8 && tiles_d <= cus && al(part, 8) &&
-                     (int64_t)tiles_d * C * M * 16 * 2 <= (int64_t)ksplit * 16 * N;
+                     (int64_t)tiles_d * C * M * 16 * 3 + 2 <= (int64_t)ksplit * 16 * N;
   const int R = 8 / WT, ntu = H / bj, D = local ? 8 * ((tiles_d + 7) / 8) * C : tiles_d * C;
   if (hc > kMixMaxHc || R * M * bj > kMixPasses * 128) return two();
   const int need_u = (ntu + R - 1) / R;
@@ -603,8 +613,9 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   a.u.out = static_cast<uint16_t*>(out);
   a.u.M = M; a.u.K = lr; a.u.H = H; a.u.hc = hc; a.u.bj = bj;
   a.sync = tickets + sync_at;
-  a.loc.gen = a.sync + kMixFlagStride + kMixGenAt;
-  a.loc.gstride = kMixFlagStride;
+  // part: the two-launch path's slots of this shape, then the pairs (zero
+  // before the first call: no zero word carries a tag)
+  a.loc.pairs = reinterpret_cast<uint64_t*>(part + (((int64_t)tiles_d * C * M * 16 + 1) & ~(int64_t)1));
   a.loc.status = a.sync + 1;
   // the closer waits only for parts of its tile that were dispatched before it
   // and wait on nothing, so its reads keep a floor whatever the flag limit
@@ -613,6 +624,7 @@ int fp4x_hc_mix(const void* x, int64_t x_stride, const void* q, const void* s, i
   a.D = D;
   a.tiles_d = tiles_d;
   a.R = R;
+  a.P = P;
   a.spin_limit = switches().hc_spin_limit;
   hipStream_t st = (hipStream_t)stream;
   auto go = [&](auto f16s, auto loc) {

@@ -287,21 +287,20 @@ __device__ __forceinline__ void stream_read_x(uint32_t xa, uint4& x0a, uint4& x0
 // its last part (c = C - 1, the highest workgroup index of the tile, so every
 // other part was dispatched before it and none of them waits on anything).
 // Parts c < C - 1 store their [M x 16] partials as 64-bit (value, tag) pairs,
-// each pair in one store, and end; the tag is the complement of the tile's
-// call generation (gen, device-coherent, read by every part at its start and
-// advanced by the closer).  The closer reads the pairs from L2 until every
+// each pair in one store, and end; the tag is the complement of the call's
+// count, which every workgroup of every call counts in a word of its own
+// (*call_count).  The closer reads the pairs until every
 // tag is its call's (s_sleep between reads, at most spin_limit reads: the
 // caller's flag limit, but never under 65,536), adds them in slot order with its
-// own partial last, runs the epilogue and advances gen.  That replaces the
+// own partial last and runs the epilogue.  That replaces the
 // slot stores' completion wait, the device-scope ticket and a separate read
 // of the slots (the served mixer 9.43 -> 9.06 us, the 640-row one 11.91 ->
 // 11.83).  A closer whose reads reach spin_limit (a part that ran on
 // another XCD, so its pairs are in another L2, or one that never got a CU)
-// writes NaN for the tile and sets bit 1 of *status; gen still advances, so
-// the next call starts clean.
+// writes NaN for the tile and sets bit 1 of *status; the next call starts
+// clean.
 struct SplitLocal {
-  int* gen;            // per-tile generation words, gstride ints apart
-  int gstride;
+  uint64_t* pairs;     // [tiles][C][M][16] (partial, tag) pairs
   int* status;
   int spin_limit;      // the closer's reads of the other parts' pairs before it gives up
 };
@@ -332,7 +331,7 @@ __device__ __forceinline__ void read_pairs_7(const uint64_t* const (&a)[7], uint
 // (wave 0 of the last-arriving workgroup), false elsewhere.
 template <bool F16S, int WPG, int JW, class Epi, bool LOCAL = false>
 __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t, int c, char* base,
-                                               const SplitLocal& loc = SplitLocal{}) {
+                                               const SplitLocal& loc = SplitLocal{}, const int* call_count = nullptr) {
   constexpr int UW = WPG * JW;                       // units per workgroup
   constexpr int XR = UW * 256 + 64;                  // LDS bytes per activation row
   static_assert(UW % 4 == 0, "activation slice in whole 1 KB pieces");
@@ -347,9 +346,6 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
     const int m = i / PPR, u = i - m * PPR;
     dma_b128(p.x + (int64_t)m * p.x_stride + (int64_t)(c * UW + u * 4) * 128 + lane * 8, base + m * XR + u * 1024);
   }
-  int gen = 0;                                       // LOCAL: the tile's generation before this call
-  if constexpr (LOCAL)
-    if (wave == 0) gen = __hip_atomic_load(loc.gen + (int64_t)t * loc.gstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int lim = p.N - 1 - t * 16;                  // rows past N read row N - 1
   const int64_t row = (int64_t)t * 16 + (n < lim ? n : lim);
   const int u0 = c * UW + wave * JW;
@@ -408,13 +404,15 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
   if constexpr (LOCAL) {
     // slot c of tile t: [M][16] 64-bit pairs (partial bits, tag), each
     // stored in one single-copy-atomic store; the tag is the complement of
-    // this call's generation (as a float, a negative NaN pattern, so float
-    // slots left in the buffer by the two-launch path do not pass for one).
-    // The closer is the tile's last part, which reads the others' pairs
-    // until every tag is this call's and adds its own partial last (slot order)
-    const int want = __builtin_amdgcn_readfirstlane(gen) + 1;
-    const uint32_t tag = ~(uint32_t)want;
-    uint64_t* pairs = reinterpret_cast<uint64_t*>(p.part) + (int64_t)t * C * p.M * 16;
+    // the call's count (*call_count, in LDS, one more every call on every
+    // workgroup of the grid), so no pair of an earlier call, whatever its
+    // shape, and no zero word passes for this call's (and, as a float, it is
+    // a negative NaN pattern, which no float slot of the two-launch path
+    // holds).  The closer is the tile's last part, which reads the others'
+    // pairs until every tag is this call's and adds its own partial last
+    // (slot order)
+    const uint32_t tag = ~(uint32_t)__builtin_amdgcn_readfirstlane(*call_count);
+    uint64_t* pairs = loc.pairs + (int64_t)t * C * p.M * 16;
     if (c != C - 1) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -459,10 +457,7 @@ __device__ __forceinline__ bool w8_splitk_item(const GemvLaunch& p, int C, int t
       const int64_t orow = (int64_t)t * 16 + nn;
       if (e < p.M * 16 && orow < p.N) Epi::apply(p, 0, m, orow, ok ? tot * p.gs : __builtin_nanf(""));
     }
-    if (lane == 0) {
-      if (!ok) __hip_atomic_fetch_or(loc.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(loc.gen + (int64_t)t * loc.gstride, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (lane == 0 && !ok) __hip_atomic_fetch_or(loc.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
   } else {
 #pragma unroll

@@ -356,7 +356,7 @@ class HCFused:
 
     def __init__(self, device, n_down=336, max_m=16, bn=32, max_ksplit=16):
         self.n_down, self.max_m, self.max_ksplit = n_down, max_m, max_ksplit
-        self.part = torch.empty(max_ksplit * MAX_M * n_down, dtype=torch.float32, device=device)
+        self.part = torch.zeros(max_ksplit * MAX_M * n_down, dtype=torch.float32, device=device)
         # one ticket per 16-row tile (the single-launch mixer: one per 128-byte
         # line, 2 * n_down ints); its count, status word and one 128-byte flag
         # line per workgroup (at most one workgroup per CU) in the last

@@ -23,7 +23,9 @@
   the two-launch path, with no NaN and no status bit;
 * single launches whose down tiles split into 2 and 8 K parts (hidden sizes
   1024 and 4096), whose closers add 1 and 7 other parts' tagged partials,
-  are bit-identical to the two-launch path.
+  are bit-identical to the two-launch path;
+* single launches of different row counts and batch sizes that share one
+  scratch are bit-identical to the two-launch path.
 """
 import ctypes
 
@@ -282,6 +284,35 @@ def test_mix_parts_per_tile(gpu, F, h):
             assert torch.equal(a, b), h
         assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
     assert took_single_launch(fx), h
+    assert not fx.wait_timeouts()
+
+
+def test_mix_shapes_share_one_buffer(gpu, F):
+    """Single launches of different row counts and batch sizes on one scratch
+    (so earlier calls leave partials of other layouts where a call keeps its
+    own), alternating with the two-launch path: every call equals the
+    two-launch result bit for bit, with no NaN and no status bit.  The
+    partials' tags come from the call's count, which every call advances in
+    every workgroup slot, so no earlier call's partial passes for a later
+    one's."""
+    rng = np.random.default_rng(515)
+    fx = F.HCFused(gpu, n_down=ND, max_ksplit=KS)
+    shapes = {}
+    for nd, lr, ks in ((ND, LR, KS), (336, 320, 8)):
+        (qd, sd), (qu, su) = layer(rng, nd=nd, lr=lr)
+        qi, si = F.HCFused.interleave_up(dev(qu), dev(su), HC, 8)
+        shapes[nd] = (dev(qd), dev(sd), qi, si, lr, ks)
+    for i, (nd, M) in enumerate(((336, 16), (ND, 3), (336, 3), (ND, 1), (336, 1), (ND, 16), (336, 3), (ND, 3))):
+        qd, sd, qi, si, lr, ks = shapes[nd]
+        x_t = bf16_dev(act(rng, M, HC * H)[0])
+        cfg = (32, 256, ks, 4)
+        di, bot = fx.down(x_t, qd, sd, lr, HC, cfg)
+        bi = F.HCFused.up(bot, qi, si, x_t, HC, (8, 64, 4))
+        one = fx.mix(x_t, qd, sd, lr, HC, qi, si, x_t, cfg)
+        for a, b in zip(one, (di, bot, bi)):
+            assert torch.equal(a, b), (i, nd, M)
+        assert int(fx.tickets[:fx._status_at].abs().sum()) == 0
+    assert took_single_launch(fx)
     assert not fx.wait_timeouts()
 
 
