@@ -261,8 +261,7 @@ __global__ __launch_bounds__(512) void hc_mix_kernel(HcMixArgs a) {
   // without a down item take them first (they issue the loads at once)
   const int ntu = u.H / u.bj, tu = (a.P - 1 - (int)blockIdx.x) * a.R + slot;
   const int tuc = tu < ntu ? tu : ntu - 1;          // padding slots recompute the last tile, store nothing
-  const int nch = u.K / F::KPC, cw = wv * 4 + g;
-  const int J = ((nch + CPS - 1) / CPS + DP - 1) / DP;
+  const int cw = wv * 4 + g;
   const int64_t urow = (int64_t)tuc * T + grp * 16 + n;
   int* flag = a.sync + kMixFlagStride * (blockIdx.x + 1);
   int gen = 0;                                      // the value this call's advances give the flag

@@ -90,7 +90,6 @@ __global__ __launch_bounds__(kThreads) void refine_kernel(RefineArgs p) {
 //      More than 4096 such slices or candidates (massive ties), or fewer than
 //      C slices, take the exact threshold path over the whole row instead;
 //      rows of at most 4096 elements sort the whole row.
-constexpr int kTkThreads = 1024;
 constexpr int kTkCap = 4096;      // candidates (and candidate slices) per row
 constexpr int kTkMaxSlices = 32768;
 
@@ -640,7 +639,7 @@ __device__ void tk_select_set_window(const uint32_t* ck, const int* cidx, int n_
   __syncthreads();
   int before = 0;
   for (int w = 0; w < wave; ++w) before += slots[w];
-  const bool in = up || (tie && before + __popcll(bt & below) < C - above);
+  const bool in = up || (tie && before + (int)__popcll(bt & below) < C - above);
   const uint64_t bi = __ballot(in);
   if (lane == 0) ext[wave] = __popcll(bi);          // (the window round's reads of ext[0, kRsWaves) are done)
   __syncthreads();
@@ -664,7 +663,7 @@ __device__ int rs_rank256(const uint32_t* a, int n, int* part) {
   for (int j = j0; j < j1; ++j) r += a[j] > mine ? 1 : 0;
   part[threadIdx.x] = r;
   __syncthreads();
-  if (threadIdx.x >= n) return -1;
+  if ((int)threadIdx.x >= n) return -1;
   int rank = 0;
   for (int p = 0; p < parts; ++p) rank += part[p * n2 + threadIdx.x];
   return rank;
