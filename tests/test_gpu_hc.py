@@ -38,7 +38,7 @@ from oracle import hc as ohc
 from oracle import ordered
 from oracle import quant as oq
 
-from gpu_helpers import act, assert_tol, bf16_bits, bf16_dev, dev, to_f32, path_switch
+from gpu_helpers import act, bf16_bits, bf16_dev, dev, to_f32, path_switch
 
 pytestmark = pytest.mark.gpu
 

@@ -6,7 +6,6 @@ and a shorter head, over the same static array); a request above the limit is
 rejected before anything runs."""
 import ctypes
 
-import numpy as np
 import pytest
 import torch
 
