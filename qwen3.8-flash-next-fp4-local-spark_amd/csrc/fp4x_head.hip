@@ -648,16 +648,18 @@ __device__ void tk_select_set_window(const uint32_t* ck, const int* cidx, int n_
   if (in) out[pos + __popcll(bi & below)] = (int64_t)cidx[t];
 }
 
-// Descending ranks of n <= 256 distinct keys a[0, n) in LDS: thread (t, q)
+// Descending ranks of n <= 256 distinct keys a[0, n) in LDS (32-bit bf16
+// composites or 64-bit fp32 ones): thread (t, q)
 // counts the keys above a[t] among a quarter (n2 = 256), an eighth (128) or a
 // sixteenth (<= 64) of them; the partial counts meet in part[1024].  Returns
 // the rank on threads t < n of the first part (threadIdx.x < n), else -1.
-__device__ int rs_rank256(const uint32_t* a, int n, int* part) {
+template <class K>
+__device__ int rs_rank256(const K* a, int n, int* part) {
   int n2 = 64;
   while (n2 < n) n2 <<= 1;
   const int parts = kRsThreads / n2, span = n2 / parts;
   const int t = threadIdx.x % n2, q = threadIdx.x / n2;
-  const uint32_t mine = t < n ? a[t] : 0xffffffffu;
+  const K mine = t < n ? a[t] : ~K(0);
   int r = 0;
   const int j0 = q * span, j1 = min(j0 + span, n);
   for (int j = j0; j < j1; ++j) r += a[j] > mine ? 1 : 0;
@@ -904,7 +906,14 @@ __global__ __launch_bounds__(kRsThreads) void topk_rowsel_kernel(const typename 
     return;
   }
   if constexpr (F32) {
-    tk_finish(cand, n_c, C, out);       // (full key, index) composites
+    // (full key, index) composites: up to 256 (the draft head's top-64) are
+    // ranked directly, each counting the composites above it; more are sorted
+    if (n_c <= 256) {
+      const int r = rs_rank256(cand, n_c, reinterpret_cast<int*>(wh));
+      if (r >= 0 && r < C) out[r] = (int64_t)(0xffffffffu - (uint32_t)(cand[threadIdx.x] & 0xffffffffu));
+    } else {
+      tk_finish(cand, n_c, C, out);
+    }
     return;
   }
   if (set_only && n_c <= kRsThreads) {             // the set only: no sort
