@@ -637,14 +637,16 @@ __device__ void tk_select_set_window(const uint32_t* ck, const int* cidx, int n_
   const uint64_t bt = __ballot(tie);
   if (lane == 0) slots[wave] = __popcll(bt);
   __syncthreads();
-  int before = 0;
-  for (int w = 0; w < wave; ++w) before += slots[w];
+  int before = 0;                                   // (all 16 counts read at once, masked)
+#pragma unroll
+  for (int w = 0; w < kRsWaves; ++w) before += w < wave ? slots[w] : 0;
   const bool in = up || (tie && before + (int)__popcll(bt & below) < C - above);
   const uint64_t bi = __ballot(in);
   if (lane == 0) ext[wave] = __popcll(bi);          // (the window round's reads of ext[0, kRsWaves) are done)
   __syncthreads();
   int pos = 0;
-  for (int w = 0; w < wave; ++w) pos += (int)ext[w];
+#pragma unroll
+  for (int w = 0; w < kRsWaves; ++w) pos += w < wave ? (int)ext[w] : 0;
   if (in) out[pos + __popcll(bi & below)] = (int64_t)cidx[t];
 }
 
