@@ -664,12 +664,19 @@ __device__ int rs_rank256(const K* a, int n, int* part) {
   const K mine = t < n ? a[t] : ~K(0);
   int r = 0;
   const int j0 = q * span, j1 = min(j0 + span, n);
-  for (int j = j0; j < j1; ++j) r += a[j] > mine ? 1 : 0;
+  int j = j0;
+  for (; j + 4 <= j1; j += 4) {                     // four reads in flight per step
+    const K a0 = a[j], a1 = a[j + 1], a2 = a[j + 2], a3 = a[j + 3];
+    r += (a0 > mine ? 1 : 0) + (a1 > mine ? 1 : 0) + (a2 > mine ? 1 : 0) + (a3 > mine ? 1 : 0);
+  }
+  for (; j < j1; ++j) r += a[j] > mine ? 1 : 0;
   part[threadIdx.x] = r;
   __syncthreads();
   if ((int)threadIdx.x >= n) return -1;
   int rank = 0;
-  for (int p = 0; p < parts; ++p) rank += part[p * n2 + threadIdx.x];
+  for (int p = 0; p < parts; p += 4)                // parts is 4, 8 or 16
+    rank += part[p * n2 + threadIdx.x] + part[(p + 1) * n2 + threadIdx.x] + part[(p + 2) * n2 + threadIdx.x] +
+            part[(p + 3) * n2 + threadIdx.x];
   return rank;
 }
 
