@@ -206,7 +206,7 @@ int fp4x_mx8_linear(const void* x, int64_t x_stride, const void* w, const void* 
   GemvLaunch p = base_launch(FP4X_FMT_MX8, x, x_stride, out, out_dtype, N, M, N, K, ksplit, part, tickets);
   p.pa.w0 = static_cast<const uint8_t*>(w);
   p.pa.s = static_cast<const uint8_t*>(s);
-  if (launch_rows_wide<FmtMX8>(p, (hipStream_t)stream)) return check_launch("mx8_rows");    // many rows, M <= 2
+  if (launch_rows_wide<FmtMX8>(p, (hipStream_t)stream)) return check_launch("mx8_rows");    // 16-20 rows per CU, M = 1
   if (launch_mx8_stream_entry(p, (hipStream_t)stream)) return check_launch("mx8_stream");   // many tiles
   if (launch_rows_gemv<FmtMX8>(p, 1, (hipStream_t)stream)) return check_launch("mx8_rows");  // fewer rows
   if (launch_mx8_stream_tile_entry(p, (hipStream_t)stream)) return check_launch("mx8_stream"); // 1/2-1 tile per CU

@@ -549,6 +549,18 @@ bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
   RowsLaunch a;
   if (!rows_launch_args(p, batch, F::KPC, a)) return false;
   const int cus = device_cus();
+  if constexpr (std::is_same<F, FmtMX8>::value || std::is_same<F, FmtNV4>::value) {
+    // MXFP8 and NVFP4 from 10 rows per CU at M >= 3 with rows of K >= 4096,
+    // and at M = 4 with any K, stream instead (one tile per workgroup): the
+    // two-row workgroups then read the activations more often than they
+    // save.  Graph replays from HBM, us, streaming against this kernel:
+    // MXFP8 [2560 x 6144] M = 3 / 4 7.15 / 7.34 against 7.59 / 8.48,
+    // [2560 x 2560] M = 4 4.87 against 5.25; NVFP4 [2560 x 6144] 6.40 / 6.60
+    // against 6.75 / 7.81, [2560 x 2560] M = 4 4.58 against 4.97, [4096 x
+    // 2560] M = 4 5.78 against 6.04 (at M = 3 and K = 2560 this kernel ties or
+    // wins: MXFP8 [2048 x 2560] 4.39 against 4.69).
+    if (p.M >= 3 && p.N >= 10 * cus && (p.pa.K >= 4096 || p.M >= 4)) return false;
+  }
   const int nch = p.pa.K / F::KPC;
   if constexpr (F::SUB == 2) {
     // W6 and NVFP4 chunks (32 weights) split over two lanes: at M >= 2, and
@@ -569,15 +581,14 @@ bool launch_rows_gemv(const GemvLaunch& p, int batch, hipStream_t st) {
   return rows_dispatch<F>(pl, RowsGemvBody<F>{a, pl, st});
 }
 
-// MXFP8 matrices of 16 to 32 rows per CU at M <= 2 (shapes its streaming
-// kernel takes): the fma kernel with 2 rows per workgroup up to 8 workgroups
-// per CU, else 4, when every workgroup is resident.  Measured as graph
-// replays from HBM, us at M = 1 / 2, this against the streaming kernel:
-// [4096 x 2560] (R = 2) 4.4 / 5.0 against 4.7 / 5.3; [8192 x 2560] (R = 4)
-// 6.2 / 6.8 against 6.3 / 7.1.  Larger matrices gain nothing ([13312 x 2560]
-// 9.4 / 9.6 against 9.3 / 9.4, [16384 x 2560] 10.3 / 10.9 against 10.3 /
-// 10.6), and at M = 3 the streaming kernel is as fast or faster (5.4 against
-// 5.6 at [4096 x 2560]).
+// MXFP8 matrices of 16 to 20 rows per CU at M = 1 (shapes its streaming
+// kernel takes): the fma kernel with 2 rows per workgroup, when every
+// workgroup is resident.  Measured as graph replays from HBM, us, this
+// against the streaming kernel: [4096 x 2560] 4.44 against 4.66 at M = 1.
+// Since the streaming kernel's five-wave geometry it is the other way round
+// at M = 2 ([4096 x 2560] 5.09 against 4.95) and for more rows ([6144 x 2560]
+// 5.60-5.74 against 5.51-5.54 at M = 1, [8192 x 2560] 6.15-6.41 against
+// 6.06-6.12), so those stream.
 //
 // W6 at M = 1 from 32 to 52 rows per CU (shapes its streaming kernel takes):
 // 2 rows per workgroup with two lanes per chunk, in as many rounds as it
@@ -595,15 +606,13 @@ bool launch_rows_wide(const GemvLaunch& p, hipStream_t st) {
     if (p.N < 32 * cus || p.N > 52 * cus || lanes > kRowsMultiMaxThreads) return false;
     return rows_fma_go<F, 2>(a, 2, lanes, st);
   }
-  if (p.M < 1 || p.M > 2 || !rows_launch_args(p, 1, F::KPC, a)) return false;
+  if (p.M != 1 || !rows_launch_args(p, 1, F::KPC, a)) return false;
   const int cus = device_cus();
   const int nch = p.pa.K / F::KPC;
   const int threads = (nch + 63) / 64 * 64;
-  if (p.N < 16 * cus || p.N > 32 * cus || nch <= 64 || threads > kRowsMultiMaxThreads) return false;
-  const int R = (p.N + 1) / 2 <= 8 * cus ? 2 : 4;
-  const int res = R == 2 ? rows_fma_resident_m<F, 2, 1>(p.M, threads) : rows_fma_resident_m<F, 4, 1>(p.M, threads);
-  if ((p.N + R - 1) / R > (int64_t)res * cus) return false;
-  return rows_fma_go<F, 1>(a, R, threads, st);
+  if (p.N < 16 * cus || p.N > 20 * cus || nch <= 64 || threads > kRowsMultiMaxThreads) return false;
+  if ((p.N + 1) / 2 > (int64_t)rows_fma_resident_m<F, 2, 1>(p.M, threads) * cus) return false;
+  return rows_fma_go<F, 1>(a, 2, threads, st);
 }
 
 }  // namespace fp4x

@@ -497,13 +497,16 @@ def test_rows_gemv_short_rows(gpu, F, N, K, M, monkeypatch):
     ((10, 0), 6144, 3),      # the attention output projection [2560 x 6144]: 2 rows per workgroup
     ((10, 0), 6144, 1),      # M = 1: W6 / NVFP4 one row per workgroup, the 384-chunk formats 2
     ((8, 1), 2560, 4),       # an odd N: the last workgroup's second row lies past N
-    ((16, 1), 2560, 2),      # MXFP8: 4 rows per workgroup ahead of its streaming kernel, N % 4 = 1
+    ((16, 1), 2560, 2),      # 2 rows per workgroup (MXFP8 streams at M = 2), N odd
     ((16, 0), 2560, 1),      # MXFP8 [4096 x 2560] at M = 1: 2 rows per workgroup
+    ((10, 0), 2560, 4),      # MXFP8 and NVFP4 stream at M = 4 from 10 rows per CU
 ])
 def test_rows_gemv_multi(gpu, F, fmt, rows, K, M, monkeypatch):
     """Matrices of at least 8 rows per CU at M = 2..4, and of rows past the
-    one-row kernel's limits, take the fma few-rows kernel with R = 2 (MXFP8 at
-    M <= 2 and 16 rows per CU or more: 2 or 4) rows per workgroup: fp32 sums
+    one-row kernel's limits, take the fma few-rows kernel with R = 2 rows per
+    workgroup (MXFP8 [4096 x 2560] at M = 1 too), except where MXFP8 and
+    NVFP4 stream (10 rows per CU or more at M >= 3 with K >= 4096 and at
+    M = 4; MXFP8 at M = 2), which must then equal the FP4X_ROWS=0 path: fp32 sums
     within the accumulation bound of the exact sums and different from the
     other path's (FP4X_ROWS=0; both within the bound), repeated calls bit for
     bit, bf16 outputs the same sums rounded."""
@@ -523,9 +526,16 @@ def test_rows_gemv_multi(gpu, F, fmt, rows, K, M, monkeypatch):
     y = to_f32(run(F, base, xd, planes, 1, torch.float32))
     with path_switch(monkeypatch, "FP4X_ROWS"):
         y_other = to_f32(run(F, base, xd, planes, 1, torch.float32))
-    assert not np.array_equal(y.view(np.uint32), y_other.view(np.uint32)), "few-rows kernel not taken"
+    # MXFP8 and NVFP4 stream from 10 rows per CU at M >= 3 with K >= 4096 and
+    # at M = 4; MXFP8 at M = 2: the same sums as with the few-rows kernels off
+    streams = (base in ("mx8", "nv4") and M >= 3 and N >= 10 * cus and (K >= 4096 or M >= 4)) or \
+        (base == "mx8" and M == 2)
+    if streams:
+        assert np.array_equal(y.view(np.uint32), y_other.view(np.uint32)), "streaming path not taken"
+    else:
+        assert not np.array_equal(y.view(np.uint32), y_other.view(np.uint32)), "few-rows kernel not taken"
     exact = ordered.exact_sum(x, w_op) * gs
-    for got, parts in ((y, 1), (y_other, 12)):
+    for got, parts in ((y, 12 if streams else 1), (y_other, 12)):
         bound = ordered.mfma_bound(x, w_op, parts) * abs(gs)
         assert np.all(np.abs(got - exact) <= bound), (np.abs(got - exact) / bound).max()
     assert_tol(y, og.matmul_f32(x, w_op) * np.float32(gs), what=f"{fmt} rows N={N} K={K} M={M}")
