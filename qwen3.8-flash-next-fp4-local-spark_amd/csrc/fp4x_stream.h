@@ -1539,7 +1539,13 @@ bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st, int64
 // tiles per CU, which (4, 2, 2) cannot: [8192 x 2560] 5.7 / 5.7 / 5.9 / 6.2 /
 // 6.1 / 6.4 against 5.8 / 7.1 / 8.0 / 8.6 / 9.4 / 10.0 on the few-rows kernel
 // (M <= 2) or the core; [13312 x 2560] 7.0 / 7.2 / 7.4 / 7.6 / 7.8 / 8.1
-// against the core's 10.0 / 10.4 / 10.9 / 11.9 / 12.8 / 13.3.
+// against the core's 10.0 / 10.4 / 10.9 / 11.9 / 12.8 / 13.3.  Rechecked with
+// the K = 2560 instantiation (us at M = 1 / 3 / 16): 16384 x 2560 (2, 2, 2)
+// 7.4 / 7.7 / 9.1 against (1, 5, 2) 8.1 / 8.3 / 10.1, (1, 10, 2) 8.7 / 9.0 /
+// 10.2, (2, 5, 2) 9.8 / 10.8 / 9.7; 13312 x 2560 7.1 / 7.4 / 9.8 against
+// (1, 5, 2) 7.9 / 8.1 / 9.9; only at exactly two tiles per CU, one round of
+// one tile per workgroup, does (1, 5, 2) gain a little (8192 x 2560 5.5 /
+// 5.8 / 6.8 against 5.7 / 5.9 / 6.9).
 inline bool launch_nv4_stream(GemvLaunch p, hipStream_t st) {
   const bool on = switches().nv4_stream;
   const int64_t tiles = (p.N + 15) / 16;
@@ -1598,7 +1604,10 @@ inline bool launch_mx8_stream(GemvLaunch p, hipStream_t st) {
 // 9.5 / 10.6; (2, 2, 5) 8.9 / 9.2 / 10.5; (2, 1, 3) 11.0 / 11.4 / 14.3.  With
 // 128-K units (four loads each, three of them 4-byte): (2, 4, 3) 8.6 / 8.8 /
 // 9.9; (2, 5, 2) 8.4 / 9.0 / 9.8; (1, 10, 2) 9.0 / 9.3 / 10.2.  The core: 9.8
-// / 10.2 / 12.4.
+// / 10.2 / 12.4.  Rechecked with the K = 2560 instantiation: 8192 x 2560 at M =
+// 16 8.3 against (1, 5, 2) 8.9, (2, 5, 2) 9.4; 16384 x 2560 at M = 1 / 3 / 16
+// (2, 2, 2) 10.6-11.3 / 10.8-10.9 / 12.5 against (1, 5, 2) 11.7-12.0 / 12.1 /
+// 14.7, (2, 5, 2) 14.0 / 12.2 / 13.3.
 inline bool launch_w6_stream(GemvLaunch p, hipStream_t st) {
   return launch_dense_stream<StreamW6, 2, 2, 2>(p, 1, switches().w6_stream, st);
 }

@@ -494,7 +494,7 @@ def test_rows_gemv_short_rows(gpu, F, N, K, M, monkeypatch):
 @pytest.mark.parametrize("fmt", ["mx8", "w8", "w8_f16", "w6", "nv4", "bf16"])
 @pytest.mark.parametrize("rows,K,M", [
     # rows as (multiple of the CUs, extra rows)
-    ((10, 0), 6144, 3),      # the attention output projection [2560 x 6144]: 2 rows per workgroup
+    ((10, 0), 6144, 3),      # the attention output projection [2560 x 6144]: 2 rows per workgroup (MXFP8 and NVFP4 stream)
     ((10, 0), 6144, 1),      # M = 1: W6 / NVFP4 one row per workgroup, the 384-chunk formats 2
     ((8, 1), 2560, 4),       # an odd N: the last workgroup's second row lies past N
     ((16, 1), 2560, 2),      # 2 rows per workgroup (MXFP8 streams at M = 2), N odd
@@ -506,7 +506,8 @@ def test_rows_gemv_multi(gpu, F, fmt, rows, K, M, monkeypatch):
     one-row kernel's limits, take the fma few-rows kernel with R = 2 rows per
     workgroup (MXFP8 [4096 x 2560] at M = 1 too), except where MXFP8 and
     NVFP4 stream (10 rows per CU or more at M >= 3 with K >= 4096 and at
-    M = 4; MXFP8 at M = 2), which must then equal the FP4X_ROWS=0 path: fp32 sums
+    M = 4; MXFP8 from 16 rows per CU at M >= 2), which must then equal the
+    FP4X_ROWS=0 path: fp32 sums
     within the accumulation bound of the exact sums and different from the
     other path's (FP4X_ROWS=0; both within the bound), repeated calls bit for
     bit, bf16 outputs the same sums rounded."""
@@ -527,9 +528,10 @@ def test_rows_gemv_multi(gpu, F, fmt, rows, K, M, monkeypatch):
     with path_switch(monkeypatch, "FP4X_ROWS"):
         y_other = to_f32(run(F, base, xd, planes, 1, torch.float32))
     # MXFP8 and NVFP4 stream from 10 rows per CU at M >= 3 with K >= 4096 and
-    # at M = 4; MXFP8 at M = 2: the same sums as with the few-rows kernels off
+    # at M = 4, MXFP8 from 16 rows per CU at M >= 2: the same sums as with the
+    # few-rows kernels off
     streams = (base in ("mx8", "nv4") and M >= 3 and N >= 10 * cus and (K >= 4096 or M >= 4)) or \
-        (base == "mx8" and M == 2)
+        (base == "mx8" and M >= 2 and N >= 16 * cus)
     if streams:
         assert np.array_equal(y.view(np.uint32), y_other.view(np.uint32)), "streaming path not taken"
     else:
