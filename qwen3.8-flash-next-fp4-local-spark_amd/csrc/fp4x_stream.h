@@ -530,6 +530,7 @@ bool launch_w8_stream_cfg(GemvLaunch p, size_t lds, int gx, hipStream_t st) {
 // batch stride 4-byte aligned, enough tiles for a full round on every CU, and
 // the LDS plan within the CU's 160 KB.
 struct StreamW8H;
+struct StreamW8F;
 template <class U, int T, int KW, int D>
 bool launch_dense_stream(GemvLaunch p, int batch, bool on, hipStream_t st, int64_t min_items = -1);
 
@@ -537,14 +538,20 @@ template <bool F16S>
 bool launch_w8_stream(GemvLaunch p, int batch, hipStream_t st) {
   constexpr int T = 6, KW = 2, D = 3;
   if (!switches().w8_stream) return false;            // FP4X_W8_STREAM=0: always the MFMA core
-  // fp16 scales: 256-K units (five loads per 256 K values instead of six).
-  // The 48 layer-batched gates [512 x 2560] at M = 3, measured back to back
-  // on one GPU: (T, KW, D) = (6, 2, 2) 15.2 us against 15.5 for this kernel's
-  // 128-K units; (6, 1, 3) 16.2, (3, 2, 3) 16.6, (2, 5, 2) 16.8.  Calls whose
-  // LDS plan does not fit (M >= 5 with two batch entries per workgroup) take
-  // the 128-K kernel below.
-  if constexpr (F16S)
+  // 256-K units (five loads per 256 K values instead of six).  The 48
+  // layer-batched gates [512 x 2560] at M = 3 with fp16 scales, measured back
+  // to back on one GPU: (T, KW, D) = (6, 2, 2) 15.2 us against 15.5 for this
+  // kernel's 128-K units; (6, 1, 3) 16.2, (3, 2, 3) 16.6, (2, 5, 2) 16.8.
+  // With fp32 scales (StreamW8F, one 4-byte scale load per lane) at M = 3 /
+  // 1: 16.2-16.7 / 15.6-15.8 us against 17.0-17.5 / 16.3-16.6 on the 128-K
+  // kernel (two interleaved pairs of runs on one box).  Calls whose LDS plan
+  // does not fit (M >= 5 with two batch entries per workgroup) take the 128-K
+  // kernel below.
+  if constexpr (F16S) {
     if (launch_dense_stream<StreamW8H, 6, 2, 2>(p, batch, true, st)) return true;
+  } else {
+    if (launch_dense_stream<StreamW8F, 6, 2, 2>(p, batch, true, st)) return true;
+  }
   const int K = p.pa.K, tiles = (p.N + 15) / 16;
   if (p.ksplit != 1 || K % 512 != 0 || p.M > 16 || (K / 128) % KW != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.pa.s) & 3) || (batch > 1 && (p.s_bstride & 3))) return false;
