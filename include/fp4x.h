@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FP4X_ABI_VERSION 11
+#define FP4X_ABI_VERSION 12
 
 enum {
   FP4X_OK = 0,
@@ -183,6 +183,20 @@ int fp4x_refine_nv4(float* out, const void* x, const int64_t* idx, int M, int C,
  * [the draft head's full(-inf) + scatter_, x/fp4patch.py:316-320] */
 int fp4x_scatter_draft(void* out, int64_t out_stride, const float* vals, const int64_t* cand, const int64_t* ids,
                        int64_t n_ids, const float* inv_t, int M, int C, int64_t vocab, void* stream);
+
+/* Draft logits out [M, vocab] bf16 (row stride out_stride) straight from the
+ * candidates: fp4x_refine_nv4 over the rows cand[m, c] of the NVFP4 matrix
+ * (wp [n_ids, K/2], s [n_ids, K/16], gs) followed by fp4x_scatter_draft of
+ * its sums to columns ids[cand[m, c]], in one launch and bit for bit:
+ * out[m, ids[cand[m, c]]] = bf16((sum * gs) * *inv_t) (bf16(sum * gs) when
+ * inv_t is NULL), -inf elsewhere.  The matrix rows and ids are the subset's,
+ * one per row; a cand value outside [0, n_ids) or an ids value outside
+ * [0, vocab) is not written.  C <= 2048, K % 32 == 0; x bf16 [M, K] and wp
+ * 16-byte aligned.  [the draft head's rescore + full(-inf) + scatter_,
+ * x/fp4x_kernels.py:391-416 and x/fp4patch.py:316-320] */
+int fp4x_draft_nv4(void* out, int64_t out_stride, const void* x, const int64_t* cand, const int64_t* ids,
+                   int64_t n_ids, const void* wp, const void* s, float gs, const float* inv_t, int M, int C, int K,
+                   int64_t vocab, void* stream);
 
 /* Weight preparation: quantize an [N, K] matrix (K % 64 == 0) group by group.
  * Source src: FP4X_SRC_F32 / _BF16 (src_a rows, contiguous), _MX8 (src_a

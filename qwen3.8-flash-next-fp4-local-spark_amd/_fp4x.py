@@ -38,6 +38,7 @@ _SIGS = {
     "fp4x_refine_mx8": ([_P, _I, _I64, _P, _P, _I, _I, _P, _P, _I, _I, _P], _I),
     "fp4x_refine_nv4": ([_P, _P, _P, _I, _I, _P, _P, ctypes.c_float, _I, _I, _P], _I),
     "fp4x_scatter_draft": ([_P, _I64, _P, _P, _P, _I64, _P, _I, _I, _I64, _P], _I),
+    "fp4x_draft_nv4": ([_P, _I64, _P, _P, _P, _I64, _P, _P, ctypes.c_float, _P, _I, _I, _I, _I64, _P], _I),
     "fp4x_quantize": ([_I, _P, _P, ctypes.c_float, _I64, _I, _I, _I, _I, ctypes.c_float, _P, _P, _P, _P], _I),
     "fp4x_quantize_w6_clip": ([_I, _P, _P, ctypes.c_float, _I64, _I, _I, _I, _P, _P, _P, _P], _I),
     "fp4x_absmax": ([_I, _P, _P, ctypes.c_float, _I64, _I, _P, _P], _I),
@@ -53,7 +54,7 @@ _SIGS = {
     "fp4x_read_ceiling": ([_P, _I64, _I, _I, _P, _P], _I),
     "fp4x_hold_cus": ([_I, _I64, _I, _P, _P], _I),
 }
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _LIB = None
 

@@ -1013,6 +1013,81 @@ __global__ __launch_bounds__(256) void scatter_draft_kernel(uint16_t* out, int64
   }
 }
 
+// The draft head's rescore and scatter in one launch (refine_nv4 followed by
+// scatter_draft, x/fp4x_kernels.py:391-416 and x/fp4patch.py:316-320):
+// workgroup (b, m) fills columns [b * 2048, b * 2048 + 2048) of row m with
+// -inf, lists the candidates whose column ids[cand[m, c]] falls in them, and
+// rescores those, each on a slot of refine_kernel's lane layout with its
+// loads, fma order and lane reduction, then writes bf16((sum * gs) * inv_t)
+// (bf16(sum * gs) without inv_t) after the fill.  So every element has one
+// writer and equals refine_nv4 + scatter_draft bit for bit, one launch and
+// one dependent round trip fewer.  A candidate outside [0, n_ids) is not
+// written.
+constexpr int kDraftMaxC = 2048;
+
+__global__ __launch_bounds__(kThreads) void draft_nv4_kernel(RefineArgs p, uint16_t* out, const int64_t* ids,
+                                                            const float* inv_t, int64_t vocab) {
+  extern __shared__ __align__(16) uint16_t lds_x[];
+  __shared__ int2 list[kDraftMaxC];               // (column within the block, weight row)
+  __shared__ int n_list;
+  const int m = blockIdx.y;
+  const int64_t c0 = (int64_t)blockIdx.x * kScatterCols;
+  uint16_t* row = out + (int64_t)m * p.out_stride;
+  if (threadIdx.x == 0) n_list = 0;
+  // the first 256 candidates' rows and columns load before the fill
+  auto fetch = [&](int c, int64_t& col, int64_t& j) {
+    col = -1;
+    j = -1;
+    if (c >= p.C) return;
+    j = p.idx[(int64_t)m * p.C + c];
+    if (j < 0 || j >= p.V) { j = -1; return; }
+    col = ids[j];
+  };
+  int64_t col, j;
+  fetch(threadIdx.x, col, j);
+  const int64_t e = c0 + (int64_t)threadIdx.x * 8;
+  if (e + 8 <= vocab && ((reinterpret_cast<uintptr_t>(row + e) & 15) == 0)) {
+    const uint32_t w = 0xFF80FF80u;
+    *reinterpret_cast<uint4*>(row + e) = make_uint4(w, w, w, w);
+  } else {
+    for (int i = 0; i < 8; ++i)
+      if (e + i < vocab) row[e + i] = 0xFF80;
+  }
+  __syncthreads();                                 // n_list = 0 is visible
+  for (int c = threadIdx.x;;) {
+    if (col >= c0 && col < c0 + kScatterCols && col < vocab) {
+      const int at = atomicAdd(&n_list, 1);
+      list[at] = make_int2((int)(col - c0), (int)j);
+    }
+    c += blockDim.x;
+    if (c >= p.C) break;
+    fetch(c, col, j);
+  }
+  __syncthreads();                                 // the fill and the list are complete
+  const int n = n_list;
+  if (n == 0) return;                              // (uniform)
+  const float t = inv_t ? *inv_t : 1.0f;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lpr = p.lpr, lrow = lane & (lpr - 1), slot = lane / lpr, spw = 64 / lpr;
+  for (int b0 = 0; b0 < n; b0 += kWaves * spw) {
+    const int li = b0 + wave * spw + slot;
+    int64_t rows[1] = {li < n ? (int64_t)list[li].y : -1};
+    float acc[1][1] = {{0.0f}};
+    for (int jb = 0; jb < p.cpl; jb += kCplBatch) {
+      ChunkBatch<FmtNV4, 1> cb;
+      load_batch_inbounds<FmtNV4>(cb, p.pa, rows[0], p.K / FmtNV4::KPC, lrow, lpr, jb, p.cpl);
+      if (b0 == 0 && jb == 0) {
+        stage_x<1>(lds_x, p.x + (int64_t)m * p.K, p.K, 1, 0, p.K);
+        __syncthreads();
+      }
+      compute_batch<FmtNV4, 1, 1, const uint16_t*, AccFma>(cb, (const uint16_t*)lds_x, p.K, 0, 1, 0,
+                                                           p.K / FmtNV4::KPC, lrow, lpr, jb, p.cpl, acc);
+    }
+    const float v = group_allreduce(acc[0][0], lpr) * p.gs;
+    if (lrow == 0 && li < n) row[c0 + list[li].x] = f32_to_bf16(inv_t ? v * t : v);
+  }
+}
+
 }  // namespace fp4x
 
 using namespace fp4x;
@@ -1117,6 +1192,37 @@ int fp4x_scatter_draft(void* out, int64_t out_stride, const float* vals, const i
   hipLaunchKernelGGL(scatter_draft_kernel, grid, dim3(256), 0, (hipStream_t)stream, static_cast<uint16_t*>(out),
                      out_stride, vals, cand, ids, n_ids, inv_t, C, vocab);
   return check_launch("scatter_draft");
+}
+
+int fp4x_draft_nv4(void* out, int64_t out_stride, const void* x, const int64_t* cand, const int64_t* ids,
+                   int64_t n_ids, const void* wp, const void* s, float gs, const float* inv_t, int M, int C, int K,
+                   int64_t vocab, void* stream) {
+  if (M < 0 || C < 0 || C > kDraftMaxC || K <= 0 || K % 32 || vocab < 1 || out_stride < vocab || n_ids < 0 ||
+      n_ids > INT32_MAX) {
+    set_error("draft_nv4: bad shape (C <= 2048, K % 32 == 0, vocab >= 1, out_stride >= vocab)");
+    return FP4X_ERR_ARG;
+  }
+  if (!al16(x) || !al16(wp) || (reinterpret_cast<uintptr_t>(s) & 1)) {
+    set_error("draft_nv4: x and wp must be 16-byte aligned, s 2-byte aligned");
+    return FP4X_ERR_ARG;
+  }
+  if (M == 0) return FP4X_OK;
+  RefineArgs p{};
+  p.out = out; p.out_dtype = FP4X_DT_BF16; p.out_stride = out_stride;
+  p.x = static_cast<const uint16_t*>(x);
+  p.idx = cand;
+  p.pa.w0 = static_cast<const uint8_t*>(wp);
+  p.pa.s = static_cast<const uint8_t*>(s);
+  p.pa.K = K;
+  p.gs = gs;
+  p.M = M; p.C = C; p.K = K; p.V = (int)n_ids;
+  const int chunks = K / FmtNV4::KPC;
+  p.lpr = layout_lpr(chunks);
+  p.cpl = (chunks + p.lpr - 1) / p.lpr;
+  dim3 grid((unsigned)((vocab + kScatterCols - 1) / kScatterCols), M);
+  hipLaunchKernelGGL(draft_nv4_kernel, grid, dim3(kThreads), (size_t)K * 2, (hipStream_t)stream, p,
+                     static_cast<uint16_t*>(out), ids, inv_t, vocab);
+  return check_launch("draft_nv4");
 }
 
 int fp4x_refine_nv4(float* out, const void* x, const int64_t* idx, int M, int C, const void* wp, const void* s, float gs,

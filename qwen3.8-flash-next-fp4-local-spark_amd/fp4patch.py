@@ -542,8 +542,8 @@ def _draft_logits(F, h, st, vocab, dc, cfg=(32, 256, 4), inv_t=None):
     if dc and h.shape[0] <= MAX_ROWS:
         # the top dc of the fp32 coarse logits (int2_logits' default dtype, as x/fp4patch.py:313-314 selects)
         _, cand = F.int2_topk(h, *st["c"], st["idx"].numel(), dc, out_dtype=torch.float32, sorted=False)
-        vals = F.refine_nv4(h, cand, st["w"], st["s"], st["gs"])
-        return F.scatter_draft(vals, cand, st["idx"], vocab, inv_t)
+        # their exact NVFP4 logits scattered into the -inf row: one launch (refine_nv4 + scatter_draft)
+        return F.draft_nv4(h, cand, st["w"], st["s"], st["gs"], st["idx"], vocab, inv_t)
     sub = F.nv4_linear(h, st["w"], st["s"], st["gs"], cfg)
     full = torch.full((h.shape[0], vocab), float("-inf"), dtype=sub.dtype, device=sub.device)
     full.index_copy_(1, st["idx"], sub)

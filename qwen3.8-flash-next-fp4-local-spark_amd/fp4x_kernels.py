@@ -24,7 +24,7 @@ import _fp4x as _L
 
 __all__ = [
     "mx8_linear", "bf16_linear", "nv4_linear", "w8_linear", "w6_linear", "int2_logits", "refine_mx8_", "refine_nv4",
-    "scatter_draft",
+    "scatter_draft", "draft_nv4",
     "topk_rows", "int2_topk", "w8_linear_layers", "HCFused", "hc_scaled_silu", "hc_gate_mean",
     "quantize_w8", "quantize_w6", "quantize_nv4", "quantize_int2", "quantize_mx8",
     "mx8_dequant", "dequant_int2", "dequant_nv4", "dequant_operand", "requantize_mx8", "requantize_nv4", "ORDER",
@@ -345,6 +345,28 @@ def scatter_draft(vals, cand, ids, vocab, inv_t=None):
     _L.check(_L.lib().fp4x_scatter_draft(_ptr(out), out.stride(0), _ptr(vals), _ptr(cand), _ptr(ids), ids.numel(),
                                          None if inv_t is None else _ptr(inv_t), m, C, vocab, _L.stream_of(vals)),
              "scatter_draft")
+    return out
+
+
+def draft_nv4(x, cand, wp, s, gs, ids, vocab, inv_t=None):
+    """Draft logits [M, vocab] bf16 from the candidates in one launch:
+    scatter_draft(refine_nv4(x, cand, wp, s, gs), cand, ids, vocab, inv_t),
+    bit for bit (wp / s: the subset's NVFP4 rows, one per entry of ids)."""
+    _need_cuda(x, cand, wp, s, ids)
+    x = x.to(torch.bfloat16).contiguous()
+    cand = cand.to(torch.int64).contiguous()
+    ids = ids.to(torch.int64).contiguous()
+    if inv_t is not None:
+        _need_cuda(inv_t)
+        if inv_t.dtype != torch.float32 or inv_t.numel() != 1:
+            raise ValueError("fp4x: draft_nv4 needs inv_t as one fp32 element")
+    if cand.dim() != 2 or cand.shape[0] != x.shape[0] or wp.shape[0] != ids.numel():
+        raise ValueError("fp4x: draft_nv4 needs cand [M, C] for x [M, K] and one ids entry per weight row")
+    m, C = cand.shape
+    out = torch.empty((m, vocab), dtype=torch.bfloat16, device=x.device)
+    _L.check(_L.lib().fp4x_draft_nv4(_ptr(out), out.stride(0), _ptr(x), _ptr(cand), _ptr(ids), ids.numel(),
+                                     _ptr(wp), _ptr(s), float(gs), None if inv_t is None else _ptr(inv_t), m, C,
+                                     x.shape[1], vocab, _L.stream_of(x)), "draft_nv4")
     return out
 
 

@@ -532,3 +532,32 @@ def test_scatter_draft(gpu, F, vocab):
     for m in range(M):
         ref[m, ids[cand[m][keep[m]]]] = vals[m][keep[m]].to(torch.bfloat16)
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("vocab,C,dense", [(248320, 64, False), (30001, 300, False), (30001, 600, True), (300, 64, True)])
+def test_draft_nv4_fused(gpu, F, vocab, C, dense):
+    """draft_nv4 (the rescore and the scatter in one launch) equals refine_nv4
+    followed by scatter_draft bit for bit: with and without inv_t, on 16-byte
+    and odd row lengths, with more candidates than threads, with many
+    candidates in one 2048-column block (dense ids: several rounds of rescore
+    slots), with repeated candidates, and with out-of-range cand entries left
+    -inf."""
+    g = torch.Generator(device=gpu).manual_seed(vocab + C)
+    M, K = 3, 2560
+    nsub = min(vocab, 6000)
+    ids = torch.arange(nsub, device=gpu) if dense else \
+        torch.sort(torch.randperm(vocab, generator=g, device=gpu)[:nsub]).values
+    P, S, gs = F.quantize_nv4(torch.randn((nsub, K), generator=g, device=gpu) * 0.02)
+    h = (torch.randn((M, K), generator=g, device=gpu)).to(torch.bfloat16)
+    cand = torch.stack([torch.randperm(nsub, generator=g, device=gpu)[:C] for _ in range(M)])
+    cand[2, 1] = cand[2, 0]                           # a repeated candidate
+    bad = cand.clone()
+    bad[0, 0], bad[1, C - 1] = -1, nsub               # out of range: not written
+    for cc in (cand, bad):
+        for inv_t in (None, torch.full((1,), 1.0 / 0.7, device=gpu)):
+            print(f"vocab={vocab} C={C} dense={dense} inv_t={inv_t is not None}", flush=True)
+            got = F.draft_nv4(h, cc, P, S, gs, ids, vocab, inv_t)
+            ref = F.scatter_draft(F.refine_nv4(h, cc, P, S, gs), cc, ids, vocab, inv_t)
+            assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+            assert int((got.view(torch.int16) != -128).sum()) == len(set(
+                (m, int(i)) for m in range(M) for i in cc[m].tolist() if 0 <= i < nsub))
