@@ -1014,69 +1014,42 @@ __global__ __launch_bounds__(256) void scatter_draft_kernel(uint16_t* out, int64
 }
 
 // The draft head's rescore and scatter in one launch (refine_nv4 followed by
-// scatter_draft, x/fp4x_kernels.py:391-416 and x/fp4patch.py:316-320):
-// workgroup (b, m) fills columns [b * 2048, b * 2048 + 2048) of row m with
-// -inf, lists the candidates whose column ids[cand[m, c]] falls in them, and
-// rescores those, each on a slot of refine_kernel's lane layout with its
-// loads, fma order and lane reduction, then writes bf16((sum * gs) * inv_t)
-// (bf16(sum * gs) without inv_t) after the fill.  So every element has one
-// writer and equals refine_nv4 + scatter_draft bit for bit, one launch and
-// one dependent round trip fewer.  A candidate outside [0, n_ids) is not
-// written.
+// scatter_draft, x/fp4x_kernels.py:391-416 and x/fp4patch.py:316-320), with
+// two kinds of workgroups that write disjoint elements, so neither waits for
+// the other:
+//   * rescore workgroups (blockIdx.x < nr): refine_kernel's candidate slots,
+//     loads, fma order and lane reduction; each writes its candidate's
+//     bf16((sum * gs) * inv_t) (bf16(sum * gs) without inv_t) at column
+//     ids[cand[m, c]], whose load goes out beside the weight loads;
+//   * fill workgroups (b, m): -inf over columns [b * 2048, b * 2048 + 2048)
+//     of row m except the candidates' columns (an LDS bitmap of them).
+// Every element has one writer (a repeated candidate writes the same value
+// twice), and the output equals refine_nv4 + scatter_draft bit for bit.  A
+// candidate outside [0, n_ids), or whose column lies outside [0, vocab), is
+// not written.
 constexpr int kDraftMaxC = 2048;
 
 __global__ __launch_bounds__(kThreads) void draft_nv4_kernel(RefineArgs p, uint16_t* out, const int64_t* ids,
-                                                            const float* inv_t, int64_t vocab) {
+                                                            const float* inv_t, int64_t vocab, int nr) {
   extern __shared__ __align__(16) uint16_t lds_x[];
-  __shared__ int2 list[kDraftMaxC];               // (column within the block, weight row)
-  __shared__ int n_list;
+  __shared__ uint32_t mark[kScatterCols / 32];    // the block's candidate columns
   const int m = blockIdx.y;
-  const int64_t c0 = (int64_t)blockIdx.x * kScatterCols;
   uint16_t* row = out + (int64_t)m * p.out_stride;
-  if (threadIdx.x == 0) n_list = 0;
-  // the first 256 candidates' rows and columns load before the fill
-  auto fetch = [&](int c, int64_t& col, int64_t& j) {
-    col = -1;
-    j = -1;
-    if (c >= p.C) return;
-    j = p.idx[(int64_t)m * p.C + c];
-    if (j < 0 || j >= p.V) { j = -1; return; }
-    col = ids[j];
-  };
-  int64_t col, j;
-  fetch(threadIdx.x, col, j);
-  const int64_t e = c0 + (int64_t)threadIdx.x * 8;
-  if (e + 8 <= vocab && ((reinterpret_cast<uintptr_t>(row + e) & 15) == 0)) {
-    const uint32_t w = 0xFF80FF80u;
-    *reinterpret_cast<uint4*>(row + e) = make_uint4(w, w, w, w);
-  } else {
-    for (int i = 0; i < 8; ++i)
-      if (e + i < vocab) row[e + i] = 0xFF80;
-  }
-  __syncthreads();                                 // n_list = 0 is visible
-  for (int c = threadIdx.x;;) {
-    if (col >= c0 && col < c0 + kScatterCols && col < vocab) {
-      const int at = atomicAdd(&n_list, 1);
-      list[at] = make_int2((int)(col - c0), (int)j);
+  if ((int)blockIdx.x < nr) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lpr = p.lpr, lrow = lane & (lpr - 1), slot = lane / lpr, spw = 64 / lpr;
+    const int cand = blockIdx.x * (kWaves * spw) + wave * spw + slot;
+    int64_t rows[1] = {-1};
+    if (cand < p.C) {
+      const int64_t r = p.idx[(int64_t)m * p.C + cand];
+      rows[0] = (r >= 0 && r < p.V) ? r : -1;
     }
-    c += blockDim.x;
-    if (c >= p.C) break;
-    fetch(c, col, j);
-  }
-  __syncthreads();                                 // the fill and the list are complete
-  const int n = n_list;
-  if (n == 0) return;                              // (uniform)
-  const float t = inv_t ? *inv_t : 1.0f;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int lpr = p.lpr, lrow = lane & (lpr - 1), slot = lane / lpr, spw = 64 / lpr;
-  for (int b0 = 0; b0 < n; b0 += kWaves * spw) {
-    const int li = b0 + wave * spw + slot;
-    int64_t rows[1] = {li < n ? (int64_t)list[li].y : -1};
+    const int64_t col = rows[0] >= 0 ? ids[rows[0]] : -1;
     float acc[1][1] = {{0.0f}};
     for (int jb = 0; jb < p.cpl; jb += kCplBatch) {
       ChunkBatch<FmtNV4, 1> cb;
       load_batch_inbounds<FmtNV4>(cb, p.pa, rows[0], p.K / FmtNV4::KPC, lrow, lpr, jb, p.cpl);
-      if (b0 == 0 && jb == 0) {
+      if (jb == 0) {
         stage_x<1>(lds_x, p.x + (int64_t)m * p.K, p.K, 1, 0, p.K);
         __syncthreads();
       }
@@ -1084,7 +1057,34 @@ __global__ __launch_bounds__(kThreads) void draft_nv4_kernel(RefineArgs p, uint1
                                                            p.K / FmtNV4::KPC, lrow, lpr, jb, p.cpl, acc);
     }
     const float v = group_allreduce(acc[0][0], lpr) * p.gs;
-    if (lrow == 0 && li < n) row[c0 + list[li].x] = f32_to_bf16(inv_t ? v * t : v);
+    if (lrow == 0 && col >= 0 && col < vocab) {
+      const float t = inv_t ? *inv_t : 1.0f;
+      row[col] = f32_to_bf16(inv_t ? v * t : v);
+    }
+    return;
+  }
+  const int64_t c0 = (int64_t)(blockIdx.x - nr) * kScatterCols;
+  if (threadIdx.x < kScatterCols / 32) mark[threadIdx.x] = 0u;
+  __syncthreads();
+  for (int c = threadIdx.x; c < p.C; c += blockDim.x) {
+    const int64_t j = p.idx[(int64_t)m * p.C + c];
+    if (j < 0 || j >= p.V) continue;
+    const int64_t col = ids[j];
+    if (col >= c0 && col < c0 + kScatterCols && col < vocab) {
+      const int o = (int)(col - c0);
+      atomicOr(&mark[o >> 5], 1u << (o & 31));
+    }
+  }
+  __syncthreads();
+  const int o = (int)threadIdx.x * 8;
+  const int64_t e = c0 + o;
+  const uint32_t mk = (mark[o >> 5] >> (o & 31)) & 0xffu;
+  if (mk == 0 && e + 8 <= vocab && ((reinterpret_cast<uintptr_t>(row + e) & 15) == 0)) {
+    const uint32_t w = 0xFF80FF80u;
+    *reinterpret_cast<uint4*>(row + e) = make_uint4(w, w, w, w);
+  } else {
+    for (int i = 0; i < 8; ++i)
+      if (e + i < vocab && !((mk >> i) & 1u)) row[e + i] = 0xFF80;
   }
 }
 
@@ -1219,9 +1219,10 @@ int fp4x_draft_nv4(void* out, int64_t out_stride, const void* x, const int64_t* 
   const int chunks = K / FmtNV4::KPC;
   p.lpr = layout_lpr(chunks);
   p.cpl = (chunks + p.lpr - 1) / p.lpr;
-  dim3 grid((unsigned)((vocab + kScatterCols - 1) / kScatterCols), M);
+  const int nr = (C + kWaves * (64 / p.lpr) - 1) / (kWaves * (64 / p.lpr));   // rescore workgroups per row
+  dim3 grid((unsigned)(nr + (vocab + kScatterCols - 1) / kScatterCols), M);
   hipLaunchKernelGGL(draft_nv4_kernel, grid, dim3(kThreads), (size_t)K * 2, (hipStream_t)stream, p,
-                     static_cast<uint16_t*>(out), ids, inv_t, vocab);
+                     static_cast<uint16_t*>(out), ids, inv_t, vocab, nr);
   return check_launch("draft_nv4");
 }
 

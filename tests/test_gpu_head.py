@@ -539,9 +539,9 @@ def test_draft_nv4_fused(gpu, F, vocab, C, dense):
     """draft_nv4 (the rescore and the scatter in one launch) equals refine_nv4
     followed by scatter_draft bit for bit: with and without inv_t, on 16-byte
     and odd row lengths, with more candidates than threads, with many
-    candidates in one 2048-column block (dense ids: several rounds of rescore
-    slots), with repeated candidates, and with out-of-range cand entries left
-    -inf."""
+    candidates in one 2048-column block (dense ids: the fill skips many
+    columns of each 8-column store), with repeated candidates, and with
+    out-of-range cand entries left -inf."""
     g = torch.Generator(device=gpu).manual_seed(vocab + C)
     M, K = 3, 2560
     nsub = min(vocab, 6000)
