@@ -191,7 +191,8 @@ int fp4x_scatter_draft(void* out, int64_t out_stride, const float* vals, const i
  * out[m, ids[cand[m, c]]] = bf16((sum * gs) * *inv_t) (bf16(sum * gs) when
  * inv_t is NULL), -inf elsewhere.  The matrix rows and ids are the subset's,
  * one per row; a cand value outside [0, n_ids) or an ids value outside
- * [0, vocab) is not written.  C <= 2048, K % 32 == 0; x bf16 [M, K] and wp
+ * [0, vocab) is not written.  C <= 2048, K % 32 == 0, n_ids > 0 (when M and
+ * C are); x bf16 [M, K] and wp
  * 16-byte aligned.  [the draft head's rescore + full(-inf) + scatter_,
  * x/fp4x_kernels.py:391-416 and x/fp4patch.py:316-320] */
 int fp4x_draft_nv4(void* out, int64_t out_stride, const void* x, const int64_t* cand, const int64_t* ids,

@@ -1198,8 +1198,8 @@ int fp4x_draft_nv4(void* out, int64_t out_stride, const void* x, const int64_t* 
                    int64_t n_ids, const void* wp, const void* s, float gs, const float* inv_t, int M, int C, int K,
                    int64_t vocab, void* stream) {
   if (M < 0 || C < 0 || C > kDraftMaxC || K <= 0 || K % 32 || vocab < 1 || out_stride < vocab || n_ids < 0 ||
-      n_ids > INT32_MAX) {
-    set_error("draft_nv4: bad shape (C <= 2048, K % 32 == 0, vocab >= 1, out_stride >= vocab)");
+      n_ids > INT32_MAX || (n_ids == 0 && M > 0 && C > 0)) {
+    set_error("draft_nv4: bad shape (C <= 2048, K % 32 == 0, vocab >= 1, out_stride >= vocab, n_ids > 0)");
     return FP4X_ERR_ARG;
   }
   if (!al16(x) || !al16(wp) || (reinterpret_cast<uintptr_t>(s) & 1)) {

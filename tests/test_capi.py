@@ -29,7 +29,7 @@ def test_header_declares_entry_points():
                  "fp4x_topk_rows", "fp4x_refine_mx8", "fp4x_hc_down", "fp4x_hc_up", "fp4x_hc_scaled_silu",
                  "fp4x_hc_gate_mean", "fp4x_bf16_linear", "fp4x_w8_linear_layers", "fp4x_mx8_dequant",
                  "fp4x_hc_mix", "fp4x_int2_topk", "fp4x_refine_nv4", "fp4x_scatter_draft", "fp4x_quantize",
-                 "fp4x_absmax"):
+                 "fp4x_absmax", "fp4x_draft_nv4"):
         assert must in names
 
 
@@ -88,6 +88,14 @@ def test_argument_errors_without_gpu(lib):
     assert b"refine_nv4" in L.fp4x_last_error()
     assert L.fp4x_scatter_draft(None, 100, None, None, None, 10, None, 3, 64, 248320, None) == _fp4x.ERR_ARG
     assert b"scatter_draft" in L.fp4x_last_error()
+    # the one-launch rescore + scatter: no weight rows (n_ids = 0), K % 32, C past 2048
+    assert L.fp4x_draft_nv4(None, 248320, None, None, None, 0, None, None, 1.0, None, 3, 64, 2560, 248320,
+                            None) == _fp4x.ERR_ARG
+    assert L.fp4x_draft_nv4(None, 248320, None, None, None, 100, None, None, 1.0, None, 3, 64, 2500, 248320,
+                            None) == _fp4x.ERR_ARG
+    assert L.fp4x_draft_nv4(None, 248320, None, None, None, 100, None, None, 1.0, None, 3, 2049, 2560, 248320,
+                            None) == _fp4x.ERR_ARG
+    assert b"draft_nv4" in L.fp4x_last_error()
     # weight preparation: K % 64, the INT2 group, W6 qmax, NVFP4 gs, packed sources without scales
     Q = L.fp4x_quantize
     assert Q(0, None, None, 0.0, 8, 96, 0, 16, 31, 0.0, None, None, None, None) == _fp4x.ERR_ARG
